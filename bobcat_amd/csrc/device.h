@@ -1,0 +1,73 @@
+// Device helpers shared by the gfx950 kernels: wave64 reductions, half
+// conversion, and the Q4_K super-block decoder.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace bch {
+
+constexpr int kWave = 64;
+
+// Sum of `v` over groups of `width` consecutive lanes (width a power of two
+// up to 64); every lane of a group receives the group's sum.
+template <int width>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int off = width / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<kWave>(v); }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+// Sum over a workgroup of `threads` threads; `scratch` holds threads/64
+// floats.  Every thread receives the total.
+template <int threads>
+__device__ __forceinline__ float block_sum(float v, float *scratch) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  if (threads > kWave) {
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < threads / kWave; w++) t += scratch[w];
+    __syncthreads();
+    return t;
+  }
+  return v;
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
+  return __half2float(__ushort_as_half((unsigned short)bits16));
+}
+
+// Byte k of a dword as a float; the backend selects v_cvt_f32_ubyte{k}.
+__device__ __forceinline__ float ubyte0(uint32_t w) { return (float)((w >> 0) & 0xffu); }
+__device__ __forceinline__ float ubyte1(uint32_t w) { return (float)((w >> 8) & 0xffu); }
+__device__ __forceinline__ float ubyte2(uint32_t w) { return (float)((w >> 16) & 0xffu); }
+__device__ __forceinline__ float ubyte3(uint32_t w) { return (float)((w >> 24) & 0xffu); }
+
+// The 6-bit scales and minimums of 32-element blocks 2p and 2p+1 of a Q4_K
+// super-block, packed as bytes (scale_2p, scale_2p+1, min_2p, min_2p+1).
+// h1, h2, h3 are header dwords 1..3 (the 12 scale bytes s[0..11]).  The
+// unpacking is q4k_scale_min (crates/bobcat/src/scalar.rs:116-125) for
+// two blocks at once.
+__device__ __forceinline__ uint32_t q4k_pair_scales(uint32_t h1, uint32_t h2, uint32_t h3, int p) {
+  const int sh = 16 * (p & 1);
+  const uint32_t a = (h1 >> sh) & 0xffffu;  // s[2p'], s[2p'+1] with p' = p & 1
+  const uint32_t b = (h2 >> sh) & 0xffffu;  // s[2p'+4], s[2p'+5]
+  if (p < 2) return (a & 0x3f3fu) | ((b & 0x3f3fu) << 16);
+  const uint32_t c = (h3 >> sh) & 0xffffu;  // s[2p+4], s[2p+5] for p >= 2
+  const uint32_t sc = (c & 0x0f0fu) | ((a >> 2) & 0x3030u);
+  const uint32_t mn = ((c >> 4) & 0x0f0fu) | ((b >> 2) & 0x3030u);
+  return sc | (mn << 16);
+}
+
+}  // namespace bch

@@ -1,0 +1,311 @@
+/* bobcat_hip.h — C ABI of the MI355X (gfx950) backend for bobcat's per-token
+ * language-model loop.
+ *
+ * The op set mirrors the concrete `bobcat_metal::Metal` API that bobcat's
+ * drivers call today (crates/bobcat-metal/src/backend.rs:1027-2699,
+ * re-exported at crates/bobcat-metal/src/lib.rs:13-17).  Every launcher takes
+ * views (buffer, byte offset) as the reference does (backend.rs:300-341),
+ * checks each view against its buffer's length before launching
+ * (backend.rs:1297-1314, 2771-2790), and returns a status code; the message of
+ * the last failure on the calling thread comes from bch_last_error().
+ *
+ * Work goes onto one in-order HIP stream per context, so the reference's
+ * barriers (backend.rs:1255) order nothing extra here and cost nothing.
+ * bch_commit() returns a monotonically increasing ticket and bch_wait(t)
+ * drains every ticket up to t (crates/bobcat-metal/src/commands.rs:293-338).
+ *
+ * Sizes are u32 as in the reference; byte offsets and lengths are u64.
+ * No HIP or torch type appears in any signature.
+ */
+#ifndef BOBCAT_HIP_H
+#define BOBCAT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ */
+/* Status codes: one per variant of bobcat_metal::Error                */
+/* (crates/bobcat-metal/src/backend.rs:162-298) that can arise here.   */
+/* ------------------------------------------------------------------ */
+typedef enum bch_status {
+  BCH_OK = 0,
+  BCH_ERR_NO_DEVICE = 1,        /* Error::NoDevice */
+  BCH_ERR_ALLOCATION = 2,       /* Error::Allocation */
+  BCH_ERR_NOT_RECORDING = 3,    /* Error::NotRecording */
+  BCH_ERR_ALREADY_RECORDING = 4,/* Error::AlreadyRecording */
+  BCH_ERR_OUT_OF_BOUNDS = 5,    /* Error::OutOfBounds */
+  BCH_ERR_FOREIGN_BUFFER = 6,   /* Error::ForeignBuffer */
+  BCH_ERR_BUSY = 7,             /* Error::Busy */
+  BCH_ERR_ACCESS = 8,           /* Error::Access */
+  BCH_ERR_ATTENTION_LIMITS = 9, /* Error::AttentionLimits */
+  BCH_ERR_UNSUPPORTED_FORMAT = 10, /* Error::NoFusedConv / NoExpansion / NoExperts */
+  BCH_ERR_DELTANET_LIMITS = 11, /* Error::DeltaNetLimits */
+  BCH_ERR_EXPERT_LIMITS = 12,   /* Error::ExpertLimits */
+  BCH_ERR_EXECUTION = 13,       /* Error::Execution */
+  BCH_ERR_ARGUMENT = 14,        /* bobcat::Error::Argument (crates/bobcat/src/error.rs) */
+  BCH_ERR_CONTEXT_FULL = 15,    /* bobcat::Error::ContextFull */
+  BCH_ERR_TOKEN = 16,           /* bobcat::Error::Token */
+  BCH_ERR_GATE_SHAPE = 17,      /* Error::GateShape */
+} bch_status;
+
+/* Return the message of the last failed call on this thread ("" if none). */
+const char *bch_last_error(void);
+
+/* ------------------------------------------------------------------ */
+/* Weight formats.  Values are ggml type ids, as TensorType::id        */
+/* (crates/bobcat-gguf/src/lib.rs:137-148); the block layouts match    */
+/* ggml's (scalar.rs:56-202).                                          */
+/* ------------------------------------------------------------------ */
+typedef enum bch_format {
+  BCH_F32 = 0,
+  BCH_F16 = 1,
+  BCH_Q4_0 = 2,
+  BCH_Q8_0 = 8,
+  BCH_Q4K = 12,
+  BCH_Q5K = 13,
+  BCH_Q6K = 14,
+  BCH_BF16 = 30,
+} bch_format;
+
+/* Bytes of one row of n_cols elements of `format` (scalar.rs:28-31), or 0
+ * when n_cols fills no whole number of blocks or the format is unknown. */
+uint64_t bch_row_bytes(uint32_t format, uint32_t n_cols);
+
+/* ------------------------------------------------------------------ */
+/* Device, buffers, views (backend.rs:1083-1230)                        */
+/* ------------------------------------------------------------------ */
+typedef struct bch_ctx bch_ctx;
+typedef struct bch_buffer bch_buffer;
+
+/* A position inside a buffer, as bobcat_metal::View (backend.rs:337-341). */
+typedef struct bch_view {
+  bch_buffer *buffer;
+  uint64_t offset;
+} bch_view;
+
+/* An RMS normalization a matrix-vector launch applies to its input first
+ * (bobcat_metal::Norm, backend.rs:344-350). */
+typedef struct bch_norm {
+  bch_view weight;
+  float eps;
+} bch_norm;
+
+/* Metal::open (backend.rs:1083).  Opens device 0 and one stream. */
+int bch_open(bch_ctx **out);
+void bch_close(bch_ctx *ctx);
+/* Name of the device and its compute-unit count, for reports. */
+int bch_device_info(bch_ctx *ctx, char *name, size_t name_len, uint32_t *n_cus);
+
+/* Metal::new_buffer (backend.rs:1124): `len` zeroed bytes of HBM. */
+int bch_buffer_new(bch_ctx *ctx, uint64_t len, bch_buffer **out);
+/* Metal::wrap_mapping (backend.rs:1145): the weights of a file.  MI355X has
+ * no unified memory, so the bytes are copied to HBM once. */
+int bch_buffer_from_host(bch_ctx *ctx, const void *data, uint64_t len, bch_buffer **out);
+void bch_buffer_free(bch_buffer *buffer);
+uint64_t bch_buffer_len(const bch_buffer *buffer);
+/* The device address of the buffer's first byte, for interop. */
+void *bch_buffer_device_ptr(const bch_buffer *buffer);
+
+/* Metal::write / Metal::read (backend.rs:1180-1230).  Fail with BCH_ERR_BUSY
+ * while committed work is in flight and with BCH_ERR_ACCESS past the end. */
+int bch_write(bch_ctx *ctx, bch_view view, const void *data, uint64_t bytes);
+int bch_read(bch_ctx *ctx, bch_view view, void *out, uint64_t bytes);
+
+/* ------------------------------------------------------------------ */
+/* Recording (backend.rs:1244-1295, commands.rs:207-411)               */
+/* ------------------------------------------------------------------ */
+int bch_begin(bch_ctx *ctx);
+void bch_discard(bch_ctx *ctx);
+/* Launches on one in-order stream are ordered already; kept for parity. */
+void bch_barrier(bch_ctx *ctx);
+int bch_commit(bch_ctx *ctx, uint64_t *ticket);
+/* Wait for `ticket` and every earlier one; *gpu_seconds (nullable) receives
+ * the device time between the commit's begin and its end. */
+int bch_wait(bch_ctx *ctx, uint64_t ticket, double *gpu_seconds);
+/* commit + wait (Metal::end, backend.rs:1276). */
+int bch_end(bch_ctx *ctx, double *gpu_seconds);
+
+/* Metal::set_profiling / profile (backend.rs:1285-1295, 376-391). */
+typedef struct bch_profile_entry {
+  char name[48];
+  uint32_t n_rows;
+  uint32_t n_cols;
+  uint64_t calls;
+  double seconds;
+  uint64_t bytes;
+} bch_profile_entry;
+void bch_set_profiling(bch_ctx *ctx, int enabled);
+uint32_t bch_profile_count(const bch_ctx *ctx);
+int bch_profile_get(const bch_ctx *ctx, uint32_t index, bch_profile_entry *out);
+
+/* ------------------------------------------------------------------ */
+/* Ops.  Each records one or more launches on the context's stream.    */
+/* ------------------------------------------------------------------ */
+
+/* Dequantize n_rows rows of n_cols weights of `format` into floats at
+ * `out` (scalar::dequantize, scalar.rs:59-79; bit-exact). */
+int bch_dequantize(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_rows,
+                   uint32_t n_cols, bch_view out);
+
+/* Metal::matvec (backend.rs:1344-1380): y (=|+=) W·x, optionally with the
+ * RMS norm of x fused in (norm may be NULL). */
+int bch_matvec(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_rows,
+               uint32_t n_cols, bch_view x, bch_view y, const bch_norm *norm,
+               int accumulate);
+
+/* Metal::matvec_swiglu (backend.rs:1385-1417): y = silu(G·n(x)) ⊙ (U·n(x)). */
+int bch_matvec_swiglu(bch_ctx *ctx, uint32_t format, bch_view gate, bch_view up,
+                      uint32_t n_rows, uint32_t n_cols, bch_view x, bch_norm norm,
+                      bch_view y);
+
+/* Metal::matvec_conv (backend.rs:2329-2377): the 3·n_embd-row input
+ * projection of a gated short convolution followed by the convolution of
+ * one token; updates `history` ((kernel_size-1)·n_embd floats). */
+int bch_matvec_conv(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_cols,
+                    bch_view x, const bch_norm *norm, bch_view taps, bch_view history,
+                    bch_view out, uint32_t n_embd, uint32_t kernel_size);
+
+/* Metal::short_conv / short_conv_batch (backend.rs:2384-2465): the gated
+ * short convolution of n_tokens tokens whose rows of 3·n_embd floats at
+ * `bcx` hold B, C and X. */
+int bch_short_conv(bch_ctx *ctx, bch_view bcx, bch_view taps, bch_view history,
+                   bch_view out, uint32_t n_embd, uint32_t kernel_size, uint32_t n_tokens);
+
+/* Metal::rms_norm (backend.rs:2034-2059). */
+int bch_rms_norm(bch_ctx *ctx, bch_view x, bch_view weight, bch_view out, uint32_t n,
+                 uint32_t n_rows, float eps);
+
+/* Metal::norm_rope (backend.rs:2070-2123). */
+int bch_norm_rope(bch_ctx *ctx, bch_view src, bch_view dst, int dst_half, bch_view weight,
+                  uint32_t n_heads, uint32_t head_dim, uint32_t n_rot,
+                  uint32_t src_head_stride, uint32_t pos, uint32_t n_tokens,
+                  uint32_t src_stride, uint32_t dst_stride, float theta, float eps);
+
+/* Metal::convert_half / copy (backend.rs:2126, 2552). */
+int bch_convert_half(bch_ctx *ctx, bch_view src, bch_view dst, uint32_t n);
+int bch_copy(bch_ctx *ctx, bch_view src, bch_view dst, uint32_t n);
+
+/* Metal::embed (backend.rs:2570-2608): dequantize rows tokens[t] of the
+ * n_vocab-row matrix into `out`, for n_tokens u32 token ids. */
+int bch_embed(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_vocab,
+              bch_view tokens, bch_view out, uint32_t n_embd, uint32_t n_tokens);
+
+/* Metal::attention (backend.rs:2150-2320): causal GQA attention of
+ * n_queries queries at positions first_pos.. over an f16 or f32 cache laid
+ * out [pos][kv_head][head_dim].  `scratch` holds
+ * bch_attention_scratch_floats(...) floats. */
+int bch_attention(bch_ctx *ctx, bch_view q, bch_view k_cache, bch_view v_cache, int kv_half,
+                  bch_view scratch, bch_view out, uint32_t n_heads, uint32_t n_kv_heads,
+                  uint32_t head_dim, uint32_t first_pos, uint32_t n_queries, uint32_t n_ctx);
+/* attention_scratch_floats (backend.rs:2739-2748). */
+uint64_t bch_attention_scratch_floats(uint32_t n_heads, uint32_t head_dim, uint32_t n_ctx,
+                                      uint32_t n_queries);
+
+/* Metal::matmul (backend.rs:2470-2516): Y[t] (store) W·X[t] for n_tokens
+ * rows of n_cols floats at x; store as bobcat_metal::Store
+ * (backend.rs:360-370). */
+typedef enum bch_store { BCH_STORE_OVERWRITE = 0, BCH_STORE_ACCUMULATE = 1, BCH_STORE_SWIGLU = 2 } bch_store;
+int bch_matmul(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_rows,
+               uint32_t n_cols, bch_view x, bch_view y, uint32_t n_tokens, uint32_t store);
+
+/* Metal::argmax (backend.rs:2612): index of the largest of n floats, ties
+ * to the lowest index, as a u32 at `out`. */
+int bch_argmax(bch_ctx *ctx, bch_view x, bch_view out, uint32_t n);
+
+/* ------------------------------------------------------------------ */
+/* LFM2 driver (crates/bobcat/src/lfm2_metal.rs:125-779)               */
+/* ------------------------------------------------------------------ */
+
+/* A matrix of the model: n_rows rows of n_cols elements of `format` at
+ * host address `data` (ggml's ne[1], ne[0]; lfm2.rs:66-71). */
+typedef struct bch_matrix {
+  uint32_t format;
+  uint32_t n_rows;
+  uint32_t n_cols;
+  const void *data;
+} bch_matrix;
+
+/* One LFM2 layer (lfm2.rs:150-170).  `is_attention` picks the mixer;
+ * `is_moe` picks the feed-forward block.  Unused members stay zero. */
+typedef struct bch_lfm2_layer {
+  uint32_t is_attention;
+  uint32_t is_moe;
+  const float *attn_norm;   /* [n_embd] */
+  const float *ffn_norm;    /* [n_embd] */
+  /* convolution mixer */
+  const float *conv_taps;   /* [n_embd][conv_kernel] */
+  bch_matrix in_proj;       /* 3·n_embd × n_embd */
+  bch_matrix out_proj;      /* n_embd × n_embd */
+  /* attention mixer */
+  bch_matrix wq, wk, wv, wo;
+  const float *q_norm;      /* [head_dim] */
+  const float *k_norm;      /* [head_dim] */
+  /* dense feed-forward */
+  bch_matrix gate, up, down;
+  /* mixture of experts: experts stacked by rows (lfm2.rs:128-142) */
+  bch_matrix router;        /* n_experts × n_embd, F32 */
+  const float *expert_bias; /* [n_experts] */
+  bch_matrix gate_exps, up_exps, down_exps;
+} bch_lfm2_layer;
+
+/* lfm2::Hyperparameters (lfm2.rs:17-49) plus the tensors. */
+typedef struct bch_lfm2_model {
+  uint32_t n_layers;
+  uint32_t n_embd;
+  uint32_t n_ff;
+  uint32_t n_experts;
+  uint32_t n_experts_used;
+  uint32_t n_ff_expert;
+  uint32_t n_heads;
+  uint32_t n_kv_heads;
+  uint32_t head_dim;
+  uint32_t n_vocab;
+  uint32_t conv_kernel;
+  float rope_theta;
+  float norm_eps;
+  const bch_lfm2_layer *layers;
+  bch_matrix token_embd;    /* n_vocab × n_embd */
+  bch_matrix output;        /* n_vocab × n_embd (tied: same data as token_embd) */
+  const float *output_norm; /* [n_embd] */
+} bch_lfm2_model;
+
+typedef struct bch_lfm2 bch_lfm2;
+
+/* Lfm2Metal::new (lfm2_metal.rs:125-220): copies the weights to HBM and
+ * allocates the caches for sequences of up to n_ctx tokens. */
+int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *model, uint32_t n_ctx, int kv_half,
+                 bch_lfm2 **out);
+void bch_lfm2_free(bch_lfm2 *lfm2);
+uint32_t bch_lfm2_n_past(const bch_lfm2 *lfm2);
+/* Lfm2Metal::reset (lfm2_metal.rs:237-247). */
+int bch_lfm2_reset(bch_lfm2 *lfm2);
+/* Lfm2Metal::step (lfm2_metal.rs:308-365); logits (nullable) receives
+ * n_vocab floats; trace arrays (nullable) receive the embedding, every
+ * layer's output and the final norm of the token. */
+int bch_lfm2_step(bch_lfm2 *lfm2, uint32_t token, float *logits, float *trace_embedding,
+                  float *trace_layers, float *trace_final);
+/* Lfm2Metal::prefill (lfm2_metal.rs:662-762), logits of the last token. */
+int bch_lfm2_prefill(bch_lfm2 *lfm2, const uint32_t *tokens, uint32_t n_tokens, float *logits);
+/* Lfm2Metal::greedy_token (lfm2_metal.rs:372-398). */
+int bch_lfm2_greedy_token(bch_lfm2 *lfm2, uint32_t *token);
+/* Lfm2Metal::generate (lfm2_metal.rs:408-411): n greedy tokens, the first
+ * the argmax of the current logits; each step runs on the GPU with no host
+ * round trip (a captured HIP graph replayed per token). */
+int bch_lfm2_generate(bch_lfm2 *lfm2, uint32_t *out, uint32_t n);
+/* Lfm2Metal::checkpoint / restore (lfm2_metal.rs:250-288).  The blob holds
+ * the reset count, n_past, the convolution history and the logits;
+ * bch_lfm2_checkpoint_bytes gives its size. */
+uint64_t bch_lfm2_checkpoint_bytes(const bch_lfm2 *lfm2);
+int bch_lfm2_checkpoint(bch_lfm2 *lfm2, void *blob, uint64_t bytes);
+int bch_lfm2_restore(bch_lfm2 *lfm2, const void *blob, uint64_t bytes);
+/* Last call's host-side recording time and device time (lfm2_metal.rs:222-230). */
+double bch_lfm2_last_gpu_seconds(const bch_lfm2 *lfm2);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,553 @@
+/* bobcat_oracle.c — TEST INFRASTRUCTURE ONLY.
+ *
+ * A CPU restatement, in plain C, of bobcat's scalar reference path: the ops of
+ * crates/bobcat/src/scalar.rs and the LFM2 forward pass of
+ * crates/bobcat/src/lfm2.rs.  The reference is Rust and cannot be compiled in
+ * this image (no cargo/rustc), so this file restates it function by function;
+ * each function cites the reference lines it follows.
+ *
+ * Only the tests, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
+ * this library, and only as the checker or the timed CPU baseline.  The
+ * product path (bobcat_amd/, libbobcat_hip.so) never links or calls it.
+ *
+ * Numerics follow the reference exactly where it fixes them: fp16/bf16 decode
+ * is bit-exact IEEE, dequantisation rounds each product separately (no FMA
+ * contraction: build with -ffp-contract=off), dot products, norms, softmax
+ * sums and the convolution accumulate in double and round once to float.
+ * Transcendentals (powf, sinf, cosf, expf) come from the host libm, as the
+ * reference takes them from the Rust/platform libm.
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "../include/bobcat_hip.h"
+
+#define EXPORT __attribute__((visibility("default")))
+
+/* ---------------------------------------------------------------- */
+/* Half and bfloat16 (scalar.rs:17-25; the `half` crate 2.7.1 does   */
+/* exact IEEE-754 conversion)                                        */
+/* ---------------------------------------------------------------- */
+
+static float bits_to_f32(uint32_t bits) {
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+static uint32_t f32_to_bits(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+
+EXPORT float orc_f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h >> 15) << 31;
+  uint32_t exp = (h >> 10) & 0x1f;
+  uint32_t man = h & 0x3ff;
+  if (exp == 0) {
+    if (man == 0) return bits_to_f32(sign);
+    /* subnormal: value = man * 2^-24, exact in float */
+    float v = (float)man * (1.0f / 16777216.0f);
+    return sign ? -v : v;
+  }
+  if (exp == 31) return bits_to_f32(sign | 0x7f800000u | (man << 13));
+  return bits_to_f32(sign | ((exp + 112) << 23) | (man << 13));
+}
+
+/* Round-to-nearest-even float -> half, as `half::f16::from_f32` and a GPU's
+ * float-to-half conversion do. */
+EXPORT uint16_t orc_f32_to_f16(float f) {
+  uint32_t x = f32_to_bits(f);
+  uint16_t sign = (uint16_t)((x >> 16) & 0x8000);
+  uint32_t exp = (x >> 23) & 0xff;
+  uint32_t man = x & 0x7fffff;
+  if (exp == 0xff) return (uint16_t)(sign | 0x7c00 | (man ? 0x200 | (man >> 13) : 0));
+  int e = (int)exp - 127 + 15;
+  if (e >= 31) return (uint16_t)(sign | 0x7c00);
+  if (e <= 0) {
+    if (e < -10) return sign;
+    man |= 0x800000;
+    int shift = 14 - e;
+    uint32_t half_man = man >> shift;
+    uint32_t rem = man & ((1u << shift) - 1);
+    uint32_t halfway = 1u << (shift - 1);
+    if (rem > halfway || (rem == halfway && (half_man & 1))) half_man++;
+    return (uint16_t)(sign | half_man);
+  }
+  uint32_t half_man = man >> 13;
+  uint32_t rem = man & 0x1fff;
+  uint16_t out = (uint16_t)(sign | ((uint32_t)e << 10) | half_man);
+  if (rem > 0x1000 || (rem == 0x1000 && (half_man & 1))) out++;
+  return out;
+}
+
+EXPORT float orc_bf16_to_f32(uint16_t b) { return bits_to_f32((uint32_t)b << 16); }
+
+static float f16_at(const uint8_t *p) { return orc_f16_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
+
+/* ---------------------------------------------------------------- */
+/* Block layouts (crates/bobcat-gguf/src/lib.rs:154-165)             */
+/* ---------------------------------------------------------------- */
+
+static int block_shape(uint32_t type, uint32_t *elements, uint32_t *bytes) {
+  switch (type) {
+    case BCH_F32: *elements = 1; *bytes = 4; return 1;
+    case BCH_F16: case BCH_BF16: *elements = 1; *bytes = 2; return 1;
+    case BCH_Q4_0: *elements = 32; *bytes = 18; return 1;
+    case BCH_Q8_0: *elements = 32; *bytes = 34; return 1;
+    case BCH_Q4K: *elements = 256; *bytes = 144; return 1;
+    case BCH_Q5K: *elements = 256; *bytes = 176; return 1;
+    case BCH_Q6K: *elements = 256; *bytes = 210; return 1;
+    default: return 0;
+  }
+}
+
+/* scalar::row_bytes (scalar.rs:28-31). */
+EXPORT uint64_t orc_row_bytes(uint32_t type, uint32_t n_cols) {
+  uint32_t e, b;
+  if (!block_shape(type, &e, &b) || n_cols % e) return 0;
+  return (uint64_t)(n_cols / e) * b;
+}
+
+/* ---------------------------------------------------------------- */
+/* Dequantisation (scalar.rs:56-202)                                 */
+/* ---------------------------------------------------------------- */
+
+/* dequantize_q4_0 (scalar.rs:95-104). */
+static void deq_q4_0(const uint8_t *blk, float *out) {
+  float d = f16_at(blk);
+  for (int i = 0; i < 16; i++) {
+    uint8_t q = blk[2 + i];
+    out[i] = (float)((int)(q & 0xf) - 8) * d;
+    out[i + 16] = (float)((int)(q >> 4) - 8) * d;
+  }
+}
+
+/* dequantize_q8_0 (scalar.rs:107-112). */
+static void deq_q8_0(const uint8_t *blk, float *out) {
+  float d = f16_at(blk);
+  for (int i = 0; i < 32; i++) out[i] = (float)(int8_t)blk[2 + i] * d;
+}
+
+/* q4k_scale_min (scalar.rs:115-125): the 6-bit scale and minimum of
+ * 32-element block j from the 12 packed bytes. */
+EXPORT void orc_q4k_scale_min(int j, const uint8_t *s, uint8_t *scale, uint8_t *min) {
+  if (j < 4) {
+    *scale = s[j] & 63;
+    *min = s[j + 4] & 63;
+  } else {
+    *scale = (uint8_t)((s[j + 4] & 0xf) | ((s[j - 4] >> 6) << 4));
+    *min = (uint8_t)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+  }
+}
+
+/* dequantize_q4k (scalar.rs:127-152): element 32j+l of a super-block is
+ * (d·sc_j)·q − (dmin·m_j), each product rounded to float on its own. */
+static void deq_q4k(const uint8_t *blk, float *out) {
+  float d = f16_at(blk), dmin = f16_at(blk + 2);
+  const uint8_t *scales = blk + 4, *quants = blk + 16;
+  for (int pair = 0; pair < 4; pair++) {
+    uint8_t sl, ml, sh, mh;
+    orc_q4k_scale_min(2 * pair, scales, &sl, &ml);
+    orc_q4k_scale_min(2 * pair + 1, scales, &sh, &mh);
+    float d_low = d * (float)sl, m_low = dmin * (float)ml;
+    float d_high = d * (float)sh, m_high = dmin * (float)mh;
+    const uint8_t *q = quants + 32 * pair;
+    float *o = out + 64 * pair;
+    for (int l = 0; l < 32; l++) {
+      float a = d_low * (float)(q[l] & 0xf);
+      float b = d_high * (float)(q[l] >> 4);
+      o[l] = a - m_low;
+      o[l + 32] = b - m_high;
+    }
+  }
+}
+
+/* dequantize_q5k (scalar.rs:157-176). */
+static void deq_q5k(const uint8_t *blk, float *out) {
+  float d = f16_at(blk), dmin = f16_at(blk + 2);
+  const uint8_t *scales = blk + 4, *high = blk + 16, *quants = blk + 48;
+  for (int j = 0; j < 8; j++) {
+    uint8_t sc, mn;
+    orc_q4k_scale_min(j, scales, &sc, &mn);
+    float s = d * (float)sc, m = dmin * (float)mn;
+    const uint8_t *q = quants + (j / 2) * 32;
+    int shift = 4 * (j % 2);
+    for (int l = 0; l < 32; l++) {
+      uint8_t v = (uint8_t)(((q[l] >> shift) & 0xf) | (((high[l] >> j) & 1) << 4));
+      float p = s * (float)v;
+      out[32 * j + l] = p - m;
+    }
+  }
+}
+
+/* dequantize_q6k (scalar.rs:181-202). */
+static void deq_q6k(const uint8_t *blk, float *out) {
+  float d = f16_at(blk + 208);
+  for (int half = 0; half < 2; half++) {
+    const uint8_t *low = blk + half * 64, *high = blk + 128 + half * 32;
+    const int8_t *sc = (const int8_t *)(blk + 192 + half * 8);
+    float *o = out + half * 128;
+    for (int l = 0; l < 32; l++) {
+      int is = l / 16;
+#define Q6(lowv, sh) ((float)((int)((lowv) | (((high[l] >> (sh)) & 3) << 4)) - 32))
+#define SC(i) (d * (float)sc[i])
+      o[l] = SC(is) * Q6(low[l] & 0xf, 0);
+      o[l + 32] = SC(is + 2) * Q6(low[l + 32] & 0xf, 2);
+      o[l + 64] = SC(is + 4) * Q6(low[l] >> 4, 4);
+      o[l + 96] = SC(is + 6) * Q6(low[l + 32] >> 4, 6);
+#undef Q6
+#undef SC
+    }
+  }
+}
+
+/* scalar::dequantize (scalar.rs:59-79): n elements of `type` at bytes. */
+EXPORT int orc_dequantize(uint32_t type, const void *bytes, uint64_t n, float *out) {
+  const uint8_t *p = (const uint8_t *)bytes;
+  uint32_t e, b;
+  if (!block_shape(type, &e, &b) || n % e) return -1;
+  uint64_t nb = n / e;
+  for (uint64_t i = 0; i < nb; i++) {
+    const uint8_t *blk = p + i * b;
+    float *o = out + i * e;
+    switch (type) {
+      case BCH_F32: memcpy(o, blk, 4); break;
+      case BCH_F16: *o = f16_at(blk); break;
+      case BCH_BF16: *o = orc_bf16_to_f32((uint16_t)(blk[0] | (blk[1] << 8))); break;
+      case BCH_Q4_0: deq_q4_0(blk, o); break;
+      case BCH_Q8_0: deq_q8_0(blk, o); break;
+      case BCH_Q4K: deq_q4k(blk, o); break;
+      case BCH_Q5K: deq_q5k(blk, o); break;
+      case BCH_Q6K: deq_q6k(blk, o); break;
+    }
+  }
+  return 0;
+}
+
+/* ---------------------------------------------------------------- */
+/* Vector ops (scalar.rs:213-304)                                    */
+/* ---------------------------------------------------------------- */
+
+/* scalar::dot (scalar.rs:292-304): double sum rounded once. */
+EXPORT float orc_dot(const float *a, const float *b, uint64_t n) {
+  double s = 0.0;
+  for (uint64_t i = 0; i < n; i++) s += (double)a[i] * (double)b[i];
+  return (float)s;
+}
+
+static int g_threads = 1;
+EXPORT void orc_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
+EXPORT int orc_get_threads(void) { return g_threads; }
+
+typedef struct {
+  uint32_t type;
+  const uint8_t *w;
+  uint64_t row_bytes;
+  const float *x;
+  float *y;
+  uint32_t cols;
+  uint64_t r0, r1;
+} mv_job;
+
+static void *mv_run(void *arg) {
+  mv_job *j = (mv_job *)arg;
+  float *row = (float *)malloc(sizeof(float) * j->cols);
+  for (uint64_t r = j->r0; r < j->r1; r++) {
+    orc_dequantize(j->type, j->w + r * j->row_bytes, j->cols, row);
+    j->y[r] = orc_dot(row, j->x, j->cols);
+  }
+  free(row);
+  return NULL;
+}
+
+/* scalar::matvec (scalar.rs:213-220): each row dequantised, then dotted with
+ * x in double.  Rows split over orc_set_threads() threads; every row's
+ * arithmetic is the same, so the result does not depend on the count. */
+EXPORT int orc_matvec(uint32_t type, const void *weights, uint32_t rows, uint32_t cols,
+                      const float *x, float *y) {
+  uint64_t rb = orc_row_bytes(type, cols);
+  if (!rb) return -1;
+  int nt = g_threads;
+  if ((uint64_t)nt > rows) nt = rows ? (int)rows : 1;
+  mv_job jobs[256];
+  pthread_t th[256];
+  if (nt > 256) nt = 256;
+  for (int t = 0; t < nt; t++) {
+    jobs[t] = (mv_job){type, (const uint8_t *)weights, rb, x, y, cols,
+                       (uint64_t)rows * t / nt, (uint64_t)rows * (t + 1) / nt};
+  }
+  if (nt == 1) {
+    mv_run(&jobs[0]);
+    return 0;
+  }
+  for (int t = 0; t < nt; t++) pthread_create(&th[t], NULL, mv_run, &jobs[t]);
+  for (int t = 0; t < nt; t++) pthread_join(th[t], NULL);
+  return 0;
+}
+
+/* rms_scale (scalar.rs:239-249): 1/sqrt(mean(x²)+eps) in double, rounded. */
+static float rms_scale(const float *x, uint64_t n, float eps) {
+  double s = 0.0;
+  for (uint64_t i = 0; i < n; i++) s += (double)x[i] * (double)x[i];
+  double mean = s / (double)n;
+  return (float)(1.0 / sqrt(mean + (double)eps));
+}
+
+/* scalar::rms_norm (scalar.rs:222-229): out = w·(x·scale). */
+EXPORT void orc_rms_norm(const float *x, const float *w, uint64_t n, float eps, float *out) {
+  float scale = rms_scale(x, n, eps);
+  for (uint64_t i = 0; i < n; i++) out[i] = w[i] * (x[i] * scale);
+}
+
+/* scalar::rope_neox (scalar.rs:251-266): element i pairs with i + d/2;
+ * frequencies and angles in float, as transformers computes them. */
+EXPORT void orc_rope_neox(float *v, uint32_t head_dim, uint32_t pos, float theta) {
+  uint32_t half = head_dim / 2;
+  for (uint32_t i = 0; i < half; i++) {
+    float inv_freq = 1.0f / powf(theta, (float)(2 * i) / (float)head_dim);
+    float angle = (float)pos * inv_freq;
+    float s = sinf(angle), c = cosf(angle);
+    float a = v[i], b = v[i + half];
+    v[i] = a * c - b * s;
+    v[i + half] = b * c + a * s;
+  }
+}
+
+/* scalar::silu (scalar.rs:268-271). */
+EXPORT float orc_silu(float x) { return x / (1.0f + expf(-x)); }
+
+/* scalar::softmax (scalar.rs:273-289): float exponentials, double sum. */
+EXPORT void orc_softmax(float *x, uint64_t n) {
+  float max = -INFINITY;
+  for (uint64_t i = 0; i < n; i++) max = fmaxf(max, x[i]);
+  double sum = 0.0;
+  for (uint64_t i = 0; i < n; i++) {
+    x[i] = expf(x[i] - max);
+    sum += (double)x[i];
+  }
+  for (uint64_t i = 0; i < n; i++) x[i] = (float)((double)x[i] / sum);
+}
+
+/* ---------------------------------------------------------------- */
+/* LFM2 forward pass (lfm2.rs:300-560, 677-722)                      */
+/* ---------------------------------------------------------------- */
+
+/* lfm2::State (lfm2.rs:565-629). */
+typedef struct orc_lfm2_state {
+  uint32_t n_ctx, n_past;
+  float *k_cache, *v_cache, *conv_history;
+  float *hidden, *normed, *block_out, *bcx, *conv_out, *q, *k, *v, *attn, *scores;
+  float *gate, *up, *router, *expert_out;
+  uint32_t *experts;
+} orc_lfm2_state;
+
+static uint32_t count_layers(const bch_lfm2_model *m, int attention) {
+  uint32_t n = 0;
+  for (uint32_t i = 0; i < m->n_layers; i++) n += (m->layers[i].is_attention != 0) == (attention != 0);
+  return n;
+}
+
+/* State::new (lfm2.rs:599-628). */
+EXPORT orc_lfm2_state *orc_lfm2_state_new(const bch_lfm2_model *m, uint32_t n_ctx) {
+  if (n_ctx == 0) return NULL;
+  orc_lfm2_state *s = (orc_lfm2_state *)calloc(1, sizeof(*s));
+  uint64_t n = m->n_embd, kv = (uint64_t)m->n_kv_heads * m->head_dim, qd = (uint64_t)m->n_heads * m->head_dim;
+  uint64_t cache = (uint64_t)count_layers(m, 1) * n_ctx * kv;
+  uint64_t conv = (uint64_t)count_layers(m, 0) * (m->conv_kernel - 1) * n;
+  uint64_t nff = m->n_ff > m->n_ff_expert ? m->n_ff : m->n_ff_expert;
+  s->n_ctx = n_ctx;
+  s->k_cache = calloc(cache + 1, 4);
+  s->v_cache = calloc(cache + 1, 4);
+  s->conv_history = calloc(conv + 1, 4);
+  s->hidden = calloc(n, 4);
+  s->normed = calloc(n, 4);
+  s->block_out = calloc(n, 4);
+  s->bcx = calloc(3 * n, 4);
+  s->conv_out = calloc(n, 4);
+  s->q = calloc(qd, 4);
+  s->k = calloc(kv + 1, 4);
+  s->v = calloc(kv + 1, 4);
+  s->attn = calloc(qd, 4);
+  s->scores = calloc(n_ctx, 4);
+  s->gate = calloc(nff, 4);
+  s->up = calloc(nff, 4);
+  s->router = calloc(m->n_experts + 1, 4);
+  s->experts = calloc(m->n_experts + 1, 4);
+  s->expert_out = calloc(n, 4);
+  return s;
+}
+
+EXPORT void orc_lfm2_state_free(orc_lfm2_state *s) {
+  if (!s) return;
+  void *ptrs[] = {s->k_cache, s->v_cache, s->conv_history, s->hidden, s->normed, s->block_out,
+                  s->bcx, s->conv_out, s->q, s->k, s->v, s->attn, s->scores, s->gate, s->up,
+                  s->router, s->experts, s->expert_out};
+  for (size_t i = 0; i < sizeof(ptrs) / sizeof(ptrs[0]); i++) free(ptrs[i]);
+  free(s);
+}
+
+EXPORT uint32_t orc_lfm2_n_past(const orc_lfm2_state *s) { return s->n_past; }
+
+static void matvec_m(const bch_matrix *mat, const float *x, float *y) {
+  orc_matvec(mat->format, mat->data, mat->n_rows, mat->n_cols, x, y);
+}
+
+/* Model::matvec_rows (lfm2.rs:397-401): rows first_row.. of a matrix. */
+static void matvec_rows(const bch_matrix *mat, uint64_t first_row, uint32_t rows, const float *x,
+                        float *y) {
+  uint64_t rb = orc_row_bytes(mat->format, mat->n_cols);
+  orc_matvec(mat->format, (const uint8_t *)mat->data + first_row * rb, rows, mat->n_cols, x, y);
+}
+
+/* swiglu (lfm2.rs:677-682). */
+static void swiglu(float *gate, const float *up, uint64_t n) {
+  for (uint64_t i = 0; i < n; i++) gate[i] = orc_silu(gate[i]) * up[i];
+}
+
+/* route (lfm2.rs:691-709): sigmoid scores, stable descending sort of
+ * score + bias (ties to the lower expert), weights = score / (Σpicked + 1e-6). */
+EXPORT void orc_lfm2_route(float *scores, const float *bias, uint32_t n_experts, uint32_t n_used,
+                           uint32_t *experts) {
+  for (uint32_t e = 0; e < n_experts; e++) scores[e] = 1.0f / (1.0f + expf(-scores[e]));
+  for (uint32_t e = 0; e < n_experts; e++) experts[e] = e;
+  /* insertion sort is stable */
+  for (uint32_t i = 1; i < n_experts; i++) {
+    uint32_t cur = experts[i];
+    float key = scores[cur] + bias[cur];
+    int32_t j = (int32_t)i - 1;
+    while (j >= 0 && scores[experts[j]] + bias[experts[j]] < key) {
+      experts[j + 1] = experts[j];
+      j--;
+    }
+    experts[j + 1] = cur;
+  }
+  float sum = 0.0f;
+  for (uint32_t i = 0; i < n_used; i++) sum += scores[experts[i]];
+  float norm = sum + 1e-6f;
+  for (uint32_t i = 0; i < n_used; i++) scores[experts[i]] /= norm;
+}
+
+/* Model::moe_block (lfm2.rs:413-440). */
+static void moe_block(const bch_lfm2_model *m, const bch_lfm2_layer *L, orc_lfm2_state *s) {
+  uint32_t n = m->n_embd, nff = m->n_ff_expert, nu = m->n_experts_used;
+  matvec_m(&L->router, s->normed, s->router);
+  orc_lfm2_route(s->router, L->expert_bias, m->n_experts, nu, s->experts);
+  memset(s->block_out, 0, sizeof(float) * n);
+  for (uint32_t i = 0; i < nu; i++) {
+    uint32_t e = s->experts[i];
+    matvec_rows(&L->gate_exps, (uint64_t)e * nff, nff, s->normed, s->gate);
+    matvec_rows(&L->up_exps, (uint64_t)e * nff, nff, s->normed, s->up);
+    swiglu(s->gate, s->up, nff);
+    matvec_rows(&L->down_exps, (uint64_t)e * n, n, s->gate, s->expert_out);
+    float w = s->router[e];
+    for (uint32_t c = 0; c < n; c++) s->block_out[c] += w * s->expert_out[c];
+  }
+}
+
+/* Model::dense_block (lfm2.rs:404-409). */
+static void dense_block(const bch_lfm2_layer *L, orc_lfm2_state *s) {
+  matvec_m(&L->gate, s->normed, s->gate);
+  matvec_m(&L->up, s->normed, s->up);
+  swiglu(s->gate, s->up, L->gate.n_rows);
+  matvec_m(&L->down, s->gate, s->block_out);
+}
+
+/* Model::conv_block (lfm2.rs:444-478). */
+static void conv_block(const bch_lfm2_model *m, const bch_lfm2_layer *L, uint32_t cache_index,
+                       orc_lfm2_state *s) {
+  uint32_t n = m->n_embd, k = m->conv_kernel;
+  float *hist = s->conv_history + (uint64_t)cache_index * (k - 1) * n;
+  matvec_m(&L->in_proj, s->normed, s->bcx);
+  const float *b = s->bcx, *c = s->bcx + n, *x = s->bcx + 2 * n;
+  for (uint32_t ch = 0; ch < n; ch++) {
+    const float *taps = L->conv_taps + (uint64_t)ch * k;
+    float bx = b[ch] * x[ch];
+    double sum = (double)taps[k - 1] * (double)bx;
+    for (uint32_t t = 0; t + 1 < k; t++) sum += (double)taps[t] * (double)hist[t * n + ch];
+    for (uint32_t t = 0; t + 2 < k; t++) hist[t * n + ch] = hist[(t + 1) * n + ch];
+    hist[(k - 2) * n + ch] = bx;
+    s->conv_out[ch] = c[ch] * (float)sum;
+  }
+  matvec_m(&L->out_proj, s->conv_out, s->block_out);
+}
+
+/* scalar::rms_norm_in_place (scalar.rs:232-237). */
+static void rms_norm_in_place(float *x, const float *w, uint64_t n, float eps) {
+  float scale = rms_scale(x, n, eps);
+  for (uint64_t i = 0; i < n; i++) x[i] = w[i] * (x[i] * scale);
+}
+
+/* Model::attention_block (lfm2.rs:482-560). */
+static void attention_block(const bch_lfm2_model *m, const bch_lfm2_layer *L, uint32_t cache_index,
+                            orc_lfm2_state *s, uint32_t pos) {
+  uint32_t hd = m->head_dim, kvd = m->n_kv_heads * hd, group = m->n_heads / m->n_kv_heads;
+  float scale = 1.0f / sqrtf((float)hd);
+  uint64_t layer_len = (uint64_t)s->n_ctx * kvd;
+  float *kc = s->k_cache + cache_index * layer_len, *vc = s->v_cache + cache_index * layer_len;
+  matvec_m(&L->wq, s->normed, s->q);
+  matvec_m(&L->wk, s->normed, s->k);
+  matvec_m(&L->wv, s->normed, s->v);
+  for (uint32_t h = 0; h < m->n_heads; h++) {
+    rms_norm_in_place(s->q + h * hd, L->q_norm, hd, m->norm_eps);
+    orc_rope_neox(s->q + h * hd, hd, pos, m->rope_theta);
+  }
+  for (uint32_t h = 0; h < m->n_kv_heads; h++) {
+    rms_norm_in_place(s->k + h * hd, L->k_norm, hd, m->norm_eps);
+    orc_rope_neox(s->k + h * hd, hd, pos, m->rope_theta);
+  }
+  memcpy(kc + (uint64_t)pos * kvd, s->k, sizeof(float) * kvd);
+  memcpy(vc + (uint64_t)pos * kvd, s->v, sizeof(float) * kvd);
+  uint32_t n_keys = pos + 1;
+  for (uint32_t h = 0; h < m->n_heads; h++) {
+    uint32_t kv_off = h / group * hd;
+    const float *qh = s->q + h * hd;
+    for (uint32_t t = 0; t < n_keys; t++) s->scores[t] = scale * orc_dot(qh, kc + (uint64_t)t * kvd + kv_off, hd);
+    orc_softmax(s->scores, n_keys);
+    for (uint32_t d = 0; d < hd; d++) {
+      double sum = 0.0;
+      for (uint32_t t = 0; t < n_keys; t++) sum += (double)s->scores[t] * (double)vc[(uint64_t)t * kvd + kv_off + d];
+      s->attn[h * hd + d] = (float)sum;
+    }
+  }
+  matvec_m(&L->wo, s->attn, s->block_out);
+}
+
+/* Model::step (lfm2.rs:308-394).  Returns 0, or -1 for a full context, -2
+ * for a token outside the vocabulary (Error::ContextFull / Error::Token). */
+EXPORT int orc_lfm2_step(const bch_lfm2_model *m, orc_lfm2_state *s, uint32_t token, float *logits,
+                         float *trace_embedding, float *trace_layers, float *trace_final) {
+  uint32_t n = m->n_embd, pos = s->n_past;
+  if (pos >= s->n_ctx) return -1;
+  if (token >= m->n_vocab) return -2;
+  uint64_t rb = orc_row_bytes(m->token_embd.format, n);
+  orc_dequantize(m->token_embd.format, (const uint8_t *)m->token_embd.data + (uint64_t)token * rb, n,
+                 s->hidden);
+  if (trace_embedding) memcpy(trace_embedding, s->hidden, sizeof(float) * n);
+  uint32_t attn_index = 0, conv_index = 0;
+  for (uint32_t il = 0; il < m->n_layers; il++) {
+    const bch_lfm2_layer *L = &m->layers[il];
+    orc_rms_norm(s->hidden, L->attn_norm, n, m->norm_eps, s->normed);
+    if (L->is_attention)
+      attention_block(m, L, attn_index++, s, pos);
+    else
+      conv_block(m, L, conv_index++, s);
+    for (uint32_t i = 0; i < n; i++) s->hidden[i] += s->block_out[i];
+    orc_rms_norm(s->hidden, L->ffn_norm, n, m->norm_eps, s->normed);
+    if (L->is_moe)
+      moe_block(m, L, s);
+    else
+      dense_block(L, s);
+    for (uint32_t i = 0; i < n; i++) s->hidden[i] += s->block_out[i];
+    if (trace_layers) memcpy(trace_layers + (uint64_t)il * n, s->hidden, sizeof(float) * n);
+  }
+  orc_rms_norm(s->hidden, m->output_norm, n, m->norm_eps, s->normed);
+  if (trace_final) memcpy(trace_final, s->normed, sizeof(float) * n);
+  if (logits) matvec_m(&m->output, s->normed, logits);
+  s->n_past++;
+  return 0;
+}
