@@ -105,6 +105,7 @@ PROTOTYPES = {
     "bch_matvec_swiglu": (_int, [_vp, _u32, View, View, _u32, _u32, View, Norm, View]),
     "bch_matvec_conv": (_int, [_vp, _u32, View, _u32, View, C.POINTER(Norm), View, View, View, _u32, _u32]),
     "bch_short_conv": (_int, [_vp, View, View, View, View, _u32, _u32, _u32]),
+    "bch_short_conv_batch": (_int, [_vp, View, View, View, View, _u32, _u32, _u32]),
     "bch_rms_norm": (_int, [_vp, View, View, View, _u32, _u32, _f32]),
     "bch_norm_rope": (_int, [_vp, View, View, _int, View, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
                              _u32, _f32, _f32]),
@@ -115,12 +116,13 @@ PROTOTYPES = {
     "bch_attention_scratch_floats": (_u64, [_u32, _u32, _u32, _u32]),
     "bch_matmul": (_int, [_vp, _u32, View, _u32, _u32, View, View, _u32, _u32]),
     "bch_argmax": (_int, [_vp, View, View, _u32]),
+    "bch_read_sum": (_int, [_vp, View, _u64, View, _u32]),
     "bch_lfm2_new": (_int, [_vp, C.POINTER(Lfm2Model), _u32, _int, C.POINTER(_vp)]),
     "bch_lfm2_free": (None, [_vp]),
     "bch_lfm2_n_past": (_u32, [_vp]),
     "bch_lfm2_reset": (_int, [_vp]),
     "bch_lfm2_step": (_int, [_vp, _u32, _FP, _FP, _FP, _FP]),
-    "bch_lfm2_prefill": (_int, [_vp, C.POINTER(_u32), _u32, _FP]),
+    "bch_lfm2_prefill": (_int, [_vp, C.POINTER(_u32), _u32, _FP, _FP, _FP, _FP]),
     "bch_lfm2_greedy_token": (_int, [_vp, C.POINTER(_u32)]),
     "bch_lfm2_generate": (_int, [_vp, C.POINTER(_u32), _u32]),
     "bch_lfm2_checkpoint_bytes": (_u64, [_vp]),

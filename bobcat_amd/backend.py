@@ -9,6 +9,7 @@ the bch_status code of the matching `bobcat_metal::Error` variant.
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 from dataclasses import dataclass
 from enum import IntEnum
 
@@ -98,9 +99,14 @@ class Hip:
         check(lib().bch_open(C.byref(handle)))
         self.handle = handle.value
         self._buffers: list[Buffer] = []
+        # Objects that hold device state of this context (model drivers);
+        # they close before the context does.
+        self._dependents = weakref.WeakSet()
 
     def close(self) -> None:
         if self.handle:
+            for d in list(self._dependents):
+                d.close()
             for b in self._buffers:
                 b.free()
             lib().bch_close(self.handle)
@@ -204,6 +210,10 @@ class Hip:
         check(lib().bch_short_conv(self.handle, _view(bcx), _view(taps), _view(history), _view(out),
                                    n_embd, kernel_size, n_tokens))
 
+    def short_conv_batch(self, bcx, taps, history, out, n_embd, kernel_size, n_tokens):
+        check(lib().bch_short_conv_batch(self.handle, _view(bcx), _view(taps), _view(history),
+                                         _view(out), n_embd, kernel_size, n_tokens))
+
     def rms_norm(self, x, weight, out, n, n_rows, eps):
         check(lib().bch_rms_norm(self.handle, _view(x), _view(weight), _view(out), n, n_rows, eps))
 
@@ -232,6 +242,9 @@ class Hip:
     def matmul(self, fmt, weights, n_rows, n_cols, x, y, n_tokens, store: Store):
         check(lib().bch_matmul(self.handle, int(fmt), _view(weights), n_rows, n_cols, _view(x),
                                _view(y), n_tokens, int(store)))
+
+    def read_sum(self, src, n_vectors, out, n_threads):
+        check(lib().bch_read_sum(self.handle, _view(src), n_vectors, _view(out), n_threads))
 
     def argmax(self, x, out, n):
         check(lib().bch_argmax(self.handle, _view(x), _view(out), n))

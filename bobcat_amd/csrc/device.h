@@ -48,11 +48,29 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
   return __half2float(__ushort_as_half((unsigned short)bits16));
 }
 
-// Byte k of a dword as a float; the backend selects v_cvt_f32_ubyte{k}.
-__device__ __forceinline__ float ubyte0(uint32_t w) { return (float)((w >> 0) & 0xffu); }
-__device__ __forceinline__ float ubyte1(uint32_t w) { return (float)((w >> 8) & 0xffu); }
-__device__ __forceinline__ float ubyte2(uint32_t w) { return (float)((w >> 16) & 0xffu); }
-__device__ __forceinline__ float ubyte3(uint32_t w) { return (float)((w >> 24) & 0xffu); }
+// Byte k of a dword as a float (v_cvt_f32_ubyte{k}).  Written as inline
+// asm so that a masked dword feeds all four conversions directly; plain C
+// makes the compiler insert a v_bfe_u32 before each conversion.
+__device__ __forceinline__ float ubyte0(uint32_t w) {
+  float r;
+  asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(w));
+  return r;
+}
+__device__ __forceinline__ float ubyte1(uint32_t w) {
+  float r;
+  asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(w));
+  return r;
+}
+__device__ __forceinline__ float ubyte2(uint32_t w) {
+  float r;
+  asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(w));
+  return r;
+}
+__device__ __forceinline__ float ubyte3(uint32_t w) {
+  float r;
+  asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(w));
+  return r;
+}
 
 // The 6-bit scales and minimums of 32-element blocks 2p and 2p+1 of a Q4_K
 // super-block, packed as bytes (scale_2p, scale_2p+1, min_2p, min_2p+1).

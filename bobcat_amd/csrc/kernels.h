@@ -1,0 +1,58 @@
+// Stream-level launchers of every kernel, shared by the C-ABI op functions
+// and the model drivers.  They check nothing: callers validate shapes and
+// views first.  `dpos`, where present, points at a device position counter
+// (see ops.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bch {
+
+// matvec.hip
+void run_matvec(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,
+                float *y, const float *norm_w, float eps, bool accumulate, uint32_t n_cus);
+void run_matvec_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const uint8_t *Wu, uint32_t n_rows,
+                       uint32_t n_cols, const float *x, float *y, const float *norm_w, float eps, uint32_t n_cus);
+void run_matvec_conv(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_cols, const float *x,
+                     const float *norm_w, float eps, const float *taps, float *history, float *out, uint32_t n_embd,
+                     uint32_t ksize, uint32_t n_cus);
+// Three projections of one input (q, k, v of an attention layer) in one
+// launch: rows [0, r0) from W0 into y0, [r0, r0+r1) from W1 into y1, the
+// rest from W2 into y2.
+void run_matvec3(hipStream_t s, uint32_t format, const uint8_t *W0, const uint8_t *W1, const uint8_t *W2, uint32_t r0,
+                 uint32_t r1, uint32_t r2, uint32_t n_cols, const float *x, float *y0, float *y1, float *y2,
+                 const float *norm_w, float eps, uint32_t n_cus);
+
+// ops.hip
+void run_rms_norm(hipStream_t s, const float *x, const float *w, float *out, uint32_t n, uint32_t rows, float eps);
+void run_norm_rope(hipStream_t s, const float *src, void *dst, bool half, const float *w, uint32_t n_heads,
+                   uint32_t head_dim, uint32_t n_rot, uint32_t src_head_stride, uint32_t pos, const uint32_t *dpos,
+                   uint32_t n_tokens, uint32_t src_stride, uint32_t dst_stride, float theta, float eps,
+                   uint64_t dst_pos_stride);
+void run_convert_half(hipStream_t s, const float *src, void *dst, uint32_t n, const uint32_t *dpos,
+                      uint64_t dst_pos_stride);
+void run_copy(hipStream_t s, const float *src, float *dst, uint32_t n, const uint32_t *dpos, uint64_t dst_pos_stride);
+void run_embed(hipStream_t s, uint32_t format, const uint8_t *W, uint64_t row_bytes, const uint32_t *tokens,
+               float *out, uint32_t n_embd, uint32_t n_tokens, const uint32_t *dpos);
+void run_argmax(hipStream_t s, const float *x, uint32_t *out, uint32_t n, uint32_t *dpos, bool advance);
+void run_short_conv(hipStream_t s, const float *bcx, const float *taps, float *hist, float *out, uint32_t n_embd,
+                    uint32_t ksize, uint32_t n_tokens);
+void run_short_conv_batch(hipStream_t s, const float *bcx, const float *taps, float *hist, float *out,
+                          uint32_t n_embd, uint32_t ksize, uint32_t n_tokens);
+
+// attention.hip.  Causal GQA attention of n_queries queries at positions
+// first_pos + dpos.. over a cache of [pos][n_kv][head_dim] (f16 when
+// kv_half).  `partials` holds attention_partial_floats() floats and
+// `counters` n_queries * n_kv_heads zeroed u32 (left zeroed on exit).
+uint32_t attention_splits(uint32_t n_keys_max, uint32_t n_kv_heads, uint32_t n_cus);
+uint64_t attention_partial_floats(uint32_t n_queries, uint32_t n_heads, uint32_t head_dim, uint32_t splits);
+void run_attention(hipStream_t s, const float *q, const void *k_cache, const void *v_cache, bool kv_half,
+                   float *partials, uint32_t *counters, float *out, uint32_t n_heads, uint32_t n_kv_heads,
+                   uint32_t head_dim, uint32_t first_pos, const uint32_t *dpos, uint32_t n_queries, uint32_t splits);
+
+// matmul.hip.  Y[t] (store) W·X[t] for n_tokens rows; store 0 overwrite,
+// 1 accumulate, 2 swiglu (y = silu(y) * product).
+void run_matmul(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,
+                float *y, uint32_t n_tokens, uint32_t store);
+
+}  // namespace bch

@@ -1,0 +1,648 @@
+// The LFM2 driver: the MI355X counterpart of Lfm2Metal
+// (crates/bobcat/src/lfm2_metal.rs:125-1548).
+//
+// * Weights are copied once into one HBM allocation, each tensor 256-byte
+//   aligned (the reference wraps the mmap'd file; MI355X has no unified
+//   memory).
+// * A decode step is the launch sequence of Recorder::record_step
+//   (lfm2_metal.rs:1162-1242) with three fusions: q/k/v projections in one
+//   launch, split-K attention with its combine in one launch, and the conv
+//   input projection fused with the convolution (as the reference does).
+// * Every kernel of a step reads the sequence position from a device
+//   counter, so the step is captured once as a HIP graph and replayed.
+//   generate() replays "argmax of the logits into the next token slot,
+//   advance the counter, run the step" with no host round trip per token
+//   (the reference keeps 3 command buffers in flight for the same reason,
+//   lfm2_metal.rs:29-31, 564-655).
+// * Prefill runs in batches of up to 512 tokens through the MFMA GEMM
+//   (Recorder::record_batch, lfm2_metal.rs:1455-1548).
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "kernels.h"
+#include "runtime.h"
+
+namespace bch {
+
+constexpr uint32_t kPrefillBatch = 512;  // PREFILL_BATCH (lfm2_metal.rs:33-34)
+constexpr uint32_t kAttnQueryBatch = 64;
+
+struct DevMatrix {
+  uint32_t format = 0, n_rows = 0, n_cols = 0;
+  const uint8_t *data = nullptr;
+};
+
+struct Layer {
+  bool attention = false;
+  uint32_t cache_index = 0;
+  const float *attn_norm = nullptr, *ffn_norm = nullptr;
+  const float *taps = nullptr;
+  DevMatrix in_proj, out_proj, wq, wk, wv, wo, gate, up, down;
+  const float *q_norm = nullptr, *k_norm = nullptr;
+};
+
+}  // namespace bch
+
+using namespace bch;
+
+struct bch_lfm2 {
+  bch_ctx *ctx = nullptr;
+  hipStream_t s = nullptr;
+  // Hyperparameters (lfm2.rs:17-49).
+  uint32_t n_layers, n_embd, n_ff, n_heads, n_kv_heads, head_dim, n_vocab, conv_kernel;
+  float rope_theta, norm_eps;
+  uint32_t n_attn = 0, n_conv = 0;
+  uint32_t q_dim, kv_dim;
+  std::vector<Layer> layers;
+  DevMatrix token_embd, output;
+  const float *output_norm = nullptr;
+  // Device memory.
+  uint8_t *weights = nullptr;
+  void *k_cache = nullptr, *v_cache = nullptr;
+  float *conv_state = nullptr, *hidden = nullptr, *normed = nullptr, *bcx = nullptr, *conv_out = nullptr;
+  float *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *ffn = nullptr, *logits = nullptr;
+  float *partials = nullptr, *trace = nullptr;
+  uint32_t trace_rows = 0;  // tokens each traced activation holds (lfm2_metal.rs:764-779)
+  uint32_t *counters = nullptr, *tokens = nullptr, *dpos = nullptr, *greedy = nullptr;
+  std::vector<void *> allocations;
+  // Sequence state.
+  uint32_t n_ctx = 0, n_past = 0, batch = 0;
+  uint64_t resets = 0;
+  bool kv_half = true;
+  bool have_logits = false;
+  uint32_t decode_splits = 1, prefill_splits = 1;
+  hipGraphExec_t step_graph = nullptr, gen_graph = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  double last_gpu_seconds = 0.0;
+  // Host staging of the small asynchronous uploads (they must outlive the call).
+  uint32_t dpos_host = 0, token_host = 0;
+
+  uint64_t cache_elems_per_layer() const { return (uint64_t)n_ctx * kv_dim; }
+  void *cache_layer(void *base, uint32_t ci) const {
+    return static_cast<char *>(base) + cache_elems_per_layer() * ci * (kv_half ? 2 : 4);
+  }
+  void *cache_slot(void *base, uint32_t ci, uint32_t pos) const {
+    return static_cast<char *>(cache_layer(base, ci)) + (uint64_t)pos * kv_dim * (kv_half ? 2 : 4);
+  }
+};
+
+namespace bch {
+
+static int dev_alloc(bch_lfm2 *m, uint64_t bytes, void **out) {
+  void *p = nullptr;
+  if (hipMalloc(&p, bytes ? bytes : 256) != hipSuccess)
+    return fail(BCH_ERR_ALLOCATION, "cannot allocate %llu bytes", (unsigned long long)bytes);
+  if (hipMemset(p, 0, bytes ? bytes : 256) != hipSuccess) return fail(BCH_ERR_ALLOCATION, "cannot clear memory");
+  m->allocations.push_back(p);
+  *out = p;
+  return BCH_OK;
+}
+
+template <class T>
+static int dev_alloc_t(bch_lfm2 *m, uint64_t count, T **out) {
+  void *p;
+  BCH_TRY(dev_alloc(m, count * sizeof(T), &p));
+  *out = static_cast<T *>(p);
+  return BCH_OK;
+}
+
+static uint64_t align256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
+
+// Host tensors -> one device allocation.  First pass sizes, second copies.
+struct Uploader {
+  std::vector<std::pair<const void *, uint64_t>> items;  // host pointer, bytes
+  std::vector<uint64_t> offsets;
+  uint64_t total = 0;
+  size_t add(const void *p, uint64_t bytes) {
+    for (size_t i = 0; i < items.size(); i++)
+      if (items[i].first == p && items[i].second == bytes) return i;  // tied tensors share a copy
+    items.push_back({p, bytes});
+    offsets.push_back(total);
+    total = align256(total + bytes);
+    return items.size() - 1;
+  }
+};
+
+static bool gemv_format(uint32_t f) { return f == BCH_Q4K || f == BCH_F16 || f == BCH_F32; }
+
+static int check_matrix(const bch_matrix &mat, uint32_t rows, uint32_t cols, const char *name) {
+  if (!mat.data) return fail(BCH_ERR_ARGUMENT, "missing tensor %s", name);
+  if (mat.n_rows != rows || mat.n_cols != cols)
+    return fail(BCH_ERR_ARGUMENT, "tensor %s is %u x %u, expected %u x %u", name, mat.n_rows, mat.n_cols, rows, cols);
+  if (!gemv_format(mat.format))
+    return fail(BCH_ERR_UNSUPPORTED_FORMAT, "tensor %s: format %u is not supported (Q4_K, F16 or F32)", name,
+                mat.format);
+  if (mat.format == BCH_Q4K && cols % 256) return fail(BCH_ERR_ARGUMENT, "tensor %s: columns not a multiple of 256", name);
+  return BCH_OK;
+}
+
+// ---------------------------------------------------------------------
+// Recording
+// ---------------------------------------------------------------------
+
+// One decode step at the position *m->dpos (Recorder::record_step).  With
+// `trace`, activations are copied into m->trace: embedding, each layer's
+// output, final norm.
+static void record_step(bch_lfm2 *m, hipStream_t s, bool want_logits, bool trace) {
+  const uint32_t n = m->n_embd, cus = m->ctx->n_cus;
+  const uint32_t *dp = m->dpos;
+  const uint64_t tstride = (uint64_t)m->trace_rows * n;  // floats per traced activation
+  run_embed(s, m->token_embd.format, m->token_embd.data, bch_row_bytes(m->token_embd.format, n), m->tokens,
+            m->hidden, n, 1, dp);
+  if (trace) run_copy(s, m->hidden, m->trace, n, nullptr, 0);
+  for (uint32_t il = 0; il < m->n_layers; il++) {
+    const Layer &L = m->layers[il];
+    if (!L.attention) {
+      float *hist = m->conv_state + (uint64_t)L.cache_index * (m->conv_kernel - 1) * n;
+      run_matvec_conv(s, L.in_proj.format, L.in_proj.data, n, m->hidden, L.attn_norm, m->norm_eps, L.taps, hist,
+                      m->conv_out, n, m->conv_kernel, cus);
+      run_matvec(s, L.out_proj.format, L.out_proj.data, n, n, m->conv_out, m->hidden, nullptr, 0.f, true, cus);
+    } else {
+      const uint32_t ci = L.cache_index;
+      run_matvec3(s, L.wq.format, L.wq.data, L.wk.data, L.wv.data, m->q_dim, m->kv_dim, m->kv_dim, n, m->hidden,
+                  m->q, m->k, m->v, L.attn_norm, m->norm_eps, cus);
+      run_norm_rope(s, m->q, m->q, false, L.q_norm, m->n_heads, m->head_dim, m->head_dim, m->head_dim, 0, dp, 1,
+                    m->q_dim, m->q_dim, m->rope_theta, m->norm_eps, 0);
+      run_norm_rope(s, m->k, m->cache_layer(m->k_cache, ci), m->kv_half, L.k_norm, m->n_kv_heads, m->head_dim,
+                    m->head_dim, m->head_dim, 0, dp, 1, m->kv_dim, m->kv_dim, m->rope_theta, m->norm_eps, m->kv_dim);
+      if (m->kv_half)
+        run_convert_half(s, m->v, m->cache_layer(m->v_cache, ci), m->kv_dim, dp, m->kv_dim);
+      else
+        run_copy(s, m->v, static_cast<float *>(m->cache_layer(m->v_cache, ci)), m->kv_dim, dp, m->kv_dim);
+      run_attention(s, m->q, m->cache_layer(m->k_cache, ci), m->cache_layer(m->v_cache, ci), m->kv_half, m->partials,
+                    m->counters, m->attn, m->n_heads, m->n_kv_heads, m->head_dim, 0, dp, 1, m->decode_splits);
+      run_matvec(s, L.wo.format, L.wo.data, n, m->q_dim, m->attn, m->hidden, nullptr, 0.f, true, cus);
+    }
+    run_matvec_swiglu(s, L.gate.format, L.gate.data, L.up.data, m->n_ff, n, m->hidden, m->ffn, L.ffn_norm,
+                      m->norm_eps, cus);
+    run_matvec(s, L.down.format, L.down.data, n, m->n_ff, m->ffn, m->hidden, nullptr, 0.f, true, cus);
+    if (trace) run_copy(s, m->hidden, m->trace + (1 + il) * tstride, n, nullptr, 0);
+  }
+  if (trace) run_rms_norm(s, m->hidden, m->output_norm, m->trace + (1 + m->n_layers) * tstride, n, 1, m->norm_eps);
+  if (want_logits)
+    run_matvec(s, m->output.format, m->output.data, m->n_vocab, n, m->hidden, m->logits, m->output_norm, m->norm_eps,
+               false, cus);
+}
+
+// With BCH_LFM2_CHECK=1 in the environment, record_batch synchronises after
+// each launch and reports on stderr the first one that leaves a non-finite
+// value in its output (a diagnostics mode, like the reference's per-launch
+// profiling in backend.rs:1285-1340).
+static bool check_mode() {
+  static const bool on = getenv("BCH_LFM2_CHECK") && atoi(getenv("BCH_LFM2_CHECK")) != 0;
+  return on;
+}
+
+static void check_finite(hipStream_t s, const char *what, uint32_t layer, const float *p, uint64_t count) {
+  if (!check_mode()) return;
+  static bool reported = false;
+  if (reported) return;
+  hipStreamSynchronize(s);
+  std::vector<float> h(count);
+  hipMemcpy(h.data(), p, count * 4, hipMemcpyDeviceToHost);
+  for (uint64_t i = 0; i < count; i++) {
+    if (!std::isfinite(h[i])) {
+      fprintf(stderr, "bch_lfm2: first non-finite value after %s of layer %u (element %llu of %llu)\n", what, layer,
+              (unsigned long long)i, (unsigned long long)count);
+      reported = true;
+      return;
+    }
+  }
+}
+
+// A prefill batch of `count` tokens at positions pos.. (record_batch).
+static void record_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count, bool want_logits, bool trace) {
+  const uint32_t n = m->n_embd, cus = m->ctx->n_cus;
+  const uint64_t tstride = (uint64_t)m->trace_rows * n;
+  run_embed(s, m->token_embd.format, m->token_embd.data, bch_row_bytes(m->token_embd.format, n), m->tokens + pos,
+            m->hidden, n, count, nullptr);
+  if (trace) run_copy(s, m->hidden, m->trace, count * n, nullptr, 0);
+  for (uint32_t il = 0; il < m->n_layers; il++) {
+    const Layer &L = m->layers[il];
+    run_rms_norm(s, m->hidden, L.attn_norm, m->normed, n, count, m->norm_eps);
+    check_finite(s, "attn_norm", il, m->normed, (uint64_t)count * n);
+    if (!L.attention) {
+      float *hist = m->conv_state + (uint64_t)L.cache_index * (m->conv_kernel - 1) * n;
+      run_matmul(s, L.in_proj.format, L.in_proj.data, 3 * n, n, m->normed, m->bcx, count, 0);
+      check_finite(s, "in_proj", il, m->bcx, (uint64_t)count * 3 * n);
+      run_short_conv_batch(s, m->bcx, L.taps, hist, m->conv_out, n, m->conv_kernel, count);
+      check_finite(s, "short_conv", il, m->conv_out, (uint64_t)count * n);
+      run_matmul(s, L.out_proj.format, L.out_proj.data, n, n, m->conv_out, m->hidden, count, 1);
+      check_finite(s, "out_proj", il, m->hidden, (uint64_t)count * n);
+    } else {
+      const uint32_t ci = L.cache_index;
+      run_matmul(s, L.wq.format, L.wq.data, m->q_dim, n, m->normed, m->q, count, 0);
+      run_matmul(s, L.wk.format, L.wk.data, m->kv_dim, n, m->normed, m->k, count, 0);
+      run_matmul(s, L.wv.format, L.wv.data, m->kv_dim, n, m->normed, m->v, count, 0);
+      check_finite(s, "q", il, m->q, (uint64_t)count * m->q_dim);
+      check_finite(s, "k", il, m->k, (uint64_t)count * m->kv_dim);
+      check_finite(s, "v", il, m->v, (uint64_t)count * m->kv_dim);
+      run_norm_rope(s, m->q, m->q, false, L.q_norm, m->n_heads, m->head_dim, m->head_dim, m->head_dim, pos, nullptr,
+                    count, m->q_dim, m->q_dim, m->rope_theta, m->norm_eps, 0);
+      run_norm_rope(s, m->k, m->cache_slot(m->k_cache, ci, pos), m->kv_half, L.k_norm, m->n_kv_heads, m->head_dim,
+                    m->head_dim, m->head_dim, pos, nullptr, count, m->kv_dim, m->kv_dim, m->rope_theta, m->norm_eps,
+                    0);
+      if (m->kv_half)
+        run_convert_half(s, m->v, m->cache_slot(m->v_cache, ci, pos), count * m->kv_dim, nullptr, 0);
+      else
+        run_copy(s, m->v, static_cast<float *>(m->cache_slot(m->v_cache, ci, pos)), count * m->kv_dim, nullptr, 0);
+      for (uint32_t q0 = 0; q0 < count; q0 += kAttnQueryBatch) {
+        const uint32_t nq = std::min(kAttnQueryBatch, count - q0);
+        const uint32_t splits =
+            std::min(m->prefill_splits, attention_splits(pos + q0 + nq, m->n_kv_heads, cus));
+        const uint64_t off = (uint64_t)q0 * m->q_dim;
+        run_attention(s, m->q + off, m->cache_layer(m->k_cache, ci), m->cache_layer(m->v_cache, ci), m->kv_half,
+                      m->partials, m->counters, m->attn + off, m->n_heads, m->n_kv_heads, m->head_dim, pos + q0,
+                      nullptr, nq, splits);
+      }
+      check_finite(s, "attention", il, m->attn, (uint64_t)count * m->q_dim);
+      run_matmul(s, L.wo.format, L.wo.data, n, m->q_dim, m->attn, m->hidden, count, 1);
+      check_finite(s, "attn_output", il, m->hidden, (uint64_t)count * n);
+    }
+    run_rms_norm(s, m->hidden, L.ffn_norm, m->normed, n, count, m->norm_eps);
+    check_finite(s, "ffn_norm", il, m->normed, (uint64_t)count * n);
+    run_matmul(s, L.gate.format, L.gate.data, m->n_ff, n, m->normed, m->ffn, count, 0);
+    check_finite(s, "gate", il, m->ffn, (uint64_t)count * m->n_ff);
+    run_matmul(s, L.up.format, L.up.data, m->n_ff, n, m->normed, m->ffn, count, 2);
+    check_finite(s, "up", il, m->ffn, (uint64_t)count * m->n_ff);
+    run_matmul(s, L.down.format, L.down.data, n, m->n_ff, m->ffn, m->hidden, count, 1);
+    check_finite(s, "down", il, m->hidden, (uint64_t)count * n);
+    if (trace) run_copy(s, m->hidden, m->trace + (1 + il) * tstride, count * n, nullptr, 0);
+  }
+  if (trace) run_rms_norm(s, m->hidden, m->output_norm, m->trace + (1 + m->n_layers) * tstride, n, count, m->norm_eps);
+  if (want_logits)
+    run_matvec(s, m->output.format, m->output.data, m->n_vocab, n, m->hidden + (uint64_t)(count - 1) * n, m->logits,
+               m->output_norm, m->norm_eps, false, cus);
+}
+
+// Grow the trace buffer to hold `rows` tokens per activation
+// (Lfm2Metal::ensure_trace_rows, lfm2_metal.rs:764-779).
+static int ensure_trace_rows(bch_lfm2 *m, uint32_t rows) {
+  if (rows <= m->trace_rows) return BCH_OK;
+  if (m->trace) {
+    hipStreamSynchronize(m->s);
+    hipFree(m->trace);
+    for (auto &p : m->allocations)
+      if (p == m->trace) p = nullptr;
+    m->trace = nullptr;
+  }
+  BCH_TRY(dev_alloc_t(m, (uint64_t)(m->n_layers + 2) * rows * m->n_embd, &m->trace));
+  m->trace_rows = rows;
+  return BCH_OK;
+}
+
+static int check_hip(hipError_t e, const char *what) {
+  if (e != hipSuccess) return fail(BCH_ERR_EXECUTION, "%s: %s", what, hipGetErrorString(e));
+  return BCH_OK;
+}
+
+static int capture(bch_lfm2 *m, bool generate, hipGraphExec_t *out) {
+  hipStream_t s = m->s;
+  BCH_TRY(check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture"));
+  if (generate) run_argmax(s, m->logits, m->tokens, m->n_vocab, m->dpos, true);
+  record_step(m, s, true, false);
+  hipGraph_t g;
+  BCH_TRY(check_hip(hipStreamEndCapture(s, &g), "end capture"));
+  hipError_t e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  return check_hip(e, "instantiate graph");
+}
+
+static int set_dpos(bch_lfm2 *m, uint32_t value) {
+  m->dpos_host = value;
+  return check_hip(hipMemcpyAsync(m->dpos, &m->dpos_host, 4, hipMemcpyHostToDevice, m->s), "write position");
+}
+
+static int finish(bch_lfm2 *m) {
+  hipEventRecord(m->ev1, m->s);
+  BCH_TRY(check_hip(hipEventSynchronize(m->ev1), "the GPU failed to run the work"));
+  float ms = 0.f;
+  hipEventElapsedTime(&ms, m->ev0, m->ev1);
+  m->last_gpu_seconds = ms * 1e-3;
+  return check_hip(hipGetLastError(), "launch");
+}
+
+static int busy_check(bch_lfm2 *m) {
+  if (m->ctx->recording || m->ctx->committed > m->ctx->waited)
+    return fail(BCH_ERR_BUSY, "the backend has recorded work in flight");
+  return BCH_OK;
+}
+
+}  // namespace bch
+
+extern "C" {
+
+int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_half, bch_lfm2 **out) {
+  *out = nullptr;
+  if (n_ctx == 0) return fail(BCH_ERR_ARGUMENT, "the context must hold a token");
+  if (!md->layers || md->n_layers == 0 || md->n_embd == 0 || md->n_heads == 0)
+    return fail(BCH_ERR_ARGUMENT, "the model has no layers");
+  const uint32_t n = md->n_embd, hd = md->head_dim;
+  if (md->conv_kernel < 2 || md->conv_kernel > 9)
+    return fail(BCH_ERR_UNSUPPORTED_FORMAT, "a convolution of 2 to 9 taps, got %u", md->conv_kernel);
+  bool any_attn = false;
+  for (uint32_t il = 0; il < md->n_layers; il++) {
+    if (md->layers[il].is_moe)
+      return fail(BCH_ERR_UNSUPPORTED_FORMAT, "layer %u: mixture-of-experts blocks are not built yet", il);
+    any_attn |= md->layers[il].is_attention != 0;
+  }
+  if (any_attn) {
+    const uint32_t group = md->n_kv_heads ? md->n_heads / md->n_kv_heads : 0;
+    if (!md->n_kv_heads || md->n_heads % md->n_kv_heads || group > 4 || hd % 32 || hd > 256 || hd == 0)
+      return fail(BCH_ERR_ATTENTION_LIMITS,
+                  "a head size that is a multiple of 32 up to 256 and at most 4 query heads per KV head, got %u and %u",
+                  hd, group);
+  }
+  auto *m = new bch_lfm2();
+  m->ctx = ctx;
+  m->s = ctx->stream;
+  m->n_layers = md->n_layers;
+  m->n_embd = n;
+  m->n_ff = md->n_ff;
+  m->n_heads = md->n_heads;
+  m->n_kv_heads = md->n_kv_heads;
+  m->head_dim = hd;
+  m->n_vocab = md->n_vocab;
+  m->conv_kernel = md->conv_kernel;
+  m->rope_theta = md->rope_theta;
+  m->norm_eps = md->norm_eps;
+  m->q_dim = md->n_heads * hd;
+  m->kv_dim = md->n_kv_heads * hd;
+  m->n_ctx = n_ctx;
+  m->kv_half = kv_half != 0;
+  m->batch = std::min(n_ctx, kPrefillBatch);
+  auto cleanup = [&](int rc) {
+    bch_lfm2_free(m);
+    return rc;
+  };
+
+  // Validate and plan the weight upload.
+  Uploader up;
+  std::vector<std::pair<const void **, size_t>> fixups;  // device pointer field -> upload slot
+  m->layers.resize(md->n_layers);
+  auto vec = [&](const float *p, uint64_t count, const float **field, const char *name) -> int {
+    if (!p) return fail(BCH_ERR_ARGUMENT, "missing tensor %s", name);
+    fixups.push_back({reinterpret_cast<const void **>(field), up.add(p, count * 4)});
+    return BCH_OK;
+  };
+  auto mat = [&](const bch_matrix &src, uint32_t rows, uint32_t cols, DevMatrix *dst, const char *name) -> int {
+    BCH_TRY(check_matrix(src, rows, cols, name));
+    dst->format = src.format;
+    dst->n_rows = rows;
+    dst->n_cols = cols;
+    fixups.push_back({reinterpret_cast<const void **>(&dst->data), up.add(src.data, bch_row_bytes(src.format, cols) * rows)});
+    return BCH_OK;
+  };
+  for (uint32_t il = 0; il < md->n_layers; il++) {
+    const bch_lfm2_layer &S = md->layers[il];
+    Layer &L = m->layers[il];
+    int rc;
+    if ((rc = vec(S.attn_norm, n, &L.attn_norm, "attn_norm")) || (rc = vec(S.ffn_norm, n, &L.ffn_norm, "ffn_norm")))
+      return cleanup(rc);
+    L.attention = S.is_attention != 0;
+    if (L.attention) {
+      L.cache_index = m->n_attn++;
+      if ((rc = mat(S.wq, m->q_dim, n, &L.wq, "attn_q")) || (rc = mat(S.wk, m->kv_dim, n, &L.wk, "attn_k")) ||
+          (rc = mat(S.wv, m->kv_dim, n, &L.wv, "attn_v")) || (rc = mat(S.wo, n, m->q_dim, &L.wo, "attn_output")) ||
+          (rc = vec(S.q_norm, hd, &L.q_norm, "attn_q_norm")) || (rc = vec(S.k_norm, hd, &L.k_norm, "attn_k_norm")))
+        return cleanup(rc);
+      if (S.wq.format != S.wk.format || S.wq.format != S.wv.format)
+        return cleanup(fail(BCH_ERR_UNSUPPORTED_FORMAT, "layer %u: q, k and v matrices of one format", il));
+    } else {
+      L.cache_index = m->n_conv++;
+      if ((rc = mat(S.in_proj, 3 * n, n, &L.in_proj, "shortconv.in_proj")) ||
+          (rc = mat(S.out_proj, n, n, &L.out_proj, "shortconv.out_proj")) ||
+          (rc = vec(S.conv_taps, (uint64_t)n * md->conv_kernel, &L.taps, "shortconv.conv")))
+        return cleanup(rc);
+      if (S.in_proj.format != BCH_Q4K)
+        return cleanup(fail(BCH_ERR_UNSUPPORTED_FORMAT, "layer %u: the fused conv projection needs Q4_K", il));
+    }
+    if ((rc = mat(S.gate, md->n_ff, n, &L.gate, "ffn_gate")) || (rc = mat(S.up, md->n_ff, n, &L.up, "ffn_up")) ||
+        (rc = mat(S.down, n, md->n_ff, &L.down, "ffn_down")))
+      return cleanup(rc);
+    if (S.gate.format != S.up.format)
+      return cleanup(fail(BCH_ERR_UNSUPPORTED_FORMAT, "layer %u: gate and up matrices of one format", il));
+  }
+  {
+    int rc;
+    if ((rc = mat(md->token_embd, md->n_vocab, n, &m->token_embd, "token_embd")) ||
+        (rc = mat(md->output, md->n_vocab, n, &m->output, "output")) ||
+        (rc = vec(md->output_norm, n, &m->output_norm, "token_embd_norm")))
+      return cleanup(rc);
+  }
+  // Upload.
+  {
+    void *w;
+    int rc = dev_alloc(m, up.total, &w);
+    if (rc) return cleanup(rc);
+    m->weights = static_cast<uint8_t *>(w);
+    for (size_t i = 0; i < up.items.size(); i++)
+      if (hipMemcpy(m->weights + up.offsets[i], up.items[i].first, up.items[i].second, hipMemcpyHostToDevice) !=
+          hipSuccess)
+        return cleanup(fail(BCH_ERR_ALLOCATION, "cannot copy the weights to the device"));
+    for (auto &f : fixups) *f.first = m->weights + up.offsets[f.second];
+  }
+  // Buffers (Lfm2Metal::new, lfm2_metal.rs:153-203).
+  {
+    const uint64_t rows = m->batch;
+    const uint64_t cache = (uint64_t)m->n_attn * n_ctx * m->kv_dim * (m->kv_half ? 2 : 4);
+    m->decode_splits = attention_splits(n_ctx, std::max(1u, m->n_kv_heads), ctx->n_cus);
+    m->prefill_splits = m->decode_splits;
+    const uint64_t partial_floats = attention_partial_floats(
+        std::min<uint32_t>(m->batch, kAttnQueryBatch), m->n_heads, hd, m->decode_splits);
+    int rc = 0;
+    (void)((rc = dev_alloc(m, cache, &m->k_cache)) || (rc = dev_alloc(m, cache, &m->v_cache)) ||
+           (rc = dev_alloc_t(m, (uint64_t)m->n_conv * (m->conv_kernel - 1) * n, &m->conv_state)) ||
+           (rc = dev_alloc_t(m, rows * n, &m->hidden)) || (rc = dev_alloc_t(m, rows * n, &m->normed)) ||
+           (rc = dev_alloc_t(m, rows * 3 * n, &m->bcx)) || (rc = dev_alloc_t(m, rows * n, &m->conv_out)) ||
+           (rc = dev_alloc_t(m, rows * m->q_dim + 4, &m->q)) || (rc = dev_alloc_t(m, rows * m->kv_dim + 4, &m->k)) ||
+           (rc = dev_alloc_t(m, rows * m->kv_dim + 4, &m->v)) || (rc = dev_alloc_t(m, rows * m->q_dim + 4, &m->attn)) ||
+           (rc = dev_alloc_t(m, rows * m->n_ff, &m->ffn)) || (rc = dev_alloc_t(m, m->n_vocab, &m->logits)) ||
+           (rc = dev_alloc_t(m, partial_floats + 4, &m->partials)) ||
+           (rc = dev_alloc_t(m, (uint64_t)kAttnQueryBatch * std::max(1u, m->n_kv_heads), &m->counters)) ||
+           (rc = dev_alloc_t(m, (uint64_t)n_ctx + 2, &m->tokens)) || (rc = dev_alloc_t(m, 4, &m->dpos)) ||
+           (rc = dev_alloc_t(m, 4, &m->greedy)));
+    if (rc) return cleanup(rc);
+  }
+  hipEventCreate(&m->ev0);
+  hipEventCreate(&m->ev1);
+  *out = m;
+  return BCH_OK;
+}
+
+void bch_lfm2_free(bch_lfm2 *m) {
+  if (!m) return;
+  // The context (and its stream) must still be open: free drivers first.
+  if (m->s) hipStreamSynchronize(m->s);
+  if (m->step_graph) hipGraphExecDestroy(m->step_graph);
+  if (m->gen_graph) hipGraphExecDestroy(m->gen_graph);
+  if (m->ev0) hipEventDestroy(m->ev0);
+  if (m->ev1) hipEventDestroy(m->ev1);
+  for (void *p : m->allocations) hipFree(p);
+  delete m;
+}
+
+uint32_t bch_lfm2_n_past(const bch_lfm2 *m) { return m->n_past; }
+double bch_lfm2_last_gpu_seconds(const bch_lfm2 *m) { return m->last_gpu_seconds; }
+
+int bch_lfm2_reset(bch_lfm2 *m) {
+  BCH_TRY(busy_check(m));
+  // A new sequence starts from zero convolution history; the KV cache needs
+  // no clearing (lfm2_metal.rs:237-247).
+  if (m->n_conv)
+    BCH_TRY(check_hip(hipMemsetAsync(m->conv_state, 0, (uint64_t)m->n_conv * (m->conv_kernel - 1) * m->n_embd * 4, m->s),
+                      "clear conv state"));
+  BCH_TRY(check_hip(hipStreamSynchronize(m->s), "reset"));
+  m->n_past = 0;
+  m->resets++;
+  m->have_logits = false;
+  return BCH_OK;
+}
+
+int bch_lfm2_step(bch_lfm2 *m, uint32_t token, float *logits, float *trace_embedding, float *trace_layers,
+                  float *trace_final) {
+  BCH_TRY(busy_check(m));
+  if (m->n_past >= m->n_ctx) return fail(BCH_ERR_CONTEXT_FULL, "the context is full");
+  if (token >= m->n_vocab) return fail(BCH_ERR_TOKEN, "token %u is outside the vocabulary of %u", token, m->n_vocab);
+  const bool trace = trace_embedding || trace_layers || trace_final;
+  if (trace) BCH_TRY(ensure_trace_rows(m, 1));
+  hipStream_t s = m->s;
+  m->token_host = token;
+  BCH_TRY(check_hip(hipMemcpyAsync(m->tokens + m->n_past, &m->token_host, 4, hipMemcpyHostToDevice, s), "write token"));
+  BCH_TRY(set_dpos(m, m->n_past));
+  hipEventRecord(m->ev0, s);
+  if (trace) {
+    record_step(m, s, true, true);
+  } else {
+    if (!m->step_graph) BCH_TRY(capture(m, false, &m->step_graph));
+    BCH_TRY(check_hip(hipGraphLaunch(m->step_graph, s), "launch step graph"));
+  }
+  BCH_TRY(finish(m));
+  const uint32_t n = m->n_embd;
+  const uint64_t tstride = (uint64_t)m->trace_rows * n;
+  if (logits) BCH_TRY(check_hip(hipMemcpy(logits, m->logits, (uint64_t)m->n_vocab * 4, hipMemcpyDeviceToHost), "read logits"));
+  if (trace_embedding) hipMemcpy(trace_embedding, m->trace, (uint64_t)n * 4, hipMemcpyDeviceToHost);
+  if (trace_layers)
+    for (uint32_t il = 0; il < m->n_layers; il++)
+      hipMemcpy(trace_layers + (uint64_t)il * n, m->trace + (1 + il) * tstride, (uint64_t)n * 4, hipMemcpyDeviceToHost);
+  if (trace_final) hipMemcpy(trace_final, m->trace + (1 + m->n_layers) * tstride, (uint64_t)n * 4, hipMemcpyDeviceToHost);
+  m->n_past++;
+  m->have_logits = true;
+  return BCH_OK;
+}
+
+int bch_lfm2_prefill(bch_lfm2 *m, const uint32_t *tokens, uint32_t n_tokens, float *logits, float *trace_embedding,
+                     float *trace_layers, float *trace_final) {
+  BCH_TRY(busy_check(m));
+  if (n_tokens == 0) return fail(BCH_ERR_ARGUMENT, "the prompt must hold a token");
+  if (n_tokens > m->n_ctx - m->n_past)
+    return fail(BCH_ERR_CONTEXT_FULL, "the prompt of %u tokens exceeds the %u free positions", n_tokens,
+                m->n_ctx - m->n_past);
+  for (uint32_t i = 0; i < n_tokens; i++)
+    if (tokens[i] >= m->n_vocab) return fail(BCH_ERR_TOKEN, "token %u is outside the vocabulary of %u", tokens[i], m->n_vocab);
+  hipStream_t s = m->s;
+  BCH_TRY(check_hip(hipMemcpyAsync(m->tokens + m->n_past, tokens, (uint64_t)n_tokens * 4, hipMemcpyHostToDevice, s),
+                    "write tokens"));
+  const bool trace = trace_embedding || trace_layers || trace_final;
+  if (trace) BCH_TRY(ensure_trace_rows(m, m->batch));
+  const uint32_t n = m->n_embd;
+  const uint64_t tstride = (uint64_t)m->trace_rows * n;
+  double gpu = 0.0;
+  for (uint32_t done = 0; done < n_tokens; done += m->batch) {
+    const uint32_t count = std::min(m->batch, n_tokens - done);
+    const bool last = done + count == n_tokens;
+    hipEventRecord(m->ev0, s);
+    record_batch(m, s, m->n_past + done, count, last, trace);
+    // A traced batch finishes before the next overwrites the trace rows, as
+    // in the reference (lfm2_metal.rs:727-746); others run back to back.
+    if (trace || last) {
+      BCH_TRY(finish(m));
+      gpu += m->last_gpu_seconds;
+    }
+    if (trace) {
+      const uint64_t rows = (uint64_t)count * n * 4;
+      if (trace_embedding) hipMemcpy(trace_embedding + (uint64_t)done * n, m->trace, rows, hipMemcpyDeviceToHost);
+      if (trace_final)
+        hipMemcpy(trace_final + (uint64_t)done * n, m->trace + (1 + m->n_layers) * tstride, rows, hipMemcpyDeviceToHost);
+      if (trace_layers)
+        for (uint32_t il = 0; il < m->n_layers; il++)
+          hipMemcpy(trace_layers + ((uint64_t)il * n_tokens + done) * n, m->trace + (1 + il) * tstride, rows,
+                    hipMemcpyDeviceToHost);
+    }
+  }
+  m->last_gpu_seconds = gpu;
+  if (logits) BCH_TRY(check_hip(hipMemcpy(logits, m->logits, (uint64_t)m->n_vocab * 4, hipMemcpyDeviceToHost), "read logits"));
+  m->n_past += n_tokens;
+  m->have_logits = true;
+  return BCH_OK;
+}
+
+int bch_lfm2_greedy_token(bch_lfm2 *m, uint32_t *token) {
+  BCH_TRY(busy_check(m));
+  if (m->n_past == 0 || !m->have_logits) return fail(BCH_ERR_ARGUMENT, "generation needs a prompt first");
+  hipEventRecord(m->ev0, m->s);
+  run_argmax(m->s, m->logits, m->greedy, m->n_vocab, nullptr, false);
+  BCH_TRY(finish(m));
+  return check_hip(hipMemcpy(token, m->greedy, 4, hipMemcpyDeviceToHost), "read token");
+}
+
+int bch_lfm2_generate(bch_lfm2 *m, uint32_t *out, uint32_t n) {
+  BCH_TRY(busy_check(m));
+  if (m->n_past == 0 || !m->have_logits) return fail(BCH_ERR_ARGUMENT, "generation needs a prompt first");
+  if (n > m->n_ctx - m->n_past)
+    return fail(BCH_ERR_CONTEXT_FULL, "%u tokens exceed the %u free positions", n, m->n_ctx - m->n_past);
+  if (n == 0) return BCH_OK;
+  if (!m->gen_graph) BCH_TRY(capture(m, true, &m->gen_graph));
+  // Each replay writes argmax(logits) into tokens[dpos + 1], advances dpos
+  // and runs the step there; dpos starts at the last consumed position.
+  BCH_TRY(set_dpos(m, m->n_past - 1));
+  hipEventRecord(m->ev0, m->s);
+  for (uint32_t i = 0; i < n; i++) BCH_TRY(check_hip(hipGraphLaunch(m->gen_graph, m->s), "launch decode graph"));
+  BCH_TRY(finish(m));
+  BCH_TRY(check_hip(hipMemcpy(out, m->tokens + m->n_past, (uint64_t)n * 4, hipMemcpyDeviceToHost), "read tokens"));
+  m->n_past += n;
+  return BCH_OK;
+}
+
+// Checkpoint blob: resets (u64), n_past (u32), pad (u32), conv state, logits.
+uint64_t bch_lfm2_checkpoint_bytes(const bch_lfm2 *m) {
+  return 16 + ((uint64_t)m->n_conv * (m->conv_kernel - 1) * m->n_embd + m->n_vocab) * 4;
+}
+
+int bch_lfm2_checkpoint(bch_lfm2 *m, void *blob, uint64_t bytes) {
+  BCH_TRY(busy_check(m));
+  if (bytes != bch_lfm2_checkpoint_bytes(m)) return fail(BCH_ERR_ARGUMENT, "checkpoint buffer of the wrong size");
+  char *p = static_cast<char *>(blob);
+  memcpy(p, &m->resets, 8);
+  memcpy(p + 8, &m->n_past, 4);
+  const uint32_t have = m->have_logits;
+  memcpy(p + 12, &have, 4);
+  const uint64_t conv = (uint64_t)m->n_conv * (m->conv_kernel - 1) * m->n_embd * 4;
+  BCH_TRY(check_hip(hipMemcpy(p + 16, m->conv_state, conv, hipMemcpyDeviceToHost), "read conv state"));
+  return check_hip(hipMemcpy(p + 16 + conv, m->logits, (uint64_t)m->n_vocab * 4, hipMemcpyDeviceToHost), "read logits");
+}
+
+int bch_lfm2_restore(bch_lfm2 *m, const void *blob, uint64_t bytes) {
+  BCH_TRY(busy_check(m));
+  if (bytes != bch_lfm2_checkpoint_bytes(m))
+    return fail(BCH_ERR_ARGUMENT, "the checkpoint comes from a different model or context");
+  const char *p = static_cast<const char *>(blob);
+  uint64_t resets;
+  uint32_t n_past, have;
+  memcpy(&resets, p, 8);
+  memcpy(&n_past, p + 8, 4);
+  memcpy(&have, p + 12, 4);
+  if (resets != m->resets) return fail(BCH_ERR_ARGUMENT, "the checkpoint predates a reset");
+  if (n_past > m->n_ctx) return fail(BCH_ERR_ARGUMENT, "the checkpoint comes from a different model or context");
+  const uint64_t conv = (uint64_t)m->n_conv * (m->conv_kernel - 1) * m->n_embd * 4;
+  BCH_TRY(check_hip(hipMemcpy(m->conv_state, p + 16, conv, hipMemcpyHostToDevice), "write conv state"));
+  BCH_TRY(check_hip(hipMemcpy(m->logits, p + 16 + conv, (uint64_t)m->n_vocab * 4, hipMemcpyHostToDevice), "write logits"));
+  m->n_past = n_past;
+  m->have_logits = have != 0;
+  return BCH_OK;
+}
+
+}  // extern "C"

@@ -16,6 +16,7 @@
 #include <cstdlib>
 
 #include "formats.h"
+#include "kernels.h"
 #include "runtime.h"
 
 namespace bch {
@@ -71,6 +72,58 @@ __global__ __launch_bounds__(kThreads) void k_matvec(const uint8_t *__restrict__
           y[first + r] = ACC ? y[first + r] + t : t;
         }
       }
+    }
+  }
+}
+
+// Rows of three matrices that share one input, as one launch: row r of the
+// stacked matrix comes from W0 (r < r0), W1 (r < r0 + r1) or W2, and goes
+// to the matching output.  Used for an attention layer's q, k and v.
+template <class F, int LPR, int R, bool NORM>
+__global__ __launch_bounds__(kThreads) void k_matvec3(const uint8_t *__restrict__ W0, const uint8_t *__restrict__ W1,
+                                                      const uint8_t *__restrict__ W2, uint32_t r0, uint32_t r1,
+                                                      uint64_t row_bytes, const float *__restrict__ x,
+                                                      float *__restrict__ y0, float *__restrict__ y1,
+                                                      float *__restrict__ y2, uint32_t n_rows, uint32_t n_units,
+                                                      const float *__restrict__ nw, float eps, uint32_t n_cols) {
+  constexpr int G = kWave / LPR;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int g = lane / LPR, li = lane % LPR;
+  const uint32_t first = ((blockIdx.x * kWaves + wave) * G + g) * R;
+  float scale = 1.f;
+  if (NORM) scale = norm_scale(x, n_cols, eps);
+  if (first < n_rows) {
+    const uint8_t *rows[R];
+    float *outs[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const uint32_t row = min(first + r, n_rows - 1);
+      if (row < r0) {
+        rows[r] = W0 + (uint64_t)row * row_bytes;
+        outs[r] = y0 + row;
+      } else if (row < r0 + r1) {
+        rows[r] = W1 + (uint64_t)(row - r0) * row_bytes;
+        outs[r] = y1 + (row - r0);
+      } else {
+        rows[r] = W2 + (uint64_t)(row - r0 - r1) * row_bytes;
+        outs[r] = y2 + (row - r0 - r1);
+      }
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.f;
+    for (uint32_t u = li; u < n_units; u += LPR) {
+      typename F::Frag f;
+      F::template load<NORM>(x, nw, u, f);
+#pragma unroll
+      for (int r = 0; r < R; r++) acc[r] += F::dot(rows[r], u, f);
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = group_sum<LPR>(acc[r]);
+    if (li == 0) {
+#pragma unroll
+      for (int r = 0; r < R; r++)
+        if (first + r < n_rows) *outs[r] = acc[r] * scale;
     }
   }
 }
@@ -198,7 +251,7 @@ static Geometry choose(uint32_t n_rows, uint32_t n_units, uint32_t n_cus, int ma
     if (forced_lpr && lpr != forced_lpr) continue;
     const uint32_t iters = (n_units + lpr - 1) / lpr;
     const double util = (double)n_units / ((double)lpr * iters);
-    for (int r : {4, 2, 1}) {
+    for (int r : {8, 4, 2, 1}) {
       if (r > max_r || (forced_r && r != forced_r)) continue;
       const double rows_per_wave = (double)(kWave / lpr) * r;
       const double waves = std::ceil(n_rows / rows_per_wave);
@@ -218,84 +271,129 @@ static uint32_t grid_for(uint32_t n_rows, Geometry g) {
   return div_ceil(n_rows, rows_per_block);
 }
 
-template <class F, int LPR, int R>
-static void launch_matvec_t(hipStream_t s, uint32_t grid, bool norm, bool acc, const uint8_t *W, uint64_t rb,
-                            const float *x, float *y, uint32_t n_rows, uint32_t n_units, const float *nw,
-                            float eps, uint32_t n_cols) {
-  if (norm && acc)
-    k_matvec<F, LPR, R, true, true><<<grid, kThreads, 0, s>>>(W, rb, x, y, n_rows, n_units, nw, eps, n_cols);
-  else if (norm)
-    k_matvec<F, LPR, R, true, false><<<grid, kThreads, 0, s>>>(W, rb, x, y, n_rows, n_units, nw, eps, n_cols);
-  else if (acc)
-    k_matvec<F, LPR, R, false, true><<<grid, kThreads, 0, s>>>(W, rb, x, y, n_rows, n_units, nw, eps, n_cols);
-  else
-    k_matvec<F, LPR, R, false, false><<<grid, kThreads, 0, s>>>(W, rb, x, y, n_rows, n_units, nw, eps, n_cols);
-}
-
-template <class F, int LPR>
-static void launch_matvec_r(hipStream_t s, Geometry g, uint32_t grid, bool norm, bool acc, const uint8_t *W,
-                            uint64_t rb, const float *x, float *y, uint32_t n_rows, uint32_t n_units,
-                            const float *nw, float eps, uint32_t n_cols) {
-  switch (g.r) {
-    case 4: launch_matvec_t<F, LPR, 4>(s, grid, norm, acc, W, rb, x, y, n_rows, n_units, nw, eps, n_cols); break;
-    case 2: launch_matvec_t<F, LPR, 2>(s, grid, norm, acc, W, rb, x, y, n_rows, n_units, nw, eps, n_cols); break;
-    default: launch_matvec_t<F, LPR, 1>(s, grid, norm, acc, W, rb, x, y, n_rows, n_units, nw, eps, n_cols); break;
+// Call f.template operator()<LPR, R>() for the runtime geometry.
+template <class Fn>
+static void dispatch_geometry(Geometry g, Fn &&f) {
+#define BCH_R_CASES(L)                                       \
+  switch (g.r) {                                             \
+    case 8: f.template operator()<L, 8>(); break;            \
+    case 4: f.template operator()<L, 4>(); break;            \
+    case 2: f.template operator()<L, 2>(); break;            \
+    default: f.template operator()<L, 1>(); break;           \
   }
+  switch (g.lpr) {
+    case 64: BCH_R_CASES(64) break;
+    case 32: BCH_R_CASES(32) break;
+    case 16: BCH_R_CASES(16) break;
+    case 8: BCH_R_CASES(8) break;
+    default: BCH_R_CASES(4) break;
+  }
+#undef BCH_R_CASES
 }
 
 template <class F>
-static void launch_matvec_f(hipStream_t s, Geometry g, bool norm, bool acc, const uint8_t *W, uint64_t rb,
-                            const float *x, float *y, uint32_t n_rows, uint32_t n_units, const float *nw,
-                            float eps, uint32_t n_cols) {
+static void matvec_f(hipStream_t s, Geometry g, const uint8_t *W, uint64_t rb, const float *x, float *y,
+                     uint32_t n_rows, uint32_t n_units, const float *nw, float eps, uint32_t n_cols, bool norm,
+                     bool acc) {
   const uint32_t grid = grid_for(n_rows, g);
-  switch (g.lpr) {
-    case 64: launch_matvec_r<F, 64>(s, g, grid, norm, acc, W, rb, x, y, n_rows, n_units, nw, eps, n_cols); break;
-    case 32: launch_matvec_r<F, 32>(s, g, grid, norm, acc, W, rb, x, y, n_rows, n_units, nw, eps, n_cols); break;
-    case 16: launch_matvec_r<F, 16>(s, g, grid, norm, acc, W, rb, x, y, n_rows, n_units, nw, eps, n_cols); break;
-    case 8: launch_matvec_r<F, 8>(s, g, grid, norm, acc, W, rb, x, y, n_rows, n_units, nw, eps, n_cols); break;
-    default: launch_matvec_r<F, 4>(s, g, grid, norm, acc, W, rb, x, y, n_rows, n_units, nw, eps, n_cols); break;
-  }
-}
-
-template <class F, int LPR>
-static void launch_swiglu_r(hipStream_t s, Geometry g, uint32_t grid, const uint8_t *Wg, const uint8_t *Wu,
-                            uint64_t rb, const float *x, float *y, uint32_t n_rows, uint32_t n_units,
-                            const float *nw, float eps, uint32_t n_cols) {
-  switch (g.r) {
-    case 4: k_matvec_swiglu<F, LPR, 4><<<grid, kThreads, 0, s>>>(Wg, Wu, rb, x, y, n_rows, n_units, nw, eps, n_cols); break;
-    case 2: k_matvec_swiglu<F, LPR, 2><<<grid, kThreads, 0, s>>>(Wg, Wu, rb, x, y, n_rows, n_units, nw, eps, n_cols); break;
-    default: k_matvec_swiglu<F, LPR, 1><<<grid, kThreads, 0, s>>>(Wg, Wu, rb, x, y, n_rows, n_units, nw, eps, n_cols); break;
-  }
+  dispatch_geometry(g, [&]<int L, int R>() {
+    if (norm && acc)
+      k_matvec<F, L, R, true, true><<<grid, kThreads, 0, s>>>(W, rb, x, y, n_rows, n_units, nw, eps, n_cols);
+    else if (norm)
+      k_matvec<F, L, R, true, false><<<grid, kThreads, 0, s>>>(W, rb, x, y, n_rows, n_units, nw, eps, n_cols);
+    else if (acc)
+      k_matvec<F, L, R, false, true><<<grid, kThreads, 0, s>>>(W, rb, x, y, n_rows, n_units, nw, eps, n_cols);
+    else
+      k_matvec<F, L, R, false, false><<<grid, kThreads, 0, s>>>(W, rb, x, y, n_rows, n_units, nw, eps, n_cols);
+  });
 }
 
 template <class F>
-static void launch_swiglu_f(hipStream_t s, Geometry g, const uint8_t *Wg, const uint8_t *Wu, uint64_t rb,
-                            const float *x, float *y, uint32_t n_rows, uint32_t n_units, const float *nw,
-                            float eps, uint32_t n_cols) {
+static void matvec3_f(hipStream_t s, Geometry g, const uint8_t *W0, const uint8_t *W1, const uint8_t *W2,
+                      uint32_t r0, uint32_t r1, uint64_t rb, const float *x, float *y0, float *y1, float *y2,
+                      uint32_t n_rows, uint32_t n_units, const float *nw, float eps, uint32_t n_cols) {
   const uint32_t grid = grid_for(n_rows, g);
-  switch (g.lpr) {
-    case 64: launch_swiglu_r<F, 64>(s, g, grid, Wg, Wu, rb, x, y, n_rows, n_units, nw, eps, n_cols); break;
-    case 32: launch_swiglu_r<F, 32>(s, g, grid, Wg, Wu, rb, x, y, n_rows, n_units, nw, eps, n_cols); break;
-    case 16: launch_swiglu_r<F, 16>(s, g, grid, Wg, Wu, rb, x, y, n_rows, n_units, nw, eps, n_cols); break;
-    case 8: launch_swiglu_r<F, 8>(s, g, grid, Wg, Wu, rb, x, y, n_rows, n_units, nw, eps, n_cols); break;
-    default: launch_swiglu_r<F, 4>(s, g, grid, Wg, Wu, rb, x, y, n_rows, n_units, nw, eps, n_cols); break;
-  }
+  dispatch_geometry(g, [&]<int L, int R>() {
+    if (nw)
+      k_matvec3<F, L, R, true><<<grid, kThreads, 0, s>>>(W0, W1, W2, r0, r1, rb, x, y0, y1, y2, n_rows, n_units, nw,
+                                                         eps, n_cols);
+    else
+      k_matvec3<F, L, R, false><<<grid, kThreads, 0, s>>>(W0, W1, W2, r0, r1, rb, x, y0, y1, y2, n_rows, n_units, nw,
+                                                          eps, n_cols);
+  });
 }
 
-template <class F, int LPR>
-static void launch_conv_l(hipStream_t s, uint32_t grid, bool norm, const uint8_t *W, uint64_t rb,
-                          const float *x, uint32_t n_units, const float *nw, float eps, uint32_t n_cols,
-                          const float *taps, float *hist, float *out, uint32_t n_embd, uint32_t k) {
-  if (norm)
-    k_matvec_conv<F, LPR, true><<<grid, kThreads, 0, s>>>(W, rb, x, n_units, nw, eps, n_cols, taps, hist, out, n_embd, k);
-  else
-    k_matvec_conv<F, LPR, false><<<grid, kThreads, 0, s>>>(W, rb, x, n_units, nw, eps, n_cols, taps, hist, out, n_embd, k);
+template <class F>
+static void swiglu_f(hipStream_t s, Geometry g, const uint8_t *Wg, const uint8_t *Wu, uint64_t rb, const float *x,
+                     float *y, uint32_t n_rows, uint32_t n_units, const float *nw, float eps, uint32_t n_cols) {
+  const uint32_t grid = grid_for(n_rows, g);
+  dispatch_geometry(g, [&]<int L, int R>() {
+    k_matvec_swiglu<F, L, R><<<grid, kThreads, 0, s>>>(Wg, Wu, rb, x, y, n_rows, n_units, nw, eps, n_cols);
+  });
 }
 
 static bool is_gemv_format(uint32_t f) { return f == Q4K::kFormat || f == F16::kFormat || f == F32::kFormat; }
 
 static uint32_t unit_of(uint32_t f) {
   return f == Q4K::kFormat ? Q4K::kUnit : f == F16::kFormat ? F16::kUnit : F32::kUnit;
+}
+
+// Call f.template operator()<Format>() for a runtime format id.
+template <class Fn>
+static void dispatch_format(uint32_t format, Fn &&f) {
+  if (format == Q4K::kFormat)
+    f.template operator()<Q4K>();
+  else if (format == F16::kFormat)
+    f.template operator()<F16>();
+  else
+    f.template operator()<F32>();
+}
+
+void run_matvec(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,
+                float *y, const float *norm_w, float eps, bool accumulate, uint32_t n_cus) {
+  const uint32_t n_units = n_cols / unit_of(format);
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  const Geometry g = choose(n_rows, n_units, n_cus, 8);
+  dispatch_format(format, [&]<class F>() {
+    matvec_f<F>(s, g, W, rb, x, y, n_rows, n_units, norm_w, eps, n_cols, norm_w != nullptr, accumulate);
+  });
+}
+
+void run_matvec3(hipStream_t s, uint32_t format, const uint8_t *W0, const uint8_t *W1, const uint8_t *W2, uint32_t r0,
+                 uint32_t r1, uint32_t r2, uint32_t n_cols, const float *x, float *y0, float *y1, float *y2,
+                 const float *norm_w, float eps, uint32_t n_cus) {
+  const uint32_t n_units = n_cols / unit_of(format);
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  const uint32_t n_rows = r0 + r1 + r2;
+  const Geometry g = choose(n_rows, n_units, n_cus, 8);
+  dispatch_format(format, [&]<class F>() {
+    matvec3_f<F>(s, g, W0, W1, W2, r0, r1, rb, x, y0, y1, y2, n_rows, n_units, norm_w, eps, n_cols);
+  });
+}
+
+void run_matvec_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const uint8_t *Wu, uint32_t n_rows,
+                       uint32_t n_cols, const float *x, float *y, const float *norm_w, float eps, uint32_t n_cus) {
+  const uint32_t n_units = n_cols / unit_of(format);
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  const Geometry g = choose(n_rows, n_units, n_cus, 4);
+  dispatch_format(format, [&]<class F>() { swiglu_f<F>(s, g, Wg, Wu, rb, x, y, n_rows, n_units, norm_w, eps, n_cols); });
+}
+
+void run_matvec_conv(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_cols, const float *x,
+                     const float *norm_w, float eps, const float *taps, float *history, float *out, uint32_t n_embd,
+                     uint32_t ksize, uint32_t n_cus) {
+  const uint32_t n_units = n_cols / Q4K::kUnit;
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  const Geometry g = choose(n_embd, n_units, n_cus, 1);
+  const uint32_t grid = div_ceil(n_embd, kWaves * (kWave / g.lpr));
+  dispatch_geometry(Geometry{g.lpr, 1}, [&]<int L, int R>() {
+    if (norm_w)
+      k_matvec_conv<Q4K, L, true><<<grid, kThreads, 0, s>>>(W, rb, x, n_units, norm_w, eps, n_cols, taps, history, out,
+                                                            n_embd, ksize);
+    else
+      k_matvec_conv<Q4K, L, false><<<grid, kThreads, 0, s>>>(W, rb, x, n_units, norm_w, eps, n_cols, taps, history,
+                                                             out, n_embd, ksize);
+  });
 }
 
 static int check_shape(const char *name, uint32_t format, uint32_t n_rows, uint32_t n_cols) {
@@ -347,17 +445,9 @@ int bch_matvec(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_rows,
   BCH_TRY(check_align("matvec", xp, 16));
   if (nw) BCH_TRY(check_align("matvec", nw, 16));
   const float eps = norm ? norm->eps : 0.f;
-  const uint32_t n_units = n_cols / unit_of(format);
-  const Geometry g = choose(n_rows, n_units, ctx->n_cus, 4);
-  const bool nm = norm != nullptr, ac = accumulate != 0;
   const char *name = format == Q4K::kFormat ? "matvec_q4k" : format == F16::kFormat ? "matvec_f16" : "matvec_f32";
   return launch(ctx, {name, n_rows, n_cols, rb * n_rows}, [&](hipStream_t s) {
-    if (format == Q4K::kFormat)
-      launch_matvec_f<Q4K>(s, g, nm, ac, W, rb, xp, yp, n_rows, n_units, nw, eps, n_cols);
-    else if (format == F16::kFormat)
-      launch_matvec_f<F16>(s, g, nm, ac, W, rb, xp, yp, n_rows, n_units, nw, eps, n_cols);
-    else
-      launch_matvec_f<F32>(s, g, nm, ac, W, rb, xp, yp, n_rows, n_units, nw, eps, n_cols);
+    run_matvec(s, format, W, n_rows, n_cols, xp, yp, nw, eps, accumulate != 0, ctx->n_cus);
   });
 }
 
@@ -377,17 +467,10 @@ int bch_matvec_swiglu(bch_ctx *ctx, uint32_t format, bch_view gate, bch_view up,
   BCH_TRY(check_align("matvec_swiglu", Wu, 16));
   BCH_TRY(check_align("matvec_swiglu", xp, 16));
   BCH_TRY(check_align("matvec_swiglu", nw, 16));
-  const uint32_t n_units = n_cols / unit_of(format);
-  const Geometry g = choose(n_rows, n_units, ctx->n_cus, 2);
   const char *name = format == Q4K::kFormat ? "matvec_swiglu_q4k" : format == F16::kFormat ? "matvec_swiglu_f16"
                                                                                           : "matvec_swiglu_f32";
   return launch(ctx, {name, n_rows, n_cols, 2 * rb * n_rows}, [&](hipStream_t s) {
-    if (format == Q4K::kFormat)
-      launch_swiglu_f<Q4K>(s, g, Wg, Wu, rb, xp, yp, n_rows, n_units, nw, norm.eps, n_cols);
-    else if (format == F16::kFormat)
-      launch_swiglu_f<F16>(s, g, Wg, Wu, rb, xp, yp, n_rows, n_units, nw, norm.eps, n_cols);
-    else
-      launch_swiglu_f<F32>(s, g, Wg, Wu, rb, xp, yp, n_rows, n_units, nw, norm.eps, n_cols);
+    run_matvec_swiglu(s, format, Wg, Wu, n_rows, n_cols, xp, yp, nw, norm.eps, ctx->n_cus);
   });
 }
 
@@ -413,19 +496,9 @@ int bch_matvec_conv(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_
   BCH_TRY(check_align("matvec_conv", W, 16));
   BCH_TRY(check_align("matvec_conv", xp, 16));
   if (nw) BCH_TRY(check_align("matvec_conv", nw, 16));
-  const uint32_t n_units = n_cols / Q4K::kUnit;
-  Geometry g = choose(n_embd, n_units, ctx->n_cus, 1);
-  const uint32_t grid = div_ceil(n_embd, kWaves * (kWave / g.lpr));
   const float eps = norm ? norm->eps : 0.f;
-  const bool nm = norm != nullptr;
   return launch(ctx, {"matvec_conv_q4k", n_rows, n_cols, rb * n_rows}, [&](hipStream_t s) {
-    switch (g.lpr) {
-      case 64: launch_conv_l<Q4K, 64>(s, grid, nm, W, rb, xp, n_units, nw, eps, n_cols, tp, hp, op, n_embd, kernel_size); break;
-      case 32: launch_conv_l<Q4K, 32>(s, grid, nm, W, rb, xp, n_units, nw, eps, n_cols, tp, hp, op, n_embd, kernel_size); break;
-      case 16: launch_conv_l<Q4K, 16>(s, grid, nm, W, rb, xp, n_units, nw, eps, n_cols, tp, hp, op, n_embd, kernel_size); break;
-      case 8: launch_conv_l<Q4K, 8>(s, grid, nm, W, rb, xp, n_units, nw, eps, n_cols, tp, hp, op, n_embd, kernel_size); break;
-      default: launch_conv_l<Q4K, 4>(s, grid, nm, W, rb, xp, n_units, nw, eps, n_cols, tp, hp, op, n_embd, kernel_size); break;
-    }
+    run_matvec_conv(s, format, W, n_cols, xp, nw, eps, tp, hp, op, n_embd, kernel_size, ctx->n_cus);
   });
 }
 

@@ -38,6 +38,8 @@ struct bch_ctx {
   // Set while a driver captures a graph: launches go to the capture stream
   // and skip profiling and synchronisation.
   bool capturing = false;
+  // Zeroed split counters of the op-level attention launcher.
+  uint32_t *counters = nullptr;
 };
 
 namespace bch {

@@ -117,6 +117,7 @@ void bch_close(bch_ctx *ctx) {
     hipEventDestroy(p.end);
   }
   if (ctx->begin_event) hipEventDestroy(ctx->begin_event);
+  if (ctx->counters) hipFree(ctx->counters);
   hipStreamDestroy(ctx->stream);
   delete ctx;
 }

@@ -174,6 +174,8 @@ int bch_matvec_conv(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_
  * `bcx` hold B, C and X. */
 int bch_short_conv(bch_ctx *ctx, bch_view bcx, bch_view taps, bch_view history,
                    bch_view out, uint32_t n_embd, uint32_t kernel_size, uint32_t n_tokens);
+int bch_short_conv_batch(bch_ctx *ctx, bch_view bcx, bch_view taps, bch_view history,
+                         bch_view out, uint32_t n_embd, uint32_t kernel_size, uint32_t n_tokens);
 
 /* Metal::rms_norm (backend.rs:2034-2059). */
 int bch_rms_norm(bch_ctx *ctx, bch_view x, bch_view weight, bch_view out, uint32_t n,
@@ -215,6 +217,11 @@ int bch_matmul(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_rows,
 /* Metal::argmax (backend.rs:2612): index of the largest of n floats, ties
  * to the lowest index, as a u32 at `out`. */
 int bch_argmax(bch_ctx *ctx, bch_view x, bch_view out, uint32_t n);
+
+/* read_sum (crates/bobcat-metal/src/bandwidth.rs:20-34): n_threads threads
+ * (a multiple of 256) each sum the float4 values of `src` at a stride of
+ * the grid into out[thread].  The streaming-read bandwidth probe. */
+int bch_read_sum(bch_ctx *ctx, bch_view src, uint64_t n_vectors, bch_view out, uint32_t n_threads);
 
 /* ------------------------------------------------------------------ */
 /* LFM2 driver (crates/bobcat/src/lfm2_metal.rs:125-779)               */
@@ -288,8 +295,13 @@ int bch_lfm2_reset(bch_lfm2 *lfm2);
  * layer's output and the final norm of the token. */
 int bch_lfm2_step(bch_lfm2 *lfm2, uint32_t token, float *logits, float *trace_embedding,
                   float *trace_layers, float *trace_final);
-/* Lfm2Metal::prefill (lfm2_metal.rs:662-762), logits of the last token. */
-int bch_lfm2_prefill(bch_lfm2 *lfm2, const uint32_t *tokens, uint32_t n_tokens, float *logits);
+/* Lfm2Metal::prefill (lfm2_metal.rs:662-762), in batches of up to 512
+ * tokens; logits (nullable) receives the last token's.  The trace arrays
+ * (nullable) receive every token's activations: trace_embedding and
+ * trace_final n_tokens·n_embd floats, trace_layers layer by layer, each
+ * layer's n_tokens rows together (lfm2.rs:630-675). */
+int bch_lfm2_prefill(bch_lfm2 *lfm2, const uint32_t *tokens, uint32_t n_tokens, float *logits,
+                     float *trace_embedding, float *trace_layers, float *trace_final);
 /* Lfm2Metal::greedy_token (lfm2_metal.rs:372-398). */
 int bch_lfm2_greedy_token(bch_lfm2 *lfm2, uint32_t *token);
 /* Lfm2Metal::generate (lfm2_metal.rs:408-411): n greedy tokens, the first

@@ -50,6 +50,8 @@ def lib() -> C.CDLL:
             "orc_silu": (C.c_float, [C.c_float]),
             "orc_softmax": (None, [fp, u64]),
             "orc_lfm2_route": (None, [fp, fp, u32, u32, C.POINTER(u32)]),
+            "orc_short_conv": (None, [fp, fp, fp, fp, u32, u32, u32]),
+            "orc_attention": (None, [fp, fp, fp, fp, u32, u32, u32, u32, u32]),
             "orc_lfm2_state_new": (vp, [vp, u32]),
             "orc_lfm2_state_free": (None, [vp]),
             "orc_lfm2_n_past": (u32, [vp]),
@@ -138,6 +140,25 @@ def route(scores: np.ndarray, bias: np.ndarray, n_used: int):
     experts = (C.c_uint32 * s.size)()
     lib().orc_lfm2_route(_fp(s), _fp(b), s.size, n_used, experts)
     return s, list(experts)
+
+
+def short_conv(bcx: np.ndarray, taps: np.ndarray, hist: np.ndarray, n_embd: int, k: int, n_tokens: int):
+    """Returns (out, new_history); `hist` is not modified."""
+    bcx = np.ascontiguousarray(bcx, np.float32)
+    taps = np.ascontiguousarray(taps, np.float32)
+    h = np.array(hist, np.float32)
+    out = np.empty(n_tokens * n_embd, np.float32)
+    lib().orc_short_conv(_fp(bcx), _fp(taps), _fp(h), _fp(out), n_embd, k, n_tokens)
+    return out, h
+
+
+def attention(q, kc, vc, n_heads, n_kv, hd, first_pos, n_queries):
+    q = np.ascontiguousarray(q, np.float32)
+    kc = np.ascontiguousarray(kc, np.float32)
+    vc = np.ascontiguousarray(vc, np.float32)
+    out = np.empty(n_queries * n_heads * hd, np.float32)
+    lib().orc_attention(_fp(q), _fp(kc), _fp(vc), _fp(out), n_heads, n_kv, hd, first_pos, n_queries)
+    return out
 
 
 class Lfm2State:

@@ -551,3 +551,49 @@ EXPORT int orc_lfm2_step(const bch_lfm2_model *m, orc_lfm2_state *s, uint32_t to
   s->n_past++;
   return 0;
 }
+
+/* ---------------------------------------------------------------- */
+/* Stand-alone pieces of the forward pass, for kernel-level checks   */
+/* ---------------------------------------------------------------- */
+
+/* The gated short convolution of conv_block (lfm2.rs:456-475) over
+ * n_tokens rows of bcx ([B | C | X] per token), carrying `history`. */
+EXPORT void orc_short_conv(const float *bcx, const float *taps, float *hist, float *out, uint32_t n,
+                           uint32_t k, uint32_t n_tokens) {
+  for (uint32_t t = 0; t < n_tokens; t++) {
+    const float *b = bcx + (uint64_t)t * 3 * n, *c = b + n, *x = b + 2 * n;
+    for (uint32_t ch = 0; ch < n; ch++) {
+      const float *tp = taps + (uint64_t)ch * k;
+      float bx = b[ch] * x[ch];
+      double sum = (double)tp[k - 1] * (double)bx;
+      for (uint32_t j = 0; j + 1 < k; j++) sum += (double)tp[j] * (double)hist[j * n + ch];
+      for (uint32_t j = 0; j + 2 < k; j++) hist[j * n + ch] = hist[(j + 1) * n + ch];
+      hist[(k - 2) * n + ch] = bx;
+      out[(uint64_t)t * n + ch] = c[ch] * (float)sum;
+    }
+  }
+}
+
+/* The causal attention of attention_block (lfm2.rs:520-556) for n_queries
+ * queries at positions first_pos.., over f32 caches [pos][n_kv][hd]. */
+EXPORT void orc_attention(const float *q, const float *kc, const float *vc, float *out, uint32_t n_heads,
+                          uint32_t n_kv, uint32_t hd, uint32_t first_pos, uint32_t n_queries) {
+  uint32_t kvd = n_kv * hd, group = n_heads / n_kv;
+  float scale = 1.0f / sqrtf((float)hd);
+  float *scores = (float *)malloc(sizeof(float) * (first_pos + n_queries));
+  for (uint32_t qi = 0; qi < n_queries; qi++) {
+    uint32_t n_keys = first_pos + qi + 1;
+    for (uint32_t h = 0; h < n_heads; h++) {
+      const float *qh = q + ((uint64_t)qi * n_heads + h) * hd;
+      uint32_t kv_off = h / group * hd;
+      for (uint32_t t = 0; t < n_keys; t++) scores[t] = scale * orc_dot(qh, kc + (uint64_t)t * kvd + kv_off, hd);
+      orc_softmax(scores, n_keys);
+      for (uint32_t d = 0; d < hd; d++) {
+        double sum = 0.0;
+        for (uint32_t t = 0; t < n_keys; t++) sum += (double)scores[t] * (double)vc[(uint64_t)t * kvd + kv_off + d];
+        out[((uint64_t)qi * n_heads + h) * hd + d] = (float)sum;
+      }
+    }
+  }
+  free(scores);
+}

@@ -1,0 +1,219 @@
+"""GPU parity of the LFM2 driver (bch_lfm2_*) against the oracle's forward pass.
+
+Mirrors crates/bobcat/tests/lfm2_reference.rs with the oracle standing in for
+the transformers dumps (the oracle itself is pinned to transformers in
+tests/test_oracle_lfm2.py):
+  * every layer's output, the final norm and the logits of each step within
+    1e-4 with an f32 KV cache and 5e-3 with an f16 cache (:17-25);
+  * greedy decoding reproduces the oracle's tokens (allowing a flip only where
+    the oracle's top-2 logits differ by less than 1e-3, the north-star rule);
+  * prefill == steps (:117-151), reset == fresh (:155-185), checkpoint and
+    restore (:190-238), generate == repeated greedy steps (:243-350);
+  * the error paths of Lfm2Metal (context full, token outside the vocabulary,
+    generation without a prompt).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from bobcat_amd import BobcatError
+from bobcat_amd.lfm2 import LFM2_TINY, LFM2_TINY_F16, Lfm2Hip, Lfm2Weights
+
+pytestmark = pytest.mark.gpu
+
+TOLERANCE = 1e-4
+HALF_TOLERANCE = 5e-3
+
+
+def rel(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    d = np.abs(got - want)
+    if np.isnan(d).any():
+        return float("inf")
+    return float(d.max() / max(np.abs(want).max(), 1e-30))
+
+
+@pytest.fixture(scope="module", params=[LFM2_TINY, LFM2_TINY_F16], ids=lambda c: c.name)
+def weights(request):
+    return Lfm2Weights(request.param, seed=7)
+
+
+def prompt(cfg, n, seed=1):
+    return np.random.default_rng(seed).integers(0, cfg.n_vocab, n).tolist()
+
+
+@pytest.mark.parametrize("kv_half", [False, True])
+def test_steps_match_oracle_layer_by_layer(hip, weights, kv_half):
+    cfg = weights.cfg
+    tol = HALF_TOLERANCE if kv_half else TOLERANCE
+    gpu = Lfm2Hip(hip, weights, n_ctx=48, kv_half=kv_half)
+    cpu = oracle.Lfm2State(weights, n_ctx=48)
+    worst = np.zeros(cfg.n_layers + 3)
+    for tok in prompt(cfg, 20):
+        lg, (emb, layers, final) = gpu.step(tok, trace=True)
+        wl, (wemb, wlayers, wfinal) = cpu.step(tok, trace=True)
+        errs = [rel(emb, wemb)]
+        errs += [rel(layers[i * cfg.n_embd:(i + 1) * cfg.n_embd], wlayers[i * cfg.n_embd:(i + 1) * cfg.n_embd])
+                 for i in range(cfg.n_layers)]
+        errs += [rel(final, wfinal), rel(lg, wl)]
+        worst = np.maximum(worst, errs)
+    assert worst.max() < tol, worst
+    gpu.close()
+
+
+@pytest.mark.parametrize("kv_half", [False, True])
+def test_prefill_trace_matches_oracle(hip, weights, kv_half):
+    """The batched pass traced for every token (lfm2_reference.rs:581-640 with
+    batched = true): half-precision weight tiles bound it by 5e-3."""
+    cfg = weights.cfg
+    toks = prompt(cfg, 20, seed=11)
+    gpu = Lfm2Hip(hip, weights, n_ctx=48, kv_half=kv_half)
+    lg, (emb, layers, final) = gpu.prefill(toks, trace=True)
+    cpu = oracle.Lfm2State(weights, n_ctx=48)
+    worst = np.zeros(cfg.n_layers + 3)
+    for t, tok in enumerate(toks):
+        wl, (wemb, wlayers, wfinal) = cpu.step(tok, trace=True)
+        errs = [rel(emb[t], wemb)]
+        errs += [rel(layers[i, t], wlayers[i * cfg.n_embd:(i + 1) * cfg.n_embd]) for i in range(cfg.n_layers)]
+        errs += [rel(final[t], wfinal), rel(lg, wl) if t + 1 == len(toks) else 0.0]
+        worst = np.maximum(worst, errs)
+    assert worst.max() < HALF_TOLERANCE, worst
+    gpu.close()
+
+
+def greedy_oracle(weights, tokens, n_gen, n_ctx):
+    """Oracle greedy continuation and, per step, the gap between its top-2 logits."""
+    cpu = oracle.Lfm2State(weights, n_ctx=n_ctx)
+    for t in tokens:
+        lg = cpu.step(t)
+    out, gaps = [], []
+    for _ in range(n_gen):
+        top = np.argsort(lg)[-2:]
+        gaps.append(float(lg[top[1]] - lg[top[0]]))
+        nxt = int(np.argmax(lg))
+        out.append(nxt)
+        lg = cpu.step(nxt)
+    return out, gaps
+
+
+def assert_greedy_matches(got, want, gaps):
+    for i, (g, w) in enumerate(zip(got, want)):
+        if g != w:
+            assert gaps[i] < 1e-3, f"token {i}: {g} vs oracle {w} (top-2 gap {gaps[i]:.3g})"
+            return  # the sequences legitimately diverge after a near-tie
+
+
+def test_greedy_generation_matches_oracle(hip, weights):
+    cfg = weights.cfg
+    toks = prompt(cfg, 16, seed=2)
+    want, gaps = greedy_oracle(weights, toks, 24, n_ctx=64)
+    gpu = Lfm2Hip(hip, weights, n_ctx=64, kv_half=False)
+    gpu.prefill(toks)
+    got = gpu.generate(24)
+    assert_greedy_matches(got.tolist(), want, gaps)
+    assert gpu.n_past == 16 + 24
+    gpu.close()
+
+
+def test_prefill_matches_steps(hip, weights):
+    """lfm2_reference.rs:117-151: one prefill of the prompt equals one step per token."""
+    cfg = weights.cfg
+    toks = prompt(cfg, 70, seed=3)  # spans two attention query batches
+    a = Lfm2Hip(hip, weights, n_ctx=96)
+    b = Lfm2Hip(hip, weights, n_ctx=96)
+    la = a.prefill(toks)
+    for t in toks:
+        lb = b.step(t)
+    assert rel(la, lb) < HALF_TOLERANCE
+    # Continuations agree too.
+    assert rel(a.step(5), b.step(5)) < HALF_TOLERANCE
+    a.close()
+    b.close()
+
+
+def test_prefill_in_batches_matches_one_batch(hip):
+    """A prompt longer than the 512-token prefill batch runs in two batches."""
+    w = Lfm2Weights(LFM2_TINY, seed=9)
+    toks = prompt(LFM2_TINY, 600, seed=4)
+    a = Lfm2Hip(hip, w, n_ctx=700)
+    la = a.prefill(toks)
+    b = Lfm2Hip(hip, w, n_ctx=700)
+    b.prefill(toks[:300])
+    lb = b.prefill(toks[300:])
+    assert rel(la, lb) < HALF_TOLERANCE
+    a.close()
+    b.close()
+
+
+def test_reset_matches_fresh_state(hip, weights):
+    cfg = weights.cfg
+    toks = prompt(cfg, 10, seed=5)
+    a = Lfm2Hip(hip, weights, n_ctx=32)
+    a.prefill(prompt(cfg, 7, seed=6))
+    a.generate(3)
+    a.reset()
+    assert a.n_past == 0
+    la = a.prefill(toks)
+    b = Lfm2Hip(hip, weights, n_ctx=32)
+    lb = b.prefill(toks)
+    assert rel(la, lb) < TOLERANCE
+    a.close()
+    b.close()
+
+
+def test_checkpoint_restore_continues(hip, weights):
+    cfg = weights.cfg
+    a = Lfm2Hip(hip, weights, n_ctx=64)
+    a.prefill(prompt(cfg, 12, seed=7))
+    ck = a.checkpoint()
+    first = a.generate(8)
+    a.restore(ck)
+    assert a.n_past == 12
+    again = a.generate(8)
+    assert np.array_equal(first, again)
+    a.reset()
+    with pytest.raises(BobcatError):
+        a.restore(ck)  # predates the reset
+    a.close()
+
+
+def test_generate_matches_greedy_steps(hip, weights):
+    """generate() on the GPU graph equals greedy_token() + step() on the host."""
+    cfg = weights.cfg
+    toks = prompt(cfg, 9, seed=8)
+    a = Lfm2Hip(hip, weights, n_ctx=64)
+    b = Lfm2Hip(hip, weights, n_ctx=64)
+    a.prefill(toks)
+    b.prefill(toks)
+    got = a.generate(12).tolist()
+    want = []
+    for _ in range(12):
+        t = b.greedy_token()
+        assert b.greedy_token() == t  # selection leaves the state unchanged
+        want.append(t)
+        b.step(t)
+    assert got == want
+    a.close()
+    b.close()
+
+
+def test_error_paths(hip):
+    w = Lfm2Weights(LFM2_TINY, seed=1)
+    m = Lfm2Hip(hip, w, n_ctx=4)
+    with pytest.raises(BobcatError) as e:
+        m.generate(1)
+    assert "prompt" in str(e.value)
+    with pytest.raises(BobcatError) as e:
+        m.step(LFM2_TINY.n_vocab)
+    assert e.value.status == 16  # Token
+    m.prefill([1, 2, 3])
+    with pytest.raises(BobcatError) as e:
+        m.prefill([1, 2])
+    assert e.value.status == 15  # ContextFull
+    m.step(4)
+    with pytest.raises(BobcatError) as e:
+        m.step(5)
+    assert e.value.status == 15
+    m.close()
