@@ -1,14 +1,20 @@
 """Benchmark: bobcat's per-token LM loop on one MI355X.
 
 Prints ONE JSON line (the driver's contract).  Legs:
-  * gemv  — BASELINE config 1: Q4_K dequant-GEMV, W [8192 x 2048], x ~ N(0,1),
-            timed over 64 rotating copies of W (604 MB > the 256 MB MALL) with
-            HIP events on the backend's own stream; gives the roofline object.
-  * cpu   — the oracle's scalar GEMV (1 thread, f64 accumulate, the
-            reference's scalar path restated) on a bounded sample.
-  * model — LFM2 decode/prefill (pp512/tg128), once the driver is built.
+  * model — pp512/tg128 on a random-init LFM2-style model (default: the
+            2.6B config of BASELINE.json configs[3], the north-star target).
+            Protocol of bobcat-bench (docs/performance/eval.md:7-13,
+            bobcat_bench.rs:91-173): 512 random prompt ids, then greedy
+            tokens; prefill rate = 512 / TTFT (TTFT includes the first output
+            token), decode rate = 127 / (t_last - t_first).  One "step" is one
+            such round.  `value` is the decode rate over the timed rounds.
+  * gemv  — BASELINE config 1: Q4_K dequant-GEMV, W [8192 x 2048], timed
+            over 64 rotating copies of W (604 MB > the 256 MB MALL) with HIP
+            events on the backend's own stream: the `roofline` object.
+  * cpu   — the oracle (a C restatement of the reference's scalar Rust path)
+            decoding the same model on the host cores, on a bounded sample.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--model lfm2-2.6b]
 """
 from __future__ import annotations
 
@@ -23,13 +29,19 @@ import numpy as np
 HBM_PEAK_GBS = 8000.0
 GEMV_ROWS, GEMV_COLS = 8192, 2048
 GEMV_BYTES = GEMV_ROWS * GEMV_COLS // 256 * 144 + GEMV_COLS * 4 + GEMV_ROWS * 4  # 9,478,144
+PROMPT, GEN = 512, 128
 
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def gemv_leg(hip, steps: int, warmup: int, copies: int = 64):
+def host_threads() -> int:
+    # The GPU box gives one GPU a 16-core share, whatever os.cpu_count() says.
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def gemv_leg(hip, reps: int, copies: int = 64):
     from bobcat_amd.backend import Format
     from bobcat_amd.synth import gemv_case
 
@@ -41,88 +53,151 @@ def gemv_leg(hip, steps: int, warmup: int, copies: int = 64):
     xb = hip.buffer_from(x)
     yb = hip.new_buffer(GEMV_ROWS * 4)
 
-    def run(n: int) -> float:
+    def run(n: int, rotate: bool = True) -> float:
         hip.begin()
         for i in range(n):
-            hip.matvec(Format.Q4K, big.at((i % copies) * wbytes), GEMV_ROWS, GEMV_COLS, xb.at(0), yb.at(0))
+            off = (i % copies) * wbytes if rotate else 0
+            hip.matvec(Format.Q4K, big.at(off), GEMV_ROWS, GEMV_COLS, xb.at(0), yb.at(0))
         return hip.end()
 
-    run(max(warmup, 1) * copies)
-    launches = steps * copies
-    seconds = run(launches)
-    per_launch = seconds / launches
-    achieved = GEMV_BYTES / per_launch / 1e9
-    # Cache-resident rate on one copy (for the record; not the roofline figure).
-    hip.begin()
-    for _ in range(copies):
-        hip.matvec(Format.Q4K, big.at(0), GEMV_ROWS, GEMV_COLS, xb.at(0), yb.at(0))
-    hot = hip.end() / copies
+    run(copies)
+    launches = reps * copies
+    per_launch = run(launches) / launches
+    hot = run(copies, rotate=False) / copies
     big.free()
-    return dict(us_per_launch=per_launch * 1e6, gbs=achieved, launches=launches,
+    return dict(us=per_launch * 1e6, gbs=GEMV_BYTES / per_launch / 1e9, launches=launches,
                 hot_us=hot * 1e6, hot_gbs=GEMV_BYTES / hot / 1e9)
 
 
-def cpu_leg(budget_s: float = 10.0):
-    import oracle
-    from bobcat_amd.synth import gemv_case
+def model_leg(hip, weights, steps: int, warmup: int, seed: int = 42):
+    from bobcat_amd.lfm2 import Lfm2Hip
 
-    w, x = gemv_case()
-    oracle.set_threads(1)
-    oracle.matvec(12, w, GEMV_ROWS, GEMV_COLS, x)  # warm
+    cfg = weights.cfg
+    rng = np.random.default_rng(seed)
+    prompt = rng.integers(0, cfg.n_vocab, PROMPT).astype(np.uint32)
+    m = Lfm2Hip(hip, weights, n_ctx=PROMPT + GEN, kv_half=True)
+    rounds = []
+    first_tokens = None
+    for r in range(warmup + steps):
+        m.reset()
+        t0 = time.perf_counter()
+        m.prefill(prompt, logits=False)
+        first = m.greedy_token()
+        t1 = time.perf_counter()
+        toks = m.generate(GEN - 1)
+        t2 = time.perf_counter()
+        gpu_decode = m.last_gpu_seconds
+        if r >= warmup:
+            rounds.append(dict(ttft=t1 - t0, decode=t2 - t1, gpu_decode=gpu_decode))
+        first_tokens = [first] + toks.tolist()
+    m.close()
+    ttft = sum(x["ttft"] for x in rounds)
+    dec = sum(x["decode"] for x in rounds)
+    gdec = sum(x["gpu_decode"] for x in rounds)
+    n = len(rounds)
+    return dict(prefill_tok_s=PROMPT * n / ttft, decode_tok_s=(GEN - 1) * n / dec,
+                decode_tok_s_device=(GEN - 1) * n / gdec, ms_per_step=(ttft + dec) / n * 1e3,
+                ttft_ms=ttft / n * 1e3, tpot_ms=dec / n / (GEN - 1) * 1e3, tokens=first_tokens)
+
+
+def cpu_leg(weights, budget_s: float, threads: int):
+    """Decode steps of the oracle on the host: the reference's scalar path
+    (f64-accumulating matvec, lfm2.rs:308-394) restated in C, rows split over
+    `threads` threads.  Bounded: a short prompt, then steps until the budget."""
+    import oracle
+
+    oracle.set_threads(threads)
+    st = oracle.Lfm2State(weights, n_ctx=64)
+    rng = np.random.default_rng(42)
+    for t in rng.integers(0, weights.cfg.n_vocab, 2):
+        st.step(int(t), logits=False)
     n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s:
-        oracle.matvec(12, w, GEMV_ROWS, GEMV_COLS, x)
+    tok = 1
+    while True:
+        lg = st.step(tok)
+        tok = int(np.argmax(lg))
         n += 1
-    dt = (time.perf_counter() - t0) / n
-    return dict(us=dt * 1e6, gbs=GEMV_BYTES / dt / 1e9, reps=n)
+        if time.perf_counter() - t0 > budget_s or n >= 32:
+            break
+    dt = time.perf_counter() - t0
+    return dict(tok_s=n / dt, steps=n, seconds=dt)
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--steps", type=int, default=3, help="timed pp512/tg128 rounds")
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--model", default="lfm2-2.6b")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--gemv-only", action="store_true", help="only the config-1 GEMV leg (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the decode loop is single-device, as in the reference).", file=sys.stderr)
+        print("bench.py measures one GPU: the decode loop is single-device (as in the reference) "
+              "and this build has no multi-GPU path; run with --gpus 1.", file=sys.stderr)
         return 2
 
     from bobcat_amd.backend import Hip
+    from bobcat_amd.lfm2 import CONFIGS, Lfm2Weights
 
+    cfg = CONFIGS[args.model]
     with Hip() as hip:
         name, cus = hip.device_info()
         log(f"device: {name}, {cus} CUs")
-        g = gemv_leg(hip, args.steps, args.warmup)
+        g = gemv_leg(hip, reps=10)
         log(f"gemv: {g}")
-    cpu = None if args.skip_cpu else cpu_leg(args.cpu_seconds)
+        if args.gemv_only:
+            return 0
+        t = time.perf_counter()
+        weights = Lfm2Weights(cfg, seed=0)
+        log(f"generated {cfg.name} weights in {time.perf_counter() - t:.1f}s")
+        mres = model_leg(hip, weights, args.steps, args.warmup)
+        log(f"model: { {k: v for k, v in mres.items() if k != 'tokens'} }")
+    threads = host_threads()
+    cpu = None if args.skip_cpu else cpu_leg(weights, args.cpu_seconds, threads)
     if cpu:
-        log(f"cpu: {cpu}")
+        log(f"cpu: {cpu} ({threads} threads)")
 
+    wb = cfg.weight_bytes()
+    # Bytes a decode token streams: all layer matrices + the output matrix
+    # + the KV cache read at the mean context of tg128 after pp512.
+    mean_ctx = PROMPT + GEN / 2
+    n_attn = len(cfg.attention_layers)
+    kv_bytes = n_attn * mean_ctx * 2 * cfg.n_kv_heads * cfg.head_dim * 2
+    token_bytes = wb["total"] + kv_bytes
+    decode_gbs = mres["decode_tok_s_device"] * token_bytes / 1e9
     line = {
-        "metric": "Q4_K GEMV GB/s vs HBM peak (config 1, 8192x2048)",
-        "value": round(g["gbs"], 2),
-        "unit": "GB/s",
+        "metric": "decode tok/s (pp512/tg128, 1 GPU)",
+        "value": round(mres["decode_tok_s"], 1),
+        "unit": "tok/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(g["us_per_launch"] * 64 / 1e3, 4),
+        "ms_per_step": round(mres["ms_per_step"], 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "q4k-f32",
-        "data": "synthetic (seeded Q4_K blocks, x ~ N(0,1))",
-        "config": {"workload": "config1_q4k_gemv_8192x2048", "rotating_copies": 64,
+        "data": "synthetic (random-init weights of the config's shapes, 512 random prompt ids)",
+        "config": {"workload": f"{cfg.name} pp512/tg128 (BASELINE configs[3])" if cfg.name == "lfm2-2.6b"
+                   else f"{cfg.name} pp512/tg128", "prompt": PROMPT, "generated": GEN, "kv_cache": "f16",
                    "parallelism": "none"},
-        "roofline": {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+        "prefill_tok_s": round(mres["prefill_tok_s"], 1),
+        "decode_tok_s_device": round(mres["decode_tok_s_device"], 1),
+        "ttft_ms": round(mres["ttft_ms"], 3),
+        "tpot_ms": round(mres["tpot_ms"], 4),
+        "decode_bytes_per_token": int(token_bytes),
+        "decode_hbm_gbs": round(decode_gbs, 1),
+        "decode_roofline_frac": round(decode_gbs / HBM_PEAK_GBS, 4),
+        "roofline": {"kernel": "matvec_q4k (config 1, 8192x2048)", "bound": "hbm",
+                     "achieved": round(g["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "us_per_launch": round(g["us"], 3)},
         "cpu_baseline": None if cpu is None else {
-            "value": round(cpu["gbs"], 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{cpu['reps']} scalar GEMVs of config 1 (oracle, f64 accumulate)"},
-        "gemv_us": round(g["us_per_launch"], 3),
-        "gemv_hot_gbs": round(g["hot_gbs"], 1),
+            "value": round(cpu["tok_s"], 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{cpu['steps']} decode steps of {cfg.name} by the oracle (C restatement of the "
+                      f"reference's scalar path, f64 accumulate, rows over {threads} threads)"},
     }
     print(json.dumps(line), flush=True)
     return 0

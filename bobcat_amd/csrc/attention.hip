@@ -142,7 +142,16 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(
         const uint32_t g = o / hd, d = o % hd;
         float a = acc[j] * alpha_s[g];
         const uint64_t base = (uint64_t)t0 * kv_dim + (uint64_t)kvh * hd + d;
-        for (uint32_t t = 0; t < len; t++) a = fmaf(p_s[g][t], load1<HALF>(vc, base + (uint64_t)t * kv_dim), a);
+        // Eight independent value loads in flight per step.
+        uint32_t t = 0;
+        for (; t + 8 <= len; t += 8) {
+          float vv[8];
+#pragma unroll
+          for (int i = 0; i < 8; i++) vv[i] = load1<HALF>(vc, base + (uint64_t)(t + i) * kv_dim);
+#pragma unroll
+          for (int i = 0; i < 8; i++) a = fmaf(p_s[g][t + i], vv[i], a);
+        }
+        for (; t < len; t++) a = fmaf(p_s[g][t], load1<HALF>(vc, base + (uint64_t)t * kv_dim), a);
         acc[j] = a;
       }
     }

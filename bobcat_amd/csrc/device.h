@@ -81,11 +81,14 @@ __device__ __forceinline__ uint32_t q4k_pair_scales(uint32_t h1, uint32_t h2, ui
   const int sh = 16 * (p & 1);
   const uint32_t a = (h1 >> sh) & 0xffffu;  // s[2p'], s[2p'+1] with p' = p & 1
   const uint32_t b = (h2 >> sh) & 0xffffu;  // s[2p'+4], s[2p'+5]
-  if (p < 2) return (a & 0x3f3fu) | ((b & 0x3f3fu) << 16);
   const uint32_t c = (h3 >> sh) & 0xffffu;  // s[2p+4], s[2p+5] for p >= 2
+  // Both cases are computed and selected without a branch: a lane-dependent
+  // branch here would make the last header dword a divergent load.
+  const uint32_t low = (a & 0x3f3fu) | ((b & 0x3f3fu) << 16);
   const uint32_t sc = (c & 0x0f0fu) | ((a >> 2) & 0x3030u);
   const uint32_t mn = ((c >> 4) & 0x0f0fu) | ((b >> 2) & 0x3030u);
-  return sc | (mn << 16);
+  const uint32_t high = sc | (mn << 16);
+  return p < 2 ? low : high;
 }
 
 }  // namespace bch

@@ -135,13 +135,21 @@ struct Q4K {
   }
   // d·(sc_lo·Σq·x + sc_hi·Σq'·x') − dmin·(m_lo·Σx + m_hi·Σx'), which is
   // Σ_l ((d·sc)·q_l − dmin·m)·x_l regrouped.
+  // The unit's 48 bytes: the super-block header and the pair's 32 quant bytes.
+  struct Raw {
+    uint4 h, q0, q1;
+  };
+  __device__ __forceinline__ static Raw fetch(const uint8_t *__restrict__ row, uint32_t u) {
+    const uint8_t *blk = row + (u >> 2) * 144;
+    const uint4 *qp = reinterpret_cast<const uint4 *>(blk + 16 + 32 * (u & 3));
+    return Raw{*reinterpret_cast<const uint4 *>(blk), qp[0], qp[1]};
+  }
   __device__ __forceinline__ static float dot(const uint8_t *__restrict__ row, uint32_t u, const Frag &f) {
-    const uint32_t sb = u >> 2;
+    return compute(fetch(row, u), u, f);
+  }
+  __device__ __forceinline__ static float compute(const Raw &raw, uint32_t u, const Frag &f) {
     const int p = u & 3;
-    const uint8_t *blk = row + sb * 144;
-    const uint4 h = *reinterpret_cast<const uint4 *>(blk);
-    const uint4 *qp = reinterpret_cast<const uint4 *>(blk + 16 + 32 * p);
-    const uint4 q0 = qp[0], q1 = qp[1];
+    const uint4 h = raw.h, q0 = raw.q0, q1 = raw.q1;
     const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
     float s_lo0 = 0.f, s_lo1 = 0.f, s_hi0 = 0.f, s_hi1 = 0.f;
 #pragma unroll
@@ -176,8 +184,14 @@ struct F16 {
   __device__ __forceinline__ static void load(const float *x, const float *nw, uint32_t u, Frag &f) {
     load_inputs<NORM>(x, nw, u * 8, f.x, 2);
   }
+  using Raw = uint4;
+  __device__ __forceinline__ static Raw fetch(const uint8_t *__restrict__ row, uint32_t u) {
+    return reinterpret_cast<const uint4 *>(row)[u];
+  }
   __device__ __forceinline__ static float dot(const uint8_t *__restrict__ row, uint32_t u, const Frag &f) {
-    const uint4 w = reinterpret_cast<const uint4 *>(row)[u];
+    return compute(fetch(row, u), u, f);
+  }
+  __device__ __forceinline__ static float compute(const Raw &w, uint32_t, const Frag &f) {
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
     float s0 = 0.f, s1 = 0.f;
 #pragma unroll
@@ -199,8 +213,14 @@ struct F32 {
   __device__ __forceinline__ static void load(const float *x, const float *nw, uint32_t u, Frag &f) {
     load_inputs<NORM>(x, nw, u * 4, f.x, 1);
   }
+  using Raw = float4;
+  __device__ __forceinline__ static Raw fetch(const uint8_t *__restrict__ row, uint32_t u) {
+    return reinterpret_cast<const float4 *>(row)[u];
+  }
   __device__ __forceinline__ static float dot(const uint8_t *__restrict__ row, uint32_t u, const Frag &f) {
-    const float4 w = reinterpret_cast<const float4 *>(row)[u];
+    return compute(fetch(row, u), u, f);
+  }
+  __device__ __forceinline__ static float compute(const Raw &w, uint32_t, const Frag &f) {
     return fmaf(w.x, f.x[0], w.y * f.x[1]) + fmaf(w.z, f.x[2], w.w * f.x[3]);
   }
 };

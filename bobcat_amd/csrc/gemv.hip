@@ -1,0 +1,347 @@
+// x-stationary matrix-vector kernels for decode (the fast path behind
+// run_matvec / run_matvec_swiglu / run_matvec3 / run_matvec_conv).
+//
+// A "group" of LPR lanes spans one whole row: lane i owns unit i of the row
+// (formats.h: 64 weights of a Q4_K super-block, 8 of an F16 row, 4 of an
+// F32 row) and keeps that unit's inputs in VGPRs for the kernel's life.
+// The group then streams RPG items (an item is one output row, or the
+// gate/up pair of a SwiGLU row, or the B/C/X rows of a conv channel) with
+// the loop fully unrolled, so all of the items' weight loads are in flight
+// together; per-item partial sums stay in registers and are reduced once at
+// the end (shuffles inside a wave, LDS across the waves of a wide group).
+// When the input is RMS-normalised, the group's own fragments already hold
+// the whole input, so the norm costs no extra pass or barrier.
+//
+// LPR is a power of two up to 64 (several groups per wave) or a multiple
+// of 64 up to 256 (one group over several waves); rows wider than 256 units
+// use the older per-unit kernel in matvec.hip.
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+
+#include "formats.h"
+#include "kernels.h"
+#include "runtime.h"
+
+namespace bch {
+
+__device__ __forceinline__ float silu_g(float v) { return v / (1.0f + expf(-v)); }
+
+// --- item policies -----------------------------------------------------
+// Each provides kRows (rows per item), row(item, j) and store(item, v[], scale).
+
+template <bool ACC>
+struct PlainItems {
+  static constexpr int kRows = 1;
+  const uint8_t *W;
+  uint64_t rb;
+  float *y;
+  __device__ const uint8_t *row(uint32_t item, int) const { return W + (uint64_t)item * rb; }
+  __device__ void store(uint32_t item, const float *v, float scale) const {
+    const float t = v[0] * scale;
+    y[item] = ACC ? y[item] + t : t;
+  }
+};
+
+struct SwigluItems {
+  static constexpr int kRows = 2;
+  const uint8_t *Wg, *Wu;
+  uint64_t rb;
+  float *y;
+  __device__ const uint8_t *row(uint32_t item, int j) const { return (j ? Wu : Wg) + (uint64_t)item * rb; }
+  __device__ void store(uint32_t item, const float *v, float scale) const {
+    y[item] = silu_g(v[0] * scale) * (v[1] * scale);
+  }
+};
+
+struct ThreeItems {
+  static constexpr int kRows = 1;
+  const uint8_t *W0, *W1, *W2;
+  uint32_t r0, r1;
+  uint64_t rb;
+  float *y0, *y1, *y2;
+  __device__ const uint8_t *row(uint32_t item, int) const {
+    if (item < r0) return W0 + (uint64_t)item * rb;
+    if (item < r0 + r1) return W1 + (uint64_t)(item - r0) * rb;
+    return W2 + (uint64_t)(item - r0 - r1) * rb;
+  }
+  __device__ void store(uint32_t item, const float *v, float scale) const {
+    const float t = v[0] * scale;
+    if (item < r0)
+      y0[item] = t;
+    else if (item < r0 + r1)
+      y1[item - r0] = t;
+    else
+      y2[item - r0 - r1] = t;
+  }
+};
+
+// The gated short convolution of one channel (matvec.metal:386-454,
+// lfm2.rs:456-475) on rows ch, n+ch, 2n+ch of the input projection.
+struct ConvItems {
+  static constexpr int kRows = 3;
+  const uint8_t *W;
+  uint64_t rb;
+  uint32_t n_embd, ksize;
+  const float *taps;
+  float *history, *out;
+  __device__ const uint8_t *row(uint32_t ch, int j) const { return W + (uint64_t)(j * n_embd + ch) * rb; }
+  __device__ void store(uint32_t ch, const float *v, float scale) const {
+    const float b = v[0] * scale, c = v[1] * scale, xin = v[2] * scale;
+    const float *t = taps + (uint64_t)ch * ksize;
+    const float bx = b * xin;
+    float sum = t[ksize - 1] * bx;
+    for (uint32_t k = 0; k + 1 < ksize; k++) sum = fmaf(t[k], history[k * n_embd + ch], sum);
+    for (uint32_t k = 0; k + 2 < ksize; k++) history[k * n_embd + ch] = history[(k + 1) * n_embd + ch];
+    history[(ksize - 2) * n_embd + ch] = bx;
+    out[ch] = c * sum;
+  }
+};
+
+// --- the kernel ----------------------------------------------------------
+
+template <class F>
+__device__ __forceinline__ float frag_sumsq(const float *x, uint32_t u) {
+  const float4 *xp = reinterpret_cast<const float4 *>(x + u * F::kUnit);
+  float s = 0.f;
+#pragma unroll
+  for (uint32_t i = 0; i < F::kUnit / 4; i++) {
+    const float4 v = xp[i];
+    s = fmaf(v.x, v.x, s);
+    s = fmaf(v.y, v.y, s);
+    s = fmaf(v.z, v.z, s);
+    s = fmaf(v.w, v.w, s);
+  }
+  return s;
+}
+
+template <int LPR>
+__device__ __forceinline__ float group_total(float v, float *lds_scratch, int slot) {
+  if constexpr (LPR <= 64) {
+    return group_sum<LPR>(v);
+  } else {
+    // One group per workgroup, LPR/64 waves: reduce in-wave, then in LDS.
+    v = wave_sum(v);
+    const int wave = threadIdx.x / 64;
+    if (threadIdx.x % 64 == 0) lds_scratch[slot * (LPR / 64) + wave] = v;
+    return 0.f;  // finished by the caller after a barrier
+  }
+}
+
+template <class F, int LPR, int RPG, bool NORM, class P>
+__global__ __launch_bounds__(256) void k_gemv(P p, const float *__restrict__ x, const float *__restrict__ nw,
+                                              float eps, uint32_t n_items, uint32_t n_units, uint32_t n_cols) {
+  constexpr int T = LPR <= 64 ? 256 : LPR;  // threads per workgroup
+  constexpr int G = T / LPR;                // groups per workgroup
+  constexpr int R = P::kRows;
+  constexpr int N = RPG * R;                // rows per batch
+  const int tid = threadIdx.x;
+  const int g = tid / LPR, li = tid % LPR;
+  const bool active = li < (int)n_units;
+  const uint32_t unit = active ? (uint32_t)li : 0u;  // idle lanes read unit 0 and drop it
+  const uint32_t n_batches = (n_items + RPG - 1) / RPG;
+  const uint32_t stride = gridDim.x * G;
+  uint32_t b = blockIdx.x * G + g;
+
+  // Weight loads of a batch: issued ahead of the batch's arithmetic.
+  typename F::Raw ra[N], rb[N];
+  auto fetch = [&](typename F::Raw *dst, uint32_t batch) {
+#pragma unroll
+    for (int it = 0; it < RPG; it++) {
+      const uint32_t item = min(batch * RPG + it, n_items - 1);
+#pragma unroll
+      for (int j = 0; j < R; j++) dst[it * R + j] = F::fetch(p.row(item, j), unit);
+    }
+  };
+  if (b < n_batches) fetch(ra, b);
+
+  // The lane's unit of the input (times the norm weights), loaded once.
+  typename F::Frag f;
+  F::template load<NORM>(x, nw, unit, f);
+  float scale = 1.f;
+  constexpr int W = LPR > 64 ? LPR / 64 : 1;
+  __shared__ float red[(N + 1) * W];
+  if (NORM) {
+    float ss = active ? frag_sumsq<F>(x, unit) : 0.f;
+    if constexpr (LPR <= 64) {
+      ss = group_sum<LPR>(ss);
+    } else {
+      ss = wave_sum(ss);
+      if (tid % 64 == 0) red[N * W + tid / 64] = ss;
+      __syncthreads();
+      ss = 0.f;
+#pragma unroll
+      for (int w = 0; w < W; w++) ss += red[N * W + w];
+      __syncthreads();
+    }
+    scale = (float)(1.0 / sqrt((double)ss / (double)n_cols + (double)eps));
+  }
+
+  // Reduce a batch over the group and store it.
+  auto finish = [&](const typename F::Raw *cur, uint32_t batch) {
+    float acc[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) acc[i] = active ? F::compute(cur[i], unit, f) : 0.f;
+    const uint32_t first = batch * RPG;
+    if constexpr (LPR <= 64) {
+#pragma unroll
+      for (int i = 0; i < N; i++) acc[i] = group_sum<LPR>(acc[i]);
+#pragma unroll
+      for (int it = 0; it < RPG; it++) {
+        if (li == it % LPR && first + it < n_items) {
+          float v[R];
+#pragma unroll
+          for (int j = 0; j < R; j++) v[j] = acc[it * R + j];
+          p.store(first + it, v, scale);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; i++) {
+        const float t = wave_sum(acc[i]);
+        if (tid % 64 == 0) red[i * W + tid / 64] = t;
+      }
+      __syncthreads();
+      if (tid < RPG && first + tid < n_items) {
+        float v[R];
+#pragma unroll
+        for (int j = 0; j < R; j++) {
+          float t = 0.f;
+#pragma unroll
+          for (int w = 0; w < W; w++) t += red[(tid * R + j) * W + w];
+          v[j] = t;
+        }
+        p.store(first + tid, v, scale);
+      }
+      __syncthreads();
+    }
+  };
+
+  // Ping-pong between two register buffers: the next batch's loads are in
+  // flight while the current batch is reduced.
+  while (true) {
+    if (b >= n_batches) break;
+    if (b + stride < n_batches) fetch(rb, b + stride);
+    finish(ra, b);
+    b += stride;
+    if (b >= n_batches) break;
+    if (b + stride < n_batches) fetch(ra, b + stride);
+    finish(rb, b);
+    b += stride;
+  }
+}
+
+// --- host side -------------------------------------------------------------
+
+// Lanes per row for n_units units (0 when the x-stationary path does not apply).
+static int lanes_for(uint32_t n_units) {
+  if (n_units > 256) return 0;
+  if (n_units <= 64) {
+    int l = 4;
+    while (l < (int)n_units) l *= 2;
+    return l;
+  }
+  return (int)((n_units + 63) / 64 * 64);
+}
+
+// Items per group: enough weight bytes in flight per lane without spilling,
+// and enough workgroups to cover the chip.
+template <int R>
+static int rpg_for(uint32_t n_items, int lpr, uint32_t n_cus) {
+  const int groups_per_block = lpr <= 64 ? 256 / lpr : 1;
+  static const int forced = getenv("BCH_GEMV_RPG") ? atoi(getenv("BCH_GEMV_RPG")) : 0;
+  if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced;
+  int rpg = R == 1 ? 4 : R == 2 ? 2 : 1;
+  const uint32_t want_blocks = 2 * (n_cus ? n_cus : 256);
+  while (rpg > 1 && (uint64_t)n_items < (uint64_t)want_blocks * groups_per_block * rpg) rpg /= 2;
+  return rpg;
+}
+
+template <class F, int LPR, int RPG, bool NORM, class P>
+static void launch_gemv(hipStream_t s, const P &p, const float *x, const float *nw, float eps, uint32_t n_items,
+                        uint32_t n_units, uint32_t n_cols) {
+  constexpr int threads = LPR <= 64 ? 256 : LPR;
+  constexpr int G = threads / LPR;
+  // Persistent groups: enough workgroups for `per_cu` per CU, each group
+  // walking batches at a stride of the whole grid.
+  static const uint32_t per_cu = getenv("BCH_GEMV_WG_PER_CU") ? atoi(getenv("BCH_GEMV_WG_PER_CU")) : 2;
+  const uint32_t n_batches = div_ceil(n_items, RPG);
+  const uint32_t grid = std::max(1u, std::min(div_ceil(n_batches, G), per_cu * 256));
+  k_gemv<F, LPR, RPG, NORM, P><<<grid, threads, 0, s>>>(p, x, nw, eps, n_items, n_units, n_cols);
+}
+
+template <class F, int LPR, bool NORM, class P>
+static void gemv_rpg(hipStream_t s, int rpg, const P &p, const float *x, const float *nw, float eps,
+                     uint32_t n_items, uint32_t n_units, uint32_t n_cols) {
+  switch (rpg) {
+    case 8: launch_gemv<F, LPR, 8, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols); break;
+    case 4: launch_gemv<F, LPR, 4, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols); break;
+    case 2: launch_gemv<F, LPR, 2, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols); break;
+    default: launch_gemv<F, LPR, 1, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols); break;
+  }
+}
+
+template <class F, bool NORM, class P>
+static bool gemv_dispatch(hipStream_t s, const P &p, const float *x, const float *nw, float eps, uint32_t n_items,
+                          uint32_t n_cols, uint32_t n_cus) {
+  const uint32_t n_units = n_cols / F::kUnit;
+  const int lpr = lanes_for(n_units);
+  if (!lpr) return false;
+  const int rpg = rpg_for<P::kRows>(n_items, lpr, n_cus);
+  switch (lpr) {
+    case 4: gemv_rpg<F, 4, NORM>(s, rpg, p, x, nw, eps, n_items, n_units, n_cols); break;
+    case 8: gemv_rpg<F, 8, NORM>(s, rpg, p, x, nw, eps, n_items, n_units, n_cols); break;
+    case 16: gemv_rpg<F, 16, NORM>(s, rpg, p, x, nw, eps, n_items, n_units, n_cols); break;
+    case 32: gemv_rpg<F, 32, NORM>(s, rpg, p, x, nw, eps, n_items, n_units, n_cols); break;
+    case 64: gemv_rpg<F, 64, NORM>(s, rpg, p, x, nw, eps, n_items, n_units, n_cols); break;
+    case 128: gemv_rpg<F, 128, NORM>(s, rpg, p, x, nw, eps, n_items, n_units, n_cols); break;
+    case 192: gemv_rpg<F, 192, NORM>(s, rpg, p, x, nw, eps, n_items, n_units, n_cols); break;
+    case 256: gemv_rpg<F, 256, NORM>(s, rpg, p, x, nw, eps, n_items, n_units, n_cols); break;
+    default: return false;
+  }
+  return true;
+}
+
+template <class P>
+static bool gemv_any(hipStream_t s, uint32_t format, const P &p, const float *x, const float *nw, float eps,
+                     uint32_t n_items, uint32_t n_cols, uint32_t n_cus) {
+  const bool norm = nw != nullptr;
+  if (format == Q4K::kFormat)
+    return norm ? gemv_dispatch<Q4K, true>(s, p, x, nw, eps, n_items, n_cols, n_cus)
+                : gemv_dispatch<Q4K, false>(s, p, x, nw, eps, n_items, n_cols, n_cus);
+  if (format == F16::kFormat)
+    return norm ? gemv_dispatch<F16, true>(s, p, x, nw, eps, n_items, n_cols, n_cus)
+                : gemv_dispatch<F16, false>(s, p, x, nw, eps, n_items, n_cols, n_cus);
+  return norm ? gemv_dispatch<F32, true>(s, p, x, nw, eps, n_items, n_cols, n_cus)
+              : gemv_dispatch<F32, false>(s, p, x, nw, eps, n_items, n_cols, n_cus);
+}
+
+bool fast_matvec(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,
+                 float *y, const float *nw, float eps, bool accumulate, uint32_t n_cus) {
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  if (accumulate) return gemv_any(s, format, PlainItems<true>{W, rb, y}, x, nw, eps, n_rows, n_cols, n_cus);
+  return gemv_any(s, format, PlainItems<false>{W, rb, y}, x, nw, eps, n_rows, n_cols, n_cus);
+}
+
+bool fast_matvec_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const uint8_t *Wu, uint32_t n_rows,
+                        uint32_t n_cols, const float *x, float *y, const float *nw, float eps, uint32_t n_cus) {
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  return gemv_any(s, format, SwigluItems{Wg, Wu, rb, y}, x, nw, eps, n_rows, n_cols, n_cus);
+}
+
+bool fast_matvec3(hipStream_t s, uint32_t format, const uint8_t *W0, const uint8_t *W1, const uint8_t *W2, uint32_t r0,
+                  uint32_t r1, uint32_t r2, uint32_t n_cols, const float *x, float *y0, float *y1, float *y2,
+                  const float *nw, float eps, uint32_t n_cus) {
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  return gemv_any(s, format, ThreeItems{W0, W1, W2, r0, r1, rb, y0, y1, y2}, x, nw, eps, r0 + r1 + r2, n_cols,
+                  n_cus);
+}
+
+bool fast_matvec_conv(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_cols, const float *x,
+                      const float *nw, float eps, const float *taps, float *history, float *out, uint32_t n_embd,
+                      uint32_t ksize, uint32_t n_cus) {
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  return gemv_any(s, format, ConvItems{W, rb, n_embd, ksize, taps, history, out}, x, nw, eps, n_embd, n_cols, n_cus);
+}
+
+}  // namespace bch

@@ -23,6 +23,19 @@ void run_matvec3(hipStream_t s, uint32_t format, const uint8_t *W0, const uint8_
                  uint32_t r1, uint32_t r2, uint32_t n_cols, const float *x, float *y0, float *y1, float *y2,
                  const float *norm_w, float eps, uint32_t n_cus);
 
+// gemv.hip: x-stationary variants of the four above for rows of at most
+// 256 units; they return false (launching nothing) for wider rows.
+bool fast_matvec(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,
+                 float *y, const float *norm_w, float eps, bool accumulate, uint32_t n_cus);
+bool fast_matvec_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const uint8_t *Wu, uint32_t n_rows,
+                        uint32_t n_cols, const float *x, float *y, const float *norm_w, float eps, uint32_t n_cus);
+bool fast_matvec3(hipStream_t s, uint32_t format, const uint8_t *W0, const uint8_t *W1, const uint8_t *W2, uint32_t r0,
+                  uint32_t r1, uint32_t r2, uint32_t n_cols, const float *x, float *y0, float *y1, float *y2,
+                  const float *norm_w, float eps, uint32_t n_cus);
+bool fast_matvec_conv(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_cols, const float *x,
+                      const float *norm_w, float eps, const float *taps, float *history, float *out, uint32_t n_embd,
+                      uint32_t ksize, uint32_t n_cus);
+
 // ops.hip
 void run_rms_norm(hipStream_t s, const float *x, const float *w, float *out, uint32_t n, uint32_t rows, float eps);
 void run_norm_rope(hipStream_t s, const float *src, void *dst, bool half, const float *w, uint32_t n_heads,

@@ -311,6 +311,14 @@ static int capture(bch_lfm2 *m, bool generate, hipGraphExec_t *out) {
   return check_hip(e, "instantiate graph");
 }
 
+// Decode steps replay a captured HIP graph unless BCH_LFM2_NO_GRAPH=1, which
+// issues the same launches on the stream one by one (for tools that do not
+// follow graph launches, such as per-kernel tracing).
+static bool use_graphs() {
+  static const bool on = !(getenv("BCH_LFM2_NO_GRAPH") && atoi(getenv("BCH_LFM2_NO_GRAPH")) != 0);
+  return on;
+}
+
 static int set_dpos(bch_lfm2 *m, uint32_t value) {
   m->dpos_host = value;
   return check_hip(hipMemcpyAsync(m->dpos, &m->dpos_host, 4, hipMemcpyHostToDevice, m->s), "write position");
@@ -516,9 +524,11 @@ int bch_lfm2_step(bch_lfm2 *m, uint32_t token, float *logits, float *trace_embed
   hipEventRecord(m->ev0, s);
   if (trace) {
     record_step(m, s, true, true);
-  } else {
+  } else if (use_graphs()) {
     if (!m->step_graph) BCH_TRY(capture(m, false, &m->step_graph));
     BCH_TRY(check_hip(hipGraphLaunch(m->step_graph, s), "launch step graph"));
+  } else {
+    record_step(m, s, true, false);
   }
   BCH_TRY(finish(m));
   const uint32_t n = m->n_embd;
@@ -595,12 +605,20 @@ int bch_lfm2_generate(bch_lfm2 *m, uint32_t *out, uint32_t n) {
   if (n > m->n_ctx - m->n_past)
     return fail(BCH_ERR_CONTEXT_FULL, "%u tokens exceed the %u free positions", n, m->n_ctx - m->n_past);
   if (n == 0) return BCH_OK;
-  if (!m->gen_graph) BCH_TRY(capture(m, true, &m->gen_graph));
   // Each replay writes argmax(logits) into tokens[dpos + 1], advances dpos
   // and runs the step there; dpos starts at the last consumed position.
   BCH_TRY(set_dpos(m, m->n_past - 1));
-  hipEventRecord(m->ev0, m->s);
-  for (uint32_t i = 0; i < n; i++) BCH_TRY(check_hip(hipGraphLaunch(m->gen_graph, m->s), "launch decode graph"));
+  if (use_graphs()) {
+    if (!m->gen_graph) BCH_TRY(capture(m, true, &m->gen_graph));
+    hipEventRecord(m->ev0, m->s);
+    for (uint32_t i = 0; i < n; i++) BCH_TRY(check_hip(hipGraphLaunch(m->gen_graph, m->s), "launch decode graph"));
+  } else {
+    hipEventRecord(m->ev0, m->s);
+    for (uint32_t i = 0; i < n; i++) {
+      run_argmax(m->s, m->logits, m->tokens, m->n_vocab, m->dpos, true);
+      record_step(m, m->s, true, false);
+    }
+  }
   BCH_TRY(finish(m));
   BCH_TRY(check_hip(hipMemcpy(out, m->tokens + m->n_past, (uint64_t)n * 4, hipMemcpyDeviceToHost), "read tokens"));
   m->n_past += n;

@@ -351,6 +351,7 @@ static void dispatch_format(uint32_t format, Fn &&f) {
 
 void run_matvec(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,
                 float *y, const float *norm_w, float eps, bool accumulate, uint32_t n_cus) {
+  if (!getenv("BCH_SLOW_GEMV") && fast_matvec(s, format, W, n_rows, n_cols, x, y, norm_w, eps, accumulate, n_cus)) return;
   const uint32_t n_units = n_cols / unit_of(format);
   const uint64_t rb = bch_row_bytes(format, n_cols);
   const Geometry g = choose(n_rows, n_units, n_cus, 8);
@@ -362,6 +363,9 @@ void run_matvec(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_row
 void run_matvec3(hipStream_t s, uint32_t format, const uint8_t *W0, const uint8_t *W1, const uint8_t *W2, uint32_t r0,
                  uint32_t r1, uint32_t r2, uint32_t n_cols, const float *x, float *y0, float *y1, float *y2,
                  const float *norm_w, float eps, uint32_t n_cus) {
+  if (!getenv("BCH_SLOW_GEMV") &&
+      fast_matvec3(s, format, W0, W1, W2, r0, r1, r2, n_cols, x, y0, y1, y2, norm_w, eps, n_cus))
+    return;
   const uint32_t n_units = n_cols / unit_of(format);
   const uint64_t rb = bch_row_bytes(format, n_cols);
   const uint32_t n_rows = r0 + r1 + r2;
@@ -373,6 +377,8 @@ void run_matvec3(hipStream_t s, uint32_t format, const uint8_t *W0, const uint8_
 
 void run_matvec_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const uint8_t *Wu, uint32_t n_rows,
                        uint32_t n_cols, const float *x, float *y, const float *norm_w, float eps, uint32_t n_cus) {
+  if (!getenv("BCH_SLOW_GEMV") && fast_matvec_swiglu(s, format, Wg, Wu, n_rows, n_cols, x, y, norm_w, eps, n_cus))
+    return;
   const uint32_t n_units = n_cols / unit_of(format);
   const uint64_t rb = bch_row_bytes(format, n_cols);
   const Geometry g = choose(n_rows, n_units, n_cus, 4);
@@ -382,6 +388,9 @@ void run_matvec_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const 
 void run_matvec_conv(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_cols, const float *x,
                      const float *norm_w, float eps, const float *taps, float *history, float *out, uint32_t n_embd,
                      uint32_t ksize, uint32_t n_cus) {
+  if (!getenv("BCH_SLOW_GEMV") &&
+      fast_matvec_conv(s, format, W, n_cols, x, norm_w, eps, taps, history, out, n_embd, ksize, n_cus))
+    return;
   const uint32_t n_units = n_cols / Q4K::kUnit;
   const uint64_t rb = bch_row_bytes(format, n_cols);
   const Geometry g = choose(n_embd, n_units, n_cus, 1);
