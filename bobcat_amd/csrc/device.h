@@ -9,21 +9,47 @@ namespace bch {
 
 constexpr int kWave = 64;
 
+// DPP lane moves within rows of 16 lanes: the source lane of each lane.
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppHalfMirror = 0x141; // 7 - lane within each 8 lanes
+constexpr int kDppMirror = 0x140;     // 15 - lane within each 16 lanes
+constexpr int kDppRor4 = 0x124;       // (lane + 4) % 16 within the row
+constexpr int kDppRor8 = 0x128;       // (lane + 8) % 16 within the row
+
+// `v` of the lane that DPP control CTRL names.  All lanes of the row must
+// be active (callers use these in code that whole rows execute together).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
 // Sum of `v` over groups of `width` consecutive lanes (width a power of two
-// up to 64); every lane of a group receives the group's sum.
+// up to 64); every lane of a group receives the group's sum.  The tree
+// pairs neighbouring lanes first: quads by DPP quad permutes, eights and
+// sixteens by the DPP mirrors (lane i and its mirror lie in the two halves),
+// and across rows by a lane shuffle.  Each step adds two group sums, so all
+// lanes of a group hold the same value.
 template <int width>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int off = width / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  if constexpr (width >= 2) v += dpp<kDppXor1>(v);
+  if constexpr (width >= 4) v += dpp<kDppXor2>(v);
+  if constexpr (width >= 8) v += dpp<kDppHalfMirror>(v);
+  if constexpr (width >= 16) v += dpp<kDppMirror>(v);
+  if constexpr (width >= 32) v += __shfl_xor(v, 16, kWave);
+  if constexpr (width >= 64) v += __shfl_xor(v, 32, kWave);
   return v;
 }
 
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<kWave>(v); }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-  return v;
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppMirror>(v));
+  v = fmaxf(v, __shfl_xor(v, 16, kWave));
+  return fmaxf(v, __shfl_xor(v, 32, kWave));
 }
 
 // Sum over a workgroup of `threads` threads; `scratch` holds threads/64

@@ -30,9 +30,18 @@ __device__ __forceinline__ float silu_g(float v) { return v / (1.0f + expf(-v));
 // --- item policies -----------------------------------------------------
 // Each provides kRows (rows per item), row(item, j) and store(item, v[], scale).
 
+// Orderable key of (value, index): larger values win, and among equal values
+// the lower index wins (the tie rule of argmax, norm.metal:142-197).
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t index) {
+  const uint32_t b = __float_as_uint(v) == 0x80000000u ? 0u : __float_as_uint(v);  // -0 ties +0
+  const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - index);
+}
+
 template <bool ACC>
 struct PlainItems {
   static constexpr int kRows = 1;
+  static constexpr bool kArgmax = false;
   const uint8_t *W;
   uint64_t rb;
   float *y;
@@ -43,8 +52,22 @@ struct PlainItems {
   }
 };
 
+// Logits: rows stored as PlainItems<false>, plus one argmax partial per
+// workgroup, so the next token needs no pass over the logits.
+struct ArgmaxItems {
+  static constexpr int kRows = 1;
+  static constexpr bool kArgmax = true;
+  const uint8_t *W;
+  uint64_t rb;
+  float *y;
+  uint64_t *partials;
+  __device__ const uint8_t *row(uint32_t item, int) const { return W + (uint64_t)item * rb; }
+  __device__ void store(uint32_t item, const float *v, float scale) const { y[item] = v[0] * scale; }
+};
+
 struct SwigluItems {
   static constexpr int kRows = 2;
+  static constexpr bool kArgmax = false;
   const uint8_t *Wg, *Wu;
   uint64_t rb;
   float *y;
@@ -56,6 +79,7 @@ struct SwigluItems {
 
 struct ThreeItems {
   static constexpr int kRows = 1;
+  static constexpr bool kArgmax = false;
   const uint8_t *W0, *W1, *W2;
   uint32_t r0, r1;
   uint64_t rb;
@@ -80,6 +104,7 @@ struct ThreeItems {
 // lfm2.rs:456-475) on rows ch, n+ch, 2n+ch of the input projection.
 struct ConvItems {
   static constexpr int kRows = 3;
+  static constexpr bool kArgmax = false;
   const uint8_t *W;
   uint64_t rb;
   uint32_t n_embd, ksize;
@@ -177,6 +202,8 @@ __global__ __launch_bounds__(256) void k_gemv(P p, const float *__restrict__ x, 
     scale = (float)(1.0 / sqrt((double)ss / (double)n_cols + (double)eps));
   }
 
+  uint64_t best = 0;  // argmax key of the items this lane stored (P::kArgmax)
+
   // Reduce a batch over the group and store it.
   auto finish = [&](const typename F::Raw *cur, uint32_t batch) {
     float acc[N];
@@ -193,6 +220,7 @@ __global__ __launch_bounds__(256) void k_gemv(P p, const float *__restrict__ x, 
 #pragma unroll
           for (int j = 0; j < R; j++) v[j] = acc[it * R + j];
           p.store(first + it, v, scale);
+          if constexpr (P::kArgmax) best = max(best, argmax_key(v[0] * scale, first + it));
         }
       }
     } else {
@@ -212,6 +240,7 @@ __global__ __launch_bounds__(256) void k_gemv(P p, const float *__restrict__ x, 
           v[j] = t;
         }
         p.store(first + tid, v, scale);
+        if constexpr (P::kArgmax) best = max(best, argmax_key(v[0] * scale, first + tid));
       }
       __syncthreads();
     }
@@ -228,6 +257,23 @@ __global__ __launch_bounds__(256) void k_gemv(P p, const float *__restrict__ x, 
     if (b + stride < n_batches) fetch(ra, b + stride);
     finish(rb, b);
     b += stride;
+  }
+  if constexpr (P::kArgmax) {
+    // One partial per workgroup: the largest key over its lanes.
+    __shared__ uint64_t best_s[T / 64];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const uint64_t o = ((uint64_t)__shfl_xor((uint32_t)(best >> 32), off, 64) << 32) |
+                         (uint64_t)__shfl_xor((uint32_t)best, off, 64);
+      best = max(best, o);
+    }
+    if (tid % 64 == 0) best_s[tid / 64] = best;
+    __syncthreads();
+    if (tid == 0) {
+#pragma unroll
+      for (int w = 1; w < T / 64; w++) best = max(best, best_s[w]);
+      p.partials[blockIdx.x] = best;
+    }
   }
 }
 
@@ -246,12 +292,14 @@ static int lanes_for(uint32_t n_units) {
 
 // Items per group: enough weight bytes in flight per lane without spilling,
 // and enough workgroups to cover the chip.
-template <int R>
+template <class P>
 static int rpg_for(uint32_t n_items, int lpr, uint32_t n_cus) {
+  constexpr int R = P::kRows;
   const int groups_per_block = lpr <= 64 ? 256 / lpr : 1;
   static const int forced = getenv("BCH_GEMV_RPG") ? atoi(getenv("BCH_GEMV_RPG")) : 0;
   if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced;
-  int rpg = R == 1 ? 4 : R == 2 ? 2 : 1;
+  // The argmax key costs the registers that keep 4 rows at 2 waves per SIMD.
+  int rpg = R == 1 ? (P::kArgmax ? 2 : 4) : R == 2 ? 2 : 1;
   const uint32_t want_blocks = 2 * (n_cus ? n_cus : 256);
   while (rpg > 1 && (uint64_t)n_items < (uint64_t)want_blocks * groups_per_block * rpg) rpg /= 2;
   return rpg;
@@ -266,7 +314,8 @@ static void launch_gemv(hipStream_t s, const P &p, const float *x, const float *
   // walking batches at a stride of the whole grid.
   static const uint32_t per_cu = getenv("BCH_GEMV_WG_PER_CU") ? atoi(getenv("BCH_GEMV_WG_PER_CU")) : 2;
   const uint32_t n_batches = div_ceil(n_items, RPG);
-  const uint32_t grid = std::max(1u, std::min(div_ceil(n_batches, G), per_cu * 256));
+  uint32_t grid = std::max(1u, std::min(div_ceil(n_batches, G), per_cu * 256));
+  if constexpr (P::kArgmax) grid = std::min(grid, kArgmaxPartials);
   k_gemv<F, LPR, RPG, NORM, P><<<grid, threads, 0, s>>>(p, x, nw, eps, n_items, n_units, n_cols);
 }
 
@@ -287,7 +336,7 @@ static bool gemv_dispatch(hipStream_t s, const P &p, const float *x, const float
   const uint32_t n_units = n_cols / F::kUnit;
   const int lpr = lanes_for(n_units);
   if (!lpr) return false;
-  const int rpg = rpg_for<P::kRows>(n_items, lpr, n_cus);
+  const int rpg = rpg_for<P>(n_items, lpr, n_cus);
   switch (lpr) {
     case 4: gemv_rpg<F, 4, NORM>(s, rpg, p, x, nw, eps, n_items, n_units, n_cols); break;
     case 8: gemv_rpg<F, 8, NORM>(s, rpg, p, x, nw, eps, n_items, n_units, n_cols); break;
@@ -321,6 +370,12 @@ bool fast_matvec(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_ro
   const uint64_t rb = bch_row_bytes(format, n_cols);
   if (accumulate) return gemv_any(s, format, PlainItems<true>{W, rb, y}, x, nw, eps, n_rows, n_cols, n_cus);
   return gemv_any(s, format, PlainItems<false>{W, rb, y}, x, nw, eps, n_rows, n_cols, n_cus);
+}
+
+bool fast_matvec_argmax(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols,
+                        const float *x, float *y, const float *nw, float eps, uint64_t *partials, uint32_t n_cus) {
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  return gemv_any(s, format, ArgmaxItems{W, rb, y, partials}, x, nw, eps, n_rows, n_cols, n_cus);
 }
 
 bool fast_matvec_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const uint8_t *Wu, uint32_t n_rows,

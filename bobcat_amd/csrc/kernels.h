@@ -8,6 +8,32 @@
 
 namespace bch {
 
+// Inverse RoPE frequencies 1/theta^(2i/n_rot), computed on the host with the
+// host's powf (as scalar::rope_neox does, crates/bobcat/src/scalar.rs:257-260)
+// so device angles equal the CPU path's bit for bit; passed by value.
+struct RopeTable {
+  float inv_freq[128];
+};
+RopeTable rope_table(float theta, uint32_t n_rot);
+
+// attn_decode.hip: decode attention of one query at position *dpos with the
+// q/k RMS norm + RoPE and the KV-cache store of the new position folded in.
+struct AttnDecodeArgs {
+  const float *q, *k, *v;          // raw projections of the token
+  const float *q_norm, *k_norm;    // [head_dim]
+  RopeTable freqs;
+  float eps, scale;
+  void *k_cache, *v_cache;         // this layer's caches, [pos][n_kv][head_dim]
+  float *partials;                 // n_heads * max_splits * (head_dim + 2)
+  uint32_t *counters;              // n_heads zeroed (left zeroed on exit)
+  float *out;                      // [n_heads * head_dim]
+  uint32_t n_heads, n_kv, head_dim, max_splits;
+  const uint32_t *dpos;
+};
+uint32_t attn_decode_keys_per_split(uint32_t head_dim, bool kv_half);
+uint32_t attn_decode_max_splits(uint32_t n_ctx, uint32_t head_dim, bool kv_half);
+void run_attn_decode(hipStream_t s, const AttnDecodeArgs &a, bool kv_half);
+
 // matvec.hip
 void run_matvec(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,
                 float *y, const float *norm_w, float eps, bool accumulate, uint32_t n_cus);
@@ -36,7 +62,19 @@ bool fast_matvec_conv(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t
                       const float *norm_w, float eps, const float *taps, float *history, float *out, uint32_t n_embd,
                       uint32_t ksize, uint32_t n_cus);
 
+// The logits GEMV with a per-workgroup argmax partial (at most
+// kArgmaxPartials); false when the shape has no fast path.
+constexpr uint32_t kArgmaxPartials = 1024;
+bool fast_matvec_argmax(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols,
+                        const float *x, float *y, const float *norm_w, float eps, uint64_t *partials, uint32_t n_cus);
+
 // ops.hip
+// argmax of n logits as partials[0] (an argmax key), with partials[1..n_partials) zeroed.
+void run_argmax_partials(hipStream_t s, const float *logits, uint32_t n, uint64_t *partials, uint32_t n_partials);
+// The next decode step's first launch: reduce the argmax partials to the
+// greedy token, store it at tokens[*dpos + 1], advance *dpos, and embed it.
+void run_embed_next(hipStream_t s, uint32_t format, const uint8_t *W, uint64_t row_bytes, uint32_t *tokens,
+                    float *out, uint32_t n_embd, uint32_t *dpos, const uint64_t *partials, uint32_t n_partials);
 void run_rms_norm(hipStream_t s, const float *x, const float *w, float *out, uint32_t n, uint32_t rows, float eps);
 void run_norm_rope(hipStream_t s, const float *src, void *dst, bool half, const float *w, uint32_t n_heads,
                    uint32_t head_dim, uint32_t n_rot, uint32_t src_head_stride, uint32_t pos, const uint32_t *dpos,

@@ -67,6 +67,7 @@ struct bch_lfm2 {
   float *partials = nullptr, *trace = nullptr;
   uint32_t trace_rows = 0;  // tokens each traced activation holds (lfm2_metal.rs:764-779)
   uint32_t *counters = nullptr, *tokens = nullptr, *dpos = nullptr, *greedy = nullptr;
+  uint64_t *argmax_partials = nullptr;  // kArgmaxPartials argmax keys of the logits
   std::vector<void *> allocations;
   // Sequence state.
   uint32_t n_ctx = 0, n_past = 0, batch = 0;
@@ -144,14 +145,21 @@ static int check_matrix(const bch_matrix &mat, uint32_t rows, uint32_t cols, con
 // ---------------------------------------------------------------------
 
 // One decode step at the position *m->dpos (Recorder::record_step).  With
-// `trace`, activations are copied into m->trace: embedding, each layer's
-// output, final norm.
-static void record_step(bch_lfm2 *m, hipStream_t s, bool want_logits, bool trace) {
+// `greedy_input`, the step first takes the greedy token of the previous
+// logits (from m->argmax_partials), stores it at tokens[*dpos + 1] and
+// advances *dpos.  The logits leave their argmax partials behind for the
+// next such step.  With `trace`, activations are copied into m->trace:
+// embedding, each layer's output, final norm.
+static void record_step(bch_lfm2 *m, hipStream_t s, bool greedy_input, bool trace) {
   const uint32_t n = m->n_embd, cus = m->ctx->n_cus;
-  const uint32_t *dp = m->dpos;
+  uint32_t *dp = m->dpos;
   const uint64_t tstride = (uint64_t)m->trace_rows * n;  // floats per traced activation
-  run_embed(s, m->token_embd.format, m->token_embd.data, bch_row_bytes(m->token_embd.format, n), m->tokens,
-            m->hidden, n, 1, dp);
+  const uint64_t embd_rb = bch_row_bytes(m->token_embd.format, n);
+  if (greedy_input)
+    run_embed_next(s, m->token_embd.format, m->token_embd.data, embd_rb, m->tokens, m->hidden, n, dp,
+                   m->argmax_partials, kArgmaxPartials);
+  else
+    run_embed(s, m->token_embd.format, m->token_embd.data, embd_rb, m->tokens, m->hidden, n, 1, dp);
   if (trace) run_copy(s, m->hidden, m->trace, n, nullptr, 0);
   for (uint32_t il = 0; il < m->n_layers; il++) {
     const Layer &L = m->layers[il];
@@ -164,16 +172,26 @@ static void record_step(bch_lfm2 *m, hipStream_t s, bool want_logits, bool trace
       const uint32_t ci = L.cache_index;
       run_matvec3(s, L.wq.format, L.wq.data, L.wk.data, L.wv.data, m->q_dim, m->kv_dim, m->kv_dim, n, m->hidden,
                   m->q, m->k, m->v, L.attn_norm, m->norm_eps, cus);
-      run_norm_rope(s, m->q, m->q, false, L.q_norm, m->n_heads, m->head_dim, m->head_dim, m->head_dim, 0, dp, 1,
-                    m->q_dim, m->q_dim, m->rope_theta, m->norm_eps, 0);
-      run_norm_rope(s, m->k, m->cache_layer(m->k_cache, ci), m->kv_half, L.k_norm, m->n_kv_heads, m->head_dim,
-                    m->head_dim, m->head_dim, 0, dp, 1, m->kv_dim, m->kv_dim, m->rope_theta, m->norm_eps, m->kv_dim);
-      if (m->kv_half)
-        run_convert_half(s, m->v, m->cache_layer(m->v_cache, ci), m->kv_dim, dp, m->kv_dim);
-      else
-        run_copy(s, m->v, static_cast<float *>(m->cache_layer(m->v_cache, ci)), m->kv_dim, dp, m->kv_dim);
-      run_attention(s, m->q, m->cache_layer(m->k_cache, ci), m->cache_layer(m->v_cache, ci), m->kv_half, m->partials,
-                    m->counters, m->attn, m->n_heads, m->n_kv_heads, m->head_dim, 0, dp, 1, m->decode_splits);
+      AttnDecodeArgs ad;
+      ad.q = m->q;
+      ad.k = m->k;
+      ad.v = m->v;
+      ad.q_norm = L.q_norm;
+      ad.k_norm = L.k_norm;
+      ad.freqs = rope_table(m->rope_theta, m->head_dim);
+      ad.eps = m->norm_eps;
+      ad.scale = 1.0f / sqrtf((float)m->head_dim);
+      ad.k_cache = m->cache_layer(m->k_cache, ci);
+      ad.v_cache = m->cache_layer(m->v_cache, ci);
+      ad.partials = m->partials;
+      ad.counters = m->counters;
+      ad.out = m->attn;
+      ad.n_heads = m->n_heads;
+      ad.n_kv = m->n_kv_heads;
+      ad.head_dim = m->head_dim;
+      ad.max_splits = attn_decode_max_splits(m->n_ctx, m->head_dim, m->kv_half);
+      ad.dpos = dp;
+      run_attn_decode(s, ad, m->kv_half);
       run_matvec(s, L.wo.format, L.wo.data, n, m->q_dim, m->attn, m->hidden, nullptr, 0.f, true, cus);
     }
     run_matvec_swiglu(s, L.gate.format, L.gate.data, L.up.data, m->n_ff, n, m->hidden, m->ffn, L.ffn_norm,
@@ -182,9 +200,12 @@ static void record_step(bch_lfm2 *m, hipStream_t s, bool want_logits, bool trace
     if (trace) run_copy(s, m->hidden, m->trace + (1 + il) * tstride, n, nullptr, 0);
   }
   if (trace) run_rms_norm(s, m->hidden, m->output_norm, m->trace + (1 + m->n_layers) * tstride, n, 1, m->norm_eps);
-  if (want_logits)
+  if (!fast_matvec_argmax(s, m->output.format, m->output.data, m->n_vocab, n, m->hidden, m->logits, m->output_norm,
+                          m->norm_eps, m->argmax_partials, cus)) {
     run_matvec(s, m->output.format, m->output.data, m->n_vocab, n, m->hidden, m->logits, m->output_norm, m->norm_eps,
                false, cus);
+    run_argmax_partials(s, m->logits, m->n_vocab, m->argmax_partials, kArgmaxPartials);
+  }
 }
 
 // With BCH_LFM2_CHECK=1 in the environment, record_batch synchronises after
@@ -302,8 +323,7 @@ static int check_hip(hipError_t e, const char *what) {
 static int capture(bch_lfm2 *m, bool generate, hipGraphExec_t *out) {
   hipStream_t s = m->s;
   BCH_TRY(check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture"));
-  if (generate) run_argmax(s, m->logits, m->tokens, m->n_vocab, m->dpos, true);
-  record_step(m, s, true, false);
+  record_step(m, s, generate, false);
   hipGraph_t g;
   BCH_TRY(check_hip(hipStreamEndCapture(s, &g), "end capture"));
   hipError_t e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
@@ -359,9 +379,9 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
   }
   if (any_attn) {
     const uint32_t group = md->n_kv_heads ? md->n_heads / md->n_kv_heads : 0;
-    if (!md->n_kv_heads || md->n_heads % md->n_kv_heads || group > 4 || hd % 32 || hd > 256 || hd == 0)
+    if (!md->n_kv_heads || md->n_heads % md->n_kv_heads || group > 4 || hd < 32 || hd > 256 || (hd & (hd - 1)))
       return fail(BCH_ERR_ATTENTION_LIMITS,
-                  "a head size that is a multiple of 32 up to 256 and at most 4 query heads per KV head, got %u and %u",
+                  "a head size of 32, 64, 128 or 256 and at most 4 query heads per KV head, got %u and %u",
                   hd, group);
   }
   auto *m = new bch_lfm2();
@@ -459,8 +479,10 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
     const uint64_t cache = (uint64_t)m->n_attn * n_ctx * m->kv_dim * (m->kv_half ? 2 : 4);
     m->decode_splits = attention_splits(n_ctx, std::max(1u, m->n_kv_heads), ctx->n_cus);
     m->prefill_splits = m->decode_splits;
-    const uint64_t partial_floats = attention_partial_floats(
-        std::min<uint32_t>(m->batch, kAttnQueryBatch), m->n_heads, hd, m->decode_splits);
+    const uint64_t partial_floats =
+        std::max(attention_partial_floats(std::min<uint32_t>(m->batch, kAttnQueryBatch), m->n_heads, hd,
+                                          m->decode_splits),
+                 attention_partial_floats(1, m->n_heads, hd, attn_decode_max_splits(n_ctx, hd, m->kv_half)));
     int rc = 0;
     (void)((rc = dev_alloc(m, cache, &m->k_cache)) || (rc = dev_alloc(m, cache, &m->v_cache)) ||
            (rc = dev_alloc_t(m, (uint64_t)m->n_conv * (m->conv_kernel - 1) * n, &m->conv_state)) ||
@@ -472,7 +494,7 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
            (rc = dev_alloc_t(m, partial_floats + 4, &m->partials)) ||
            (rc = dev_alloc_t(m, (uint64_t)kAttnQueryBatch * std::max(1u, m->n_kv_heads), &m->counters)) ||
            (rc = dev_alloc_t(m, (uint64_t)n_ctx + 2, &m->tokens)) || (rc = dev_alloc_t(m, 4, &m->dpos)) ||
-           (rc = dev_alloc_t(m, 4, &m->greedy)));
+           (rc = dev_alloc_t(m, 4, &m->greedy)) || (rc = dev_alloc_t(m, kArgmaxPartials, &m->argmax_partials)));
     if (rc) return cleanup(rc);
   }
   hipEventCreate(&m->ev0);
@@ -523,12 +545,12 @@ int bch_lfm2_step(bch_lfm2 *m, uint32_t token, float *logits, float *trace_embed
   BCH_TRY(set_dpos(m, m->n_past));
   hipEventRecord(m->ev0, s);
   if (trace) {
-    record_step(m, s, true, true);
+    record_step(m, s, false, true);
   } else if (use_graphs()) {
     if (!m->step_graph) BCH_TRY(capture(m, false, &m->step_graph));
     BCH_TRY(check_hip(hipGraphLaunch(m->step_graph, s), "launch step graph"));
   } else {
-    record_step(m, s, true, false);
+    record_step(m, s, false, false);
   }
   BCH_TRY(finish(m));
   const uint32_t n = m->n_embd;
@@ -606,18 +628,17 @@ int bch_lfm2_generate(bch_lfm2 *m, uint32_t *out, uint32_t n) {
     return fail(BCH_ERR_CONTEXT_FULL, "%u tokens exceed the %u free positions", n, m->n_ctx - m->n_past);
   if (n == 0) return BCH_OK;
   // Each replay writes argmax(logits) into tokens[dpos + 1], advances dpos
-  // and runs the step there; dpos starts at the last consumed position.
+  // and runs the step there; dpos starts at the last consumed position.  The
+  // current logits (from a prefill, a step or a restore) are reduced to
+  // argmax partials once; every step then leaves its own.
   BCH_TRY(set_dpos(m, m->n_past - 1));
+  hipEventRecord(m->ev0, m->s);
+  run_argmax_partials(m->s, m->logits, m->n_vocab, m->argmax_partials, kArgmaxPartials);
   if (use_graphs()) {
     if (!m->gen_graph) BCH_TRY(capture(m, true, &m->gen_graph));
-    hipEventRecord(m->ev0, m->s);
     for (uint32_t i = 0; i < n; i++) BCH_TRY(check_hip(hipGraphLaunch(m->gen_graph, m->s), "launch decode graph"));
   } else {
-    hipEventRecord(m->ev0, m->s);
-    for (uint32_t i = 0; i < n; i++) {
-      run_argmax(m->s, m->logits, m->tokens, m->n_vocab, m->dpos, true);
-      record_step(m, m->s, true, false);
-    }
+    for (uint32_t i = 0; i < n; i++) record_step(m, m->s, true, false);
   }
   BCH_TRY(finish(m));
   BCH_TRY(check_hip(hipMemcpy(out, m->tokens + m->n_past, (uint64_t)n * 4, hipMemcpyDeviceToHost), "read tokens"));

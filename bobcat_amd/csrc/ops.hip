@@ -33,19 +33,6 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float *__restrict__ x, c
   for (uint32_t i = threadIdx.x; i < n; i += 256) orow[i] = w[i] * (xr[i] * scale);
 }
 
-// The inverse frequencies 1/theta^(2i/n_rot) of the rotated pairs, computed
-// on the host with the host's powf (as scalar::rope_neox does,
-// scalar.rs:257-260), so device angles equal the CPU path's bit for bit.
-struct RopeFreqs {
-  float inv_freq[128];
-};
-
-static RopeFreqs rope_freqs(float theta, uint32_t n_rot) {
-  RopeFreqs f{};
-  for (uint32_t i = 0; i < n_rot / 2 && i < 128; i++) f.inv_freq[i] = 1.0f / powf(theta, (float)(2 * i) / (float)n_rot);
-  return f;
-}
-
 // norm_rope (norm.metal:43-91): one wave per (head, token); lane i holds
 // elements i and i+64 .. of the head.  Per-head RMS norm scaled by `w`,
 // then NeoX rotation of the first n_rot elements (i pairs with
@@ -56,7 +43,7 @@ static RopeFreqs rope_freqs(float theta, uint32_t n_rot) {
 template <bool HALF>
 __global__ __launch_bounds__(64) void k_norm_rope(const float *src, void *dst, const float *__restrict__ w,
                                                   uint32_t head_dim, uint32_t pos, const uint32_t *dpos,
-                                                  const RopeFreqs freqs, float eps, uint32_t src_stride,
+                                                  const RopeTable freqs, float eps, uint32_t src_stride,
                                                   uint32_t dst_stride, uint32_t n_rot,
                                                   uint32_t src_head_stride, uint64_t dst_pos_stride) {
   const uint32_t head = blockIdx.x, token = blockIdx.y, lane = threadIdx.x;
@@ -258,6 +245,63 @@ __global__ void k_short_conv_history(const float *__restrict__ bcx, float *__res
   for (uint32_t k = 0; k < nh; k++) hist[k * n_embd + ch] = next[k];
 }
 
+// Greedy selection folded into the decode graph: the logits GEMV leaves one
+// (value, index) key per workgroup; these kernels produce and consume them.
+__device__ __forceinline__ uint64_t max_key(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__global__ __launch_bounds__(1024) void k_argmax_partials(const float *__restrict__ x, uint32_t n,
+                                                          uint64_t *__restrict__ partials, uint32_t n_partials) {
+  __shared__ uint64_t best_s[16];
+  uint64_t best = 0;
+  for (uint32_t i = threadIdx.x; i < n; i += 1024) {
+    const uint32_t b = __float_as_uint(x[i]) == 0x80000000u ? 0u : __float_as_uint(x[i]);  // -0 ties +0
+    const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    best = max_key(best, ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - i));
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint64_t o = ((uint64_t)__shfl_xor((uint32_t)(best >> 32), off, 64) << 32) |
+                       (uint64_t)__shfl_xor((uint32_t)best, off, 64);
+    best = max_key(best, o);
+  }
+  if (threadIdx.x % 64 == 0) best_s[threadIdx.x / 64] = best;
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < n_partials; i += 1024) partials[i] = 0;
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 16; w++) best = max_key(best, best_s[w]);
+    partials[0] = best;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_embed_next(uint32_t format, const uint8_t *__restrict__ W, uint64_t row_bytes,
+                                                    uint32_t *tokens, float *__restrict__ out, uint32_t n_embd,
+                                                    uint32_t *dpos, const uint64_t *__restrict__ partials,
+                                                    uint32_t n_partials) {
+  __shared__ uint64_t best_s[4];
+  __shared__ uint32_t token_s;
+  const uint32_t p = *dpos;
+  uint64_t best = 0;
+  for (uint32_t i = threadIdx.x; i < n_partials; i += 256) best = max_key(best, partials[i]);
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint64_t o = ((uint64_t)__shfl_xor((uint32_t)(best >> 32), off, 64) << 32) |
+                       (uint64_t)__shfl_xor((uint32_t)best, off, 64);
+    best = max_key(best, o);
+  }
+  if (threadIdx.x % 64 == 0) best_s[threadIdx.x / 64] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; w++) best = max_key(best, best_s[w]);
+    token_s = 0xffffffffu - (uint32_t)best;
+  }
+  __syncthreads();
+  const uint32_t tok = token_s;
+  const uint8_t *row = W + (uint64_t)tok * row_bytes;
+  for (uint32_t i = threadIdx.x; i < n_embd; i += 256) out[i] = dequant_elem(format, row, i);
+  if (threadIdx.x == 0) {
+    tokens[p + 1] = tok;
+    *dpos = p + 1;  // every thread read p above, before this store
+  }
+}
+
 // ------------------------------------------------------------------
 // Stream-level launchers shared with the model driver.
 // ------------------------------------------------------------------
@@ -271,7 +315,7 @@ void run_norm_rope(hipStream_t s, const float *src, void *dst, bool half, const 
                    uint32_t n_tokens, uint32_t src_stride, uint32_t dst_stride, float theta, float eps,
                    uint64_t dst_pos_stride) {
   dim3 grid(n_heads, n_tokens);
-  const RopeFreqs f = rope_freqs(theta, n_rot);
+  const RopeTable f = rope_table(theta, n_rot);
   if (half)
     k_norm_rope<true><<<grid, 64, 0, s>>>(src, dst, w, head_dim, pos, dpos, f, eps, src_stride, dst_stride, n_rot,
                                           src_head_stride, dst_pos_stride);
@@ -297,6 +341,15 @@ void run_embed(hipStream_t s, uint32_t format, const uint8_t *W, uint64_t row_by
 
 void run_argmax(hipStream_t s, const float *x, uint32_t *out, uint32_t n, uint32_t *dpos, bool advance) {
   k_argmax<<<1, 1024, 0, s>>>(x, out, n, dpos, advance ? 1 : 0);
+}
+
+void run_argmax_partials(hipStream_t s, const float *logits, uint32_t n, uint64_t *partials, uint32_t n_partials) {
+  k_argmax_partials<<<1, 1024, 0, s>>>(logits, n, partials, n_partials);
+}
+
+void run_embed_next(hipStream_t s, uint32_t format, const uint8_t *W, uint64_t row_bytes, uint32_t *tokens,
+                    float *out, uint32_t n_embd, uint32_t *dpos, const uint64_t *partials, uint32_t n_partials) {
+  k_embed_next<<<1, 256, 0, s>>>(format, W, row_bytes, tokens, out, n_embd, dpos, partials, n_partials);
 }
 
 void run_short_conv(hipStream_t s, const float *bcx, const float *taps, float *hist, float *out, uint32_t n_embd,

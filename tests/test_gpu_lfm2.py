@@ -147,6 +147,25 @@ def test_prefill_in_batches_matches_one_batch(hip):
     b.close()
 
 
+@pytest.mark.parametrize("kv_half", [False, True])
+def test_decode_across_attention_splits(hip, kv_half):
+    """Decode steps at positions 1020-1027 cross the split boundary at 1024
+    (a split holds 512 f32 or 1024 f16 positions of a 64-wide head), so they
+    run with one, two and three splits and the cross-workgroup combine."""
+    w = Lfm2Weights(LFM2_TINY, seed=11)
+    toks = prompt(LFM2_TINY, 1028, seed=6)
+    gpu = Lfm2Hip(hip, w, n_ctx=1100, kv_half=kv_half)
+    cpu = oracle.Lfm2State(w, n_ctx=1100)
+    gpu.prefill(toks[:1020], logits=False)
+    for t in toks[:1020]:
+        cpu.step(t)
+    tol = HALF_TOLERANCE if kv_half else TOLERANCE
+    for t in toks[1020:]:
+        got, want = gpu.step(t), cpu.step(t)
+        assert rel(got, want) < tol, (t, rel(got, want))
+    gpu.close()
+
+
 def test_reset_matches_fresh_state(hip, weights):
     cfg = weights.cfg
     toks = prompt(cfg, 10, seed=5)
