@@ -133,6 +133,24 @@ struct Q4K {
     f.sum_lo = a;
     f.sum_hi = b;
   }
+  // The unit's inputs from 64 consecutive floats (16-byte aligned, in LDS).
+  __device__ __forceinline__ static void from_lds(const float *p, Frag &f) {
+    const float4 *p4 = reinterpret_cast<const float4 *>(p);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float4 a = p4[i], b = p4[8 + i];
+      f.lo[4 * i] = a.x, f.lo[4 * i + 1] = a.y, f.lo[4 * i + 2] = a.z, f.lo[4 * i + 3] = a.w;
+      f.hi[4 * i] = b.x, f.hi[4 * i + 1] = b.y, f.hi[4 * i + 2] = b.z, f.hi[4 * i + 3] = b.w;
+    }
+    float sa = 0.f, sb = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+      sa += f.lo[i];
+      sb += f.hi[i];
+    }
+    f.sum_lo = sa;
+    f.sum_hi = sb;
+  }
   // d·(sc_lo·Σq·x + sc_hi·Σq'·x') − dmin·(m_lo·Σx + m_hi·Σx'), which is
   // Σ_l ((d·sc)·q_l − dmin·m)·x_l regrouped.
   // The unit's 48 bytes: the super-block header and the pair's 32 quant bytes.
@@ -184,6 +202,10 @@ struct F16 {
   __device__ __forceinline__ static void load(const float *x, const float *nw, uint32_t u, Frag &f) {
     load_inputs<NORM>(x, nw, u * 8, f.x, 2);
   }
+  __device__ __forceinline__ static void from_lds(const float *p, Frag &f) {
+    const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
+    f.x[0] = a.x, f.x[1] = a.y, f.x[2] = a.z, f.x[3] = a.w, f.x[4] = b.x, f.x[5] = b.y, f.x[6] = b.z, f.x[7] = b.w;
+  }
   using Raw = uint4;
   __device__ __forceinline__ static Raw fetch(const uint8_t *__restrict__ row, uint32_t u) {
     return reinterpret_cast<const uint4 *>(row)[u];
@@ -212,6 +234,10 @@ struct F32 {
   template <bool NORM>
   __device__ __forceinline__ static void load(const float *x, const float *nw, uint32_t u, Frag &f) {
     load_inputs<NORM>(x, nw, u * 4, f.x, 1);
+  }
+  __device__ __forceinline__ static void from_lds(const float *p, Frag &f) {
+    const float4 a = reinterpret_cast<const float4 *>(p)[0];
+    f.x[0] = a.x, f.x[1] = a.y, f.x[2] = a.z, f.x[3] = a.w;
   }
   using Raw = float4;
   __device__ __forceinline__ static Raw fetch(const uint8_t *__restrict__ row, uint32_t u) {

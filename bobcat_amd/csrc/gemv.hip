@@ -9,8 +9,9 @@
 // the loop fully unrolled, so all of the items' weight loads are in flight
 // together; per-item partial sums stay in registers and are reduced once at
 // the end (shuffles inside a wave, LDS across the waves of a wide group).
-// When the input is RMS-normalised, the group's own fragments already hold
-// the whole input, so the norm costs no extra pass or barrier.
+// The workgroup first stages the input in LDS with coalesced loads (times
+// the norm weights, with the sum of squares of an RMS norm reduced on the
+// way), then every lane takes its unit's fragment from LDS.
 //
 // LPR is a power of two up to 64 (several groups per wave) or a multiple
 // of 64 up to 256 (one group over several waves); rows wider than 256 units
@@ -125,21 +126,6 @@ struct ConvItems {
 
 // --- the kernel ----------------------------------------------------------
 
-template <class F>
-__device__ __forceinline__ float frag_sumsq(const float *x, uint32_t u) {
-  const float4 *xp = reinterpret_cast<const float4 *>(x + u * F::kUnit);
-  float s = 0.f;
-#pragma unroll
-  for (uint32_t i = 0; i < F::kUnit / 4; i++) {
-    const float4 v = xp[i];
-    s = fmaf(v.x, v.x, s);
-    s = fmaf(v.y, v.y, s);
-    s = fmaf(v.z, v.z, s);
-    s = fmaf(v.w, v.w, s);
-  }
-  return s;
-}
-
 template <int LPR>
 __device__ __forceinline__ float group_total(float v, float *lds_scratch, int slot) {
   if constexpr (LPR <= 64) {
@@ -178,29 +164,63 @@ __global__ __launch_bounds__(256) void k_gemv(P p, const float *__restrict__ x, 
       for (int j = 0; j < R; j++) dst[it * R + j] = F::fetch(p.row(item, j), unit);
     }
   };
-  if (b < n_batches) fetch(ra, b);
-
-  // The lane's unit of the input (times the norm weights), loaded once.
-  typename F::Frag f;
-  F::template load<NORM>(x, nw, unit, f);
-  float scale = 1.f;
-  constexpr int W = LPR > 64 ? LPR / 64 : 1;
-  __shared__ float red[(N + 1) * W];
-  if (NORM) {
-    float ss = active ? frag_sumsq<F>(x, unit) : 0.f;
-    if constexpr (LPR <= 64) {
-      ss = group_sum<LPR>(ss);
-    } else {
-      ss = wave_sum(ss);
-      if (tid % 64 == 0) red[N * W + tid / 64] = ss;
-      __syncthreads();
-      ss = 0.f;
+  // The input (times the norm weights) is staged once per workgroup in LDS
+  // with coalesced loads, one padded slot of kSlot floats per unit, and each
+  // lane then reads its unit's fragment from there.  (Loading each lane's
+  // unit straight from memory would make every wave load touch 64 cache
+  // lines.)  The x loads go out first and the weight loads right after, so
+  // waiting for x does not wait for the weights.
+  constexpr uint32_t kPad = F::kUnit >= 64 ? 4 : 0;  // spreads the fragment reads over the LDS banks
+  constexpr uint32_t kSlot = F::kUnit + kPad;
+  constexpr int kPer = 8;  // float4 loads per thread per pass
+  extern __shared__ float4 xs4[];
+  float *xs = reinterpret_cast<float *>(xs4);
+  const uint32_t n4 = n_cols / 4;
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  const float4 *w4 = reinterpret_cast<const float4 *>(nw);
+  float ss = 0.f;
+  for (uint32_t base = 0; base < n4; base += kPer * T) {
+    float4 xv[kPer], wv[kPer];
 #pragma unroll
-      for (int w = 0; w < W; w++) ss += red[N * W + w];
-      __syncthreads();
+    for (int k = 0; k < kPer; k++) {
+      const uint32_t i = base + tid + k * T;
+      if (i < n4) {
+        xv[k] = x4[i];
+        if (NORM) wv[k] = w4[i];
+      }
     }
+    if (base == 0 && b < n_batches) fetch(ra, b);
+#pragma unroll
+    for (int k = 0; k < kPer; k++) {
+      const uint32_t i = base + tid + k * T;
+      if (i < n4) {
+        float4 v = xv[k];
+        if (NORM) {
+          ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
+          v.x *= wv[k].x, v.y *= wv[k].y, v.z *= wv[k].z, v.w *= wv[k].w;
+        }
+        const uint32_t e = 4 * i;
+        *reinterpret_cast<float4 *>(xs + (e / F::kUnit) * kSlot + e % F::kUnit) = v;
+      }
+    }
+  }
+  __shared__ float ss_s[T / 64];
+  if (NORM) {
+    ss = wave_sum(ss);
+    if (tid % 64 == 0) ss_s[tid / 64] = ss;
+  }
+  __syncthreads();
+  typename F::Frag f;
+  F::from_lds(xs + unit * kSlot, f);
+  float scale = 1.f;
+  if (NORM) {
+    ss = 0.f;
+#pragma unroll
+    for (int w = 0; w < T / 64; w++) ss += ss_s[w];
     scale = (float)(1.0 / sqrt((double)ss / (double)n_cols + (double)eps));
   }
+  constexpr int W = LPR > 64 ? LPR / 64 : 1;
+  __shared__ float red[N * W];
 
   uint64_t best = 0;  // argmax key of the items this lane stored (P::kArgmax)
 
@@ -316,7 +336,14 @@ static void launch_gemv(hipStream_t s, const P &p, const float *x, const float *
   const uint32_t n_batches = div_ceil(n_items, RPG);
   uint32_t grid = std::max(1u, std::min(div_ceil(n_batches, G), per_cu * 256));
   if constexpr (P::kArgmax) grid = std::min(grid, kArgmaxPartials);
-  k_gemv<F, LPR, RPG, NORM, P><<<grid, threads, 0, s>>>(p, x, nw, eps, n_items, n_units, n_cols);
+  // LDS for the staged input: one padded slot per unit (up to 68 KiB).
+  constexpr uint32_t kSlot = F::kUnit + (F::kUnit >= 64 ? 4 : 0);
+  const uint32_t lds = n_units * kSlot * 4;
+  static const bool lds_limit_set =
+      hipFuncSetAttribute(reinterpret_cast<const void *>(k_gemv<F, LPR, RPG, NORM, P>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, 256 * kSlot * 4) == hipSuccess;
+  (void)lds_limit_set;
+  k_gemv<F, LPR, RPG, NORM, P><<<grid, threads, lds, s>>>(p, x, nw, eps, n_items, n_units, n_cols);
 }
 
 template <class F, int LPR, bool NORM, class P>
@@ -333,6 +360,7 @@ static void gemv_rpg(hipStream_t s, int rpg, const P &p, const float *x, const f
 template <class F, bool NORM, class P>
 static bool gemv_dispatch(hipStream_t s, const P &p, const float *x, const float *nw, float eps, uint32_t n_items,
                           uint32_t n_cols, uint32_t n_cus) {
+  if (n_cols % F::kUnit) return false;  // a row must be whole units
   const uint32_t n_units = n_cols / F::kUnit;
   const int lpr = lanes_for(n_units);
   if (!lpr) return false;
