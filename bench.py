@@ -30,6 +30,25 @@ HBM_PEAK_GBS = 8000.0
 GEMV_ROWS, GEMV_COLS = 8192, 2048
 GEMV_BYTES = GEMV_ROWS * GEMV_COLS // 256 * 144 + GEMV_COLS * 4 + GEMV_ROWS * 4  # 9,478,144
 PROMPT, GEN = 512, 128
+READ_THREADS = 256 * 1024
+READ_REPS = 5
+COPY_BYTES = 64 << 20
+ROOT = os.path.dirname(os.path.abspath(__file__))
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "matvec_q4k_config1_traffic.txt")
+
+
+def measured_traffic():
+    """HBM bytes per config-1 GEMV launch from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE scaled by the calibration launches), or
+    None when there is none."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def log(msg: str) -> None:
@@ -47,7 +66,8 @@ def gemv_leg(hip, reps: int, copies: int = 64):
 
     w, x = gemv_case()
     wbytes = w.nbytes
-    big = hip.new_buffer(wbytes * copies)
+    big_bytes = wbytes * copies
+    big = hip.new_buffer(big_bytes)
     for c in range(copies):
         hip.write(big.at(c * wbytes), w)
     xb = hip.buffer_from(x)
@@ -64,9 +84,25 @@ def gemv_leg(hip, reps: int, copies: int = 64):
     launches = reps * copies
     per_launch = run(launches) / launches
     hot = run(copies, rotate=False) / copies
+
+    # Calibration launches of known traffic, for scaling the FETCH_SIZE and
+    # WRITE_SIZE counters of a profiled run (and the streaming-read rate the
+    # GEMV is compared with, as the reference's read_sum probe does):
+    # read_sum reads all of `big` READ_REPS times; copy moves COPY_BYTES.
+    sums = hip.new_buffer(READ_THREADS * 4)
+    hip.begin()
+    for _ in range(READ_REPS):
+        hip.read_sum(big.at(0), big_bytes // 16, sums.at(0), READ_THREADS)
+    read_s = hip.end() / READ_REPS
+    dst = hip.new_buffer(COPY_BYTES)
+    hip.begin()
+    hip.copy(big.at(0), dst.at(0), COPY_BYTES // 4)
+    hip.end()
+    sums.free()
+    dst.free()
     big.free()
     return dict(us=per_launch * 1e6, gbs=GEMV_BYTES / per_launch / 1e9, launches=launches,
-                hot_us=hot * 1e6, hot_gbs=GEMV_BYTES / hot / 1e9)
+                hot_us=hot * 1e6, hot_gbs=GEMV_BYTES / hot / 1e9, read_gbs=big_bytes / read_s / 1e9)
 
 
 def model_leg(hip, weights, steps: int, warmup: int, seed: int = 42):
@@ -192,8 +228,8 @@ def main() -> int:
         "decode_roofline_frac": round(decode_gbs / HBM_PEAK_GBS, 4),
         "roofline": {"kernel": "matvec_q4k (config 1, 8192x2048)", "bound": "hbm",
                      "achieved": round(g["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "us_per_launch": round(g["us"], 3)},
+                     "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "us_per_launch": round(g["us"], 3), "streaming_read_gbs": round(g["read_gbs"], 1)},
         "cpu_baseline": None if cpu is None else {
             "value": round(cpu["tok_s"], 4), "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"{cpu['steps']} decode steps of {cfg.name} by the oracle (C restatement of the "
