@@ -117,6 +117,10 @@ PROTOTYPES = {
     "bch_matmul": (_int, [_vp, _u32, View, _u32, _u32, View, View, _u32, _u32]),
     "bch_argmax": (_int, [_vp, View, View, _u32]),
     "bch_read_sum": (_int, [_vp, View, _u64, View, _u32]),
+    "bch_route_bytes": (_u64, [_u32, _u32]),
+    "bch_moe_route": (_int, [_vp, View, C.POINTER(Norm), View, View, View, View, _u32, _u32, _u32, _u32]),
+    "bch_matvec_experts_swiglu": (_int, [_vp, _u32, View, View, _u32, _u32, _u32, View, View, _u32, View, _u32]),
+    "bch_matvec_experts_down": (_int, [_vp, _u32, View, _u32, _u32, _u32, View, View, _u32, View, _u32]),
     "bch_lfm2_new": (_int, [_vp, C.POINTER(Lfm2Model), _u32, _int, C.POINTER(_vp)]),
     "bch_lfm2_free": (None, [_vp]),
     "bch_lfm2_n_past": (_u32, [_vp]),

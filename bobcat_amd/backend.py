@@ -246,6 +246,20 @@ class Hip:
     def read_sum(self, src, n_vectors, out, n_threads):
         check(lib().bch_read_sum(self.handle, _view(src), n_vectors, _view(out), n_threads))
 
+    def moe_route(self, x, norm: NormSpec | None, normed, router, bias, route, n_cols, n_experts, n_used,
+                  n_tokens):
+        n = C.byref(norm.c()) if norm is not None else None
+        check(lib().bch_moe_route(self.handle, _view(x), n, _view(normed if normed is not None else x),
+                                  _view(router), _view(bias), _view(route), n_cols, n_experts, n_used, n_tokens))
+
+    def matvec_experts_swiglu(self, fmt, gate, up, n_rows, n_cols, n_experts, x, route, n_used, y, n_tokens):
+        check(lib().bch_matvec_experts_swiglu(self.handle, int(fmt), _view(gate), _view(up), n_rows, n_cols,
+                                              n_experts, _view(x), _view(route), n_used, _view(y), n_tokens))
+
+    def matvec_experts_down(self, fmt, weights, n_rows, n_cols, n_experts, x, route, n_used, y, n_tokens):
+        check(lib().bch_matvec_experts_down(self.handle, int(fmt), _view(weights), n_rows, n_cols, n_experts,
+                                            _view(x), _view(route), n_used, _view(y), n_tokens))
+
     def argmax(self, x, out, n):
         check(lib().bch_argmax(self.handle, _view(x), _view(out), n))
 

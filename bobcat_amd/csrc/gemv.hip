@@ -78,6 +78,27 @@ struct SwigluItems {
   }
 };
 
+// The SwiGLU rows of the experts a token's route picked: item i is row
+// i % n_ff of the expert in route slot i / n_ff (gate and up stack the
+// experts, n_ff rows each; lfm2.rs:128-142).
+struct ExpertSwigluItems {
+  static constexpr int kRows = 2;
+  static constexpr bool kArgmax = false;
+  const uint8_t *Wg, *Wu;
+  uint64_t rb;
+  const uint32_t *ids;
+  uint32_t n_ff;
+  float *y;
+  __device__ const uint8_t *row(uint32_t item, int j) const {
+    const uint32_t slot = item / n_ff;
+    const uint64_t r = (uint64_t)ids[slot] * n_ff + (item - slot * n_ff);
+    return (j ? Wu : Wg) + r * rb;
+  }
+  __device__ void store(uint32_t item, const float *v, float scale) const {
+    y[item] = silu_g(v[0] * scale) * (v[1] * scale);
+  }
+};
+
 struct ThreeItems {
   static constexpr int kRows = 1;
   static constexpr bool kArgmax = false;
@@ -404,6 +425,14 @@ bool fast_matvec_argmax(hipStream_t s, uint32_t format, const uint8_t *W, uint32
                         const float *x, float *y, const float *nw, float eps, uint64_t *partials, uint32_t n_cus) {
   const uint64_t rb = bch_row_bytes(format, n_cols);
   return gemv_any(s, format, ArgmaxItems{W, rb, y, partials}, x, nw, eps, n_rows, n_cols, n_cus);
+}
+
+bool fast_matvec_experts_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const uint8_t *Wu, uint32_t n_ff,
+                                uint32_t n_cols, const uint32_t *ids, uint32_t n_used, const float *x, float *y,
+                                uint32_t n_cus) {
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  return gemv_any(s, format, ExpertSwigluItems{Wg, Wu, rb, ids, n_ff, y}, x, nullptr, 0.f, n_used * n_ff, n_cols,
+                  n_cus);
 }
 
 bool fast_matvec_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const uint8_t *Wu, uint32_t n_rows,

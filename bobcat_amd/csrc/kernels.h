@@ -68,6 +68,25 @@ constexpr uint32_t kArgmaxPartials = 1024;
 bool fast_matvec_argmax(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols,
                         const float *x, float *y, const float *norm_w, float eps, uint64_t *partials, uint32_t n_cus);
 
+// moe.hip + gemv.hip: mixture of experts.  A route holds, per token, the
+// n_used expert ids the router picked and then their n_used weights as
+// float bits (route_bytes = 2 * n_used * n_tokens * 4).
+constexpr uint32_t kMoeMaxExperts = 128;  // MOE_MAX_EXPERTS
+constexpr uint32_t kMoeMaxUsed = 8;       // MOE_MAX_USED
+// Route n_tokens tokens of x; with norm_w, RMS-normalise each token first
+// and store it at `normed`.
+void run_moe_route(hipStream_t s, const float *x, const float *norm_w, float eps, float *normed, const float *router,
+                   const float *bias, uint32_t *route, uint32_t n_cols, uint32_t n_experts, uint32_t n_used,
+                   uint32_t n_tokens);
+// y[slot][r] = silu(G_e·x)[r] · (U_e·x)[r] for the n_used experts e of `ids`.
+bool fast_matvec_experts_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const uint8_t *Wu, uint32_t n_ff,
+                                uint32_t n_cols, const uint32_t *ids, uint32_t n_used, const float *x, float *y,
+                                uint32_t n_cus);
+// y[r] += Σ_slot weight_slot · (D_e · x[slot])[r] for one token's route;
+// false when the shape or format has no kernel.
+bool run_experts_down(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols,
+                      const float *x, const uint32_t *route, uint32_t n_used, float *y, uint32_t n_cus);
+
 // ops.hip
 // argmax of n logits as partials[0] (an argmax key), with partials[1..n_partials) zeroed.
 void run_argmax_partials(hipStream_t s, const float *logits, uint32_t n, uint64_t *partials, uint32_t n_partials);

@@ -42,6 +42,11 @@ struct Layer {
   const float *taps = nullptr;
   DevMatrix in_proj, out_proj, wq, wk, wv, wo, gate, up, down;
   const float *q_norm = nullptr, *k_norm = nullptr;
+  // Mixture of experts (lfm2.rs:128-142): the F32 router, the routing bias
+  // and the stacked expert matrices.
+  bool moe = false;
+  DevMatrix router, gate_exps, up_exps, down_exps;
+  const float *expert_bias = nullptr;
 };
 
 }  // namespace bch
@@ -53,6 +58,7 @@ struct bch_lfm2 {
   hipStream_t s = nullptr;
   // Hyperparameters (lfm2.rs:17-49).
   uint32_t n_layers, n_embd, n_ff, n_heads, n_kv_heads, head_dim, n_vocab, conv_kernel;
+  uint32_t n_experts = 0, n_used = 0, n_ff_expert = 0;
   float rope_theta, norm_eps;
   uint32_t n_attn = 0, n_conv = 0;
   uint32_t q_dim, kv_dim;
@@ -67,6 +73,7 @@ struct bch_lfm2 {
   float *partials = nullptr, *trace = nullptr;
   uint32_t trace_rows = 0;  // tokens each traced activation holds (lfm2_metal.rs:764-779)
   uint32_t *counters = nullptr, *tokens = nullptr, *dpos = nullptr, *greedy = nullptr;
+  uint32_t *route = nullptr;  // expert routes of a batch (route_bytes(n_used, batch))
   uint64_t *argmax_partials = nullptr;  // kArgmaxPartials argmax keys of the logits
   std::vector<void *> allocations;
   // Sequence state.
@@ -144,6 +151,24 @@ static int check_matrix(const bch_matrix &mat, uint32_t rows, uint32_t cols, con
 // Recording
 // ---------------------------------------------------------------------
 
+// The mixture of experts of one token (Recorder::moe with n = 1,
+// lfm2_metal.rs:1251-1313): route `x` (RMS-normalised into `normed` when
+// `norm` is given, else `x` is already normalised), the SwiGLU rows of the
+// picked experts into m->ffn, then their weighted down projections added
+// to `residual`.
+static void record_moe_token(bch_lfm2 *m, hipStream_t s, const Layer &L, const float *x, const float *norm,
+                             float *normed, uint32_t *route, float *residual) {
+  const uint32_t n = m->n_embd, cus = m->ctx->n_cus;
+  if (norm)
+    run_moe_route(s, x, norm, m->norm_eps, normed, reinterpret_cast<const float *>(L.router.data), L.expert_bias,
+                  route, n, m->n_experts, m->n_used, 1);
+  const float *in = norm ? normed : x;
+  fast_matvec_experts_swiglu(s, L.gate_exps.format, L.gate_exps.data, L.up_exps.data, m->n_ff_expert, n, route,
+                             m->n_used, in, m->ffn, cus);
+  run_experts_down(s, L.down_exps.format, L.down_exps.data, n, m->n_ff_expert, m->ffn, route, m->n_used, residual,
+                   cus);
+}
+
 // One decode step at the position *m->dpos (Recorder::record_step).  With
 // `greedy_input`, the step first takes the greedy token of the previous
 // logits (from m->argmax_partials), stores it at tokens[*dpos + 1] and
@@ -194,9 +219,13 @@ static void record_step(bch_lfm2 *m, hipStream_t s, bool greedy_input, bool trac
       run_attn_decode(s, ad, m->kv_half);
       run_matvec(s, L.wo.format, L.wo.data, n, m->q_dim, m->attn, m->hidden, nullptr, 0.f, true, cus);
     }
-    run_matvec_swiglu(s, L.gate.format, L.gate.data, L.up.data, m->n_ff, n, m->hidden, m->ffn, L.ffn_norm,
-                      m->norm_eps, cus);
-    run_matvec(s, L.down.format, L.down.data, n, m->n_ff, m->ffn, m->hidden, nullptr, 0.f, true, cus);
+    if (L.moe) {
+      record_moe_token(m, s, L, m->hidden, L.ffn_norm, m->normed, m->route, m->hidden);
+    } else {
+      run_matvec_swiglu(s, L.gate.format, L.gate.data, L.up.data, m->n_ff, n, m->hidden, m->ffn, L.ffn_norm,
+                        m->norm_eps, cus);
+      run_matvec(s, L.down.format, L.down.data, n, m->n_ff, m->ffn, m->hidden, nullptr, 0.f, true, cus);
+    }
     if (trace) run_copy(s, m->hidden, m->trace + (1 + il) * tstride, n, nullptr, 0);
   }
   if (trace) run_rms_norm(s, m->hidden, m->output_norm, m->trace + (1 + m->n_layers) * tstride, n, 1, m->norm_eps);
@@ -285,12 +314,22 @@ static void record_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t coun
     }
     run_rms_norm(s, m->hidden, L.ffn_norm, m->normed, n, count, m->norm_eps);
     check_finite(s, "ffn_norm", il, m->normed, (uint64_t)count * n);
-    run_matmul(s, L.gate.format, L.gate.data, m->n_ff, n, m->normed, m->ffn, count, 0);
-    check_finite(s, "gate", il, m->ffn, (uint64_t)count * m->n_ff);
-    run_matmul(s, L.up.format, L.up.data, m->n_ff, n, m->normed, m->ffn, count, 2);
-    check_finite(s, "up", il, m->ffn, (uint64_t)count * m->n_ff);
-    run_matmul(s, L.down.format, L.down.data, n, m->n_ff, m->ffn, m->hidden, count, 1);
-    check_finite(s, "down", il, m->hidden, (uint64_t)count * n);
+    if (L.moe) {
+      // Route the whole batch in one launch, then each token's experts.
+      run_moe_route(s, m->normed, nullptr, 0.f, nullptr, reinterpret_cast<const float *>(L.router.data),
+                    L.expert_bias, m->route, n, m->n_experts, m->n_used, count);
+      for (uint32_t t = 0; t < count; t++)
+        record_moe_token(m, s, L, m->normed + (uint64_t)t * n, nullptr, nullptr,
+                         m->route + (uint64_t)t * 2 * m->n_used, m->hidden + (uint64_t)t * n);
+      check_finite(s, "moe", il, m->hidden, (uint64_t)count * n);
+    } else {
+      run_matmul(s, L.gate.format, L.gate.data, m->n_ff, n, m->normed, m->ffn, count, 0);
+      check_finite(s, "gate", il, m->ffn, (uint64_t)count * m->n_ff);
+      run_matmul(s, L.up.format, L.up.data, m->n_ff, n, m->normed, m->ffn, count, 2);
+      check_finite(s, "up", il, m->ffn, (uint64_t)count * m->n_ff);
+      run_matmul(s, L.down.format, L.down.data, n, m->n_ff, m->ffn, m->hidden, count, 1);
+      check_finite(s, "down", il, m->hidden, (uint64_t)count * n);
+    }
     if (trace) run_copy(s, m->hidden, m->trace + (1 + il) * tstride, count * n, nullptr, 0);
   }
   if (trace) run_rms_norm(s, m->hidden, m->output_norm, m->trace + (1 + m->n_layers) * tstride, n, count, m->norm_eps);
@@ -371,11 +410,20 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
   const uint32_t n = md->n_embd, hd = md->head_dim;
   if (md->conv_kernel < 2 || md->conv_kernel > 9)
     return fail(BCH_ERR_UNSUPPORTED_FORMAT, "a convolution of 2 to 9 taps, got %u", md->conv_kernel);
-  bool any_attn = false;
+  bool any_attn = false, any_moe = false;
   for (uint32_t il = 0; il < md->n_layers; il++) {
-    if (md->layers[il].is_moe)
-      return fail(BCH_ERR_UNSUPPORTED_FORMAT, "layer %u: mixture-of-experts blocks are not built yet", il);
+    any_moe |= md->layers[il].is_moe != 0;
     any_attn |= md->layers[il].is_attention != 0;
+  }
+  if (any_moe) {
+    // check_experts (lfm2_metal.rs:842-866) and this build's kernel limits.
+    if (md->n_experts > kMoeMaxExperts || md->n_experts_used > kMoeMaxUsed || md->n_experts_used == 0 ||
+        md->n_experts_used > md->n_experts)
+      return fail(BCH_ERR_EXPERT_LIMITS, "at most %u of %u experts per token, got %u of %u", kMoeMaxUsed,
+                  kMoeMaxExperts, md->n_experts_used, md->n_experts);
+    if (n % 4 || n > 16384 || md->n_ff_expert == 0 || md->n_ff_expert > 4096 || md->n_ff_expert % 256)
+      return fail(BCH_ERR_UNSUPPORTED_FORMAT, "expert shapes %u x %u are outside the expert kernels", md->n_ff_expert,
+                  n);
   }
   if (any_attn) {
     const uint32_t group = md->n_kv_heads ? md->n_heads / md->n_kv_heads : 0;
@@ -395,6 +443,9 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
   m->head_dim = hd;
   m->n_vocab = md->n_vocab;
   m->conv_kernel = md->conv_kernel;
+  m->n_experts = any_moe ? md->n_experts : 0;
+  m->n_used = any_moe ? md->n_experts_used : 0;
+  m->n_ff_expert = any_moe ? md->n_ff_expert : 0;
   m->rope_theta = md->rope_theta;
   m->norm_eps = md->norm_eps;
   m->q_dim = md->n_heads * hd;
@@ -448,11 +499,29 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
       if (S.in_proj.format != BCH_Q4K)
         return cleanup(fail(BCH_ERR_UNSUPPORTED_FORMAT, "layer %u: the fused conv projection needs Q4_K", il));
     }
-    if ((rc = mat(S.gate, md->n_ff, n, &L.gate, "ffn_gate")) || (rc = mat(S.up, md->n_ff, n, &L.up, "ffn_up")) ||
-        (rc = mat(S.down, n, md->n_ff, &L.down, "ffn_down")))
-      return cleanup(rc);
-    if (S.gate.format != S.up.format)
-      return cleanup(fail(BCH_ERR_UNSUPPORTED_FORMAT, "layer %u: gate and up matrices of one format", il));
+    L.moe = S.is_moe != 0;
+    if (L.moe) {
+      const uint32_t ne = md->n_experts, nff = md->n_ff_expert;
+      if ((rc = mat(S.router, ne, n, &L.router, "ffn_gate_inp")) ||
+          (rc = vec(S.expert_bias, ne, &L.expert_bias, "exp_probs_b")) ||
+          (rc = mat(S.gate_exps, ne * nff, n, &L.gate_exps, "ffn_gate_exps")) ||
+          (rc = mat(S.up_exps, ne * nff, n, &L.up_exps, "ffn_up_exps")) ||
+          (rc = mat(S.down_exps, ne * n, nff, &L.down_exps, "ffn_down_exps")))
+        return cleanup(rc);
+      if (S.router.format != BCH_F32)
+        return cleanup(fail(BCH_ERR_UNSUPPORTED_FORMAT, "layer %u: the router must be F32, got format %u", il,
+                            S.router.format));
+      if (S.gate_exps.format != S.up_exps.format || (S.gate_exps.format != BCH_Q4K && S.gate_exps.format != BCH_F16 &&
+                                                     S.gate_exps.format != BCH_F32) ||
+          (S.down_exps.format != BCH_Q4K && S.down_exps.format != BCH_F16 && S.down_exps.format != BCH_F32))
+        return cleanup(fail(BCH_ERR_UNSUPPORTED_FORMAT, "layer %u: experts in Q4_K, F16 or F32", il));
+    } else {
+      if ((rc = mat(S.gate, md->n_ff, n, &L.gate, "ffn_gate")) || (rc = mat(S.up, md->n_ff, n, &L.up, "ffn_up")) ||
+          (rc = mat(S.down, n, md->n_ff, &L.down, "ffn_down")))
+        return cleanup(rc);
+      if (S.gate.format != S.up.format)
+        return cleanup(fail(BCH_ERR_UNSUPPORTED_FORMAT, "layer %u: gate and up matrices of one format", il));
+    }
   }
   {
     int rc;
@@ -490,11 +559,12 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
            (rc = dev_alloc_t(m, rows * 3 * n, &m->bcx)) || (rc = dev_alloc_t(m, rows * n, &m->conv_out)) ||
            (rc = dev_alloc_t(m, rows * m->q_dim + 4, &m->q)) || (rc = dev_alloc_t(m, rows * m->kv_dim + 4, &m->k)) ||
            (rc = dev_alloc_t(m, rows * m->kv_dim + 4, &m->v)) || (rc = dev_alloc_t(m, rows * m->q_dim + 4, &m->attn)) ||
-           (rc = dev_alloc_t(m, rows * m->n_ff, &m->ffn)) || (rc = dev_alloc_t(m, m->n_vocab, &m->logits)) ||
+           (rc = dev_alloc_t(m, std::max<uint64_t>(rows * m->n_ff, (uint64_t)m->n_used * m->n_ff_expert), &m->ffn)) || (rc = dev_alloc_t(m, m->n_vocab, &m->logits)) ||
            (rc = dev_alloc_t(m, partial_floats + 4, &m->partials)) ||
            (rc = dev_alloc_t(m, (uint64_t)kAttnQueryBatch * std::max(1u, m->n_kv_heads), &m->counters)) ||
            (rc = dev_alloc_t(m, (uint64_t)n_ctx + 2, &m->tokens)) || (rc = dev_alloc_t(m, 4, &m->dpos)) ||
-           (rc = dev_alloc_t(m, 4, &m->greedy)) || (rc = dev_alloc_t(m, kArgmaxPartials, &m->argmax_partials)));
+           (rc = dev_alloc_t(m, 4, &m->greedy)) || (rc = dev_alloc_t(m, kArgmaxPartials, &m->argmax_partials)) ||
+           (rc = dev_alloc_t(m, 2 * (uint64_t)std::max(1u, m->n_used) * rows, &m->route)));
     if (rc) return cleanup(rc);
   }
   hipEventCreate(&m->ev0);

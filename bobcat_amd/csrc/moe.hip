@@ -1,0 +1,318 @@
+// Mixture-of-experts kernels: the router and the weighted down projection of
+// the experts it picks (the expert SwiGLU rows run through the persistent
+// GEMV of gemv.hip).  Counterparts of moe_route / matvec_experts_down
+// (crates/bobcat-metal/src/moe.metal:21-121, 237-307) and of the CPU
+// Model::moe_block / route (crates/bobcat/src/lfm2.rs:413-440, 691-709).
+#include <algorithm>
+#include <cmath>
+
+#include "formats.h"
+#include "kernels.h"
+#include "runtime.h"
+
+namespace bch {
+
+// Orderable key of (value, index): larger values first, ties to the lower
+// index (the order of the reference's stable descending sort).
+__device__ __forceinline__ uint64_t route_key(float v, uint32_t index) {
+  uint32_t b = __float_as_uint(v);
+  if (b == 0x80000000u) b = 0;  // -0 ties +0
+  const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - index);
+}
+
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint64_t o = ((uint64_t)__shfl_xor((uint32_t)(k >> 32), off, 64) << 32) |
+                       (uint64_t)__shfl_xor((uint32_t)k, off, 64);
+    k = k > o ? k : o;
+  }
+  return k;
+}
+
+// One workgroup per token.  The token (RMS-normalised when norm_w is given,
+// as rms_norm does: w·(x·scale)) is staged in LDS; wave w scores experts
+// w, w+16, ... with the F32 router rows; wave 0 then picks the n_used experts
+// of largest sigmoid score + bias and writes their ids and normalised weights.
+__global__ __launch_bounds__(1024) void k_moe_route(const float *__restrict__ x, const float *__restrict__ norm_w,
+                                                    float eps, float *__restrict__ normed,
+                                                    const float *__restrict__ router, const float *__restrict__ bias,
+                                                    uint32_t *__restrict__ route, uint32_t n_cols, uint32_t n_experts,
+                                                    uint32_t n_used) {
+  extern __shared__ float xs[];
+  __shared__ float red[16];
+  __shared__ float score[kMoeMaxExperts];
+  const uint32_t t = blockIdx.x, tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+  const float *row = x + (uint64_t)t * n_cols;
+  float ss = 0.f;
+  for (uint32_t i = tid; i < n_cols; i += 1024) {
+    const float v = row[i];
+    xs[i] = v;
+    ss = fmaf(v, v, ss);
+  }
+  if (norm_w) {
+    ss = block_sum<1024>(ss, red);
+    const float scale = (float)(1.0 / sqrt((double)ss / (double)n_cols + (double)eps));
+    for (uint32_t i = tid; i < n_cols; i += 1024) {
+      const float v = norm_w[i] * (xs[i] * scale);
+      xs[i] = v;
+      normed[(uint64_t)t * n_cols + i] = v;
+    }
+  }
+  __syncthreads();
+  for (uint32_t e = wave; e < n_experts; e += 16) {
+    const float4 *r4 = reinterpret_cast<const float4 *>(router + (uint64_t)e * n_cols);
+    float acc = 0.f;
+    for (uint32_t i = lane; i < n_cols / 4; i += 64) {
+      const float4 w = r4[i];
+      const float4 v = reinterpret_cast<const float4 *>(xs)[i];
+      acc = fmaf(w.x, v.x, fmaf(w.y, v.y, fmaf(w.z, v.z, fmaf(w.w, v.w, acc))));
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) score[e] = 1.0f / (1.0f + expf(-acc));
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  // Lane l holds experts l and l + 64.
+  uint64_t k0 = lane < n_experts ? route_key(score[lane] + bias[lane], lane) : 0;
+  uint64_t k1 = lane + 64 < n_experts ? route_key(score[lane + 64] + bias[lane + 64], lane + 64) : 0;
+  uint32_t *out = route + (uint64_t)t * 2 * n_used;
+  float sum = 0.f;
+  uint32_t picked[kMoeMaxUsed];
+  for (uint32_t k = 0; k < n_used; k++) {
+    const uint64_t best = wave_max_key(k0 > k1 ? k0 : k1);
+    const uint32_t e = 0xffffffffu - (uint32_t)best;
+    if (e == lane) k0 = 0;
+    if (e == lane + 64) k1 = 0;
+    picked[k] = e;
+    sum += score[e];  // in pick order, as the reference sums the sorted picks
+  }
+  const float norm = sum + 1e-6f;  // transformers adds 1e-6 (lfm2.rs:703-705)
+  if (lane == 0) {
+    for (uint32_t k = 0; k < n_used; k++) {
+      out[k] = picked[k];
+      out[n_used + k] = __float_as_uint(score[picked[k]] / norm);
+    }
+  }
+}
+
+// y[r] += Σ_slot w_slot · (W_{e_slot} row r) · x_slot for one token.  The
+// workgroup stages the USED inputs in LDS (a padded slot per unit, as the
+// GEMV does); a group of LPR lanes takes a row, lane i unit i, loads the
+// row of every picked expert at once, and adds the experts in route order.
+template <class F, int LPR, int USED>
+__global__ __launch_bounds__(256) void k_experts_down(const uint8_t *__restrict__ W, uint64_t rb, uint32_t n_rows,
+                                                      uint32_t n_cols, const float *__restrict__ x,
+                                                      const uint32_t *__restrict__ route, float *__restrict__ y) {
+  constexpr int T = 256, G = T / LPR;
+  constexpr uint32_t kSlot = F::kUnit + (F::kUnit >= 64 ? 4 : 0);
+  extern __shared__ float4 xs4[];
+  float *xs = reinterpret_cast<float *>(xs4);
+  const uint32_t tid = threadIdx.x, n_units = n_cols / F::kUnit, per_input = n_units * kSlot;
+  for (int k = 0; k < USED; k++) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + (uint64_t)k * n_cols);
+    for (uint32_t i = tid; i < n_cols / 4; i += T) {
+      const uint32_t e = 4 * i;
+      *reinterpret_cast<float4 *>(xs + k * per_input + (e / F::kUnit) * kSlot + e % F::kUnit) = x4[i];
+    }
+  }
+  __syncthreads();
+  uint32_t ids[USED];
+  float wts[USED];
+#pragma unroll
+  for (int k = 0; k < USED; k++) {
+    ids[k] = route[k];
+    wts[k] = __uint_as_float(route[USED + k]);
+  }
+  const uint32_t g = tid / LPR, li = tid % LPR;
+  const bool active = li < n_units;
+  const uint32_t unit = active ? li : 0u;
+  for (uint32_t r = blockIdx.x * G + g; r < n_rows; r += gridDim.x * G) {
+    typename F::Raw raw[USED];
+#pragma unroll
+    for (int k = 0; k < USED; k++) raw[k] = F::fetch(W + ((uint64_t)ids[k] * n_rows + r) * rb, unit);
+    float dots[USED];
+#pragma unroll
+    for (int k = 0; k < USED; k++) {
+      typename F::Frag f;
+      F::from_lds(xs + k * per_input + unit * kSlot, f);
+      dots[k] = group_sum<LPR>(active ? F::compute(raw[k], unit, f) : 0.f);
+    }
+    if (li == 0) {
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < USED; k++) acc += wts[k] * dots[k];
+      y[r] += acc;
+    }
+  }
+}
+
+void run_moe_route(hipStream_t s, const float *x, const float *norm_w, float eps, float *normed, const float *router,
+                   const float *bias, uint32_t *route, uint32_t n_cols, uint32_t n_experts, uint32_t n_used,
+                   uint32_t n_tokens) {
+  const size_t lds = (size_t)n_cols * 4;
+  static const bool lds_limit_set =
+      hipFuncSetAttribute(reinterpret_cast<const void *>(k_moe_route), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          131072) == hipSuccess;
+  (void)lds_limit_set;
+  k_moe_route<<<n_tokens, 1024, lds, s>>>(x, norm_w, eps, normed, router, bias, route, n_cols, n_experts, n_used);
+}
+
+template <class F, int LPR>
+static void launch_down(hipStream_t s, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,
+                        const uint32_t *route, uint32_t n_used, float *y, uint32_t n_cus) {
+  constexpr uint32_t kSlot = F::kUnit + (F::kUnit >= 64 ? 4 : 0);
+  const uint64_t rb = bch_row_bytes(F::kFormat, n_cols);
+  const size_t lds = (size_t)n_used * (n_cols / F::kUnit) * kSlot * 4;
+  const uint32_t groups = 256 / LPR;
+  const uint32_t grid = std::max(1u, std::min((n_rows + groups - 1) / groups, 2 * n_cus));
+  switch (n_used) {
+#define BCH_DOWN(U)                                                                                              \
+  case U: {                                                                                                      \
+    static const bool set = hipFuncSetAttribute(reinterpret_cast<const void *>(k_experts_down<F, LPR, U>),     \
+                                                hipFuncAttributeMaxDynamicSharedMemorySize, 163840) == hipSuccess; \
+    (void)set;                                                                                                   \
+    k_experts_down<F, LPR, U><<<grid, 256, lds, s>>>(W, rb, n_rows, n_cols, x, route, y);                        \
+    break;                                                                                                       \
+  }
+    BCH_DOWN(1) BCH_DOWN(2) BCH_DOWN(3) BCH_DOWN(4) BCH_DOWN(5) BCH_DOWN(6) BCH_DOWN(7) BCH_DOWN(8)
+#undef BCH_DOWN
+    default: break;
+  }
+}
+
+template <class F>
+static bool down_for(hipStream_t s, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,
+                     const uint32_t *route, uint32_t n_used, float *y, uint32_t n_cus) {
+  if (n_cols % F::kUnit) return false;
+  const uint32_t n_units = n_cols / F::kUnit;
+  constexpr uint32_t kSlot = F::kUnit + (F::kUnit >= 64 ? 4 : 0);
+  if ((uint64_t)n_used * n_units * kSlot * 4 > 163840) return false;  // the inputs must fit in LDS
+  if (n_units <= 4) launch_down<F, 4>(s, W, n_rows, n_cols, x, route, n_used, y, n_cus);
+  else if (n_units <= 8) launch_down<F, 8>(s, W, n_rows, n_cols, x, route, n_used, y, n_cus);
+  else if (n_units <= 16) launch_down<F, 16>(s, W, n_rows, n_cols, x, route, n_used, y, n_cus);
+  else if (n_units <= 32) launch_down<F, 32>(s, W, n_rows, n_cols, x, route, n_used, y, n_cus);
+  else if (n_units <= 64) launch_down<F, 64>(s, W, n_rows, n_cols, x, route, n_used, y, n_cus);
+  else return false;
+  return true;
+}
+
+bool run_experts_down(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols,
+                      const float *x, const uint32_t *route, uint32_t n_used, float *y, uint32_t n_cus) {
+  if (n_used == 0 || n_used > kMoeMaxUsed) return false;
+  if (format == Q4K::kFormat) return down_for<Q4K>(s, W, n_rows, n_cols, x, route, n_used, y, n_cus);
+  if (format == F16::kFormat) return down_for<F16>(s, W, n_rows, n_cols, x, route, n_used, y, n_cus);
+  if (format == F32::kFormat) return down_for<F32>(s, W, n_rows, n_cols, x, route, n_used, y, n_cus);
+  return false;
+}
+
+}  // namespace bch
+
+// ---------------------------------------------------------------------
+// C ABI (Metal::moe_route / matvec_experts_swiglu / matvec_experts_down /
+// route_bytes, crates/bobcat-metal/src/backend.rs:1428-1597, 2724-2734).
+// ---------------------------------------------------------------------
+
+using namespace bch;
+
+static int check_experts(uint32_t n_experts, uint32_t n_used) {
+  if (n_experts > kMoeMaxExperts || n_used > kMoeMaxUsed || n_used == 0 || n_used > n_experts)
+    return fail(BCH_ERR_EXPERT_LIMITS, "at most %u of %u experts per token, got %u of %u", kMoeMaxUsed,
+                kMoeMaxExperts, n_used, n_experts);
+  return BCH_OK;
+}
+
+static bool expert_format(uint32_t format) {
+  return format == Q4K::kFormat || format == F16::kFormat || format == F32::kFormat;
+}
+
+extern "C" uint64_t bch_route_bytes(uint32_t n_used, uint32_t n_tokens) { return 2ull * n_used * n_tokens * 4; }
+
+extern "C" int bch_moe_route(bch_ctx *ctx, bch_view x, const bch_norm *norm, bch_view normed, bch_view router,
+                             bch_view bias, bch_view route, uint32_t n_cols, uint32_t n_experts, uint32_t n_used,
+                             uint32_t n_tokens) {
+  BCH_TRY(check_experts(n_experts, n_used));
+  if (n_cols == 0 || n_cols % 4 || n_cols > 32768 || n_tokens == 0)
+    return fail(BCH_ERR_ARGUMENT, "moe_route: %u columns (a positive multiple of 4 up to 32768), %u tokens", n_cols,
+                n_tokens);
+  const uint64_t token_bytes = (uint64_t)n_tokens * n_cols * 4;
+  const float *xp, *rp, *bp, *nw = nullptr;
+  float *np = nullptr;
+  uint32_t *route_p;
+  BCH_TRY(view_ptr(ctx, "moe_route", x, token_bytes, &xp));
+  BCH_TRY(view_ptr(ctx, "moe_route", router, (uint64_t)n_experts * n_cols * 4, &rp));
+  BCH_TRY(view_ptr(ctx, "moe_route", bias, (uint64_t)n_experts * 4, &bp));
+  BCH_TRY(view_ptr(ctx, "moe_route", route, bch_route_bytes(n_used, n_tokens), &route_p));
+  if (norm) {
+    BCH_TRY(view_ptr(ctx, "moe_route", norm->weight, (uint64_t)n_cols * 4, &nw));
+    BCH_TRY(view_ptr(ctx, "moe_route", normed, token_bytes, &np));
+  }
+  if (reinterpret_cast<uintptr_t>(rp) % 16)
+    return fail(BCH_ERR_ARGUMENT, "moe_route: the router is not 16-byte aligned");
+  const float eps = norm ? norm->eps : 0.f;
+  return launch(ctx, {"moe_route", n_experts, n_cols, (uint64_t)n_experts * n_cols * 4}, [&](hipStream_t s) {
+    run_moe_route(s, xp, nw, eps, np, rp, bp, route_p, n_cols, n_experts, n_used, n_tokens);
+  });
+}
+
+extern "C" int bch_matvec_experts_swiglu(bch_ctx *ctx, uint32_t format, bch_view gate, bch_view up, uint32_t n_rows,
+                                         uint32_t n_cols, uint32_t n_experts, bch_view x, bch_view route,
+                                         uint32_t n_used, bch_view y, uint32_t n_tokens) {
+  if (!expert_format(format))
+    return fail(BCH_ERR_UNSUPPORTED_FORMAT, "format %u has no expert kernels", format);
+  BCH_TRY(check_experts(n_experts, n_used));
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  if (rb == 0 || n_rows == 0 || n_tokens == 0)
+    return fail(BCH_ERR_ARGUMENT, "matvec_experts_swiglu: %u x %u of format %u", n_rows, n_cols, format);
+  const uint8_t *gp, *up_p;
+  const float *xp;
+  const uint32_t *rp;
+  float *yp;
+  const uint64_t stacked = rb * n_rows * n_experts;
+  BCH_TRY(view_ptr(ctx, "matvec_experts_swiglu", gate, stacked, &gp));
+  BCH_TRY(view_ptr(ctx, "matvec_experts_swiglu", up, stacked, &up_p));
+  BCH_TRY(view_ptr(ctx, "matvec_experts_swiglu", x, (uint64_t)n_tokens * n_cols * 4, &xp));
+  BCH_TRY(view_ptr(ctx, "matvec_experts_swiglu", route, bch_route_bytes(n_used, n_tokens), &rp));
+  BCH_TRY(view_ptr(ctx, "matvec_experts_swiglu", y, (uint64_t)n_tokens * n_used * n_rows * 4, &yp));
+  if (reinterpret_cast<uintptr_t>(gp) % 16 || reinterpret_cast<uintptr_t>(up_p) % 16 ||
+      reinterpret_cast<uintptr_t>(xp) % 16)
+    return fail(BCH_ERR_ARGUMENT, "matvec_experts_swiglu: operands must be 16-byte aligned");
+  bool ok = true;
+  BCH_TRY(launch(ctx, {"matvec_experts_swiglu", n_rows, n_cols, 2 * rb * n_rows * n_used}, [&](hipStream_t s) {
+    for (uint32_t t = 0; t < n_tokens && ok; t++)
+      ok = fast_matvec_experts_swiglu(s, format, gp, up_p, n_rows, n_cols, rp + (uint64_t)t * 2 * n_used, n_used,
+                                      xp + (uint64_t)t * n_cols, yp + (uint64_t)t * n_used * n_rows, ctx->n_cus);
+  }));
+  if (!ok) return fail(BCH_ERR_UNSUPPORTED_FORMAT, "matvec_experts_swiglu: rows of %u columns are too wide", n_cols);
+  return BCH_OK;
+}
+
+extern "C" int bch_matvec_experts_down(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_rows,
+                                       uint32_t n_cols, uint32_t n_experts, bch_view x, bch_view route,
+                                       uint32_t n_used, bch_view y, uint32_t n_tokens) {
+  if (!expert_format(format))
+    return fail(BCH_ERR_UNSUPPORTED_FORMAT, "format %u has no expert kernels", format);
+  BCH_TRY(check_experts(n_experts, n_used));
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  if (rb == 0 || n_rows == 0 || n_tokens == 0)
+    return fail(BCH_ERR_ARGUMENT, "matvec_experts_down: %u x %u of format %u", n_rows, n_cols, format);
+  const uint8_t *wp;
+  const float *xp;
+  const uint32_t *rp;
+  float *yp;
+  BCH_TRY(view_ptr(ctx, "matvec_experts_down", weights, rb * n_rows * n_experts, &wp));
+  BCH_TRY(view_ptr(ctx, "matvec_experts_down", x, (uint64_t)n_tokens * n_used * n_cols * 4, &xp));
+  BCH_TRY(view_ptr(ctx, "matvec_experts_down", route, bch_route_bytes(n_used, n_tokens), &rp));
+  BCH_TRY(view_ptr(ctx, "matvec_experts_down", y, (uint64_t)n_tokens * n_rows * 4, &yp));
+  if (reinterpret_cast<uintptr_t>(wp) % 16 || reinterpret_cast<uintptr_t>(xp) % 16)
+    return fail(BCH_ERR_ARGUMENT, "matvec_experts_down: operands must be 16-byte aligned");
+  bool ok = true;
+  BCH_TRY(launch(ctx, {"matvec_experts_down", n_rows, n_cols, rb * n_rows * n_used}, [&](hipStream_t s) {
+    for (uint32_t t = 0; t < n_tokens && ok; t++)
+      ok = run_experts_down(s, format, wp, n_rows, n_cols, xp + (uint64_t)t * n_used * n_cols,
+                            rp + (uint64_t)t * 2 * n_used, n_used, yp + (uint64_t)t * n_rows, ctx->n_cus);
+  }));
+  if (!ok) return fail(BCH_ERR_UNSUPPORTED_FORMAT, "matvec_experts_down: rows of %u columns are too wide", n_cols);
+  return BCH_OK;
+}

@@ -36,6 +36,15 @@ class Lfm2Config:
     norm_eps: float = 1e-5
     embd_format: int = Format.Q4K
     layer_format: int = Format.Q4K
+    # Mixture of experts (lfm2.rs:17-49): layers from n_dense_layers on use
+    # n_experts experts of width n_ff_expert, n_experts_used per token.
+    n_experts: int = 0
+    n_experts_used: int = 0
+    n_ff_expert: int = 0
+    n_dense_layers: int = 0
+
+    def is_moe(self, il: int) -> bool:
+        return self.n_experts > 0 and il >= self.n_dense_layers
 
     @property
     def hp(self) -> dict:
@@ -53,7 +62,11 @@ class Lfm2Config:
                 layers += (q + 2 * kv) * rb(self.layer_format, n) + n * rb(self.layer_format, q)
             else:
                 layers += 3 * n * rb(self.layer_format, n) + n * rb(self.layer_format, n)
-            layers += 2 * self.n_ff * rb(self.layer_format, n) + n * rb(self.layer_format, self.n_ff)
+            if self.is_moe(il):  # the router (F32) and the picked experts
+                layers += self.n_experts * n * 4 + self.n_experts_used * (
+                    2 * self.n_ff_expert * rb(self.layer_format, n) + n * rb(self.layer_format, self.n_ff_expert))
+            else:
+                layers += 2 * self.n_ff * rb(self.layer_format, n) + n * rb(self.layer_format, self.n_ff)
         output = self.n_vocab * rb(self.embd_format, n)
         return dict(layers=layers, output=output, total=layers + output)
 
@@ -71,7 +84,15 @@ LFM2_TINY = Lfm2Config("lfm2-tiny", n_embd=256, n_ff=512, n_heads=4, n_kv_heads=
                        attention_layers=[1, 3], n_layers=4)
 LFM2_TINY_F16 = Lfm2Config("lfm2-tiny-f16", n_embd=256, n_ff=768, n_heads=4, n_kv_heads=1, n_vocab=777,
                            attention_layers=[0, 2], n_layers=3, embd_format=Format.F16)
-CONFIGS = {c.name: c for c in (LFM2_350M, LFM2_2_6B, LFM2_TINY, LFM2_TINY_F16)}
+# LFM2-style 8B-A1B (18 conv + 6 GQA layers; the
+# first 2 layers dense, the rest 32 experts, top 4, expert width 1792).
+LFM2_8B_A1B = Lfm2Config("lfm2-8b-a1b", n_embd=2048, n_ff=7168, n_heads=32, n_kv_heads=8, n_vocab=65536,
+                         attention_layers=[2, 6, 10, 14, 18, 21], n_layers=24, n_experts=32, n_experts_used=4,
+                         n_ff_expert=1792, n_dense_layers=2)
+LFM2_TINY_MOE = Lfm2Config("lfm2-tiny-moe", n_embd=256, n_ff=512, n_heads=4, n_kv_heads=2, n_vocab=1000,
+                           attention_layers=[1, 3], n_layers=4, n_experts=8, n_experts_used=2, n_ff_expert=256,
+                           n_dense_layers=1)
+CONFIGS = {c.name: c for c in (LFM2_350M, LFM2_2_6B, LFM2_TINY, LFM2_TINY_F16, LFM2_8B_A1B, LFM2_TINY_MOE)}
 
 
 def _matrix(fmt: int, rows: int, cols: int, rng: np.random.Generator) -> np.ndarray:
@@ -121,13 +142,26 @@ class Lfm2Weights:
                 L.out_proj = mat(f"{il}.out_proj", lf, n, n)
                 a[f"{il}.taps"] = rng.uniform(-0.5, 0.5, n * cfg.conv_kernel).astype(np.float32)
                 L.conv_taps = fp(a[f"{il}.taps"])
-            L.gate = mat(f"{il}.gate", lf, cfg.n_ff, n)
-            L.up = mat(f"{il}.up", lf, cfg.n_ff, n)
-            L.down = mat(f"{il}.down", lf, n, cfg.n_ff)
+            if cfg.is_moe(il):
+                L.is_moe = 1
+                ne, nff = cfg.n_experts, cfg.n_ff_expert
+                # Router logits ~N(0, 1) on a normalised token.
+                a[f"{il}.router"] = (rng.standard_normal(ne * n) / np.sqrt(n)).astype(np.float32)
+                L.router = Matrix(int(Format.F32), ne, n, a[f"{il}.router"].ctypes.data)
+                a[f"{il}.expert_bias"] = rng.uniform(-0.05, 0.05, ne).astype(np.float32)
+                L.expert_bias = fp(a[f"{il}.expert_bias"])
+                L.gate_exps = mat(f"{il}.gate_exps", lf, ne * nff, n)
+                L.up_exps = mat(f"{il}.up_exps", lf, ne * nff, n)
+                L.down_exps = mat(f"{il}.down_exps", lf, ne * n, nff)
+            else:
+                L.gate = mat(f"{il}.gate", lf, cfg.n_ff, n)
+                L.up = mat(f"{il}.up", lf, cfg.n_ff, n)
+                L.down = mat(f"{il}.down", lf, n, cfg.n_ff)
         embd = mat("token_embd", cfg.embd_format, cfg.n_vocab, n)
         a["output_norm"] = vec(n, 0.1)
         self.c_model = Lfm2Model(
-            n_layers=cfg.n_layers, n_embd=n, n_ff=cfg.n_ff, n_experts=0, n_experts_used=0, n_ff_expert=0,
+            n_layers=cfg.n_layers, n_embd=n, n_ff=cfg.n_ff, n_experts=cfg.n_experts,
+            n_experts_used=cfg.n_experts_used, n_ff_expert=cfg.n_ff_expert,
             n_heads=cfg.n_heads, n_kv_heads=cfg.n_kv_heads, head_dim=cfg.head_dim, n_vocab=cfg.n_vocab,
             conv_kernel=cfg.conv_kernel, rope_theta=cfg.rope_theta, norm_eps=cfg.norm_eps,
             layers=self._layers, token_embd=embd, output=embd, output_norm=fp(a["output_norm"]))

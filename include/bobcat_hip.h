@@ -224,6 +224,33 @@ int bch_argmax(bch_ctx *ctx, bch_view x, bch_view out, uint32_t n);
 int bch_read_sum(bch_ctx *ctx, bch_view src, uint64_t n_vectors, bch_view out, uint32_t n_threads);
 
 /* ------------------------------------------------------------------ */
+/* Mixture of experts.  A route holds, per token, the n_used expert ids */
+/* the router picked, then their n_used weights as float bits          */
+/* (moe.metal:1-6).  Limits: n_experts <= 128, 1 <= n_used <= 8        */
+/* (backend.rs:2728-2734).  Expert matrices stack the experts by rows. */
+/* ------------------------------------------------------------------ */
+
+/* route_bytes (backend.rs:2724-2726): 2 * n_used * n_tokens * 4. */
+uint64_t bch_route_bytes(uint32_t n_used, uint32_t n_tokens);
+/* Metal::moe_route (backend.rs:1428-1479): sigmoid scores of the F32
+ * router [n_experts x n_cols], top n_used by score + bias (ties to the
+ * lower expert), weights = score / (sum of picked scores + 1e-6).  With
+ * `norm` (nullable), each token is first RMS-normalised into `normed`. */
+int bch_moe_route(bch_ctx *ctx, bch_view x, const bch_norm *norm, bch_view normed, bch_view router,
+                  bch_view bias, bch_view route, uint32_t n_cols, uint32_t n_experts, uint32_t n_used,
+                  uint32_t n_tokens);
+/* Metal::matvec_experts_swiglu (backend.rs:1481-1536): row n_used·t + s of
+ * y [n_rows floats] = silu(G_e·x_t) ⊙ U_e·x_t for the expert e in slot s. */
+int bch_matvec_experts_swiglu(bch_ctx *ctx, uint32_t format, bch_view gate, bch_view up, uint32_t n_rows,
+                              uint32_t n_cols, uint32_t n_experts, bch_view x, bch_view route, uint32_t n_used,
+                              bch_view y, uint32_t n_tokens);
+/* Metal::matvec_experts_down (backend.rs:1538-1597): y_t += Σ_s w_s ·
+ * D_e·x_{n_used·t+s}, the experts added in route order. */
+int bch_matvec_experts_down(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_rows, uint32_t n_cols,
+                            uint32_t n_experts, bch_view x, bch_view route, uint32_t n_used, bch_view y,
+                            uint32_t n_tokens);
+
+/* ------------------------------------------------------------------ */
 /* LFM2 driver (crates/bobcat/src/lfm2_metal.rs:125-779)               */
 /* ------------------------------------------------------------------ */
 

@@ -19,7 +19,7 @@ import pytest
 
 import oracle
 from bobcat_amd import BobcatError
-from bobcat_amd.lfm2 import LFM2_TINY, LFM2_TINY_F16, Lfm2Hip, Lfm2Weights
+from bobcat_amd.lfm2 import LFM2_TINY, LFM2_TINY_F16, LFM2_TINY_MOE, Lfm2Hip, Lfm2Weights
 
 pytestmark = pytest.mark.gpu
 
@@ -35,7 +35,7 @@ def rel(got, want):
     return float(d.max() / max(np.abs(want).max(), 1e-30))
 
 
-@pytest.fixture(scope="module", params=[LFM2_TINY, LFM2_TINY_F16], ids=lambda c: c.name)
+@pytest.fixture(scope="module", params=[LFM2_TINY, LFM2_TINY_F16, LFM2_TINY_MOE], ids=lambda c: c.name)
 def weights(request):
     return Lfm2Weights(request.param, seed=7)
 

@@ -1,5 +1,6 @@
 """Pins the oracle's LFM2 forward pass (orc_lfm2_step, restating lfm2.rs:308-560)
-against an independent implementation: transformers' Lfm2ForCausalLM, the
+against an independent implementation: transformers' Lfm2ForCausalLM (and
+Lfm2MoeForCausalLM for the mixture-of-experts block, lfm2.rs:413-440, 691-709), the
 same model code the reference's own model tests were generated from
 (tools/ref_dump.py, lfm2_reference.rs:1-7).
 
@@ -15,7 +16,7 @@ import numpy as np
 import pytest
 
 import oracle
-from bobcat_amd.lfm2 import LFM2_TINY, LFM2_TINY_F16, Lfm2Weights
+from bobcat_amd.lfm2 import LFM2_TINY, LFM2_TINY_F16, LFM2_TINY_MOE, Lfm2Weights
 
 torch = pytest.importorskip("torch")
 transformers = pytest.importorskip("transformers")
@@ -27,18 +28,27 @@ def rel(got, want):
 
 
 def hf_model(w: Lfm2Weights):
-    from transformers import Lfm2Config, Lfm2ForCausalLM
+    from transformers import Lfm2Config, Lfm2ForCausalLM, Lfm2MoeConfig, Lfm2MoeForCausalLM
 
     cfg = w.cfg
-    hc = Lfm2Config(
+    moe = cfg.n_experts > 0
+    # The MoE model (Lfm2MoeForCausalLM) is the one transformers implements the
+    # LFM2-MoE router in: sigmoid scores, top-k of score + expert_bias,
+    # weights normalised over the picks (+1e-6), scaling factor 1.
+    config_cls, model_cls = (Lfm2MoeConfig, Lfm2MoeForCausalLM) if moe else (Lfm2Config, Lfm2ForCausalLM)
+    extra = dict(moe_intermediate_size=cfg.n_ff_expert, num_experts=cfg.n_experts,
+                 num_experts_per_tok=cfg.n_experts_used, num_dense_layers=cfg.n_dense_layers,
+                 norm_topk_prob=True, routed_scaling_factor=1.0, use_expert_bias=True) if moe else \
+        dict(block_auto_adjust_ff_dim=False)
+    hc = config_cls(
         vocab_size=cfg.n_vocab, hidden_size=cfg.n_embd, intermediate_size=cfg.n_ff,
         num_hidden_layers=cfg.n_layers, num_attention_heads=cfg.n_heads,
         num_key_value_heads=cfg.n_kv_heads, max_position_embeddings=4096, norm_eps=cfg.norm_eps,
-        conv_L_cache=cfg.conv_kernel, conv_bias=False, block_auto_adjust_ff_dim=False,
+        conv_L_cache=cfg.conv_kernel, conv_bias=False,
         layer_types=["full_attention" if i in cfg.attention_layers else "conv" for i in range(cfg.n_layers)],
-        rope_parameters={"rope_type": "default", "rope_theta": cfg.rope_theta}, tie_word_embeddings=True)
+        rope_parameters={"rope_type": "default", "rope_theta": cfg.rope_theta}, tie_word_embeddings=True, **extra)
     hc._attn_implementation = "eager"
-    model = Lfm2ForCausalLM(hc).float().eval()
+    model = model_cls(hc).float().eval()
     n = cfg.n_embd
     a = w.arrays
 
@@ -63,9 +73,18 @@ def hf_model(w: Lfm2Weights):
             sd[p + "conv.in_proj.weight"] = deq(f"{il}.in_proj", lf, 3 * n, n)
             sd[p + "conv.out_proj.weight"] = deq(f"{il}.out_proj", lf, n, n)
             sd[p + "conv.conv.weight"] = torch.from_numpy(a[f"{il}.taps"].reshape(n, 1, cfg.conv_kernel))
-        sd[p + "feed_forward.w1.weight"] = deq(f"{il}.gate", lf, cfg.n_ff, n)
-        sd[p + "feed_forward.w3.weight"] = deq(f"{il}.up", lf, cfg.n_ff, n)
-        sd[p + "feed_forward.w2.weight"] = deq(f"{il}.down", lf, n, cfg.n_ff)
+        if cfg.is_moe(il):
+            ne, nff = cfg.n_experts, cfg.n_ff_expert
+            gate = deq(f"{il}.gate_exps", lf, ne * nff, n).reshape(ne, nff, n)
+            up = deq(f"{il}.up_exps", lf, ne * nff, n).reshape(ne, nff, n)
+            sd[p + "feed_forward.experts.gate_up_proj"] = torch.cat([gate, up], dim=1)
+            sd[p + "feed_forward.experts.down_proj"] = deq(f"{il}.down_exps", lf, ne * n, nff).reshape(ne, n, nff)
+            sd[p + "feed_forward.gate.weight"] = torch.from_numpy(a[f"{il}.router"].reshape(ne, n))
+            sd[p + "feed_forward.expert_bias"] = torch.from_numpy(a[f"{il}.expert_bias"])
+        else:
+            sd[p + "feed_forward.w1.weight"] = deq(f"{il}.gate", lf, cfg.n_ff, n)
+            sd[p + "feed_forward.w3.weight"] = deq(f"{il}.up", lf, cfg.n_ff, n)
+            sd[p + "feed_forward.w2.weight"] = deq(f"{il}.down", lf, n, cfg.n_ff)
     emb = deq("token_embd", cfg.embd_format, cfg.n_vocab, n)
     sd["model.embed_tokens.weight"] = emb
     sd["lm_head.weight"] = emb
@@ -76,7 +95,7 @@ def hf_model(w: Lfm2Weights):
     return model
 
 
-@pytest.mark.parametrize("cfg", [LFM2_TINY, LFM2_TINY_F16], ids=lambda c: c.name)
+@pytest.mark.parametrize("cfg", [LFM2_TINY, LFM2_TINY_F16, LFM2_TINY_MOE], ids=lambda c: c.name)
 def test_oracle_step_matches_transformers(cfg):
     w = Lfm2Weights(cfg, seed=3)
     model = hf_model(w)
