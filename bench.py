@@ -90,10 +90,13 @@ def gemv_leg(hip, reps: int, copies: int = 64):
     # GEMV is compared with, as the reference's read_sum probe does):
     # read_sum reads all of `big` READ_REPS times; copy moves COPY_BYTES.
     sums = hip.new_buffer(READ_THREADS * 4)
+    hip.set_profiling(True)  # per-launch event timing: no host time in the figure
     hip.begin()
     for _ in range(READ_REPS):
         hip.read_sum(big.at(0), big_bytes // 16, sums.at(0), READ_THREADS)
-    read_s = hip.end() / READ_REPS
+    hip.end()
+    read_s = sum(e["seconds"] for e in hip.profile()) / READ_REPS
+    hip.set_profiling(False)
     dst = hip.new_buffer(COPY_BYTES)
     hip.begin()
     hip.copy(big.at(0), dst.at(0), COPY_BYTES // 4)
