@@ -33,6 +33,11 @@ class View(C.Structure):
     _fields_ = [("buffer", C.c_void_p), ("offset", C.c_uint64)]
 
 
+class Sampling(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float), ("min_p", C.c_float),
+                ("repeat_penalty", C.c_float)]
+
+
 class Norm(C.Structure):
     _fields_ = [("weight", View), ("eps", C.c_float)]
 
@@ -118,6 +123,8 @@ PROTOTYPES = {
     "bch_argmax": (_int, [_vp, View, View, _u32]),
     "bch_read_sum": (_int, [_vp, View, _u64, View, _u32]),
     "bch_route_bytes": (_u64, [_u32, _u32]),
+    "bch_sample": (_int, [_vp, View, _u32, View, _u32, C.POINTER(Sampling), View, View]),
+    "bch_lfm2_generate_sampled": (_int, [_vp, C.POINTER(C.c_uint32), _u32, C.POINTER(Sampling), _u64]),
     "bch_moe_route": (_int, [_vp, View, C.POINTER(Norm), View, View, View, View, _u32, _u32, _u32, _u32]),
     "bch_matvec_experts_swiglu": (_int, [_vp, _u32, View, View, _u32, _u32, _u32, View, View, _u32, View, _u32]),
     "bch_matvec_experts_down": (_int, [_vp, _u32, View, _u32, _u32, _u32, View, View, _u32, View, _u32]),

@@ -260,6 +260,10 @@ class Hip:
         check(lib().bch_matvec_experts_down(self.handle, int(fmt), _view(weights), n_rows, n_cols, n_experts,
                                             _view(x), _view(route), n_used, _view(y), n_tokens))
 
+    def sample(self, logits, n_vocab, recent, n_recent, settings, rng_state, out):
+        check(lib().bch_sample(self.handle, _view(logits), n_vocab, _view(recent), n_recent, C.byref(settings),
+                               _view(rng_state), _view(out)))
+
     def argmax(self, x, out, n):
         check(lib().bch_argmax(self.handle, _view(x), _view(out), n))
 

@@ -87,6 +87,23 @@ bool fast_matvec_experts_swiglu(hipStream_t s, uint32_t format, const uint8_t *W
 bool run_experts_down(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols,
                       const float *x, const uint32_t *route, uint32_t n_used, float *y, uint32_t n_cus);
 
+// sample.hip: Sampler::sample on the GPU.  With dpos, the recent tokens
+// are recent[0..*dpos] and the token goes to out[*dpos + 1], advancing
+// *dpos; otherwise recent holds n_recent tokens and the token goes to out[0].
+constexpr uint32_t kMaxCandidates = 4096;  // candidates kept after top-k, at most
+struct SampleArgs {
+  float *logits;  // penalised in place
+  uint32_t n;
+  const uint32_t *recent;
+  uint32_t n_recent;
+  uint32_t *dpos;
+  uint32_t *out;
+  uint64_t *rng;  // wyrand state
+  float temperature, top_p, min_p, penalty;
+  uint32_t top_k;
+};
+void run_sample(hipStream_t s, const SampleArgs &a);
+
 // ops.hip
 // argmax of n logits as partials[0] (an argmax key), with partials[1..n_partials) zeroed.
 void run_argmax_partials(hipStream_t s, const float *logits, uint32_t n, uint64_t *partials, uint32_t n_partials);

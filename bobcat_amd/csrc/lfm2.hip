@@ -75,6 +75,9 @@ struct bch_lfm2 {
   uint32_t *counters = nullptr, *tokens = nullptr, *dpos = nullptr, *greedy = nullptr;
   uint32_t *route = nullptr;  // expert routes of a batch (route_bytes(n_used, batch))
   uint64_t *argmax_partials = nullptr;  // kArgmaxPartials argmax keys of the logits
+  uint64_t *rng = nullptr;              // sampler state
+  uint64_t rng_host = 0;
+  bch_sampling sample_settings{};       // the settings sample_graph was captured with
   std::vector<void *> allocations;
   // Sequence state.
   uint32_t n_ctx = 0, n_past = 0, batch = 0;
@@ -82,7 +85,7 @@ struct bch_lfm2 {
   bool kv_half = true;
   bool have_logits = false;
   uint32_t decode_splits = 1, prefill_splits = 1;
-  hipGraphExec_t step_graph = nullptr, gen_graph = nullptr;
+  hipGraphExec_t step_graph = nullptr, gen_graph = nullptr, sample_graph = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   double last_gpu_seconds = 0.0;
   // Host staging of the small asynchronous uploads (they must outlive the call).
@@ -564,7 +567,8 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
            (rc = dev_alloc_t(m, (uint64_t)kAttnQueryBatch * std::max(1u, m->n_kv_heads), &m->counters)) ||
            (rc = dev_alloc_t(m, (uint64_t)n_ctx + 2, &m->tokens)) || (rc = dev_alloc_t(m, 4, &m->dpos)) ||
            (rc = dev_alloc_t(m, 4, &m->greedy)) || (rc = dev_alloc_t(m, kArgmaxPartials, &m->argmax_partials)) ||
-           (rc = dev_alloc_t(m, 2 * (uint64_t)std::max(1u, m->n_used) * rows, &m->route)));
+           (rc = dev_alloc_t(m, 2 * (uint64_t)std::max(1u, m->n_used) * rows, &m->route)) ||
+           (rc = dev_alloc_t(m, 1, &m->rng)));
     if (rc) return cleanup(rc);
   }
   hipEventCreate(&m->ev0);
@@ -579,6 +583,7 @@ void bch_lfm2_free(bch_lfm2 *m) {
   if (m->s) hipStreamSynchronize(m->s);
   if (m->step_graph) hipGraphExecDestroy(m->step_graph);
   if (m->gen_graph) hipGraphExecDestroy(m->gen_graph);
+  if (m->sample_graph) hipGraphExecDestroy(m->sample_graph);
   if (m->ev0) hipEventDestroy(m->ev0);
   if (m->ev1) hipEventDestroy(m->ev1);
   for (void *p : m->allocations) hipFree(p);
@@ -709,6 +714,66 @@ int bch_lfm2_generate(bch_lfm2 *m, uint32_t *out, uint32_t n) {
     for (uint32_t i = 0; i < n; i++) BCH_TRY(check_hip(hipGraphLaunch(m->gen_graph, m->s), "launch decode graph"));
   } else {
     for (uint32_t i = 0; i < n; i++) record_step(m, m->s, true, false);
+  }
+  BCH_TRY(finish(m));
+  BCH_TRY(check_hip(hipMemcpy(out, m->tokens + m->n_past, (uint64_t)n * 4, hipMemcpyDeviceToHost), "read tokens"));
+  m->n_past += n;
+  return BCH_OK;
+}
+
+static SampleArgs sample_args(bch_lfm2 *m, const bch_sampling &st) {
+  SampleArgs a{};
+  a.logits = m->logits;
+  a.n = m->n_vocab;
+  a.recent = m->tokens;
+  a.dpos = m->dpos;
+  a.out = m->tokens;
+  a.rng = m->rng;
+  a.temperature = st.temperature;
+  a.top_p = st.top_p;
+  a.min_p = st.min_p;
+  a.penalty = st.repeat_penalty;
+  a.top_k = st.top_k;
+  return a;
+}
+
+int bch_lfm2_generate_sampled(bch_lfm2 *m, uint32_t *out, uint32_t n, const bch_sampling *settings, uint64_t seed) {
+  BCH_TRY(busy_check(m));
+  if (!settings) return fail(BCH_ERR_ARGUMENT, "no sampling settings");
+  if (m->n_past == 0 || !m->have_logits) return fail(BCH_ERR_ARGUMENT, "generation needs a prompt first");
+  if (n > m->n_ctx - m->n_past)
+    return fail(BCH_ERR_CONTEXT_FULL, "%u tokens exceed the %u free positions", n, m->n_ctx - m->n_past);
+  if (n == 0) return BCH_OK;
+  // Each replay samples the current logits into tokens[dpos + 1], advances
+  // dpos and runs the step there; the settings are captured into the graph.
+  BCH_TRY(set_dpos(m, m->n_past - 1));
+  m->rng_host = seed;
+  BCH_TRY(check_hip(hipMemcpyAsync(m->rng, &m->rng_host, 8, hipMemcpyHostToDevice, m->s), "seed the sampler"));
+  const SampleArgs sa = sample_args(m, *settings);
+  hipEventRecord(m->ev0, m->s);
+  if (use_graphs()) {
+    if (m->sample_graph && memcmp(&m->sample_settings, settings, sizeof(bch_sampling)) != 0) {
+      hipGraphExecDestroy(m->sample_graph);
+      m->sample_graph = nullptr;
+    }
+    if (!m->sample_graph) {
+      hipStream_t s = m->s;
+      BCH_TRY(check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture"));
+      run_sample(s, sa);
+      record_step(m, s, false, false);
+      hipGraph_t g;
+      BCH_TRY(check_hip(hipStreamEndCapture(s, &g), "end capture"));
+      hipError_t e = hipGraphInstantiate(&m->sample_graph, g, nullptr, nullptr, 0);
+      hipGraphDestroy(g);
+      BCH_TRY(check_hip(e, "instantiate graph"));
+      m->sample_settings = *settings;
+    }
+    for (uint32_t i = 0; i < n; i++) BCH_TRY(check_hip(hipGraphLaunch(m->sample_graph, m->s), "launch sampling graph"));
+  } else {
+    for (uint32_t i = 0; i < n; i++) {
+      run_sample(m->s, sa);
+      record_step(m, m->s, false, false);
+    }
   }
   BCH_TRY(finish(m));
   BCH_TRY(check_hip(hipMemcpy(out, m->tokens + m->n_past, (uint64_t)n * 4, hipMemcpyDeviceToHost), "read tokens"));

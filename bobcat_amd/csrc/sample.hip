@@ -1,0 +1,316 @@
+// Token sampling on the GPU: the CLI's Sampler::sample
+// (crates/bobcat-cli/src/sampler.rs:45-112) as one workgroup, so that a
+// non-greedy decode also stays inside the captured graph.
+//
+// Steps, in the reference's (llama.cpp's) order:
+//   1. repetition penalty on each distinct token of the last 64, in place;
+//   2. temperature <= 0: argmax (ties to the lowest id);
+//   3. top-k: a radix select finds the k-th largest logit and a scan-based
+//      compaction keeps the k candidates (ties at the threshold by lowest
+//      id), at most kMaxCandidates of them;
+//   4. the candidates are sorted by logit (bitonic sort in LDS), then
+//      softmax at temperature 1, the top-p prefix, the min-p floor, log and
+//      softmax at the temperature, and a draw walking the sorted candidates.
+// The draw comes from a wyrand generator whose 64-bit state lives in device
+// memory, so graph replays continue the stream.  Sums run as tree
+// reductions/scans instead of the reference's sequential loops, so draws
+// that land within rounding of a candidate boundary may differ.
+#include <cmath>
+
+#include "device.h"
+#include "kernels.h"
+#include "runtime.h"
+
+namespace bch {
+
+constexpr uint32_t kSampleThreads = 1024;
+constexpr uint32_t kRepeatLastN = 64;  // REPEAT_LAST_N (sampler.rs:8-9)
+
+__device__ __forceinline__ uint32_t ord_key(float v) {
+  uint32_t b = __float_as_uint(v);
+  if (b == 0x80000000u) b = 0;  // -0 ties +0
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// wyrand, the generator of fastrand 2 (the reference's Rng): state += c0;
+// the 128-bit product state * (state ^ c1) folded to 64 bits.
+__device__ __forceinline__ uint64_t wyrand(uint64_t *state) {
+  const uint64_t s = *state + 0x2d358dccaa6c78a5ull;
+  *state = s;
+  const uint64_t t = s ^ 0x8bb84b93962eacc9ull;
+  const uint64_t lo = s * t, hi = __umul64hi(s, t);
+  return lo ^ hi;
+}
+
+// fastrand's f32 in [0, 1): 23 high bits of a 32-bit draw as the mantissa of
+// a float in [1, 2), minus one.
+__device__ __forceinline__ float wyrand_f32(uint64_t *state) {
+  const uint32_t u = (uint32_t)wyrand(state);
+  return __uint_as_float(0x3f800000u | (u >> 9)) - 1.0f;
+}
+
+// Exclusive prefix sum of one value per thread over the workgroup; `total`
+// receives the sum.  Uses shuffles within a wave and LDS across waves.
+template <class T>
+__device__ T block_scan(T v, T *lds16, T *total) {
+  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  T incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const T o = __shfl_up(incl, off, 64);
+    if (lane >= (uint32_t)off) incl += o;
+  }
+  if (lane == 63) lds16[wave] = incl;
+  __syncthreads();
+  T base = 0, sum = 0;
+  for (uint32_t w = 0; w < kSampleThreads / 64; w++) {
+    if (w < wave) base += lds16[w];
+    sum += lds16[w];
+  }
+  __syncthreads();
+  *total = sum;
+  return base + incl - v;
+}
+
+__global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
+  __shared__ float cval[kMaxCandidates];
+  __shared__ uint32_t cidx[kMaxCandidates];
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t u16[16];
+  __shared__ float f16s[16];
+  __shared__ uint64_t k16[16];
+  __shared__ uint32_t prefix_s, remain_s, keep_s, token_s;
+  const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const uint32_t n = a.n;
+  float *logits = a.logits;
+  const uint32_t p = a.dpos ? *a.dpos : 0u;
+
+  // 1. Repetition penalty: each distinct recent token once (sampler.rs:48-64).
+  if (fabsf(a.penalty - 1.0f) > 1.1920929e-7f) {
+    const uint32_t n_recent = a.dpos ? p + 1 : a.n_recent;
+    const uint32_t start = n_recent > kRepeatLastN ? n_recent - kRepeatLastN : 0;
+    if (tid < n_recent - start) {
+      const uint32_t tok = a.recent[start + tid];
+      bool first = true;
+      for (uint32_t j = start; j < start + tid; j++) first &= a.recent[j] != tok;
+      if (first && tok < n) {
+        const float l = logits[tok];
+        logits[tok] = l > 0.f ? l / a.penalty : l * a.penalty;
+      }
+    }
+    __syncthreads();
+  }
+
+  // 2. Greedy.
+  if (a.temperature <= 0.f) {
+    uint64_t best = 0;
+    for (uint32_t i = tid; i < n; i += kSampleThreads) {
+      const uint64_t k = ((uint64_t)ord_key(logits[i]) << 32) | (uint64_t)(0xffffffffu - i);
+      best = best > k ? best : k;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const uint64_t o = ((uint64_t)__shfl_xor((uint32_t)(best >> 32), off, 64) << 32) |
+                         (uint64_t)__shfl_xor((uint32_t)best, off, 64);
+      best = best > o ? best : o;
+    }
+    if (lane == 0) k16[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+      for (int w = 1; w < 16; w++) best = best > k16[w] ? best : k16[w];
+      token_s = 0xffffffffu - (uint32_t)best;
+    }
+    __syncthreads();
+  } else {
+    // 3. Candidates: the kc largest logits (radix select of the kc-th).
+    const uint32_t k = (a.top_k > 0 && a.top_k < n) ? a.top_k : n;
+    const uint32_t kc = k < kMaxCandidates ? k : kMaxCandidates;
+    uint32_t prefix = 0, need = kc;  // the threshold's key bits so far, and how many of its bucket to take
+    if (kc < n) {
+      for (int shift = 24; shift >= 0; shift -= 8) {
+        for (uint32_t i = tid; i < 256; i += kSampleThreads) hist[i] = 0;
+        __syncthreads();
+        const uint32_t hi_mask = shift == 24 ? 0u : ~0u << (shift + 8);
+        for (uint32_t i = tid; i < n; i += kSampleThreads) {
+          const uint32_t key = ord_key(logits[i]);
+          if ((key & hi_mask) == (prefix & hi_mask)) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid == 0) {
+          uint32_t acc = 0, bin = 255;
+          for (int b = 255; b >= 0; b--) {
+            if (acc + hist[b] >= need) {
+              bin = (uint32_t)b;
+              break;
+            }
+            acc += hist[b];
+          }
+          prefix_s = prefix | (bin << shift);
+          remain_s = need - acc;
+        }
+        __syncthreads();
+        prefix = prefix_s;
+        need = remain_s;
+      }
+    }
+    // Deterministic compaction: thread t scans a contiguous range; keys above
+    // the threshold all go in, ties by lowest id until kc are in.
+    const uint32_t per = (n + kSampleThreads - 1) / kSampleThreads;
+    const uint32_t lo = tid * per, hi = min(n, lo + per);
+    uint32_t n_gt = 0, n_eq = 0;
+    if (kc < n) {
+      for (uint32_t i = lo; i < hi; i++) {
+        const uint32_t key = ord_key(logits[i]);
+        n_gt += key > prefix;
+        n_eq += key == prefix;
+      }
+    } else {
+      n_gt = hi > lo ? hi - lo : 0;
+    }
+    uint32_t tot_gt, tot_eq;
+    const uint32_t base_gt = block_scan<uint32_t>(n_gt, u16, &tot_gt);
+    const uint32_t base_eq = block_scan<uint32_t>(n_eq, u16, &tot_eq);
+    {
+      uint32_t g = base_gt, e = base_eq;
+      for (uint32_t i = lo; i < hi; i++) {
+        const float v = logits[i];
+        const uint32_t key = ord_key(v);
+        if (kc >= n || key > prefix) {
+          cval[g] = v;
+          cidx[g] = i;
+          g++;
+        } else if (key == prefix) {
+          if (tot_gt + e < kc) {
+            cval[tot_gt + e] = v;
+            cidx[tot_gt + e] = i;
+          }
+          e++;
+        }
+      }
+    }
+    uint32_t m = kc;  // candidates, padded to a power of two for the sort
+    uint32_t P = 1;
+    while (P < m) P <<= 1;
+    for (uint32_t i = m + tid; i < P; i += kSampleThreads) {
+      cval[i] = -INFINITY;
+      cidx[i] = 0xffffffffu;
+    }
+    __syncthreads();
+    // 4a. Bitonic sort: logit descending, id ascending on ties.
+    for (uint32_t size = 2; size <= P; size <<= 1) {
+      for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+        for (uint32_t i = tid; i < P; i += kSampleThreads) {
+          const uint32_t j = i ^ stride;
+          if (j > i) {
+            const bool desc = (i & size) == 0;
+            const float vi = cval[i], vj = cval[j];
+            const uint32_t ii = cidx[i], ij = cidx[j];
+            const bool i_first = vi > vj || (vi == vj && ii < ij);
+            if (desc != i_first) {
+              cval[i] = vj;
+              cval[j] = vi;
+              cidx[i] = ij;
+              cidx[j] = ii;
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+    // 4b. Softmax at temperature 1 (sampler.rs:82-83, 116-128).
+    const float mx = cval[0];
+    float sum_part = 0.f;
+    for (uint32_t i = tid; i < m; i += kSampleThreads) sum_part += expf(cval[i] - mx);
+    const float S = block_sum<kSampleThreads>(sum_part, f16s);
+    // Each thread owns a contiguous run of candidates for the scans.
+    const uint32_t cper = (m + kSampleThreads - 1) / kSampleThreads;
+    const uint32_t c0 = tid * cper, c1 = min(m, c0 + cper);
+    float run = 0.f;
+    for (uint32_t i = c0; i < c1; i++) run += expf(cval[i] - mx) / S;
+    float total;
+    float cum = block_scan<float>(run, f16s, &total);
+    // Top-p: the shortest prefix reaching top_p; min-p: drop below p0·min_p.
+    if (tid == 0) keep_s = m;
+    __syncthreads();
+    for (uint32_t i = c0; i < c1; i++) {
+      cum += expf(cval[i] - mx) / S;
+      if (cum >= a.top_p) {
+        atomicMin(&keep_s, i + 1);
+        break;
+      }
+    }
+    __syncthreads();
+    const float floor_p = (1.0f / S) * a.min_p;  // the first candidate's probability times min_p
+    for (uint32_t i = tid; i < keep_s; i += kSampleThreads)
+      if (expf(cval[i] - mx) / S < floor_p) atomicMin(&keep_s, i);
+    __syncthreads();
+    const uint32_t keep = keep_s > 0 ? keep_s : 1;
+    // 4c. Temperature over the kept log-probabilities, then the draw.
+    const float l0 = logf(1.0f / S);
+    float qs = 0.f;
+    for (uint32_t i = tid; i < keep; i += kSampleThreads) qs += expf((logf(expf(cval[i] - mx) / S) - l0) / a.temperature);
+    const float Sq = block_sum<kSampleThreads>(qs, f16s);
+    const uint32_t q0 = tid * ((keep + kSampleThreads - 1) / kSampleThreads);
+    const uint32_t q1 = min(keep, q0 + (keep + kSampleThreads - 1) / kSampleThreads);
+    float qrun = 0.f;
+    for (uint32_t i = q0; i < q1; i++) qrun += expf((logf(expf(cval[i] - mx) / S) - l0) / a.temperature) / Sq;
+    float qtotal;
+    float qcum = block_scan<float>(qrun, f16s, &qtotal);
+    __shared__ float draw_s;
+    if (tid == 0) {
+      uint64_t st = *a.rng;
+      draw_s = wyrand_f32(&st);
+      *a.rng = st;
+      token_s = cidx[keep - 1];  // the last kept candidate when rounding leaves the draw uncovered
+      keep_s = keep;             // reused below as the first index whose cumulative mass passes the draw
+    }
+    __syncthreads();
+    const float u = draw_s;
+    for (uint32_t i = q0; i < q1; i++) {
+      qcum += expf((logf(expf(cval[i] - mx) / S) - l0) / a.temperature) / Sq;
+      if (u < qcum) {
+        atomicMin(&keep_s, i);
+        break;
+      }
+    }
+    __syncthreads();
+    if (tid == 0 && keep_s < keep) token_s = cidx[keep_s];
+    __syncthreads();
+  }
+
+  if (tid == 0) {
+    const uint32_t tok = token_s;
+    if (a.dpos) {
+      a.out[p + 1] = tok;
+      *a.dpos = p + 1;
+    } else {
+      a.out[0] = tok;
+    }
+  }
+}
+
+void run_sample(hipStream_t s, const SampleArgs &a) { k_sample<<<1, kSampleThreads, 0, s>>>(a); }
+
+}  // namespace bch
+
+using namespace bch;
+
+extern "C" int bch_sample(bch_ctx *ctx, bch_view logits, uint32_t n_vocab, bch_view recent, uint32_t n_recent,
+                          const bch_sampling *settings, bch_view rng_state, bch_view out) {
+  if (!settings) return fail(BCH_ERR_ARGUMENT, "sample: no settings");
+  if (n_vocab == 0) return fail(BCH_ERR_ARGUMENT, "sample: an empty vocabulary");
+  SampleArgs a{};
+  BCH_TRY(view_ptr(ctx, "sample", logits, (uint64_t)n_vocab * 4, &a.logits));
+  if (n_recent) BCH_TRY(view_ptr(ctx, "sample", recent, (uint64_t)n_recent * 4, &a.recent));
+  BCH_TRY(view_ptr(ctx, "sample", rng_state, 8, &a.rng));
+  BCH_TRY(view_ptr(ctx, "sample", out, 4, &a.out));
+  if (reinterpret_cast<uintptr_t>(a.rng) % 8) return fail(BCH_ERR_ARGUMENT, "sample: the generator state is not 8-byte aligned");
+  a.n = n_vocab;
+  a.n_recent = n_recent;
+  a.temperature = settings->temperature;
+  a.top_k = settings->top_k;
+  a.top_p = settings->top_p;
+  a.min_p = settings->min_p;
+  a.penalty = settings->repeat_penalty;
+  return launch(ctx, {"sample", 1, n_vocab, 0}, [&](hipStream_t s) { run_sample(s, a); });
+}

@@ -238,6 +238,13 @@ class Lfm2Hip:
         check(lib().bch_lfm2_generate(self.handle, out.ctypes.data_as(C.POINTER(C.c_uint32)), n))
         return out
 
+    def generate_sampled(self, n: int, settings, seed: int) -> np.ndarray:
+        """n tokens drawn by the GPU sampler (settings: a bch_sampling)."""
+        out = np.empty(n, np.uint32)
+        check(lib().bch_lfm2_generate_sampled(self.handle, out.ctypes.data_as(C.POINTER(C.c_uint32)), n,
+                                              C.byref(settings), seed))
+        return out
+
     def checkpoint(self) -> bytes:
         nb = lib().bch_lfm2_checkpoint_bytes(self.handle)
         buf = (C.c_uint8 * nb)()

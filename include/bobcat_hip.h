@@ -251,6 +251,28 @@ int bch_matvec_experts_down(bch_ctx *ctx, uint32_t format, bch_view weights, uin
                             uint32_t n_tokens);
 
 /* ------------------------------------------------------------------ */
+/* Sampling                                                            */
+/* ------------------------------------------------------------------ */
+
+/* bobcat::Sampling (crates/bobcat/src/lfm2.rs:53-64). */
+typedef struct bch_sampling {
+  float temperature;    /* <= 0 picks the most likely token */
+  uint32_t top_k;       /* 0 keeps every token */
+  float top_p;
+  float min_p;
+  float repeat_penalty; /* 1 turns the penalty off */
+} bch_sampling;
+
+/* Sampler::sample (crates/bobcat-cli/src/sampler.rs:45-112) on the GPU:
+ * penalty over the distinct tokens of the last 64 of `recent` (applied to
+ * `logits` in place), top-k, top-p, min-p, temperature, then a draw from the
+ * wyrand generator whose 8-byte state is at `rng_state` (advanced by one
+ * draw).  The token goes to `out` (4 bytes).  At most 4096 candidates
+ * survive top-k (top_k = 0 or > 4096 keeps the 4096 largest logits). */
+int bch_sample(bch_ctx *ctx, bch_view logits, uint32_t n_vocab, bch_view recent, uint32_t n_recent,
+               const bch_sampling *settings, bch_view rng_state, bch_view out);
+
+/* ------------------------------------------------------------------ */
 /* LFM2 driver (crates/bobcat/src/lfm2_metal.rs:125-779)               */
 /* ------------------------------------------------------------------ */
 
@@ -338,6 +360,12 @@ int bch_lfm2_generate(bch_lfm2 *lfm2, uint32_t *out, uint32_t n);
 /* Lfm2Metal::checkpoint / restore (lfm2_metal.rs:250-288).  The blob holds
  * the reset count, n_past, the convolution history and the logits;
  * bch_lfm2_checkpoint_bytes gives its size. */
+/* generate with Sampler::sample instead of argmax (engine.rs:615-630 runs
+ * the sampler on the CPU; here it runs inside the replayed graph): n tokens,
+ * the generator seeded with `seed`; the recent tokens of the penalty are
+ * the sequence's own. */
+int bch_lfm2_generate_sampled(bch_lfm2 *lfm2, uint32_t *out, uint32_t n, const bch_sampling *settings,
+                              uint64_t seed);
 uint64_t bch_lfm2_checkpoint_bytes(const bch_lfm2 *lfm2);
 int bch_lfm2_checkpoint(bch_lfm2 *lfm2, void *blob, uint64_t bytes);
 int bch_lfm2_restore(bch_lfm2 *lfm2, const void *blob, uint64_t bytes);

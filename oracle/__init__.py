@@ -142,6 +142,23 @@ def route(scores: np.ndarray, bias: np.ndarray, n_used: int):
     return s, list(experts)
 
 
+class Sampling(C.Structure):
+    """bch_sampling / bobcat::Sampling."""
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float), ("min_p", C.c_float),
+                ("repeat_penalty", C.c_float)]
+
+
+def sample(logits, recent, settings: Sampling, state: int):
+    """Sampler::sample; returns (token, the generator state after the draw)."""
+    lg = np.array(logits, np.float32)
+    rc = np.ascontiguousarray(recent, np.uint32)
+    st = C.c_uint64(state)
+    lib().orc_sample.restype = C.c_uint32
+    tok = lib().orc_sample(_fp(lg), lg.size, rc.ctypes.data_as(C.POINTER(C.c_uint32)), rc.size, C.byref(settings),
+                           C.byref(st))
+    return int(tok), int(st.value)
+
+
 def short_conv(bcx: np.ndarray, taps: np.ndarray, hist: np.ndarray, n_embd: int, k: int, n_tokens: int):
     """Returns (out, new_history); `hist` is not modified."""
     bcx = np.ascontiguousarray(bcx, np.float32)

@@ -597,3 +597,99 @@ EXPORT void orc_attention(const float *q, const float *kc, const float *vc, floa
   }
   free(scores);
 }
+
+/* ---------------------------------------------------------------- */
+/* Sampling: Sampler::sample (crates/bobcat-cli/src/sampler.rs:45-129)  */
+/* ---------------------------------------------------------------- */
+
+/* wyrand as in fastrand 2.5.0 (Cargo.lock:956-958; not vendored in the
+ * reference): state += 0x2d358dccaa6c78a5; the 128-bit product of the state
+ * and state ^ 0x8bb84b93962eacc9 folded to 64 bits.  f32: the 23 high bits
+ * of the low 32-bit half as the mantissa of [1, 2), minus one.  No golden
+ * draws exist in the reference, so the draw stream is parity unpinned. */
+EXPORT uint64_t orc_wyrand(uint64_t *state) {
+  uint64_t s = *state + 0x2d358dccaa6c78a5ull;
+  *state = s;
+  unsigned __int128 t = (unsigned __int128)s * (unsigned __int128)(s ^ 0x8bb84b93962eacc9ull);
+  return (uint64_t)t ^ (uint64_t)(t >> 64);
+}
+
+EXPORT float orc_wyrand_f32(uint64_t *state) {
+  uint32_t u = (uint32_t)orc_wyrand(state);
+  uint32_t bits = 0x3f800000u | (u >> 9);
+  float f;
+  memcpy(&f, &bits, 4);
+  return f - 1.0f;
+}
+
+typedef struct { uint32_t id; float v; } orc_cand;
+
+static int by_logit_desc(const void *a, const void *b) {
+  const orc_cand *x = a, *y = b;
+  if (x->v > y->v) return -1;
+  if (x->v < y->v) return 1;
+  return x->id < y->id ? -1 : x->id > y->id;
+}
+
+/* softmax (sampler.rs:116-128): sequential f32 sums, as the reference. */
+static void cand_softmax(orc_cand *c, uint32_t n, float temperature) {
+  float max = -INFINITY;
+  for (uint32_t i = 0; i < n; i++) max = c[i].v > max ? c[i].v : max;
+  float sum = 0.0f;
+  for (uint32_t i = 0; i < n; i++) {
+    c[i].v = expf((c[i].v - max) / temperature);
+    sum += c[i].v;
+  }
+  for (uint32_t i = 0; i < n; i++) c[i].v /= sum;
+}
+
+EXPORT uint32_t orc_sample(float *logits, uint32_t n, const uint32_t *recent, uint32_t n_recent,
+                           const bch_sampling *st, uint64_t *rng) {
+  if (fabsf(st->repeat_penalty - 1.0f) > 1.1920929e-7f) {
+    uint32_t start = n_recent > 64 ? n_recent - 64 : 0;
+    for (uint32_t i = start; i < n_recent; i++) {
+      int seen = 0;
+      for (uint32_t j = start; j < i; j++) seen |= recent[j] == recent[i];
+      if (seen || recent[i] >= n) continue;
+      float *l = &logits[recent[i]];
+      *l = *l > 0.0f ? *l / st->repeat_penalty : *l * st->repeat_penalty;
+    }
+  }
+  if (st->temperature <= 0.0f) {
+    uint32_t best = 0;
+    for (uint32_t i = 1; i < n; i++)
+      if (logits[i] > logits[best]) best = i;
+    return best;
+  }
+  orc_cand *c = malloc((size_t)n * sizeof(orc_cand));
+  for (uint32_t i = 0; i < n; i++) c[i] = (orc_cand){i, logits[i]};
+  qsort(c, n, sizeof(orc_cand), by_logit_desc);
+  uint32_t m = (st->top_k > 0 && st->top_k < n) ? st->top_k : n;
+  cand_softmax(c, m, 1.0f);
+  float cum = 0.0f;
+  uint32_t keep = m;
+  for (uint32_t i = 0; i < m; i++) {
+    cum += c[i].v;
+    if (cum >= st->top_p) {
+      keep = i + 1;
+      break;
+    }
+  }
+  float floor_p = c[0].v * st->min_p;
+  uint32_t kept = 0;
+  for (uint32_t i = 0; i < keep; i++)
+    if (c[i].v >= floor_p) c[kept++] = c[i];
+  for (uint32_t i = 0; i < kept; i++) c[i].v = logf(c[i].v);
+  cand_softmax(c, kept, st->temperature);
+  float draw = orc_wyrand_f32(rng);
+  uint32_t token = kept ? c[kept - 1].id : 0;
+  for (uint32_t i = 0; i < kept; i++) {
+    if (draw < c[i].v) {
+      token = c[i].id;
+      break;
+    }
+    draw -= c[i].v;
+  }
+  free(c);
+  return token;
+}
