@@ -68,6 +68,27 @@ class Lfm2Layer(C.Structure):
     ]
 
 
+class Qwen35Layer(C.Structure):
+    _fields_ = [
+        ("is_attention", C.c_uint32), ("attn_norm", _FP), ("ffn_norm", _FP),
+        ("wq", Matrix), ("wk", Matrix), ("wv", Matrix), ("wo", Matrix), ("q_norm", _FP), ("k_norm", _FP),
+        ("qkv", Matrix), ("z", Matrix), ("beta", Matrix), ("alpha", Matrix),
+        ("conv_taps", _FP), ("dt_bias", _FP), ("a", _FP), ("ssm_norm", _FP), ("out", Matrix),
+        ("gate", Matrix), ("up", Matrix), ("down", Matrix),
+    ]
+
+
+class Qwen35Model(C.Structure):
+    _fields_ = [
+        ("n_layers", C.c_uint32), ("n_embd", C.c_uint32), ("n_ff", C.c_uint32), ("n_vocab", C.c_uint32),
+        ("n_heads", C.c_uint32), ("n_kv_heads", C.c_uint32), ("head_dim", C.c_uint32), ("n_rot", C.c_uint32),
+        ("rope_theta", C.c_float), ("norm_eps", C.c_float), ("conv_kernel", C.c_uint32),
+        ("n_k_heads", C.c_uint32), ("n_v_heads", C.c_uint32), ("k_head_dim", C.c_uint32),
+        ("v_head_dim", C.c_uint32), ("layers", C.POINTER(Qwen35Layer)),
+        ("token_embd", Matrix), ("output", Matrix), ("output_norm", _FP),
+    ]
+
+
 class Lfm2Model(C.Structure):
     _fields_ = [
         ("n_layers", C.c_uint32), ("n_embd", C.c_uint32), ("n_ff", C.c_uint32),

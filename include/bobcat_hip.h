@@ -372,6 +372,60 @@ int bch_lfm2_restore(bch_lfm2 *lfm2, const void *blob, uint64_t bytes);
 /* Last call's host-side recording time and device time (lfm2_metal.rs:222-230). */
 double bch_lfm2_last_gpu_seconds(const bch_lfm2 *lfm2);
 
+/* ------------------------------------------------------------------ */
+/* Qwen3.5 (crates/bobcat/src/qwen35.rs, qwen35_metal.rs)              */
+/* ------------------------------------------------------------------ */
+
+/* One Qwen3.5 layer (qwen35.rs:86-145): a gated attention mixer or a Gated
+ * DeltaNet mixer, then a SwiGLU block.  Norm weights are as the GGUF stores
+ * them (the +1 of the zero-centred norms baked in); `a` is -exp(A_log). */
+typedef struct bch_qwen35_layer {
+  uint32_t is_attention;
+  const float *attn_norm;   /* [n_embd] */
+  const float *ffn_norm;    /* [n_embd] (post_attention_norm) */
+  /* gated attention */
+  bch_matrix wq;            /* 2·n_heads·head_dim × n_embd: per head its queries, then its gate */
+  bch_matrix wk, wv;        /* n_kv_heads·head_dim × n_embd */
+  bch_matrix wo;            /* n_embd × n_heads·head_dim */
+  const float *q_norm;      /* [head_dim] */
+  const float *k_norm;      /* [head_dim] */
+  /* Gated DeltaNet */
+  bch_matrix qkv;           /* conv_dim × n_embd: queries, keys, values */
+  bch_matrix z;             /* value_dim × n_embd: the gate of the output norm */
+  bch_matrix beta;          /* n_v_heads × n_embd */
+  bch_matrix alpha;         /* n_v_heads × n_embd */
+  const float *conv_taps;   /* [conv_dim][conv_kernel], the oldest first */
+  const float *dt_bias;     /* [n_v_heads] */
+  const float *a;           /* [n_v_heads], -exp(A_log) */
+  const float *ssm_norm;    /* [v_head_dim] */
+  bch_matrix out;           /* n_embd × value_dim */
+  /* feed-forward */
+  bch_matrix gate, up, down;
+} bch_qwen35_layer;
+
+/* qwen35::Hyperparameters (qwen35.rs:31-67) plus the tensors. */
+typedef struct bch_qwen35_model {
+  uint32_t n_layers;
+  uint32_t n_embd;
+  uint32_t n_ff;
+  uint32_t n_vocab;
+  uint32_t n_heads;
+  uint32_t n_kv_heads;
+  uint32_t head_dim;
+  uint32_t n_rot;           /* leading elements of a head that RoPE rotates */
+  float rope_theta;
+  float norm_eps;
+  uint32_t conv_kernel;
+  uint32_t n_k_heads;       /* DeltaNet query/key heads */
+  uint32_t n_v_heads;       /* DeltaNet value heads, a multiple of n_k_heads */
+  uint32_t k_head_dim;
+  uint32_t v_head_dim;
+  const bch_qwen35_layer *layers;
+  bch_matrix token_embd;
+  bch_matrix output;        /* tied: same data as token_embd */
+  const float *output_norm;
+} bch_qwen35_model;
+
 #ifdef __cplusplus
 }
 #endif

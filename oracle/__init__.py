@@ -56,6 +56,12 @@ def lib() -> C.CDLL:
             "orc_lfm2_state_free": (None, [vp]),
             "orc_lfm2_n_past": (u32, [vp]),
             "orc_lfm2_step": (C.c_int, [vp, vp, u32, fp, fp, fp, fp]),
+            "orc_qwen35_state_new": (vp, [vp, u32]),
+            "orc_qwen35_state_free": (None, [vp]),
+            "orc_qwen35_n_past": (u32, [vp]),
+            "orc_qwen35_step": (C.c_int, [vp, vp, u32, fp, fp, fp, fp]),
+            "orc_sample": (u32, [fp, u32, C.POINTER(u32), u32, vp, C.POINTER(C.c_uint64)]),
+            "orc_wyrand": (C.c_uint64, [C.POINTER(C.c_uint64)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(h, name)
@@ -153,9 +159,8 @@ def sample(logits, recent, settings: Sampling, state: int):
     lg = np.array(logits, np.float32)
     rc = np.ascontiguousarray(recent, np.uint32)
     st = C.c_uint64(state)
-    lib().orc_sample.restype = C.c_uint32
-    tok = lib().orc_sample(_fp(lg), lg.size, rc.ctypes.data_as(C.POINTER(C.c_uint32)), rc.size, C.byref(settings),
-                           C.byref(st))
+    tok = lib().orc_sample(_fp(lg), lg.size, rc.ctypes.data_as(C.POINTER(C.c_uint32)), rc.size,
+                           C.cast(C.byref(settings), C.c_void_p), C.byref(st))
     return int(tok), int(st.value)
 
 
@@ -208,5 +213,34 @@ class Lfm2State:
     def __del__(self):
         try:
             lib().orc_lfm2_state_free(self.handle)
+        except Exception:
+            pass
+
+
+class Qwen35State:
+    """qwen35::State and Model::step on the CPU (qwen35.rs:280-516, 533-640)."""
+
+    def __init__(self, model, n_ctx: int):
+        """`model` is a bobcat_amd.qwen35.Qwen35Weights."""
+        self.model = model
+        cfg = model.cfg
+        self.n_vocab, self.n_embd, self.n_layers = cfg.n_vocab, cfg.n_embd, cfg.n_layers
+        self.handle = lib().orc_qwen35_state_new(C.addressof(model.c_model), n_ctx)
+        assert self.handle
+
+    def step(self, token: int, logits: bool = True, trace: bool = False):
+        lg = np.empty(self.n_vocab, np.float32) if logits else None
+        te = np.empty(self.n_embd, np.float32) if trace else None
+        tl = np.empty(self.n_layers * self.n_embd, np.float32) if trace else None
+        tf = np.empty(self.n_embd, np.float32) if trace else None
+        rc = lib().orc_qwen35_step(C.addressof(self.model.c_model), self.handle, token,
+                                   *(None if a is None else _fp(a) for a in (lg, te, tl, tf)))
+        if rc != 0:
+            raise ValueError({-1: "context full", -2: "token outside the vocabulary"}[rc])
+        return (lg, (te, tl, tf)) if trace else lg
+
+    def __del__(self):
+        try:
+            lib().orc_qwen35_state_free(self.handle)
         except Exception:
             pass

@@ -693,3 +693,206 @@ EXPORT uint32_t orc_sample(float *logits, uint32_t n, const uint32_t *recent, ui
   free(c);
   return token;
 }
+
+/* ---------------------------------------------------------------- */
+/* Qwen3.5 forward pass (qwen35.rs:280-516, 761-778)                 */
+/* ---------------------------------------------------------------- */
+
+/* qwen35::State (qwen35.rs:533-640): caches, DeltaNet states, scratch. */
+typedef struct orc_qwen35_state {
+  uint32_t n_ctx, n_past;
+  float *k_cache, *v_cache;         /* [attn layer][pos][kv_dim] */
+  float *conv, *state;              /* [delta layer][conv_dim][k-1], [delta layer][n_v][k_dim][v_dim] */
+  float *h, *x, *mixer_out, *ffn_gate, *ffn_up, *q_gate, *q, *attn_gate, *k, *v, *attn, *scores;
+  float *qkv, *conv_out, *z, *beta, *alpha, *delta, *delta_out;
+} orc_qwen35_state;
+
+static uint32_t q35_count(const bch_qwen35_model *m, int attention) {
+  uint32_t n = 0;
+  for (uint32_t i = 0; i < m->n_layers; i++) n += (m->layers[i].is_attention != 0) == (attention != 0);
+  return n;
+}
+
+EXPORT orc_qwen35_state *orc_qwen35_state_new(const bch_qwen35_model *m, uint32_t n_ctx) {
+  if (n_ctx == 0) return NULL;
+  orc_qwen35_state *s = calloc(1, sizeof(*s));
+  uint64_t n = m->n_embd, kvd = (uint64_t)m->n_kv_heads * m->head_dim, qd = (uint64_t)m->n_heads * m->head_dim;
+  uint64_t key_dim = (uint64_t)m->n_k_heads * m->k_head_dim, value_dim = (uint64_t)m->n_v_heads * m->v_head_dim;
+  uint64_t conv_dim = 2 * key_dim + value_dim;
+  uint32_t na = q35_count(m, 1), nd = q35_count(m, 0);
+  s->n_ctx = n_ctx;
+  s->k_cache = calloc((uint64_t)na * n_ctx * kvd + 1, 4);
+  s->v_cache = calloc((uint64_t)na * n_ctx * kvd + 1, 4);
+  s->conv = calloc((uint64_t)nd * conv_dim * (m->conv_kernel - 1) + 1, 4);
+  s->state = calloc((uint64_t)nd * m->n_v_heads * m->k_head_dim * m->v_head_dim + 1, 4);
+  s->h = calloc(n, 4);
+  s->x = calloc(n, 4);
+  s->mixer_out = calloc(n, 4);
+  s->ffn_gate = calloc(m->n_ff, 4);
+  s->ffn_up = calloc(m->n_ff, 4);
+  s->q_gate = calloc(2 * qd + 1, 4);
+  s->q = calloc(qd + 1, 4);
+  s->attn_gate = calloc(qd + 1, 4);
+  s->k = calloc(kvd + 1, 4);
+  s->v = calloc(kvd + 1, 4);
+  s->attn = calloc(qd + 1, 4);
+  s->scores = calloc(n_ctx, 4);
+  s->qkv = calloc(conv_dim + 1, 4);
+  s->conv_out = calloc(conv_dim + 1, 4);
+  s->z = calloc(value_dim + 1, 4);
+  s->beta = calloc(m->n_v_heads + 1, 4);
+  s->alpha = calloc(m->n_v_heads + 1, 4);
+  s->delta = calloc(m->v_head_dim + 1, 4);
+  s->delta_out = calloc(value_dim + 1, 4);
+  return s;
+}
+
+EXPORT void orc_qwen35_state_free(orc_qwen35_state *s) {
+  if (!s) return;
+  void *p[] = {s->k_cache, s->v_cache, s->conv, s->state, s->h, s->x, s->mixer_out, s->ffn_gate, s->ffn_up,
+               s->q_gate, s->q, s->attn_gate, s->k, s->v, s->attn, s->scores, s->qkv, s->conv_out, s->z,
+               s->beta, s->alpha, s->delta, s->delta_out};
+  for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) free(p[i]);
+  free(s);
+}
+
+EXPORT uint32_t orc_qwen35_n_past(const orc_qwen35_state *s) { return s->n_past; }
+
+static float q35_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+/* softplus (qwen35.rs:775-778): x above 20, else ln(1 + e^x). */
+static float q35_softplus(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+/* l2_normalize (qwen35.rs:761-768): sequential f32 sum, eps 1e-6. */
+static void q35_l2(float *x, uint32_t n, float scale) {
+  float sum = 0.0f;
+  for (uint32_t i = 0; i < n; i++) sum += x[i] * x[i];
+  float factor = scale / sqrtf(sum + 1e-6f);
+  for (uint32_t i = 0; i < n; i++) x[i] *= factor;
+}
+
+/* Model::attention (qwen35.rs:369-426). */
+static void q35_attention(const bch_qwen35_model *m, const bch_qwen35_layer *L, uint32_t ci, uint32_t pos,
+                          orc_qwen35_state *s) {
+  uint32_t hd = m->head_dim, nh = m->n_heads, nkv = m->n_kv_heads, kvd = nkv * hd, group = nh / nkv;
+  matvec_m(&L->wq, s->x, s->q_gate);
+  matvec_m(&L->wk, s->x, s->k);
+  matvec_m(&L->wv, s->x, s->v);
+  for (uint32_t h = 0; h < nh; h++) {
+    const float *block = s->q_gate + 2ull * h * hd;
+    float *q = s->q + (uint64_t)h * hd;
+    memcpy(q, block, 4ull * hd);
+    rms_norm_in_place(q, L->q_norm, hd, m->norm_eps);
+    orc_rope_neox(q, m->n_rot, pos, m->rope_theta);
+    memcpy(s->attn_gate + (uint64_t)h * hd, block + hd, 4ull * hd);
+  }
+  for (uint32_t h = 0; h < nkv; h++) {
+    float *k = s->k + (uint64_t)h * hd;
+    rms_norm_in_place(k, L->k_norm, hd, m->norm_eps);
+    orc_rope_neox(k, m->n_rot, pos, m->rope_theta);
+  }
+  float *kc = s->k_cache + (uint64_t)ci * s->n_ctx * kvd, *vc = s->v_cache + (uint64_t)ci * s->n_ctx * kvd;
+  memcpy(kc + (uint64_t)pos * kvd, s->k, 4ull * kvd);
+  memcpy(vc + (uint64_t)pos * kvd, s->v, 4ull * kvd);
+  uint32_t n_keys = pos + 1;
+  float scale = 1.0f / sqrtf((float)hd);
+  for (uint32_t h = 0; h < nh; h++) {
+    uint32_t kvh = h / group;
+    const float *q = s->q + (uint64_t)h * hd;
+    for (uint32_t t = 0; t < n_keys; t++) s->scores[t] = orc_dot(q, kc + (uint64_t)t * kvd + kvh * hd, hd) * scale;
+    orc_softmax(s->scores, n_keys);
+    float *out = s->attn + (uint64_t)h * hd;
+    for (uint32_t d = 0; d < hd; d++) out[d] = 0.0f;
+    for (uint32_t t = 0; t < n_keys; t++) {
+      const float *v = vc + (uint64_t)t * kvd + kvh * hd;
+      for (uint32_t d = 0; d < hd; d++) out[d] += s->scores[t] * v[d];
+    }
+  }
+  for (uint64_t i = 0; i < (uint64_t)nh * hd; i++) s->attn[i] *= q35_sigmoid(s->attn_gate[i]);
+  matvec_m(&L->wo, s->attn, s->mixer_out);
+}
+
+/* Model::delta_net (qwen35.rs:430-516). */
+static void q35_delta(const bch_qwen35_model *m, const bch_qwen35_layer *L, uint32_t ci, orc_qwen35_state *s) {
+  uint32_t K = m->conv_kernel, hist = K - 1, nk = m->n_k_heads, nv = m->n_v_heads, dk = m->k_head_dim,
+           dv = m->v_head_dim;
+  uint64_t key_dim = (uint64_t)nk * dk, conv_dim = 2 * key_dim + (uint64_t)nv * dv;
+  float *conv = s->conv + (uint64_t)ci * conv_dim * hist;
+  float *state = s->state + (uint64_t)ci * nv * dk * dv;
+  matvec_m(&L->qkv, s->x, s->qkv);
+  matvec_m(&L->z, s->x, s->z);
+  matvec_m(&L->beta, s->x, s->beta);
+  matvec_m(&L->alpha, s->x, s->alpha);
+  for (uint64_t c = 0; c < conv_dim; c++) {
+    const float *taps = L->conv_taps + c * K;
+    float *past = conv + c * hist;
+    float input = s->qkv[c];
+    float sum = taps[hist] * input;
+    for (uint32_t j = 0; j < hist; j++) sum += taps[j] * past[j];
+    s->conv_out[c] = orc_silu(sum);
+    for (uint32_t j = 0; j + 1 < hist; j++) past[j] = past[j + 1];
+    if (hist) past[hist - 1] = input;
+  }
+  float *q = s->conv_out, *k = s->conv_out + key_dim, *v = s->conv_out + 2 * key_dim;
+  float q_scale = 1.0f / sqrtf((float)dk);
+  for (uint32_t h = 0; h < nk; h++) {
+    q35_l2(q + (uint64_t)h * dk, dk, q_scale);
+    q35_l2(k + (uint64_t)h * dk, dk, 1.0f);
+  }
+  for (uint32_t h = 0; h < nv; h++) {
+    uint32_t kh = h % nk;
+    const float *qh = q + (uint64_t)kh * dk, *kk = k + (uint64_t)kh * dk, *vh = v + (uint64_t)h * dv;
+    float beta = q35_sigmoid(s->beta[h]);
+    float decay = expf(L->a[h] * q35_softplus(s->alpha[h] + L->dt_bias[h]));
+    float *S = state + (uint64_t)h * dk * dv;
+    for (uint64_t i = 0; i < (uint64_t)dk * dv; i++) S[i] *= decay;
+    for (uint32_t j = 0; j < dv; j++) s->delta[j] = 0.0f;
+    for (uint32_t r = 0; r < dk; r++)
+      for (uint32_t j = 0; j < dv; j++) s->delta[j] += S[(uint64_t)r * dv + j] * kk[r];
+    for (uint32_t j = 0; j < dv; j++) s->delta[j] = (vh[j] - s->delta[j]) * beta;
+    float *out = s->delta_out + (uint64_t)h * dv;
+    for (uint32_t j = 0; j < dv; j++) out[j] = 0.0f;
+    for (uint32_t r = 0; r < dk; r++)
+      for (uint32_t j = 0; j < dv; j++) {
+        S[(uint64_t)r * dv + j] += kk[r] * s->delta[j];
+        out[j] += S[(uint64_t)r * dv + j] * qh[r];
+      }
+    rms_norm_in_place(out, L->ssm_norm, dv, m->norm_eps);
+    const float *g = s->z + (uint64_t)h * dv;
+    for (uint32_t j = 0; j < dv; j++) out[j] *= orc_silu(g[j]);
+  }
+  matvec_m(&L->out, s->delta_out, s->mixer_out);
+}
+
+/* Model::step (qwen35.rs:280-365); traces as orc_lfm2_step. */
+EXPORT int orc_qwen35_step(const bch_qwen35_model *m, orc_qwen35_state *s, uint32_t token, float *logits,
+                           float *trace_embedding, float *trace_layers, float *trace_final) {
+  uint32_t n = m->n_embd, pos = s->n_past;
+  if (pos >= s->n_ctx) return -1;
+  if (token >= m->n_vocab) return -2;
+  uint64_t rb = orc_row_bytes(m->token_embd.format, n);
+  orc_dequantize(m->token_embd.format, (const uint8_t *)m->token_embd.data + (uint64_t)token * rb, n, s->h);
+  if (trace_embedding) memcpy(trace_embedding, s->h, 4ull * n);
+  uint32_t ai = 0, di = 0;
+  for (uint32_t il = 0; il < m->n_layers; il++) {
+    const bch_qwen35_layer *L = &m->layers[il];
+    orc_rms_norm(s->h, L->attn_norm, n, m->norm_eps, s->x);
+    if (L->is_attention)
+      q35_attention(m, L, ai++, pos, s);
+    else
+      q35_delta(m, L, di++, s);
+    for (uint32_t i = 0; i < n; i++) s->h[i] += s->mixer_out[i];
+    orc_rms_norm(s->h, L->ffn_norm, n, m->norm_eps, s->x);
+    matvec_m(&L->gate, s->x, s->ffn_gate);
+    matvec_m(&L->up, s->x, s->ffn_up);
+    for (uint32_t i = 0; i < m->n_ff; i++) s->ffn_gate[i] = orc_silu(s->ffn_gate[i]) * s->ffn_up[i];
+    matvec_m(&L->down, s->ffn_gate, s->mixer_out);
+    for (uint32_t i = 0; i < n; i++) s->h[i] += s->mixer_out[i];
+    if (trace_layers) memcpy(trace_layers + (uint64_t)il * n, s->h, 4ull * n);
+  }
+  orc_rms_norm(s->h, m->output_norm, n, m->norm_eps, s->x);
+  if (trace_final) memcpy(trace_final, s->x, 4ull * n);
+  if (logits) matvec_m(&m->output, s->x, logits);
+  s->n_past++;
+  return 0;
+}
