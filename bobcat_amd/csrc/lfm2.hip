@@ -22,18 +22,11 @@
 #include <cstring>
 #include <vector>
 
-#include "kernels.h"
-#include "runtime.h"
+#include "driver.h"
 
 namespace bch {
 
-constexpr uint32_t kPrefillBatch = 512;  // PREFILL_BATCH (lfm2_metal.rs:33-34)
 constexpr uint32_t kAttnQueryBatch = 64;
-
-struct DevMatrix {
-  uint32_t format = 0, n_rows = 0, n_cols = 0;
-  const uint8_t *data = nullptr;
-};
 
 struct Layer {
   bool attention = false;
@@ -53,11 +46,9 @@ struct Layer {
 
 using namespace bch;
 
-struct bch_lfm2 {
-  bch_ctx *ctx = nullptr;
-  hipStream_t s = nullptr;
+struct bch_lfm2 : bch::Sequence {
   // Hyperparameters (lfm2.rs:17-49).
-  uint32_t n_layers, n_embd, n_ff, n_heads, n_kv_heads, head_dim, n_vocab, conv_kernel;
+  uint32_t n_ff, n_heads, n_kv_heads, head_dim, conv_kernel;
   uint32_t n_experts = 0, n_used = 0, n_ff_expert = 0;
   float rope_theta, norm_eps;
   uint32_t n_attn = 0, n_conv = 0;
@@ -66,30 +57,14 @@ struct bch_lfm2 {
   DevMatrix token_embd, output;
   const float *output_norm = nullptr;
   // Device memory.
-  uint8_t *weights = nullptr;
   void *k_cache = nullptr, *v_cache = nullptr;
   float *conv_state = nullptr, *hidden = nullptr, *normed = nullptr, *bcx = nullptr, *conv_out = nullptr;
-  float *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *ffn = nullptr, *logits = nullptr;
-  float *partials = nullptr, *trace = nullptr;
-  uint32_t trace_rows = 0;  // tokens each traced activation holds (lfm2_metal.rs:764-779)
-  uint32_t *counters = nullptr, *tokens = nullptr, *dpos = nullptr, *greedy = nullptr;
+  float *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *ffn = nullptr;
+  float *partials = nullptr;
+  uint32_t *counters = nullptr;
   uint32_t *route = nullptr;  // expert routes of a batch (route_bytes(n_used, batch))
-  uint64_t *argmax_partials = nullptr;  // kArgmaxPartials argmax keys of the logits
-  uint64_t *rng = nullptr;              // sampler state
-  uint64_t rng_host = 0;
-  bch_sampling sample_settings{};       // the settings sample_graph was captured with
-  std::vector<void *> allocations;
-  // Sequence state.
-  uint32_t n_ctx = 0, n_past = 0, batch = 0;
-  uint64_t resets = 0;
   bool kv_half = true;
-  bool have_logits = false;
   uint32_t decode_splits = 1, prefill_splits = 1;
-  hipGraphExec_t step_graph = nullptr, gen_graph = nullptr, sample_graph = nullptr;
-  hipEvent_t ev0 = nullptr, ev1 = nullptr;
-  double last_gpu_seconds = 0.0;
-  // Host staging of the small asynchronous uploads (they must outlive the call).
-  uint32_t dpos_host = 0, token_host = 0;
 
   uint64_t cache_elems_per_layer() const { return (uint64_t)n_ctx * kv_dim; }
   void *cache_layer(void *base, uint32_t ci) const {
@@ -98,57 +73,15 @@ struct bch_lfm2 {
   void *cache_slot(void *base, uint32_t ci, uint32_t pos) const {
     return static_cast<char *>(cache_layer(base, ci)) + (uint64_t)pos * kv_dim * (kv_half ? 2 : 4);
   }
-};
 
-namespace bch {
-
-static int dev_alloc(bch_lfm2 *m, uint64_t bytes, void **out) {
-  void *p = nullptr;
-  if (hipMalloc(&p, bytes ? bytes : 256) != hipSuccess)
-    return fail(BCH_ERR_ALLOCATION, "cannot allocate %llu bytes", (unsigned long long)bytes);
-  if (hipMemset(p, 0, bytes ? bytes : 256) != hipSuccess) return fail(BCH_ERR_ALLOCATION, "cannot clear memory");
-  m->allocations.push_back(p);
-  *out = p;
-  return BCH_OK;
-}
-
-template <class T>
-static int dev_alloc_t(bch_lfm2 *m, uint64_t count, T **out) {
-  void *p;
-  BCH_TRY(dev_alloc(m, count * sizeof(T), &p));
-  *out = static_cast<T *>(p);
-  return BCH_OK;
-}
-
-static uint64_t align256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
-
-// Host tensors -> one device allocation.  First pass sizes, second copies.
-struct Uploader {
-  std::vector<std::pair<const void *, uint64_t>> items;  // host pointer, bytes
-  std::vector<uint64_t> offsets;
-  uint64_t total = 0;
-  size_t add(const void *p, uint64_t bytes) {
-    for (size_t i = 0; i < items.size(); i++)
-      if (items[i].first == p && items[i].second == bytes) return i;  // tied tensors share a copy
-    items.push_back({p, bytes});
-    offsets.push_back(total);
-    total = align256(total + bytes);
-    return items.size() - 1;
+  void record_step(hipStream_t st, bool greedy_input, bool trace) override;
+  void record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool want_logits, bool trace) override;
+  std::vector<std::pair<void *, uint64_t>> state_regions() const override {
+    return {{conv_state, (uint64_t)n_conv * (conv_kernel - 1) * n_embd * 4}};
   }
 };
 
-static bool gemv_format(uint32_t f) { return f == BCH_Q4K || f == BCH_F16 || f == BCH_F32; }
-
-static int check_matrix(const bch_matrix &mat, uint32_t rows, uint32_t cols, const char *name) {
-  if (!mat.data) return fail(BCH_ERR_ARGUMENT, "missing tensor %s", name);
-  if (mat.n_rows != rows || mat.n_cols != cols)
-    return fail(BCH_ERR_ARGUMENT, "tensor %s is %u x %u, expected %u x %u", name, mat.n_rows, mat.n_cols, rows, cols);
-  if (!gemv_format(mat.format))
-    return fail(BCH_ERR_UNSUPPORTED_FORMAT, "tensor %s: format %u is not supported (Q4_K, F16 or F32)", name,
-                mat.format);
-  if (mat.format == BCH_Q4K && cols % 256) return fail(BCH_ERR_ARGUMENT, "tensor %s: columns not a multiple of 256", name);
-  return BCH_OK;
-}
+namespace bch {
 
 // ---------------------------------------------------------------------
 // Recording
@@ -178,7 +111,7 @@ static void record_moe_token(bch_lfm2 *m, hipStream_t s, const Layer &L, const f
 // advances *dpos.  The logits leave their argmax partials behind for the
 // next such step.  With `trace`, activations are copied into m->trace:
 // embedding, each layer's output, final norm.
-static void record_step(bch_lfm2 *m, hipStream_t s, bool greedy_input, bool trace) {
+static void lfm2_step(bch_lfm2 *m, hipStream_t s, bool greedy_input, bool trace) {
   const uint32_t n = m->n_embd, cus = m->ctx->n_cus;
   uint32_t *dp = m->dpos;
   const uint64_t tstride = (uint64_t)m->trace_rows * n;  // floats per traced activation
@@ -267,7 +200,7 @@ static void check_finite(hipStream_t s, const char *what, uint32_t layer, const 
 }
 
 // A prefill batch of `count` tokens at positions pos.. (record_batch).
-static void record_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count, bool want_logits, bool trace) {
+static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count, bool want_logits, bool trace) {
   const uint32_t n = m->n_embd, cus = m->ctx->n_cus;
   const uint64_t tstride = (uint64_t)m->trace_rows * n;
   run_embed(s, m->token_embd.format, m->token_embd.data, bch_row_bytes(m->token_embd.format, n), m->tokens + pos,
@@ -341,66 +274,14 @@ static void record_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t coun
                m->output_norm, m->norm_eps, false, cus);
 }
 
-// Grow the trace buffer to hold `rows` tokens per activation
-// (Lfm2Metal::ensure_trace_rows, lfm2_metal.rs:764-779).
-static int ensure_trace_rows(bch_lfm2 *m, uint32_t rows) {
-  if (rows <= m->trace_rows) return BCH_OK;
-  if (m->trace) {
-    hipStreamSynchronize(m->s);
-    hipFree(m->trace);
-    for (auto &p : m->allocations)
-      if (p == m->trace) p = nullptr;
-    m->trace = nullptr;
-  }
-  BCH_TRY(dev_alloc_t(m, (uint64_t)(m->n_layers + 2) * rows * m->n_embd, &m->trace));
-  m->trace_rows = rows;
-  return BCH_OK;
+}  // namespace bch
+
+void bch_lfm2::record_step(hipStream_t st, bool greedy_input, bool trace) { lfm2_step(this, st, greedy_input, trace); }
+void bch_lfm2::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool want_logits, bool trace) {
+  lfm2_batch(this, st, pos, count, want_logits, trace);
 }
 
-static int check_hip(hipError_t e, const char *what) {
-  if (e != hipSuccess) return fail(BCH_ERR_EXECUTION, "%s: %s", what, hipGetErrorString(e));
-  return BCH_OK;
-}
-
-static int capture(bch_lfm2 *m, bool generate, hipGraphExec_t *out) {
-  hipStream_t s = m->s;
-  BCH_TRY(check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture"));
-  record_step(m, s, generate, false);
-  hipGraph_t g;
-  BCH_TRY(check_hip(hipStreamEndCapture(s, &g), "end capture"));
-  hipError_t e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
-  hipGraphDestroy(g);
-  return check_hip(e, "instantiate graph");
-}
-
-// Decode steps replay a captured HIP graph unless BCH_LFM2_NO_GRAPH=1, which
-// issues the same launches on the stream one by one (for tools that do not
-// follow graph launches, such as per-kernel tracing).
-static bool use_graphs() {
-  static const bool on = !(getenv("BCH_LFM2_NO_GRAPH") && atoi(getenv("BCH_LFM2_NO_GRAPH")) != 0);
-  return on;
-}
-
-static int set_dpos(bch_lfm2 *m, uint32_t value) {
-  m->dpos_host = value;
-  return check_hip(hipMemcpyAsync(m->dpos, &m->dpos_host, 4, hipMemcpyHostToDevice, m->s), "write position");
-}
-
-static int finish(bch_lfm2 *m) {
-  hipEventRecord(m->ev1, m->s);
-  BCH_TRY(check_hip(hipEventSynchronize(m->ev1), "the GPU failed to run the work"));
-  float ms = 0.f;
-  hipEventElapsedTime(&ms, m->ev0, m->ev1);
-  m->last_gpu_seconds = ms * 1e-3;
-  return check_hip(hipGetLastError(), "launch");
-}
-
-static int busy_check(bch_lfm2 *m) {
-  if (m->ctx->recording || m->ctx->committed > m->ctx->waited)
-    return fail(BCH_ERR_BUSY, "the backend has recorded work in flight");
-  return BCH_OK;
-}
-
+namespace bch {
 }  // namespace bch
 
 extern "C" {
@@ -463,20 +344,12 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
 
   // Validate and plan the weight upload.
   Uploader up;
-  std::vector<std::pair<const void **, size_t>> fixups;  // device pointer field -> upload slot
   m->layers.resize(md->n_layers);
-  auto vec = [&](const float *p, uint64_t count, const float **field, const char *name) -> int {
-    if (!p) return fail(BCH_ERR_ARGUMENT, "missing tensor %s", name);
-    fixups.push_back({reinterpret_cast<const void **>(field), up.add(p, count * 4)});
-    return BCH_OK;
+  auto vec = [&](const float *p, uint64_t count, const float **field, const char *name) {
+    return up.vec(p, count, field, name);
   };
-  auto mat = [&](const bch_matrix &src, uint32_t rows, uint32_t cols, DevMatrix *dst, const char *name) -> int {
-    BCH_TRY(check_matrix(src, rows, cols, name));
-    dst->format = src.format;
-    dst->n_rows = rows;
-    dst->n_cols = cols;
-    fixups.push_back({reinterpret_cast<const void **>(&dst->data), up.add(src.data, bch_row_bytes(src.format, cols) * rows)});
-    return BCH_OK;
+  auto mat = [&](const bch_matrix &src, uint32_t rows, uint32_t cols, DevMatrix *dst, const char *name) {
+    return up.mat(src, rows, cols, dst, name);
   };
   for (uint32_t il = 0; il < md->n_layers; il++) {
     const bch_lfm2_layer &S = md->layers[il];
@@ -533,18 +406,7 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
         (rc = vec(md->output_norm, n, &m->output_norm, "token_embd_norm")))
       return cleanup(rc);
   }
-  // Upload.
-  {
-    void *w;
-    int rc = dev_alloc(m, up.total, &w);
-    if (rc) return cleanup(rc);
-    m->weights = static_cast<uint8_t *>(w);
-    for (size_t i = 0; i < up.items.size(); i++)
-      if (hipMemcpy(m->weights + up.offsets[i], up.items[i].first, up.items[i].second, hipMemcpyHostToDevice) !=
-          hipSuccess)
-        return cleanup(fail(BCH_ERR_ALLOCATION, "cannot copy the weights to the device"));
-    for (auto &f : fixups) *f.first = m->weights + up.offsets[f.second];
-  }
+  if (int rc = m->upload(up)) return cleanup(rc);
   // Buffers (Lfm2Metal::new, lfm2_metal.rs:153-203).
   {
     const uint64_t rows = m->batch;
@@ -556,267 +418,47 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
                                           m->decode_splits),
                  attention_partial_floats(1, m->n_heads, hd, attn_decode_max_splits(n_ctx, hd, m->kv_half)));
     int rc = 0;
-    (void)((rc = dev_alloc(m, cache, &m->k_cache)) || (rc = dev_alloc(m, cache, &m->v_cache)) ||
-           (rc = dev_alloc_t(m, (uint64_t)m->n_conv * (m->conv_kernel - 1) * n, &m->conv_state)) ||
-           (rc = dev_alloc_t(m, rows * n, &m->hidden)) || (rc = dev_alloc_t(m, rows * n, &m->normed)) ||
-           (rc = dev_alloc_t(m, rows * 3 * n, &m->bcx)) || (rc = dev_alloc_t(m, rows * n, &m->conv_out)) ||
-           (rc = dev_alloc_t(m, rows * m->q_dim + 4, &m->q)) || (rc = dev_alloc_t(m, rows * m->kv_dim + 4, &m->k)) ||
-           (rc = dev_alloc_t(m, rows * m->kv_dim + 4, &m->v)) || (rc = dev_alloc_t(m, rows * m->q_dim + 4, &m->attn)) ||
-           (rc = dev_alloc_t(m, std::max<uint64_t>(rows * m->n_ff, (uint64_t)m->n_used * m->n_ff_expert), &m->ffn)) || (rc = dev_alloc_t(m, m->n_vocab, &m->logits)) ||
-           (rc = dev_alloc_t(m, partial_floats + 4, &m->partials)) ||
-           (rc = dev_alloc_t(m, (uint64_t)kAttnQueryBatch * std::max(1u, m->n_kv_heads), &m->counters)) ||
-           (rc = dev_alloc_t(m, (uint64_t)n_ctx + 2, &m->tokens)) || (rc = dev_alloc_t(m, 4, &m->dpos)) ||
-           (rc = dev_alloc_t(m, 4, &m->greedy)) || (rc = dev_alloc_t(m, kArgmaxPartials, &m->argmax_partials)) ||
-           (rc = dev_alloc_t(m, 2 * (uint64_t)std::max(1u, m->n_used) * rows, &m->route)) ||
-           (rc = dev_alloc_t(m, 1, &m->rng)));
+    (void)((rc = m->alloc(cache, &m->k_cache)) || (rc = m->alloc(cache, &m->v_cache)) ||
+           (rc = m->alloc_t((uint64_t)m->n_conv * (m->conv_kernel - 1) * n, &m->conv_state)) ||
+           (rc = m->alloc_t(rows * n, &m->hidden)) || (rc = m->alloc_t(rows * n, &m->normed)) ||
+           (rc = m->alloc_t(rows * 3 * n, &m->bcx)) || (rc = m->alloc_t(rows * n, &m->conv_out)) ||
+           (rc = m->alloc_t(rows * m->q_dim + 4, &m->q)) || (rc = m->alloc_t(rows * m->kv_dim + 4, &m->k)) ||
+           (rc = m->alloc_t(rows * m->kv_dim + 4, &m->v)) || (rc = m->alloc_t(rows * m->q_dim + 4, &m->attn)) ||
+           (rc = m->alloc_t(std::max<uint64_t>(rows * m->n_ff, (uint64_t)m->n_used * m->n_ff_expert), &m->ffn)) ||
+           (rc = m->alloc_t(partial_floats + 4, &m->partials)) ||
+           (rc = m->alloc_t((uint64_t)kAttnQueryBatch * std::max(1u, m->n_kv_heads), &m->counters)) ||
+           (rc = m->alloc_t(2 * (uint64_t)std::max(1u, m->n_used) * rows, &m->route)) || (rc = m->alloc_common()));
     if (rc) return cleanup(rc);
   }
-  hipEventCreate(&m->ev0);
-  hipEventCreate(&m->ev1);
   *out = m;
   return BCH_OK;
 }
 
-void bch_lfm2_free(bch_lfm2 *m) {
-  if (!m) return;
-  // The context (and its stream) must still be open: free drivers first.
-  if (m->s) hipStreamSynchronize(m->s);
-  if (m->step_graph) hipGraphExecDestroy(m->step_graph);
-  if (m->gen_graph) hipGraphExecDestroy(m->gen_graph);
-  if (m->sample_graph) hipGraphExecDestroy(m->sample_graph);
-  if (m->ev0) hipEventDestroy(m->ev0);
-  if (m->ev1) hipEventDestroy(m->ev1);
-  for (void *p : m->allocations) hipFree(p);
-  delete m;
-}
+void bch_lfm2_free(bch_lfm2 *m) { delete m; }
 
 uint32_t bch_lfm2_n_past(const bch_lfm2 *m) { return m->n_past; }
 double bch_lfm2_last_gpu_seconds(const bch_lfm2 *m) { return m->last_gpu_seconds; }
-
-int bch_lfm2_reset(bch_lfm2 *m) {
-  BCH_TRY(busy_check(m));
-  // A new sequence starts from zero convolution history; the KV cache needs
-  // no clearing (lfm2_metal.rs:237-247).
-  if (m->n_conv)
-    BCH_TRY(check_hip(hipMemsetAsync(m->conv_state, 0, (uint64_t)m->n_conv * (m->conv_kernel - 1) * m->n_embd * 4, m->s),
-                      "clear conv state"));
-  BCH_TRY(check_hip(hipStreamSynchronize(m->s), "reset"));
-  m->n_past = 0;
-  m->resets++;
-  m->have_logits = false;
-  return BCH_OK;
-}
+int bch_lfm2_reset(bch_lfm2 *m) { return m->reset(); }
 
 int bch_lfm2_step(bch_lfm2 *m, uint32_t token, float *logits, float *trace_embedding, float *trace_layers,
                   float *trace_final) {
-  BCH_TRY(busy_check(m));
-  if (m->n_past >= m->n_ctx) return fail(BCH_ERR_CONTEXT_FULL, "the context is full");
-  if (token >= m->n_vocab) return fail(BCH_ERR_TOKEN, "token %u is outside the vocabulary of %u", token, m->n_vocab);
-  const bool trace = trace_embedding || trace_layers || trace_final;
-  if (trace) BCH_TRY(ensure_trace_rows(m, 1));
-  hipStream_t s = m->s;
-  m->token_host = token;
-  BCH_TRY(check_hip(hipMemcpyAsync(m->tokens + m->n_past, &m->token_host, 4, hipMemcpyHostToDevice, s), "write token"));
-  BCH_TRY(set_dpos(m, m->n_past));
-  hipEventRecord(m->ev0, s);
-  if (trace) {
-    record_step(m, s, false, true);
-  } else if (use_graphs()) {
-    if (!m->step_graph) BCH_TRY(capture(m, false, &m->step_graph));
-    BCH_TRY(check_hip(hipGraphLaunch(m->step_graph, s), "launch step graph"));
-  } else {
-    record_step(m, s, false, false);
-  }
-  BCH_TRY(finish(m));
-  const uint32_t n = m->n_embd;
-  const uint64_t tstride = (uint64_t)m->trace_rows * n;
-  if (logits) BCH_TRY(check_hip(hipMemcpy(logits, m->logits, (uint64_t)m->n_vocab * 4, hipMemcpyDeviceToHost), "read logits"));
-  if (trace_embedding) hipMemcpy(trace_embedding, m->trace, (uint64_t)n * 4, hipMemcpyDeviceToHost);
-  if (trace_layers)
-    for (uint32_t il = 0; il < m->n_layers; il++)
-      hipMemcpy(trace_layers + (uint64_t)il * n, m->trace + (1 + il) * tstride, (uint64_t)n * 4, hipMemcpyDeviceToHost);
-  if (trace_final) hipMemcpy(trace_final, m->trace + (1 + m->n_layers) * tstride, (uint64_t)n * 4, hipMemcpyDeviceToHost);
-  m->n_past++;
-  m->have_logits = true;
-  return BCH_OK;
+  return m->step(token, logits, trace_embedding, trace_layers, trace_final);
 }
 
 int bch_lfm2_prefill(bch_lfm2 *m, const uint32_t *tokens, uint32_t n_tokens, float *logits, float *trace_embedding,
                      float *trace_layers, float *trace_final) {
-  BCH_TRY(busy_check(m));
-  if (n_tokens == 0) return fail(BCH_ERR_ARGUMENT, "the prompt must hold a token");
-  if (n_tokens > m->n_ctx - m->n_past)
-    return fail(BCH_ERR_CONTEXT_FULL, "the prompt of %u tokens exceeds the %u free positions", n_tokens,
-                m->n_ctx - m->n_past);
-  for (uint32_t i = 0; i < n_tokens; i++)
-    if (tokens[i] >= m->n_vocab) return fail(BCH_ERR_TOKEN, "token %u is outside the vocabulary of %u", tokens[i], m->n_vocab);
-  hipStream_t s = m->s;
-  BCH_TRY(check_hip(hipMemcpyAsync(m->tokens + m->n_past, tokens, (uint64_t)n_tokens * 4, hipMemcpyHostToDevice, s),
-                    "write tokens"));
-  const bool trace = trace_embedding || trace_layers || trace_final;
-  if (trace) BCH_TRY(ensure_trace_rows(m, m->batch));
-  const uint32_t n = m->n_embd;
-  const uint64_t tstride = (uint64_t)m->trace_rows * n;
-  double gpu = 0.0;
-  for (uint32_t done = 0; done < n_tokens; done += m->batch) {
-    const uint32_t count = std::min(m->batch, n_tokens - done);
-    const bool last = done + count == n_tokens;
-    hipEventRecord(m->ev0, s);
-    record_batch(m, s, m->n_past + done, count, last, trace);
-    // A traced batch finishes before the next overwrites the trace rows, as
-    // in the reference (lfm2_metal.rs:727-746); others run back to back.
-    if (trace || last) {
-      BCH_TRY(finish(m));
-      gpu += m->last_gpu_seconds;
-    }
-    if (trace) {
-      const uint64_t rows = (uint64_t)count * n * 4;
-      if (trace_embedding) hipMemcpy(trace_embedding + (uint64_t)done * n, m->trace, rows, hipMemcpyDeviceToHost);
-      if (trace_final)
-        hipMemcpy(trace_final + (uint64_t)done * n, m->trace + (1 + m->n_layers) * tstride, rows, hipMemcpyDeviceToHost);
-      if (trace_layers)
-        for (uint32_t il = 0; il < m->n_layers; il++)
-          hipMemcpy(trace_layers + ((uint64_t)il * n_tokens + done) * n, m->trace + (1 + il) * tstride, rows,
-                    hipMemcpyDeviceToHost);
-    }
-  }
-  m->last_gpu_seconds = gpu;
-  if (logits) BCH_TRY(check_hip(hipMemcpy(logits, m->logits, (uint64_t)m->n_vocab * 4, hipMemcpyDeviceToHost), "read logits"));
-  m->n_past += n_tokens;
-  m->have_logits = true;
-  return BCH_OK;
+  return m->prefill(tokens, n_tokens, logits, trace_embedding, trace_layers, trace_final);
 }
 
-int bch_lfm2_greedy_token(bch_lfm2 *m, uint32_t *token) {
-  BCH_TRY(busy_check(m));
-  if (m->n_past == 0 || !m->have_logits) return fail(BCH_ERR_ARGUMENT, "generation needs a prompt first");
-  hipEventRecord(m->ev0, m->s);
-  run_argmax(m->s, m->logits, m->greedy, m->n_vocab, nullptr, false);
-  BCH_TRY(finish(m));
-  return check_hip(hipMemcpy(token, m->greedy, 4, hipMemcpyDeviceToHost), "read token");
-}
-
-int bch_lfm2_generate(bch_lfm2 *m, uint32_t *out, uint32_t n) {
-  BCH_TRY(busy_check(m));
-  if (m->n_past == 0 || !m->have_logits) return fail(BCH_ERR_ARGUMENT, "generation needs a prompt first");
-  if (n > m->n_ctx - m->n_past)
-    return fail(BCH_ERR_CONTEXT_FULL, "%u tokens exceed the %u free positions", n, m->n_ctx - m->n_past);
-  if (n == 0) return BCH_OK;
-  // Each replay writes argmax(logits) into tokens[dpos + 1], advances dpos
-  // and runs the step there; dpos starts at the last consumed position.  The
-  // current logits (from a prefill, a step or a restore) are reduced to
-  // argmax partials once; every step then leaves its own.
-  BCH_TRY(set_dpos(m, m->n_past - 1));
-  hipEventRecord(m->ev0, m->s);
-  run_argmax_partials(m->s, m->logits, m->n_vocab, m->argmax_partials, kArgmaxPartials);
-  if (use_graphs()) {
-    if (!m->gen_graph) BCH_TRY(capture(m, true, &m->gen_graph));
-    for (uint32_t i = 0; i < n; i++) BCH_TRY(check_hip(hipGraphLaunch(m->gen_graph, m->s), "launch decode graph"));
-  } else {
-    for (uint32_t i = 0; i < n; i++) record_step(m, m->s, true, false);
-  }
-  BCH_TRY(finish(m));
-  BCH_TRY(check_hip(hipMemcpy(out, m->tokens + m->n_past, (uint64_t)n * 4, hipMemcpyDeviceToHost), "read tokens"));
-  m->n_past += n;
-  return BCH_OK;
-}
-
-static SampleArgs sample_args(bch_lfm2 *m, const bch_sampling &st) {
-  SampleArgs a{};
-  a.logits = m->logits;
-  a.n = m->n_vocab;
-  a.recent = m->tokens;
-  a.dpos = m->dpos;
-  a.out = m->tokens;
-  a.rng = m->rng;
-  a.temperature = st.temperature;
-  a.top_p = st.top_p;
-  a.min_p = st.min_p;
-  a.penalty = st.repeat_penalty;
-  a.top_k = st.top_k;
-  return a;
-}
-
+int bch_lfm2_greedy_token(bch_lfm2 *m, uint32_t *token) { return m->greedy_token(token); }
+int bch_lfm2_generate(bch_lfm2 *m, uint32_t *out, uint32_t n) { return m->generate(out, n); }
 int bch_lfm2_generate_sampled(bch_lfm2 *m, uint32_t *out, uint32_t n, const bch_sampling *settings, uint64_t seed) {
-  BCH_TRY(busy_check(m));
-  if (!settings) return fail(BCH_ERR_ARGUMENT, "no sampling settings");
-  if (m->n_past == 0 || !m->have_logits) return fail(BCH_ERR_ARGUMENT, "generation needs a prompt first");
-  if (n > m->n_ctx - m->n_past)
-    return fail(BCH_ERR_CONTEXT_FULL, "%u tokens exceed the %u free positions", n, m->n_ctx - m->n_past);
-  if (n == 0) return BCH_OK;
-  // Each replay samples the current logits into tokens[dpos + 1], advances
-  // dpos and runs the step there; the settings are captured into the graph.
-  BCH_TRY(set_dpos(m, m->n_past - 1));
-  m->rng_host = seed;
-  BCH_TRY(check_hip(hipMemcpyAsync(m->rng, &m->rng_host, 8, hipMemcpyHostToDevice, m->s), "seed the sampler"));
-  const SampleArgs sa = sample_args(m, *settings);
-  hipEventRecord(m->ev0, m->s);
-  if (use_graphs()) {
-    if (m->sample_graph && memcmp(&m->sample_settings, settings, sizeof(bch_sampling)) != 0) {
-      hipGraphExecDestroy(m->sample_graph);
-      m->sample_graph = nullptr;
-    }
-    if (!m->sample_graph) {
-      hipStream_t s = m->s;
-      BCH_TRY(check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture"));
-      run_sample(s, sa);
-      record_step(m, s, false, false);
-      hipGraph_t g;
-      BCH_TRY(check_hip(hipStreamEndCapture(s, &g), "end capture"));
-      hipError_t e = hipGraphInstantiate(&m->sample_graph, g, nullptr, nullptr, 0);
-      hipGraphDestroy(g);
-      BCH_TRY(check_hip(e, "instantiate graph"));
-      m->sample_settings = *settings;
-    }
-    for (uint32_t i = 0; i < n; i++) BCH_TRY(check_hip(hipGraphLaunch(m->sample_graph, m->s), "launch sampling graph"));
-  } else {
-    for (uint32_t i = 0; i < n; i++) {
-      run_sample(m->s, sa);
-      record_step(m, m->s, false, false);
-    }
-  }
-  BCH_TRY(finish(m));
-  BCH_TRY(check_hip(hipMemcpy(out, m->tokens + m->n_past, (uint64_t)n * 4, hipMemcpyDeviceToHost), "read tokens"));
-  m->n_past += n;
-  return BCH_OK;
+  return m->generate_sampled(out, n, settings, seed);
 }
 
-// Checkpoint blob: resets (u64), n_past (u32), pad (u32), conv state, logits.
-uint64_t bch_lfm2_checkpoint_bytes(const bch_lfm2 *m) {
-  return 16 + ((uint64_t)m->n_conv * (m->conv_kernel - 1) * m->n_embd + m->n_vocab) * 4;
-}
-
-int bch_lfm2_checkpoint(bch_lfm2 *m, void *blob, uint64_t bytes) {
-  BCH_TRY(busy_check(m));
-  if (bytes != bch_lfm2_checkpoint_bytes(m)) return fail(BCH_ERR_ARGUMENT, "checkpoint buffer of the wrong size");
-  char *p = static_cast<char *>(blob);
-  memcpy(p, &m->resets, 8);
-  memcpy(p + 8, &m->n_past, 4);
-  const uint32_t have = m->have_logits;
-  memcpy(p + 12, &have, 4);
-  const uint64_t conv = (uint64_t)m->n_conv * (m->conv_kernel - 1) * m->n_embd * 4;
-  BCH_TRY(check_hip(hipMemcpy(p + 16, m->conv_state, conv, hipMemcpyDeviceToHost), "read conv state"));
-  return check_hip(hipMemcpy(p + 16 + conv, m->logits, (uint64_t)m->n_vocab * 4, hipMemcpyDeviceToHost), "read logits");
-}
-
-int bch_lfm2_restore(bch_lfm2 *m, const void *blob, uint64_t bytes) {
-  BCH_TRY(busy_check(m));
-  if (bytes != bch_lfm2_checkpoint_bytes(m))
-    return fail(BCH_ERR_ARGUMENT, "the checkpoint comes from a different model or context");
-  const char *p = static_cast<const char *>(blob);
-  uint64_t resets;
-  uint32_t n_past, have;
-  memcpy(&resets, p, 8);
-  memcpy(&n_past, p + 8, 4);
-  memcpy(&have, p + 12, 4);
-  if (resets != m->resets) return fail(BCH_ERR_ARGUMENT, "the checkpoint predates a reset");
-  if (n_past > m->n_ctx) return fail(BCH_ERR_ARGUMENT, "the checkpoint comes from a different model or context");
-  const uint64_t conv = (uint64_t)m->n_conv * (m->conv_kernel - 1) * m->n_embd * 4;
-  BCH_TRY(check_hip(hipMemcpy(m->conv_state, p + 16, conv, hipMemcpyHostToDevice), "write conv state"));
-  BCH_TRY(check_hip(hipMemcpy(m->logits, p + 16 + conv, (uint64_t)m->n_vocab * 4, hipMemcpyHostToDevice), "write logits"));
-  m->n_past = n_past;
-  m->have_logits = have != 0;
-  return BCH_OK;
-}
+// The checkpoint carries resets, n_past, the convolution state and the logits.
+uint64_t bch_lfm2_checkpoint_bytes(const bch_lfm2 *m) { return m->checkpoint_bytes(); }
+int bch_lfm2_checkpoint(bch_lfm2 *m, void *blob, uint64_t bytes) { return m->checkpoint(blob, bytes); }
+int bch_lfm2_restore(bch_lfm2 *m, const void *blob, uint64_t bytes) { return m->restore(blob, bytes); }
 
 }  // extern "C"
