@@ -38,6 +38,10 @@ class Sampling(C.Structure):
                 ("repeat_penalty", C.c_float)]
 
 
+class DeltaShape(C.Structure):
+    _fields_ = [("n_k_heads", C.c_uint32), ("n_v_heads", C.c_uint32), ("k_dim", C.c_uint32), ("v_dim", C.c_uint32)]
+
+
 class Norm(C.Structure):
     _fields_ = [("weight", View), ("eps", C.c_float)]
 
@@ -144,6 +148,24 @@ PROTOTYPES = {
     "bch_argmax": (_int, [_vp, View, View, _u32]),
     "bch_read_sum": (_int, [_vp, View, _u64, View, _u32]),
     "bch_route_bytes": (_u64, [_u32, _u32]),
+    "bch_gdn_conv": (_int, [_vp, View, View, View, View, _u32, _u32, _u32]),
+    "bch_gdn_gates": (_int, [_vp, View, View, View, View, _u32, _u32]),
+    "bch_gdn_recurrence": (_int, [_vp, View, View, View, View, View, C.POINTER(DeltaShape), _u32, C.c_float]),
+    "bch_gdn_gated_norm": (_int, [_vp, View, View, View, _u32, _u32, C.c_float]),
+    "bch_attention_gate": (_int, [_vp, View, View, _u32, _u32, _u32]),
+    "bch_qwen35_new": (_int, [_vp, C.POINTER(Qwen35Model), _u32, _int, C.POINTER(_vp)]),
+    "bch_qwen35_free": (None, [_vp]),
+    "bch_qwen35_n_past": (_u32, [_vp]),
+    "bch_qwen35_reset": (_int, [_vp]),
+    "bch_qwen35_step": (_int, [_vp, _u32, _FP, _FP, _FP, _FP]),
+    "bch_qwen35_prefill": (_int, [_vp, C.POINTER(C.c_uint32), _u32, _FP, _FP, _FP, _FP]),
+    "bch_qwen35_greedy_token": (_int, [_vp, C.POINTER(C.c_uint32)]),
+    "bch_qwen35_generate": (_int, [_vp, C.POINTER(C.c_uint32), _u32]),
+    "bch_qwen35_generate_sampled": (_int, [_vp, C.POINTER(C.c_uint32), _u32, C.POINTER(Sampling), _u64]),
+    "bch_qwen35_checkpoint_bytes": (_u64, [_vp]),
+    "bch_qwen35_checkpoint": (_int, [_vp, _vp, _u64]),
+    "bch_qwen35_restore": (_int, [_vp, _vp, _u64]),
+    "bch_qwen35_last_gpu_seconds": (C.c_double, [_vp]),
     "bch_sample": (_int, [_vp, View, _u32, View, _u32, C.POINTER(Sampling), View, View]),
     "bch_lfm2_generate_sampled": (_int, [_vp, C.POINTER(C.c_uint32), _u32, C.POINTER(Sampling), _u64]),
     "bch_moe_route": (_int, [_vp, View, C.POINTER(Norm), View, View, View, View, _u32, _u32, _u32, _u32]),

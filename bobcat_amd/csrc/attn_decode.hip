@@ -14,14 +14,16 @@
 //   1. issues all its key and value loads at once: coalesced 16-byte chunks,
 //      a cache row shared by consecutive lanes, eight chunks of K and eight
 //      of V per lane held in registers;
-//   2. meanwhile normalises and rotates its query head into LDS and, if it
-//      owns the newest position, the new key and value (the group's first
-//      head also stores them in the cache; no other split reads them);
+//   2. meanwhile normalises and rotates (the first n_rot elements of) its
+//      query head into LDS and, if it owns the newest position, the new key
+//      and value (the group's first head also stores them in the cache; no
+//      other split reads them);
 //   3. scores the keys with a DPP reduction over each row's lanes, takes the
 //      softmax, and accumulates P·V from the value registers, reduced by lane
 //      moves within a wave and through LDS across waves; waves past the last
 //      key skip both;
-//   4. with several splits, writes (max, sum, output) partials through
+//   4. scales the output by the sigmoid gate of gated attention when given;
+//      with several splits, writes (max, sum, output) partials through
 //      device-coherent stores and counts itself in; the last split to arrive
 //      combines.  Data cross XCDs via sc1 stores/loads instead of device-scope
 //      fences, which would write back the whole L2.
@@ -151,9 +153,10 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
   // head of the group rotates the new key for itself; the group's first
   // head also stores key and value in the cache.
   const float position = (float)pos;
-  if (wave == 0) norm_rope_wave(a.q + (uint64_t)head * hd, a.q_norm, a.freqs, hd, hd, position, a.eps, q_s);
+  if (wave == 0)
+    norm_rope_wave(a.q + (uint64_t)head * a.q_head_stride, a.q_norm, a.freqs, hd, a.n_rot, position, a.eps, q_s);
   if (owns_new && wave == 1) {
-    norm_rope_wave(a.k + (uint64_t)kvh * hd, a.k_norm, a.freqs, hd, hd, position, a.eps, knew_s);
+    norm_rope_wave(a.k + (uint64_t)kvh * hd, a.k_norm, a.freqs, hd, a.n_rot, position, a.eps, knew_s);
     const bool store = head % group == 0;
     for (uint32_t i = lane; i < hd; i += 64) {
       const uint64_t at = (uint64_t)pos * kv_dim + (uint64_t)kvh * hd + i;
@@ -284,8 +287,10 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
 #pragma unroll
     for (int w = 0; w < kWaves; w++) o += red_s[w][tid];
   }
+  // The output gate of gated attention (qwen35.rs:422-424).
+  const float gate = (a.gate && tid < hd) ? 1.0f / (1.0f + expf(-a.gate[(uint64_t)head * a.gate_head_stride + tid])) : 1.0f;
   if (n_splits == 1) {
-    if (tid < hd) a.out[(uint64_t)head * hd + tid] = o / l_s;
+    if (tid < hd) a.out[(uint64_t)head * hd + tid] = o / l_s * gate;
     return;
   }
   const uint32_t stride = hd + 2;
@@ -315,7 +320,7 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
       L = fmaf(coherent_load(pp + sp * stride + 1), w, L);
       O = fmaf(coherent_load(pp + sp * stride + 2 + tid), w, O);
     }
-    a.out[(uint64_t)head * hd + tid] = O / L;
+    a.out[(uint64_t)head * hd + tid] = O / L * gate;
   }
   if (tid == 0) coherent_store(&a.counters[head], 0u);
 }

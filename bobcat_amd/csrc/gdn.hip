@@ -1,0 +1,279 @@
+// Gated DeltaNet kernels and the output gate of Qwen3.5's attention: the
+// MI355X counterparts of gdn_conv / gdn_gates / gdn_recurrence /
+// gdn_gated_norm / attention_gate (crates/bobcat-metal/src/gdn.metal) and of
+// the CPU Model::delta_net (crates/bobcat/src/qwen35.rs:430-516).
+//
+// The recurrence gives every column of a value head's state its own wave:
+// a column evolves on its own given the token's key, query, value entry and
+// gates (remembered_c = Σ_r S[r][c]·k[r], S[r][c] += k[r]·β(v_c − remembered_c),
+// out_c = Σ_r S[r][c]·q[r]), so the k_dim rows of a column live in the
+// registers of one wave (k_dim/64 per lane) for a whole prefill batch and the
+// two dot products per token are wave reductions.  16 heads of 128 columns
+// make 2048 waves.  The next token's query, key and value are loaded before
+// the current token's update, which does not depend on them.
+#include <cmath>
+
+#include "device.h"
+#include "kernels.h"
+#include "runtime.h"
+
+namespace bch {
+
+constexpr int kGdnCols = 4;  // columns (waves) per workgroup
+
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+// transformers' softplus returns its input above 20 (qwen35.rs:775-778).
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+template <int RPL>
+__global__ __launch_bounds__(kGdnCols * 64) void k_gdn_recurrence(GdnArgs a) {
+  const uint32_t lane = threadIdx.x % 64, col = blockIdx.x * kGdnCols + threadIdx.x / 64, head = blockIdx.y;
+  const uint32_t key_head = head % a.n_k, key_dim = a.n_k * a.k_dim, conv_dim = 2 * key_dim + a.n_v * a.v_dim;
+  const uint32_t r0 = lane * RPL;
+  float *S = a.state + (uint64_t)head * a.k_dim * a.v_dim;
+  float rows[RPL];
+#pragma unroll
+  for (int i = 0; i < RPL; i++) rows[i] = S[(uint64_t)(r0 + i) * a.v_dim + col];
+  auto load = [&](uint32_t t, float *q, float *k, float &v, float &b, float &d) {
+    const float *tok = a.y + (uint64_t)t * conv_dim;
+#pragma unroll
+    for (int i = 0; i < RPL; i++) {
+      q[i] = tok[key_head * a.k_dim + r0 + i];
+      k[i] = tok[key_dim + key_head * a.k_dim + r0 + i];
+    }
+    v = tok[2 * key_dim + head * a.v_dim + col];
+    b = a.beta[(uint64_t)t * a.n_v + head];
+    d = a.alpha[(uint64_t)t * a.n_v + head];
+  };
+  float q[RPL], k[RPL], v, b, d;
+  load(0, q, k, v, b, d);
+  for (uint32_t t = 0; t < a.n_tokens; t++) {
+    float nq[RPL], nk[RPL], nv = 0.f, nb = 0.f, nd = 0.f;
+    if (t + 1 < a.n_tokens) load(t + 1, nq, nk, nv, nb, nd);
+    // l2_normalize of the query (times q_scale) and the key (qwen35.rs:464-470).
+    float sq = 0.f, sk = 0.f;
+#pragma unroll
+    for (int i = 0; i < RPL; i++) {
+      sq = fmaf(q[i], q[i], sq);
+      sk = fmaf(k[i], k[i], sk);
+    }
+    sq = wave_sum(sq);
+    sk = wave_sum(sk);
+    const float fq = a.q_scale / sqrtf(sq + 1e-6f), fk = 1.0f / sqrtf(sk + 1e-6f);
+    const float beta = a.raw_gates ? sigmoid_f(b) : b;
+    const float decay = a.raw_gates ? expf(a.a[head] * softplus_f(d + a.dt_bias[head])) : d;
+    float rem = 0.f;
+#pragma unroll
+    for (int i = 0; i < RPL; i++) {
+      rows[i] *= decay;
+      rem = fmaf(rows[i], k[i] * fk, rem);
+    }
+    rem = wave_sum(rem);
+    const float delta = (v - rem) * beta;
+    float o = 0.f;
+#pragma unroll
+    for (int i = 0; i < RPL; i++) {
+      rows[i] = fmaf(k[i] * fk, delta, rows[i]);
+      o = fmaf(rows[i], q[i] * fq, o);
+    }
+    o = wave_sum(o);
+    if (lane == 0) a.out[(uint64_t)t * a.n_v * a.v_dim + head * a.v_dim + col] = o;
+#pragma unroll
+    for (int i = 0; i < RPL; i++) {
+      q[i] = nq[i];
+      k[i] = nk[i];
+    }
+    v = nv;
+    b = nb;
+    d = nd;
+  }
+#pragma unroll
+  for (int i = 0; i < RPL; i++) S[(uint64_t)(r0 + i) * a.v_dim + col] = rows[i];
+}
+
+bool run_gdn_recurrence(hipStream_t s, const GdnArgs &a) {
+  if (a.v_dim % kGdnCols || a.n_tokens == 0) return false;
+  const dim3 grid(a.v_dim / kGdnCols, a.n_v);
+  if (a.k_dim == 64)
+    k_gdn_recurrence<1><<<grid, kGdnCols * 64, 0, s>>>(a);
+  else if (a.k_dim == 128)
+    k_gdn_recurrence<2><<<grid, kGdnCols * 64, 0, s>>>(a);
+  else
+    return false;
+  return true;
+}
+
+// The causal convolution with SiLU of gdn_conv / the DeltaNet step
+// (qwen35.rs:448-462): thread c walks the tokens of channel c with its
+// history in registers, then leaves the latest k-1 inputs in `hist`.
+__global__ void k_gdn_conv(const float *__restrict__ x, const float *__restrict__ taps, float *__restrict__ hist,
+                           float *__restrict__ y, uint32_t channels, uint32_t ksize, uint32_t n_tokens) {
+  const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= channels) return;
+  const uint32_t past = ksize - 1;
+  float window[kGdnMaxKernel - 1];
+  float tp[kGdnMaxKernel];
+#pragma unroll
+  for (uint32_t i = 0; i < kGdnMaxKernel; i++) tp[i] = i < ksize ? taps[(uint64_t)c * ksize + i] : 0.f;
+#pragma unroll
+  for (uint32_t i = 0; i < kGdnMaxKernel - 1; i++) window[i] = i < past ? hist[(uint64_t)c * past + i] : 0.f;
+  for (uint32_t t = 0; t < n_tokens; t++) {
+    const float input = x[(uint64_t)t * channels + c];
+    // The newest term first, then the history oldest first, as the reference adds them.
+    float sum = tp[past] * input;
+#pragma unroll
+    for (uint32_t i = 0; i < kGdnMaxKernel - 1; i++)
+      if (i < past) sum += tp[i] * window[i];
+    y[(uint64_t)t * channels + c] = sum / (1.0f + expf(-sum));
+#pragma unroll
+    for (uint32_t i = 0; i + 1 < kGdnMaxKernel - 1; i++)
+      if (i + 1 < past) window[i] = window[i + 1];
+#pragma unroll
+    for (uint32_t i = 0; i < kGdnMaxKernel - 1; i++)
+      if (i + 1 == past) window[i] = input;
+  }
+#pragma unroll
+  for (uint32_t i = 0; i < kGdnMaxKernel - 1; i++)
+    if (i < past) hist[(uint64_t)c * past + i] = window[i];
+}
+
+void run_gdn_conv(hipStream_t s, const float *x, const float *taps, float *hist, float *y, uint32_t channels,
+                  uint32_t ksize, uint32_t n_tokens) {
+  k_gdn_conv<<<(channels + 255) / 256, 256, 0, s>>>(x, taps, hist, y, channels, ksize, n_tokens);
+}
+
+// gdn_gates (gdn.metal:125-149): beta <- sigmoid(beta), alpha <- the decay
+// exp(a·softplus(alpha + dt_bias)), per value head of each token.
+__global__ void k_gdn_gates(float *beta, float *alpha, const float *a, const float *dt_bias, uint32_t n_v,
+                            uint32_t n) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t h = i % n_v;
+  beta[i] = sigmoid_f(beta[i]);
+  alpha[i] = expf(a[h] * softplus_f(alpha[i] + dt_bias[h]));
+}
+
+void run_gdn_gates(hipStream_t s, float *beta, float *alpha, const float *a, const float *dt_bias, uint32_t n_v,
+                   uint32_t n) {
+  k_gdn_gates<<<(n + 255) / 256, 256, 0, s>>>(beta, alpha, a, dt_bias, n_v, n);
+}
+
+// The gated output norm (qwen35.rs:505-511): one wave per row of v_dim.
+__global__ __launch_bounds__(64) void k_gdn_gated_norm(float *x, const float *__restrict__ w,
+                                                       const float *__restrict__ z, uint32_t v_dim, float eps) {
+  float *row = x + (uint64_t)blockIdx.x * v_dim;
+  const float *g = z + (uint64_t)blockIdx.x * v_dim;
+  float ss = 0.f;
+  for (uint32_t i = threadIdx.x; i < v_dim; i += 64) ss = fmaf(row[i], row[i], ss);
+  ss = wave_sum(ss);
+  const float scale = (float)(1.0 / sqrt((double)ss / (double)v_dim + (double)eps));
+  for (uint32_t i = threadIdx.x; i < v_dim; i += 64) {
+    const float gi = g[i];
+    row[i] = w[i] * (row[i] * scale) * (gi / (1.0f + expf(-gi)));
+  }
+}
+
+void run_gdn_gated_norm(hipStream_t s, float *x, const float *w, const float *z, uint32_t v_dim, uint32_t n_rows,
+                        float eps) {
+  k_gdn_gated_norm<<<n_rows, 64, 0, s>>>(x, w, z, v_dim, eps);
+}
+
+// attention_gate (gdn.metal:306-322): each query head's output times the
+// sigmoid of its gate, which follows its queries in the projection.
+__global__ void k_attention_gate(float *attn, const float *q_gate, uint32_t head_dim, uint32_t q_dim, uint64_t n) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t t = i / q_dim;
+  const uint32_t e = (uint32_t)(i % q_dim), h = e / head_dim, d = e % head_dim;
+  attn[i] *= sigmoid_f(q_gate[t * 2 * q_dim + (uint64_t)(2 * h + 1) * head_dim + d]);
+}
+
+void run_attention_gate(hipStream_t s, float *attn, const float *q_gate, uint32_t head_dim, uint32_t q_dim,
+                        uint32_t n_tokens) {
+  const uint64_t n = (uint64_t)n_tokens * q_dim;
+  k_attention_gate<<<(uint32_t)((n + 255) / 256), 256, 0, s>>>(attn, q_gate, head_dim, q_dim, n);
+}
+
+}  // namespace bch
+
+// ---------------------------------------------------------------------
+// C ABI (Metal::gdn_conv / gdn_gates / gdn_recurrence / gdn_gated_norm /
+// attention_gate, crates/bobcat-metal/src/backend.rs).
+// ---------------------------------------------------------------------
+
+using namespace bch;
+
+extern "C" int bch_gdn_conv(bch_ctx *ctx, bch_view x, bch_view taps, bch_view history, bch_view y, uint32_t channels,
+                            uint32_t kernel_size, uint32_t n_tokens) {
+  if (kernel_size < 2 || kernel_size > kGdnMaxKernel)
+    return fail(BCH_ERR_DELTANET_LIMITS, "gdn_conv: 2 to %u taps, got %u", kGdnMaxKernel, kernel_size);
+  const float *xp, *tp;
+  float *hp, *yp;
+  BCH_TRY(view_ptr(ctx, "gdn_conv", x, (uint64_t)n_tokens * channels * 4, &xp));
+  BCH_TRY(view_ptr(ctx, "gdn_conv", taps, (uint64_t)channels * kernel_size * 4, &tp));
+  BCH_TRY(view_ptr(ctx, "gdn_conv", history, (uint64_t)channels * (kernel_size - 1) * 4, &hp));
+  BCH_TRY(view_ptr(ctx, "gdn_conv", y, (uint64_t)n_tokens * channels * 4, &yp));
+  return launch(ctx, {"gdn_conv", channels, kernel_size, 0},
+                [&](hipStream_t s) { run_gdn_conv(s, xp, tp, hp, yp, channels, kernel_size, n_tokens); });
+}
+
+extern "C" int bch_gdn_gates(bch_ctx *ctx, bch_view beta, bch_view alpha, bch_view a, bch_view dt_bias,
+                             uint32_t n_v_heads, uint32_t n) {
+  if (n_v_heads == 0) return fail(BCH_ERR_ARGUMENT, "gdn_gates: no heads");
+  float *bp, *ap;
+  const float *a_p, *dp;
+  BCH_TRY(view_ptr(ctx, "gdn_gates", beta, (uint64_t)n * 4, &bp));
+  BCH_TRY(view_ptr(ctx, "gdn_gates", alpha, (uint64_t)n * 4, &ap));
+  BCH_TRY(view_ptr(ctx, "gdn_gates", a, (uint64_t)n_v_heads * 4, &a_p));
+  BCH_TRY(view_ptr(ctx, "gdn_gates", dt_bias, (uint64_t)n_v_heads * 4, &dp));
+  return launch(ctx, {"gdn_gates", n, n_v_heads, 0}, [&](hipStream_t s) { run_gdn_gates(s, bp, ap, a_p, dp, n_v_heads, n); });
+}
+
+extern "C" int bch_gdn_recurrence(bch_ctx *ctx, bch_view y, bch_view beta, bch_view decay, bch_view state,
+                                  bch_view out, const bch_delta_shape *shape, uint32_t n_tokens, float q_scale) {
+  if (!shape) return fail(BCH_ERR_ARGUMENT, "gdn_recurrence: no shape");
+  const uint32_t nk = shape->n_k_heads, nv = shape->n_v_heads, dk = shape->k_dim, dv = shape->v_dim;
+  if (nk == 0 || nv % nk || (dk != 64 && dk != 128) || dv == 0 || dv % kGdnCols)
+    return fail(BCH_ERR_DELTANET_LIMITS,
+                "gdn_recurrence: key heads of 64 or 128, value heads a multiple of %d and of the key heads "
+                "(got %u/%u heads of %u/%u)", kGdnCols, nk, nv, dk, dv);
+  GdnArgs a{};
+  const uint64_t conv_dim = 2ull * nk * dk + (uint64_t)nv * dv;
+  BCH_TRY(view_ptr(ctx, "gdn_recurrence", y, (uint64_t)n_tokens * conv_dim * 4, &a.y));
+  BCH_TRY(view_ptr(ctx, "gdn_recurrence", beta, (uint64_t)n_tokens * nv * 4, &a.beta));
+  BCH_TRY(view_ptr(ctx, "gdn_recurrence", decay, (uint64_t)n_tokens * nv * 4, &a.alpha));
+  BCH_TRY(view_ptr(ctx, "gdn_recurrence", state, (uint64_t)nv * dk * dv * 4, &a.state));
+  BCH_TRY(view_ptr(ctx, "gdn_recurrence", out, (uint64_t)n_tokens * nv * dv * 4, &a.out));
+  a.n_k = nk;
+  a.n_v = nv;
+  a.k_dim = dk;
+  a.v_dim = dv;
+  a.n_tokens = n_tokens;
+  a.q_scale = q_scale;
+  a.raw_gates = false;
+  if (n_tokens == 0) return BCH_OK;
+  return launch(ctx, {"gdn_recurrence", nv, dv, (uint64_t)nv * dk * dv * 8},
+                [&](hipStream_t s) { run_gdn_recurrence(s, a); });
+}
+
+extern "C" int bch_gdn_gated_norm(bch_ctx *ctx, bch_view x, bch_view weight, bch_view z, uint32_t v_dim, uint32_t n_rows,
+                                  float eps) {
+  float *xp;
+  const float *wp, *zp;
+  BCH_TRY(view_ptr(ctx, "gdn_gated_norm", x, (uint64_t)n_rows * v_dim * 4, &xp));
+  BCH_TRY(view_ptr(ctx, "gdn_gated_norm", weight, (uint64_t)v_dim * 4, &wp));
+  BCH_TRY(view_ptr(ctx, "gdn_gated_norm", z, (uint64_t)n_rows * v_dim * 4, &zp));
+  return launch(ctx, {"gdn_gated_norm", n_rows, v_dim, 0},
+                [&](hipStream_t s) { run_gdn_gated_norm(s, xp, wp, zp, v_dim, n_rows, eps); });
+}
+
+extern "C" int bch_attention_gate(bch_ctx *ctx, bch_view attn, bch_view q_gate, uint32_t head_dim, uint32_t q_dim,
+                                  uint32_t n_tokens) {
+  if (head_dim == 0 || q_dim % head_dim) return fail(BCH_ERR_GATE_SHAPE, "attention_gate: %u is not whole heads of %u", q_dim, head_dim);
+  float *ap;
+  const float *gp;
+  BCH_TRY(view_ptr(ctx, "attention_gate", attn, (uint64_t)n_tokens * q_dim * 4, &ap));
+  BCH_TRY(view_ptr(ctx, "attention_gate", q_gate, (uint64_t)n_tokens * 2 * q_dim * 4, &gp));
+  return launch(ctx, {"attention_gate", n_tokens, q_dim, 0},
+                [&](hipStream_t s) { run_attention_gate(s, ap, gp, head_dim, q_dim, n_tokens); });
+}

@@ -99,6 +99,48 @@ struct ExpertSwigluItems {
   }
 };
 
+// The input projections of a Gated DeltaNet token in one launch
+// (qwen35.rs:442-462): rows [0, r0) are the q/k/v channels, each followed by
+// its causal convolution and SiLU as qwen35.rs:448-462 runs them (history
+// [channel][k-1], the oldest first), rows [r0, r0+r1) the output gate z,
+// then r2 rows of beta and r2 of alpha (raw; the recurrence gates them).
+struct GdnInItems {
+  static constexpr int kRows = 1;
+  static constexpr bool kArgmax = false;
+  const uint8_t *Wqkv, *Wz, *Wb, *Wa;
+  uint32_t r0, r1, r2;
+  uint64_t rb;
+  const float *taps;
+  float *hist;
+  uint32_t ksize;
+  float *conv_out, *z, *beta, *alpha;
+  __device__ const uint8_t *row(uint32_t item, int) const {
+    if (item < r0) return Wqkv + (uint64_t)item * rb;
+    if (item < r0 + r1) return Wz + (uint64_t)(item - r0) * rb;
+    if (item < r0 + r1 + r2) return Wb + (uint64_t)(item - r0 - r1) * rb;
+    return Wa + (uint64_t)(item - r0 - r1 - r2) * rb;
+  }
+  __device__ void store(uint32_t item, const float *v, float scale) const {
+    const float y = v[0] * scale;
+    if (item < r0) {
+      const uint32_t past = ksize - 1;
+      const float *tp = taps + (uint64_t)item * ksize;
+      float *h = hist + (uint64_t)item * past;
+      float sum = tp[past] * y;
+      for (uint32_t j = 0; j < past; j++) sum += tp[j] * h[j];
+      conv_out[item] = silu_g(sum);
+      for (uint32_t j = 0; j + 1 < past; j++) h[j] = h[j + 1];
+      h[past - 1] = y;
+    } else if (item < r0 + r1) {
+      z[item - r0] = y;
+    } else if (item < r0 + r1 + r2) {
+      beta[item - r0 - r1] = y;
+    } else {
+      alpha[item - r0 - r1 - r2] = y;
+    }
+  }
+};
+
 struct ThreeItems {
   static constexpr int kRows = 1;
   static constexpr bool kArgmax = false;
@@ -433,6 +475,16 @@ bool fast_matvec_experts_swiglu(hipStream_t s, uint32_t format, const uint8_t *W
   const uint64_t rb = bch_row_bytes(format, n_cols);
   return gemv_any(s, format, ExpertSwigluItems{Wg, Wu, rb, ids, n_ff, y}, x, nullptr, 0.f, n_used * n_ff, n_cols,
                   n_cus);
+}
+
+bool fast_matvec_gdn_in(hipStream_t s, uint32_t format, const uint8_t *Wqkv, const uint8_t *Wz, const uint8_t *Wb,
+                        const uint8_t *Wa, uint32_t conv_dim, uint32_t value_dim, uint32_t n_v, uint32_t n_cols,
+                        const float *x, const float *nw, float eps, const float *taps, float *hist, uint32_t ksize,
+                        float *conv_out, float *z, float *beta, float *alpha, uint32_t n_cus) {
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  return gemv_any(s, format,
+                  GdnInItems{Wqkv, Wz, Wb, Wa, conv_dim, value_dim, n_v, rb, taps, hist, ksize, conv_out, z, beta, alpha},
+                  x, nw, eps, conv_dim + value_dim + 2 * n_v, n_cols, n_cus);
 }
 
 bool fast_matvec_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const uint8_t *Wu, uint32_t n_rows,

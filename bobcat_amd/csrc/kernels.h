@@ -29,6 +29,10 @@ struct AttnDecodeArgs {
   float *out;                      // [n_heads * head_dim]
   uint32_t n_heads, n_kv, head_dim, max_splits;
   const uint32_t *dpos;
+  uint32_t q_head_stride;          // floats from one query head to the next in q
+  uint32_t n_rot;                  // leading elements of a head that RoPE rotates
+  const float *gate;               // nullable: out[h] *= sigmoid(gate[h·gate_head_stride ..])
+  uint32_t gate_head_stride;
 };
 uint32_t attn_decode_keys_per_split(uint32_t head_dim, bool kv_half);
 uint32_t attn_decode_max_splits(uint32_t n_ctx, uint32_t head_dim, bool kv_half);
@@ -86,6 +90,38 @@ bool fast_matvec_experts_swiglu(hipStream_t s, uint32_t format, const uint8_t *W
 // false when the shape or format has no kernel.
 bool run_experts_down(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols,
                       const float *x, const uint32_t *route, uint32_t n_used, float *y, uint32_t n_cus);
+
+// gdn.hip + gemv.hip: Gated DeltaNet (qwen35.rs:430-516).  A DeltaNet token
+// holds conv_dim = 2·n_k·k_dim + n_v·v_dim floats after its projection: the
+// query heads, the key heads, the value heads; value head j reads key head
+// j % n_k.  States are [head][k_dim rows][v_dim columns] (qwen35.rs:570-576).
+constexpr uint32_t kGdnMaxKernel = 8;  // GDN_MAX_KERNEL
+bool fast_matvec_gdn_in(hipStream_t s, uint32_t format, const uint8_t *Wqkv, const uint8_t *Wz, const uint8_t *Wb,
+                        const uint8_t *Wa, uint32_t conv_dim, uint32_t value_dim, uint32_t n_v, uint32_t n_cols,
+                        const float *x, const float *nw, float eps, const float *taps, float *hist, uint32_t ksize,
+                        float *conv_out, float *z, float *beta, float *alpha, uint32_t n_cus);
+struct GdnArgs {
+  const float *y;                 // [n_tokens][conv_dim], after the convolution
+  const float *beta, *alpha;      // [n_tokens][n_v]: raw projections (raw_gates) or gated
+  const float *a, *dt_bias;       // [n_v], for raw gates
+  float *state;                   // [n_v][k_dim][v_dim]
+  float *out;                     // [n_tokens][n_v·v_dim]
+  uint32_t n_k, n_v, k_dim, v_dim, n_tokens;
+  float q_scale;
+  bool raw_gates;
+};
+// false when k_dim is not 64 or 128 (or v_dim not a multiple of the columns per workgroup).
+bool run_gdn_recurrence(hipStream_t s, const GdnArgs &a);
+void run_gdn_conv(hipStream_t s, const float *x, const float *taps, float *hist, float *y, uint32_t channels,
+                  uint32_t ksize, uint32_t n_tokens);
+void run_gdn_gates(hipStream_t s, float *beta, float *alpha, const float *a, const float *dt_bias, uint32_t n_v,
+                   uint32_t n);
+// x[r] (v_dim floats per row) = w ⊙ rmsnorm(x[r]) ⊙ silu(z[r]), in place.
+void run_gdn_gated_norm(hipStream_t s, float *x, const float *w, const float *z, uint32_t v_dim, uint32_t n_rows,
+                        float eps);
+// attn[t][h·hd + d] *= sigmoid(q_gate[t][(2h + 1)·hd + d]).
+void run_attention_gate(hipStream_t s, float *attn, const float *q_gate, uint32_t head_dim, uint32_t q_dim,
+                        uint32_t n_tokens);
 
 // sample.hip: Sampler::sample on the GPU.  With dpos, the recent tokens
 // are recent[0..*dpos] and the token goes to out[*dpos + 1], advancing

@@ -152,6 +152,10 @@ static void lfm2_step(bch_lfm2 *m, hipStream_t s, bool greedy_input, bool trace)
       ad.head_dim = m->head_dim;
       ad.max_splits = attn_decode_max_splits(m->n_ctx, m->head_dim, m->kv_half);
       ad.dpos = dp;
+      ad.q_head_stride = m->head_dim;
+      ad.n_rot = m->head_dim;
+      ad.gate = nullptr;
+      ad.gate_head_stride = 0;
       run_attn_decode(s, ad, m->kv_half);
       run_matvec(s, L.wo.format, L.wo.data, n, m->q_dim, m->attn, m->hidden, nullptr, 0.f, true, cus);
     }

@@ -171,20 +171,25 @@ class Lfm2Weights:
         return self.cfg.hp
 
 
-class Lfm2Hip:
-    """bch_lfm2: one LFM2 sequence on the GPU (Lfm2Metal's API)."""
+class SequenceHip:
+    """One sequence of a model driver on the GPU (the API of Lfm2Metal and
+    Qwen35Metal); subclasses name the C functions' prefix."""
+    _prefix = ""
+
+    def _fn(self, name: str):
+        return getattr(lib(), self._prefix + name)
 
     def __init__(self, hip: Hip, weights: Lfm2Weights, n_ctx: int, kv_half: bool = True):
         self.hip, self.weights, self.cfg = hip, weights, weights.cfg
         h = C.c_void_p()
-        check(lib().bch_lfm2_new(hip.handle, C.byref(weights.c_model), n_ctx, int(kv_half), C.byref(h)))
+        check(self._fn("new")(hip.handle, C.byref(weights.c_model), n_ctx, int(kv_half), C.byref(h)))
         self.handle = h.value
         self.n_ctx = n_ctx
         hip._dependents.add(self)
 
     def close(self):
         if self.handle:
-            lib().bch_lfm2_free(self.handle)
+            self._fn("free")(self.handle)
             self.handle = None
 
     def __del__(self):
@@ -195,14 +200,14 @@ class Lfm2Hip:
 
     @property
     def n_past(self) -> int:
-        return lib().bch_lfm2_n_past(self.handle)
+        return self._fn("n_past")(self.handle)
 
     @property
     def last_gpu_seconds(self) -> float:
-        return lib().bch_lfm2_last_gpu_seconds(self.handle)
+        return self._fn("last_gpu_seconds")(self.handle)
 
     def reset(self) -> None:
-        check(lib().bch_lfm2_reset(self.handle))
+        check(self._fn("reset")(self.handle))
 
     def step(self, token: int, logits: bool = True, trace: bool = False):
         cfg = self.cfg
@@ -211,7 +216,7 @@ class Lfm2Hip:
         tl = np.empty(cfg.n_layers * cfg.n_embd, np.float32) if trace else None
         tf = np.empty(cfg.n_embd, np.float32) if trace else None
         ptr = lambda a: None if a is None else a.ctypes.data_as(C.POINTER(C.c_float))
-        check(lib().bch_lfm2_step(self.handle, token, ptr(lg), ptr(te), ptr(tl), ptr(tf)))
+        check(self._fn("step")(self.handle, token, ptr(lg), ptr(te), ptr(tl), ptr(tf)))
         return (lg, (te, tl, tf)) if trace else lg
 
     def prefill(self, tokens, logits: bool = True, trace: bool = False):
@@ -224,33 +229,38 @@ class Lfm2Hip:
         tl = np.empty((cfg.n_layers, t.size, cfg.n_embd), np.float32) if trace else None
         tf = np.empty((t.size, cfg.n_embd), np.float32) if trace else None
         ptr = lambda a: None if a is None else a.ctypes.data_as(C.POINTER(C.c_float))
-        check(lib().bch_lfm2_prefill(self.handle, t.ctypes.data_as(C.POINTER(C.c_uint32)), t.size,
+        check(self._fn("prefill")(self.handle, t.ctypes.data_as(C.POINTER(C.c_uint32)), t.size,
                                      ptr(lg), ptr(te), ptr(tl), ptr(tf)))
         return (lg, (te, tl, tf)) if trace else lg
 
     def greedy_token(self) -> int:
         t = C.c_uint32()
-        check(lib().bch_lfm2_greedy_token(self.handle, C.byref(t)))
+        check(self._fn("greedy_token")(self.handle, C.byref(t)))
         return t.value
 
     def generate(self, n: int) -> np.ndarray:
         out = np.empty(n, np.uint32)
-        check(lib().bch_lfm2_generate(self.handle, out.ctypes.data_as(C.POINTER(C.c_uint32)), n))
+        check(self._fn("generate")(self.handle, out.ctypes.data_as(C.POINTER(C.c_uint32)), n))
         return out
 
     def generate_sampled(self, n: int, settings, seed: int) -> np.ndarray:
         """n tokens drawn by the GPU sampler (settings: a bch_sampling)."""
         out = np.empty(n, np.uint32)
-        check(lib().bch_lfm2_generate_sampled(self.handle, out.ctypes.data_as(C.POINTER(C.c_uint32)), n,
+        check(self._fn("generate_sampled")(self.handle, out.ctypes.data_as(C.POINTER(C.c_uint32)), n,
                                               C.byref(settings), seed))
         return out
 
     def checkpoint(self) -> bytes:
-        nb = lib().bch_lfm2_checkpoint_bytes(self.handle)
+        nb = self._fn("checkpoint_bytes")(self.handle)
         buf = (C.c_uint8 * nb)()
-        check(lib().bch_lfm2_checkpoint(self.handle, buf, nb))
+        check(self._fn("checkpoint")(self.handle, buf, nb))
         return bytes(buf)
 
     def restore(self, blob: bytes) -> None:
         buf = (C.c_uint8 * len(blob)).from_buffer_copy(blob)
-        check(lib().bch_lfm2_restore(self.handle, buf, len(blob)))
+        check(self._fn("restore")(self.handle, buf, len(blob)))
+
+
+class Lfm2Hip(SequenceHip):
+    """bch_lfm2: one LFM2 sequence on the GPU (Lfm2Metal's API)."""
+    _prefix = "bch_lfm2_"

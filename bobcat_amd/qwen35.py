@@ -16,7 +16,7 @@ import numpy as np
 
 from ._lib import Matrix, Qwen35Layer, Qwen35Model, check, lib
 from .backend import Format, Hip
-from .lfm2 import _matrix
+from .lfm2 import SequenceHip, _matrix
 
 
 @dataclass
@@ -153,3 +153,8 @@ class Qwen35Weights:
     @property
     def hp(self) -> dict:
         return self.cfg.hp
+
+
+class Qwen35Hip(SequenceHip):
+    """bch_qwen35: one Qwen3.5 sequence on the GPU (Qwen35Metal's API)."""
+    _prefix = "bch_qwen35_"

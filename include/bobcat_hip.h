@@ -273,6 +273,47 @@ int bch_sample(bch_ctx *ctx, bch_view logits, uint32_t n_vocab, bch_view recent,
                const bch_sampling *settings, bch_view rng_state, bch_view out);
 
 /* ------------------------------------------------------------------ */
+/* Gated DeltaNet and gated attention (Qwen3.5)                        */
+/* A DeltaNet token holds conv_dim = 2·n_k·k_dim + n_v·v_dim floats:    */
+/* the query heads, the key heads, the value heads; value head j reads  */
+/* key head j % n_k (gdn.metal:1-6).  States are [n_v][k_dim][v_dim].   */
+/* ------------------------------------------------------------------ */
+
+/* DeltaShape (backend.rs, gdn_recurrence's shape argument). */
+typedef struct bch_delta_shape {
+  uint32_t n_k_heads;
+  uint32_t n_v_heads;
+  uint32_t k_dim;
+  uint32_t v_dim;
+} bch_delta_shape;
+
+/* Metal::gdn_conv (gdn.metal:8-42): causal convolution of n_tokens tokens
+ * of `channels` floats with kernel_size (2..8) taps per channel, the oldest
+ * first, SiLU of each result into y; `history` [channels][kernel_size-1]
+ * moves forward. */
+int bch_gdn_conv(bch_ctx *ctx, bch_view x, bch_view taps, bch_view history, bch_view y, uint32_t channels,
+                 uint32_t kernel_size, uint32_t n_tokens);
+/* Metal::gdn_gates (gdn.metal:125-149): beta <- sigmoid(beta), alpha <-
+ * exp(a·softplus(alpha + dt_bias)) for n values, n_v_heads per token. */
+int bch_gdn_gates(bch_ctx *ctx, bch_view beta, bch_view alpha, bch_view a, bch_view dt_bias, uint32_t n_v_heads,
+                  uint32_t n);
+/* Metal::gdn_recurrence (gdn.metal:204-290): the gated delta rule over
+ * n_tokens tokens of y (after gdn_conv) with the gated beta and decay;
+ * queries and keys are L2-normalised here (eps 1e-6), queries times q_scale.
+ * Key heads of 64 or 128. */
+int bch_gdn_recurrence(bch_ctx *ctx, bch_view y, bch_view beta, bch_view decay, bch_view state, bch_view out,
+                       const bch_delta_shape *shape, uint32_t n_tokens, float q_scale);
+/* Metal::gdn_gated_norm (gdn.metal:100-123): each row of v_dim floats of x
+ * <- weight ⊙ rmsnorm(row) ⊙ silu(z row), in place. */
+int bch_gdn_gated_norm(bch_ctx *ctx, bch_view x, bch_view weight, bch_view z, uint32_t v_dim, uint32_t n_rows,
+                       float eps);
+/* Metal::attention_gate (gdn.metal:300-322): attn [n_tokens][q_dim] *=
+ * sigmoid of the gate half of each head's block in q_gate
+ * [n_tokens][2·q_dim]. */
+int bch_attention_gate(bch_ctx *ctx, bch_view attn, bch_view q_gate, uint32_t head_dim, uint32_t q_dim,
+                       uint32_t n_tokens);
+
+/* ------------------------------------------------------------------ */
 /* LFM2 driver (crates/bobcat/src/lfm2_metal.rs:125-779)               */
 /* ------------------------------------------------------------------ */
 
@@ -425,6 +466,34 @@ typedef struct bch_qwen35_model {
   bch_matrix output;        /* tied: same data as token_embd */
   const float *output_norm;
 } bch_qwen35_model;
+
+typedef struct bch_qwen35 bch_qwen35;
+
+/* Qwen35Metal::new: copies the weights to HBM and allocates the KV caches,
+ * convolution histories and DeltaNet states for sequences of up to n_ctx
+ * tokens.  Limits: attention as LFM2 plus an even n_rot <= head_dim;
+ * DeltaNet 2..8 taps, key heads of 64 or 128 (DeltaNetLimits). */
+int bch_qwen35_new(bch_ctx *ctx, const bch_qwen35_model *model, uint32_t n_ctx, int kv_half, bch_qwen35 **out);
+void bch_qwen35_free(bch_qwen35 *qwen);
+uint32_t bch_qwen35_n_past(const bch_qwen35 *qwen);
+/* Qwen35Metal::reset: zero histories and states, n_past = 0. */
+int bch_qwen35_reset(bch_qwen35 *qwen);
+/* Qwen35Metal::step / prefill / greedy_token / generate, with the same
+ * arguments and traces as the bch_lfm2_ functions. */
+int bch_qwen35_step(bch_qwen35 *qwen, uint32_t token, float *logits, float *trace_embedding, float *trace_layers,
+                    float *trace_final);
+int bch_qwen35_prefill(bch_qwen35 *qwen, const uint32_t *tokens, uint32_t n_tokens, float *logits,
+                       float *trace_embedding, float *trace_layers, float *trace_final);
+int bch_qwen35_greedy_token(bch_qwen35 *qwen, uint32_t *token);
+int bch_qwen35_generate(bch_qwen35 *qwen, uint32_t *out, uint32_t n);
+int bch_qwen35_generate_sampled(bch_qwen35 *qwen, uint32_t *out, uint32_t n, const bch_sampling *settings,
+                                uint64_t seed);
+/* Qwen35Metal::checkpoint / restore (qwen35::Checkpoint): resets, n_past,
+ * the convolution histories, the DeltaNet states and the logits. */
+uint64_t bch_qwen35_checkpoint_bytes(const bch_qwen35 *qwen);
+int bch_qwen35_checkpoint(bch_qwen35 *qwen, void *blob, uint64_t bytes);
+int bch_qwen35_restore(bch_qwen35 *qwen, const void *blob, uint64_t bytes);
+double bch_qwen35_last_gpu_seconds(const bch_qwen35 *qwen);
 
 #ifdef __cplusplus
 }
