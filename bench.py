@@ -31,7 +31,6 @@ GEMV_ROWS, GEMV_COLS = 8192, 2048
 GEMV_BYTES = GEMV_ROWS * GEMV_COLS // 256 * 144 + GEMV_COLS * 4 + GEMV_ROWS * 4  # 9,478,144
 PROMPT, GEN = 512, 128
 READ_THREADS = 256 * 1024
-READ_REPS = 5
 COPY_BYTES = 64 << 20
 ROOT = os.path.dirname(os.path.abspath(__file__))
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "matvec_q4k_config1_traffic.txt")
@@ -86,17 +85,12 @@ def gemv_leg(hip, reps: int, copies: int = 64):
     hot = run(copies, rotate=False) / copies
 
     # Calibration launches of known traffic, for scaling the FETCH_SIZE and
-    # WRITE_SIZE counters of a profiled run (and the streaming-read rate the
-    # GEMV is compared with, as the reference's read_sum probe does):
-    # read_sum reads all of `big` READ_REPS times; copy moves COPY_BYTES.
+    # WRITE_SIZE counters of a profiled run: read_sum reads all of `big`, copy
+    # moves COPY_BYTES.
     sums = hip.new_buffer(READ_THREADS * 4)
-    hip.set_profiling(True)  # per-launch event timing: no host time in the figure
     hip.begin()
-    for _ in range(READ_REPS):
-        hip.read_sum(big.at(0), big_bytes // 16, sums.at(0), READ_THREADS)
+    hip.read_sum(big.at(0), big_bytes // 16, sums.at(0), READ_THREADS)
     hip.end()
-    read_s = sum(e["seconds"] for e in hip.profile()) / READ_REPS
-    hip.set_profiling(False)
     dst = hip.new_buffer(COPY_BYTES)
     hip.begin()
     hip.copy(big.at(0), dst.at(0), COPY_BYTES // 4)
@@ -105,13 +99,15 @@ def gemv_leg(hip, reps: int, copies: int = 64):
     dst.free()
     big.free()
     return dict(us=per_launch * 1e6, gbs=GEMV_BYTES / per_launch / 1e9, launches=launches,
-                hot_us=hot * 1e6, hot_gbs=GEMV_BYTES / hot / 1e9, read_gbs=big_bytes / read_s / 1e9)
+                hot_us=hot * 1e6, hot_gbs=GEMV_BYTES / hot / 1e9)
 
 
 def model_leg(hip, weights, steps: int, warmup: int, seed: int = 42):
     from bobcat_amd.lfm2 import Lfm2Hip
+    from bobcat_amd.qwen35 import Qwen35Hip, Qwen35Weights
 
     cfg = weights.cfg
+    Lfm2Hip = Qwen35Hip if isinstance(weights, Qwen35Weights) else Lfm2Hip
     rng = np.random.default_rng(seed)
     prompt = rng.integers(0, cfg.n_vocab, PROMPT).astype(np.uint32)
     m = Lfm2Hip(hip, weights, n_ctx=PROMPT + GEN, kv_half=True)
@@ -146,7 +142,7 @@ def cpu_leg(weights, budget_s: float, threads: int):
     import oracle
 
     oracle.set_threads(threads)
-    st = oracle.Lfm2State(weights, n_ctx=64)
+    st = (oracle.Qwen35State if hasattr(weights.cfg, "n_k_heads") else oracle.Lfm2State)(weights, n_ctx=64)
     rng = np.random.default_rng(42)
     for t in rng.integers(0, weights.cfg.n_vocab, 2):
         st.step(int(t), logits=False)
@@ -179,8 +175,12 @@ def main() -> int:
 
     from bobcat_amd.backend import Hip
     from bobcat_amd.lfm2 import CONFIGS, Lfm2Weights
+    from bobcat_amd.qwen35 import CONFIGS as QWEN_CONFIGS, Qwen35Weights
 
-    cfg = CONFIGS[args.model]
+    if args.model in QWEN_CONFIGS:
+        cfg, Lfm2Weights = QWEN_CONFIGS[args.model], Qwen35Weights
+    else:
+        cfg = CONFIGS[args.model]
     with Hip() as hip:
         name, cus = hip.device_info()
         log(f"device: {name}, {cus} CUs")
@@ -202,7 +202,8 @@ def main() -> int:
     # Bytes a decode token streams: all layer matrices + the output matrix
     # + the KV cache read at the mean context of tg128 after pp512.
     mean_ctx = PROMPT + GEN / 2
-    n_attn = len(cfg.attention_layers)
+    n_attn = (len(cfg.attention_layers) if hasattr(cfg, "attention_layers")
+              else sum(cfg.is_attention(i) for i in range(cfg.n_layers)))
     kv_bytes = n_attn * mean_ctx * 2 * cfg.n_kv_heads * cfg.head_dim * 2
     token_bytes = wb["total"] + kv_bytes
     decode_gbs = mres["decode_tok_s_device"] * token_bytes / 1e9
@@ -232,7 +233,7 @@ def main() -> int:
         "roofline": {"kernel": "matvec_q4k (config 1, 8192x2048)", "bound": "hbm",
                      "achieved": round(g["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "us_per_launch": round(g["us"], 3), "streaming_read_gbs": round(g["read_gbs"], 1)},
+                     "us_per_launch": round(g["us"], 3)},
         "cpu_baseline": None if cpu is None else {
             "value": round(cpu["tok_s"], 4), "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"{cpu['steps']} decode steps of {cfg.name} by the oracle (C restatement of the "
