@@ -6,74 +6,94 @@
 // a full 512-token batch; here each workgroup dequantises its weight tile
 // straight into LDS instead, so the expanded matrix never touches HBM.
 //
-// Tile: 64 weight rows x 64 tokens x 256 columns (one Q4_K super-block per
-// row).  256 threads = 4 waves in a 2x2 arrangement, each wave owning a
-// 32x32 output block computed with v_mfma_f32_32x32x8_f16.  Weights go to
-// LDS as fp16 (the reference's expanded half tiles); each token's inputs
-// are scaled by a power of two into fp16 range and split into an fp16 high
-// part and an fp16 residual, both multiplied, so the inputs keep ~22 bits
-// whatever their magnitude.  Accumulation is fp32.
+// Tile: 128 weight rows x 64 tokens, in pipeline steps of 128 columns;
+// v_mfma_f32_32x32x8_f16 on LDS tiles.  Weights go to LDS as fp16 (the
+// reference's expanded half tiles); each token's inputs are scaled by a
+// power of two into fp16 range and split into an fp16 high part and an fp16
+// residual, both multiplied, so the inputs keep ~22 bits whatever their
+// magnitude.  Accumulation is fp32.
 #include "formats.h"
 #include "kernels.h"
 #include "runtime.h"
 
 namespace bch {
 
-constexpr int kBM = 64;       // weight rows per tile
+constexpr int kBM = 128;      // weight rows per tile
 constexpr int kBN = 64;       // tokens per tile
-constexpr int kBK = 256;      // columns per step
+constexpr int kBK = 256;      // columns a row must be a multiple of (one Q4_K super-block)
+constexpr int kStep = 128;    // columns per pipeline step (half a super-block)
 constexpr int kPad = 8;       // halves of padding per LDS row (bank spread, 16-byte rows)
-constexpr int kLds = kBK + kPad;
+constexpr int kLds = kStep + kPad;
 
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
 
-// Dequantise 64 consecutive weights of row `row` starting at column k0+64p
-// into fp16 at dst (64 halves).
-template <uint32_t FMT>
-__device__ __forceinline__ void dequant64(const uint8_t *__restrict__ row, uint32_t k0, int p, _Float16 *dst) {
-  if constexpr (FMT == 12) {
-    const uint8_t *blk = row + (k0 / 256) * 144;
-    const uint4 h = *reinterpret_cast<const uint4 *>(blk);
-    const uint4 *qp = reinterpret_cast<const uint4 *>(blk + 16 + 32 * p);
-    const uint4 q0 = qp[0], q1 = qp[1];
-    const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    const uint32_t sc = q4k_pair_scales(h.y, h.z, h.w, p);
-    const float d = half_bits_to_float(h.x & 0xffffu), dmin = half_bits_to_float(h.x >> 16);
-    const float a_lo = d * ubyte0(sc), a_hi = d * ubyte1(sc);
-    const float b_lo = dmin * ubyte2(sc), b_hi = dmin * ubyte3(sc);
+// The raw bytes of 64 consecutive weights of a row (one Q4_K unit: the
+// super-block header and the pair's 32 quant bytes), for prefetching.
+struct RawUnit {
+  uint4 h, q0, q1;
+};
+
+__device__ __forceinline__ RawUnit fetch_q4k(const uint8_t *__restrict__ row, uint32_t k256, int p) {
+  const uint8_t *blk = row + (k256 / 256) * 144;
+  const uint4 *qp = reinterpret_cast<const uint4 *>(blk + 16 + 32 * p);
+  return RawUnit{*reinterpret_cast<const uint4 *>(blk), qp[0], qp[1]};
+}
+
+// Q4_K unit p of a super-block to 64 halves: (d·sc)·q − dmin·m per element.
+__device__ __forceinline__ void expand_q4k(const RawUnit &u, int p, _Float16 *dst) {
+  const uint32_t qw[8] = {u.q0.x, u.q0.y, u.q0.z, u.q0.w, u.q1.x, u.q1.y, u.q1.z, u.q1.w};
+  const uint32_t sc = q4k_pair_scales(u.h.y, u.h.z, u.h.w, p);
+  const float d = half_bits_to_float(u.h.x & 0xffffu), dmin = half_bits_to_float(u.h.x >> 16);
+  const float a_lo = d * ubyte0(sc), a_hi = d * ubyte1(sc);
+  const float b_lo = dmin * ubyte2(sc), b_hi = dmin * ubyte3(sc);
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const uint32_t lo = qw[k] & 0x0f0f0f0fu, hi = (qw[k] >> 4) & 0x0f0f0f0fu;
-      dst[4 * k + 0] = (_Float16)(a_lo * ubyte0(lo) - b_lo);
-      dst[4 * k + 1] = (_Float16)(a_lo * ubyte1(lo) - b_lo);
-      dst[4 * k + 2] = (_Float16)(a_lo * ubyte2(lo) - b_lo);
-      dst[4 * k + 3] = (_Float16)(a_lo * ubyte3(lo) - b_lo);
-      dst[32 + 4 * k + 0] = (_Float16)(a_hi * ubyte0(hi) - b_hi);
-      dst[32 + 4 * k + 1] = (_Float16)(a_hi * ubyte1(hi) - b_hi);
-      dst[32 + 4 * k + 2] = (_Float16)(a_hi * ubyte2(hi) - b_hi);
-      dst[32 + 4 * k + 3] = (_Float16)(a_hi * ubyte3(hi) - b_hi);
-    }
-  } else if constexpr (FMT == 1) {
-    const uint4 *src = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(row) + k0 + 64 * p);
+  for (int k = 0; k < 8; k++) {
+    const uint32_t lo = qw[k] & 0x0f0f0f0fu, hi = (qw[k] >> 4) & 0x0f0f0f0fu;
+    half4_t l4, h4;
+    l4[0] = (_Float16)(a_lo * ubyte0(lo) - b_lo);
+    l4[1] = (_Float16)(a_lo * ubyte1(lo) - b_lo);
+    l4[2] = (_Float16)(a_lo * ubyte2(lo) - b_lo);
+    l4[3] = (_Float16)(a_lo * ubyte3(lo) - b_lo);
+    h4[0] = (_Float16)(a_hi * ubyte0(hi) - b_hi);
+    h4[1] = (_Float16)(a_hi * ubyte1(hi) - b_hi);
+    h4[2] = (_Float16)(a_hi * ubyte2(hi) - b_hi);
+    h4[3] = (_Float16)(a_hi * ubyte3(hi) - b_hi);
+    *reinterpret_cast<half4_t *>(dst + 4 * k) = l4;
+    *reinterpret_cast<half4_t *>(dst + 32 + 4 * k) = h4;
+  }
+}
+
+// F16/F32 rows: 64 consecutive weights from column k to halves.
+template <uint32_t FMT>
+__device__ __forceinline__ void expand_float(const uint8_t *__restrict__ row, uint32_t k, _Float16 *dst) {
+  if constexpr (FMT == 1) {
+    const uint4 *src = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(row) + k);
     uint4 *o = reinterpret_cast<uint4 *>(dst);
 #pragma unroll
     for (int i = 0; i < 8; i++) o[i] = src[i];
-  } else {  // F32
-    const float4 *src = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(row) + k0 + 64 * p);
+  } else {
+    const float4 *src = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(row) + k);
 #pragma unroll
     for (int i = 0; i < 16; i++) {
       const float4 v = src[i];
-      dst[4 * i + 0] = (_Float16)v.x;
-      dst[4 * i + 1] = (_Float16)v.y;
-      dst[4 * i + 2] = (_Float16)v.z;
-      dst[4 * i + 3] = (_Float16)v.w;
+      half4_t h;
+      h[0] = (_Float16)v.x;
+      h[1] = (_Float16)v.y;
+      h[2] = (_Float16)v.z;
+      h[3] = (_Float16)v.w;
+      *reinterpret_cast<half4_t *>(dst + 4 * i) = h;
     }
   }
 }
 
+// Tile 128 weight rows x 64 tokens; 256 threads = 4 waves in a 2x2
+// arrangement, each wave owning 64 rows x 32 tokens as two 32x32 MFMA
+// blocks.  A pipeline step covers 128 columns: thread t expands weight row
+// t/2, unit t%2, and splits 32 inputs of token t/4.  The next step's weight
+// and input loads are issued into registers before this step's MFMAs.
 template <uint32_t FMT, int STORE>
 __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, uint64_t row_bytes,
                                                 const float *__restrict__ X, float *__restrict__ Y, uint32_t n_rows,
@@ -82,102 +102,120 @@ __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, u
   _Float16 *A = lds;                    // [kBM][kLds]
   _Float16 *Bh = A + kBM * kLds;        // [kBN][kLds]
   _Float16 *Bl = Bh + kBN * kLds;       // [kBN][kLds]
-  __shared__ float unscale[kBN];        // 2^-k that undoes each token's input scaling
+  __shared__ float unscale[kBN];        // 2^-k that undoes each token's input scaling in this step
   const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
   const uint32_t row0 = blockIdx.x * kBM, tok0 = blockIdx.y * kBN;
   const int wm = wave / 2, wn = wave % 2;
 
-  float16_t total;
-#pragma unroll
-  for (int i = 0; i < 16; i++) total[i] = 0.f;
+  // This thread's weight row and unit, and token and quarter.
+  const int ar = tid / 2, aq = tid % 2;
+  const uint8_t *wrow = W + (uint64_t)min(row0 + ar, n_rows - 1) * row_bytes;
+  const int bt = tid / 4, bq = tid % 4;
+  const bool tok_ok = tok0 + bt < n_tokens;
+  const float *xrow = X + (uint64_t)min(tok0 + bt, n_tokens - 1) * n_cols + 32 * bq;
 
-  for (uint32_t k0 = 0; k0 < n_cols; k0 += kBK) {
-    // Weights: thread -> (row, quarter of the 256 columns).
-    {
-      const int r = tid / 4, p = tid % 4;
-      const uint32_t grow = min(row0 + r, n_rows - 1);
-      dequant64<FMT>(W + (uint64_t)grow * row_bytes, k0, p, A + r * kLds + 64 * p);
-    }
-    // Inputs: thread -> (token, quarter).  Each token's 256 inputs are
-    // scaled by a power of two that brings their largest magnitude just
-    // under 2^14 (so half precision cannot overflow), then split into an
-    // fp16 high part and an fp16 residual.  The scaling is exact and is
-    // undone on the tile's products below.
-    {
-      const int t = tid / 4, p = tid % 4;
-      const uint32_t gt = tok0 + t;
-      _Float16 *dh = Bh + t * kLds + 64 * p, *dl = Bl + t * kLds + 64 * p;
-      float v[64];
-      if (gt < n_tokens) {
-        const float4 *src = reinterpret_cast<const float4 *>(X + (uint64_t)gt * n_cols + k0 + 64 * p);
+  RawUnit ra{};
+  float4 xv[8];
+  auto prefetch = [&](uint32_t k0) {
+    if constexpr (FMT == 12) ra = fetch_q4k(wrow, k0 & ~255u, (int)((k0 & 255u) / 64) + aq);
+    const float4 *src = reinterpret_cast<const float4 *>(xrow + k0);
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-          const float4 q = src[i];
-          v[4 * i] = q.x;
-          v[4 * i + 1] = q.y;
-          v[4 * i + 2] = q.z;
-          v[4 * i + 3] = q.w;
-        }
-      } else {
+    for (int i = 0; i < 8; i++) xv[i] = src[i];
+  };
+
+  float16_t total[2], acc[2];
 #pragma unroll
-        for (int i = 0; i < 64; i++) v[i] = 0.f;
-      }
+  for (int b = 0; b < 2; b++)
+#pragma unroll
+    for (int i = 0; i < 16; i++) total[b][i] = 0.f;
+
+  prefetch(0);
+  for (uint32_t k0 = 0; k0 < n_cols; k0 += kStep) {
+    // Stage this step: weights to halves, inputs scaled and split.
+    if constexpr (FMT == 12)
+      expand_q4k(ra, (int)((k0 & 255u) / 64) + aq, A + ar * kLds + 64 * aq);
+    else
+      expand_float<FMT>(wrow, k0 + 64 * aq, A + ar * kLds + 64 * aq);
+    {
+      // Each token's 128 inputs are scaled by a power of two that brings
+      // their largest magnitude just under 2^14 (half precision cannot
+      // overflow), then split into an fp16 high part and an fp16 residual:
+      // ~22 bits whatever their magnitude.  The scaling is undone on the
+      // step's products.
       float mx = 0.f;
 #pragma unroll
-      for (int i = 0; i < 64; i++) mx = fmaxf(mx, fabsf(v[i]));
+      for (int i = 0; i < 8; i++)
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xv[i].x), fabsf(xv[i].y)), fmaxf(fabsf(xv[i].z), fabsf(xv[i].w))));
       mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+      if (!tok_ok) mx = 0.f;
       int ex = 0;
-      if (mx > 0.f) frexpf(mx, &ex);          // mx < 2^ex
+      if (mx > 0.f) frexpf(mx, &ex);  // mx < 2^ex
       const int k = max(-100, min(100, 14 - ex));
-      const float scale = ldexpf(1.0f, k);
-      if (p == 0) unscale[t] = ldexpf(1.0f, -k);
+      const float scale = tok_ok ? ldexpf(1.0f, k) : 0.f;
+      if (bq == 0) unscale[bt] = ldexpf(1.0f, -k);
+      _Float16 *dh = Bh + bt * kLds + 32 * bq, *dl = Bl + bt * kLds + 32 * bq;
 #pragma unroll
-      for (int i = 0; i < 64; i++) {
-        const float sv = v[i] * scale;
-        const _Float16 h = (_Float16)sv;
-        dh[i] = h;
-        dl[i] = (_Float16)(sv - (float)h);
+      for (int i = 0; i < 8; i++) {
+        const float v[4] = {xv[i].x * scale, xv[i].y * scale, xv[i].z * scale, xv[i].w * scale};
+        half4_t h, l;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          h[j] = (_Float16)v[j];
+          l[j] = (_Float16)(v[j] - (float)h[j]);
+        }
+        *reinterpret_cast<half4_t *>(dh + 4 * i) = h;
+        *reinterpret_cast<half4_t *>(dl + 4 * i) = l;
       }
     }
     __syncthreads();
-    // 32 k-steps of 8: lane supplies A[row = lane%32][k + 4*(lane/32) .. +4].
-    const _Float16 *arow = A + (wm * 32 + lane % 32) * kLds + 4 * (lane / 32);
+    if (k0 + kStep < n_cols) prefetch(k0 + kStep);
+    // 16 k-steps of 8: lane supplies A[row = lane%32][k + 4*(lane/32) .. +4].
+    const _Float16 *arow0 = A + (wm * 64 + lane % 32) * kLds + 4 * (lane / 32);
+    const _Float16 *arow1 = arow0 + 32 * kLds;
     const _Float16 *bhrow = Bh + (wn * 32 + lane % 32) * kLds + 4 * (lane / 32);
     const _Float16 *blrow = Bl + (wn * 32 + lane % 32) * kLds + 4 * (lane / 32);
-    float16_t acc;
 #pragma unroll
-    for (int i = 0; i < 16; i++) acc[i] = 0.f;
-#pragma unroll 8
-    for (int kk = 0; kk < kBK; kk += 8) {
-      const half4_t a = *reinterpret_cast<const half4_t *>(arow + kk);
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) acc[b][i] = 0.f;
+#pragma unroll 4
+    for (int kk = 0; kk < kStep; kk += 8) {
+      const half4_t a0 = *reinterpret_cast<const half4_t *>(arow0 + kk);
+      const half4_t a1 = *reinterpret_cast<const half4_t *>(arow1 + kk);
       const half4_t bh = *reinterpret_cast<const half4_t *>(bhrow + kk);
       const half4_t bl = *reinterpret_cast<const half4_t *>(blrow + kk);
-      acc = __builtin_amdgcn_mfma_f32_32x32x8f16(a, bh, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x8f16(a, bl, acc, 0, 0, 0);
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x8f16(a0, bh, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x8f16(a1, bh, acc[1], 0, 0, 0);
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x8f16(a0, bl, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x8f16(a1, bl, acc[1], 0, 0, 0);
     }
     // Every accumulator of a lane belongs to token column lane%32.
     const float us = unscale[wn * 32 + lane % 32];
 #pragma unroll
-    for (int i = 0; i < 16; i++) total[i] = fmaf(acc[i], us, total[i]);
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) total[b][i] = fmaf(acc[b][i], us, total[b][i]);
     __syncthreads();
   }
-  // total[r] holds D[row = 8*(r/4) + 4*(lane/32) + r%4][token = lane%32].
+  // total[b][r] holds D[row = 32b + 8*(r/4) + 4*(lane/32) + r%4][token = lane%32].
   const uint32_t tok = tok0 + wn * 32 + lane % 32;
   if (tok >= n_tokens) return;
 #pragma unroll
-  for (int r = 0; r < 16; r++) {
-    const uint32_t row = row0 + wm * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-    if (row < n_rows) {
-      float *y = Y + (uint64_t)tok * n_rows + row;
-      if (STORE == 0)
-        *y = total[r];
-      else if (STORE == 1)
-        *y += total[r];
-      else
-        *y = silu_f(*y) * total[r];
+  for (int b = 0; b < 2; b++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const uint32_t row = row0 + wm * 64 + 32 * b + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+      if (row < n_rows) {
+        float *y = Y + (uint64_t)tok * n_rows + row;
+        if (STORE == 0)
+          *y = total[b][r];
+        else if (STORE == 1)
+          *y += total[b][r];
+        else
+          *y = silu_f(*y) * total[b][r];
+      }
     }
-  }
 }
 
 template <uint32_t FMT>
