@@ -106,7 +106,10 @@ __device__ __forceinline__ float column_sum(float v) {
 }
 
 // CPR: 16-byte chunks per cache row (head_dim * element size / 16).
-template <bool HALF, int CPR>
+// FUSED: one decode query at *dpos with its norm/RoPE and cache store;
+// otherwise query z of a prefill batch at first_pos + z, already normalised
+// and rotated, with every key already in the cache.
+template <bool HALF, int CPR, bool FUSED>
 __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
   constexpr uint32_t kElem = HALF ? 2 : 4;
   constexpr uint32_t kEpc = 16 / kElem;             // elements per chunk
@@ -117,13 +120,14 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
   const uint32_t head = blockIdx.x, split = blockIdx.y, tid = threadIdx.x;
   const uint32_t wave = tid / 64, lane = tid % 64;
   const uint32_t group = a.n_heads / a.n_kv, kvh = head / group, kv_dim = a.n_kv * hd;
-  const uint32_t pos = *a.dpos;
+  const uint32_t qz = blockIdx.z;
+  const uint32_t pos = FUSED ? *a.dpos : a.first_pos + qz;
   const uint32_t n_keys = pos + 1;
   const uint32_t n_splits = (n_keys + kps - 1) / kps;
   if (split >= n_splits) return;
   const uint32_t k0 = split * kps, k1 = min(k0 + kps, n_keys);
   const uint32_t len = k1 - k0;
-  const bool owns_new = k1 == n_keys;
+  const bool owns_new = FUSED && k1 == n_keys;
   // Chunk i of this thread lies in row tid / CPR + i * kRowsPerPass, at
   // column c (head elements c * kEpc ..), the same column for every chunk.
   // A wave's rows of chunk i start at wave_row0 + i * kRowsPerPass.
@@ -153,8 +157,14 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
   // head of the group rotates the new key for itself; the group's first
   // head also stores key and value in the cache.
   const float position = (float)pos;
-  if (wave == 0)
-    norm_rope_wave(a.q + (uint64_t)head * a.q_head_stride, a.q_norm, a.freqs, hd, a.n_rot, position, a.eps, q_s);
+  if (wave == 0) {
+    const float *qsrc = a.q + (uint64_t)qz * a.q_stride + (uint64_t)head * a.q_head_stride;
+    if (FUSED) {
+      norm_rope_wave(qsrc, a.q_norm, a.freqs, hd, a.n_rot, position, a.eps, q_s);
+    } else {
+      for (uint32_t i = lane; i < hd; i += 64) q_s[i] = qsrc[i];
+    }
+  }
   if (owns_new && wave == 1) {
     norm_rope_wave(a.k + (uint64_t)kvh * hd, a.k_norm, a.freqs, hd, a.n_rot, position, a.eps, knew_s);
     const bool store = head % group == 0;
@@ -288,14 +298,19 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
     for (int w = 0; w < kWaves; w++) o += red_s[w][tid];
   }
   // The output gate of gated attention (qwen35.rs:422-424).
-  const float gate = (a.gate && tid < hd) ? 1.0f / (1.0f + expf(-a.gate[(uint64_t)head * a.gate_head_stride + tid])) : 1.0f;
+  const float gate =
+      (a.gate && tid < hd)
+          ? 1.0f / (1.0f + expf(-a.gate[(uint64_t)qz * a.gate_query_stride + (uint64_t)head * a.gate_head_stride + tid]))
+          : 1.0f;
+  float *outp = a.out + (uint64_t)qz * a.out_stride + (uint64_t)head * hd;
+  const uint32_t slot = qz * a.n_heads + head;  // (query, head) of the partials and counters
   if (n_splits == 1) {
-    if (tid < hd) a.out[(uint64_t)head * hd + tid] = o / l_s * gate;
+    if (tid < hd) outp[tid] = o / l_s * gate;
     return;
   }
   const uint32_t stride = hd + 2;
   if (tid < hd) {
-    float *pp = a.partials + ((uint64_t)head * a.max_splits + split) * stride;
+    float *pp = a.partials + ((uint64_t)slot * a.max_splits + split) * stride;
     coherent_store(pp + 2 + tid, o);
     if (tid == 0) {
       coherent_store(pp, m_s);
@@ -305,13 +320,13 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&a.counters[head], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = __hip_atomic_fetch_add(&a.counters[slot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last_s = prev == n_splits - 1;
   }
   __syncthreads();
   if (!last_s) return;
   if (tid < hd) {
-    const float *pp = a.partials + (uint64_t)head * a.max_splits * stride;
+    const float *pp = a.partials + (uint64_t)slot * a.max_splits * stride;
     float M = -INFINITY;
     for (uint32_t sp = 0; sp < n_splits; sp++) M = fmaxf(M, coherent_load(pp + sp * stride));
     float L = 0.f, O = 0.f;
@@ -320,9 +335,9 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
       L = fmaf(coherent_load(pp + sp * stride + 1), w, L);
       O = fmaf(coherent_load(pp + sp * stride + 2 + tid), w, O);
     }
-    a.out[(uint64_t)head * hd + tid] = O / L * gate;
+    outp[tid] = O / L * gate;
   }
-  if (tid == 0) coherent_store(&a.counters[head], 0u);
+  if (tid == 0) coherent_store(&a.counters[slot], 0u);
 }
 
 uint32_t attn_decode_keys_per_split(uint32_t head_dim, bool kv_half) {
@@ -342,14 +357,14 @@ RopeTable rope_table(float theta, uint32_t n_rot) {
   return f;
 }
 
-template <bool HALF>
+template <bool HALF, bool FUSED>
 static void launch_attn_decode(hipStream_t s, const AttnDecodeArgs &a, dim3 grid) {
   switch (a.head_dim * (HALF ? 2 : 4) / 16) {
-    case 4: k_attn_decode<HALF, 4><<<grid, kDecThreads, 0, s>>>(a); break;
-    case 8: k_attn_decode<HALF, 8><<<grid, kDecThreads, 0, s>>>(a); break;
-    case 16: k_attn_decode<HALF, 16><<<grid, kDecThreads, 0, s>>>(a); break;
-    case 32: k_attn_decode<HALF, 32><<<grid, kDecThreads, 0, s>>>(a); break;
-    case 64: k_attn_decode<HALF, 64><<<grid, kDecThreads, 0, s>>>(a); break;
+    case 4: k_attn_decode<HALF, 4, FUSED><<<grid, kDecThreads, 0, s>>>(a); break;
+    case 8: k_attn_decode<HALF, 8, FUSED><<<grid, kDecThreads, 0, s>>>(a); break;
+    case 16: k_attn_decode<HALF, 16, FUSED><<<grid, kDecThreads, 0, s>>>(a); break;
+    case 32: k_attn_decode<HALF, 32, FUSED><<<grid, kDecThreads, 0, s>>>(a); break;
+    case 64: k_attn_decode<HALF, 64, FUSED><<<grid, kDecThreads, 0, s>>>(a); break;
     default: break;  // rejected when the driver was created
   }
 }
@@ -357,9 +372,17 @@ static void launch_attn_decode(hipStream_t s, const AttnDecodeArgs &a, dim3 grid
 void run_attn_decode(hipStream_t s, const AttnDecodeArgs &a, bool kv_half) {
   dim3 grid(a.n_heads, a.max_splits);
   if (kv_half)
-    launch_attn_decode<true>(s, a, grid);
+    launch_attn_decode<true, true>(s, a, grid);
   else
-    launch_attn_decode<false>(s, a, grid);
+    launch_attn_decode<false, true>(s, a, grid);
+}
+
+void run_attn_prefill(hipStream_t s, const AttnDecodeArgs &a, bool kv_half, uint32_t n_queries) {
+  dim3 grid(a.n_heads, a.max_splits, n_queries);
+  if (kv_half)
+    launch_attn_decode<true, false>(s, a, grid);
+  else
+    launch_attn_decode<false, false>(s, a, grid);
 }
 
 }  // namespace bch

@@ -33,10 +33,17 @@ struct AttnDecodeArgs {
   uint32_t n_rot;                  // leading elements of a head that RoPE rotates
   const float *gate;               // nullable: out[h] *= sigmoid(gate[h·gate_head_stride ..])
   uint32_t gate_head_stride;
+  // Prefill (run_attn_prefill): query z sits at first_pos + z, its query at
+  // q + z·q_stride, its output at out + z·out_stride, its gate at
+  // gate + z·gate_query_stride; partials and counters hold n_queries·n_heads slots.
+  uint32_t first_pos, q_stride, out_stride, gate_query_stride;
 };
 uint32_t attn_decode_keys_per_split(uint32_t head_dim, bool kv_half);
 uint32_t attn_decode_max_splits(uint32_t n_ctx, uint32_t head_dim, bool kv_half);
 void run_attn_decode(hipStream_t s, const AttnDecodeArgs &a, bool kv_half);
+// Attention of n_queries prefill queries with normalised, rotated queries and
+// every key already in the cache; max_splits must cover first_pos + n_queries.
+void run_attn_prefill(hipStream_t s, const AttnDecodeArgs &a, bool kv_half, uint32_t n_queries);
 
 // matvec.hip
 void run_matvec(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,

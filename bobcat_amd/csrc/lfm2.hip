@@ -241,12 +241,23 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
         run_copy(s, m->v, static_cast<float *>(m->cache_slot(m->v_cache, ci, pos)), count * m->kv_dim, nullptr, 0);
       for (uint32_t q0 = 0; q0 < count; q0 += kAttnQueryBatch) {
         const uint32_t nq = std::min(kAttnQueryBatch, count - q0);
-        const uint32_t splits =
-            std::min(m->prefill_splits, attention_splits(pos + q0 + nq, m->n_kv_heads, cus));
-        const uint64_t off = (uint64_t)q0 * m->q_dim;
-        run_attention(s, m->q + off, m->cache_layer(m->k_cache, ci), m->cache_layer(m->v_cache, ci), m->kv_half,
-                      m->partials, m->counters, m->attn + off, m->n_heads, m->n_kv_heads, m->head_dim, pos + q0,
-                      nullptr, nq, splits);
+        AttnDecodeArgs ad{};
+        ad.q = m->q + (uint64_t)q0 * m->q_dim;
+        ad.q_stride = m->q_dim;
+        ad.q_head_stride = m->head_dim;
+        ad.scale = 1.0f / sqrtf((float)m->head_dim);
+        ad.k_cache = m->cache_layer(m->k_cache, ci);
+        ad.v_cache = m->cache_layer(m->v_cache, ci);
+        ad.partials = m->partials;
+        ad.counters = m->counters;
+        ad.out = m->attn + (uint64_t)q0 * m->q_dim;
+        ad.out_stride = m->q_dim;
+        ad.n_heads = m->n_heads;
+        ad.n_kv = m->n_kv_heads;
+        ad.head_dim = m->head_dim;
+        ad.first_pos = pos + q0;
+        ad.max_splits = attn_decode_max_splits(pos + q0 + nq, m->head_dim, m->kv_half);
+        run_attn_prefill(s, ad, m->kv_half, nq);
       }
       check_finite(s, "attention", il, m->attn, (uint64_t)count * m->q_dim);
       run_matmul(s, L.wo.format, L.wo.data, n, m->q_dim, m->attn, m->hidden, count, 1);
@@ -417,10 +428,8 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
     const uint64_t cache = (uint64_t)m->n_attn * n_ctx * m->kv_dim * (m->kv_half ? 2 : 4);
     m->decode_splits = attention_splits(n_ctx, std::max(1u, m->n_kv_heads), ctx->n_cus);
     m->prefill_splits = m->decode_splits;
-    const uint64_t partial_floats =
-        std::max(attention_partial_floats(std::min<uint32_t>(m->batch, kAttnQueryBatch), m->n_heads, hd,
-                                          m->decode_splits),
-                 attention_partial_floats(1, m->n_heads, hd, attn_decode_max_splits(n_ctx, hd, m->kv_half)));
+    const uint64_t partial_floats = attention_partial_floats(std::min<uint32_t>(m->batch, kAttnQueryBatch), m->n_heads,
+                                                            hd, attn_decode_max_splits(n_ctx, hd, m->kv_half));
     int rc = 0;
     (void)((rc = m->alloc(cache, &m->k_cache)) || (rc = m->alloc(cache, &m->v_cache)) ||
            (rc = m->alloc_t((uint64_t)m->n_conv * (m->conv_kernel - 1) * n, &m->conv_state)) ||
@@ -430,7 +439,7 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
            (rc = m->alloc_t(rows * m->kv_dim + 4, &m->v)) || (rc = m->alloc_t(rows * m->q_dim + 4, &m->attn)) ||
            (rc = m->alloc_t(std::max<uint64_t>(rows * m->n_ff, (uint64_t)m->n_used * m->n_ff_expert), &m->ffn)) ||
            (rc = m->alloc_t(partial_floats + 4, &m->partials)) ||
-           (rc = m->alloc_t((uint64_t)kAttnQueryBatch * std::max(1u, m->n_kv_heads), &m->counters)) ||
+           (rc = m->alloc_t((uint64_t)kAttnQueryBatch * std::max(1u, m->n_heads), &m->counters)) ||
            (rc = m->alloc_t(2 * (uint64_t)std::max(1u, m->n_used) * rows, &m->route)) || (rc = m->alloc_common()));
     if (rc) return cleanup(rc);
   }

@@ -179,14 +179,30 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
         run_convert_half(st, v, cache_slot(v_cache, ci, pos), count * kv_dim, nullptr, 0);
       else
         run_copy(st, v, static_cast<float *>(cache_slot(v_cache, ci, pos)), count * kv_dim, nullptr, 0);
+      // Attention with the output gate of each head applied in the same launch.
       for (uint32_t q0 = 0; q0 < count; q0 += kQwenAttnQueryBatch) {
         const uint32_t nq = std::min(kQwenAttnQueryBatch, count - q0);
-        const uint32_t splits = std::min(prefill_splits, attention_splits(pos + q0 + nq, n_kv_heads, cus));
-        const uint64_t off = (uint64_t)q0 * q_dim;
-        run_attention(st, q + off, cache_layer(k_cache, ci), cache_layer(v_cache, ci), kv_half, partials, counters,
-                      attn + off, n_heads, n_kv_heads, head_dim, pos + q0, nullptr, nq, splits);
+        AttnDecodeArgs ad{};
+        ad.q = q + (uint64_t)q0 * q_dim;
+        ad.q_stride = q_dim;
+        ad.q_head_stride = head_dim;
+        ad.scale = 1.0f / sqrtf((float)head_dim);
+        ad.k_cache = cache_layer(k_cache, ci);
+        ad.v_cache = cache_layer(v_cache, ci);
+        ad.partials = partials;
+        ad.counters = counters;
+        ad.out = attn + (uint64_t)q0 * q_dim;
+        ad.out_stride = q_dim;
+        ad.gate = q_gate + (uint64_t)q0 * 2 * q_dim + head_dim;
+        ad.gate_head_stride = 2 * head_dim;
+        ad.gate_query_stride = 2 * q_dim;
+        ad.n_heads = n_heads;
+        ad.n_kv = n_kv_heads;
+        ad.head_dim = head_dim;
+        ad.first_pos = pos + q0;
+        ad.max_splits = attn_decode_max_splits(pos + q0 + nq, head_dim, kv_half);
+        run_attn_prefill(st, ad, kv_half, nq);
       }
-      run_attention_gate(st, attn, q_gate, head_dim, q_dim, count);
       run_matmul(st, L.wo.format, L.wo.data, n, q_dim, attn, hidden, count, 1);
     } else {
       const uint32_t di = L.cache_index;
@@ -336,10 +352,8 @@ int bch_qwen35_new(bch_ctx *ctx, const bch_qwen35_model *md, uint32_t n_ctx, int
     const uint64_t rows = m->batch;
     const uint64_t cache = (uint64_t)m->n_attn * n_ctx * m->kv_dim * (m->kv_half ? 2 : 4);
     m->prefill_splits = attention_splits(n_ctx, std::max(1u, m->n_kv_heads), ctx->n_cus);
-    const uint64_t partial_floats =
-        std::max(attention_partial_floats(std::min<uint32_t>(m->batch, kQwenAttnQueryBatch), m->n_heads, hd,
-                                          m->prefill_splits),
-                 attention_partial_floats(1, m->n_heads, hd, attn_decode_max_splits(n_ctx, hd, m->kv_half)));
+    const uint64_t partial_floats = attention_partial_floats(std::min<uint32_t>(m->batch, kQwenAttnQueryBatch),
+                                                            m->n_heads, hd, attn_decode_max_splits(n_ctx, hd, m->kv_half));
     int rc = 0;
     (void)((rc = m->alloc(cache, &m->k_cache)) || (rc = m->alloc(cache, &m->v_cache)) ||
            (rc = m->alloc_t((uint64_t)m->n_delta * m->conv_dim * (m->conv_kernel - 1), &m->conv_state)) ||
