@@ -18,7 +18,7 @@
 
 namespace bch {
 
-constexpr int kBM = 128;      // weight rows per tile
+constexpr int kBM = 128;      // weight rows of the larger tile
 constexpr int kBN = 64;       // tokens per tile
 constexpr int kBK = 256;      // columns a row must be a multiple of (one Q4_K super-block)
 constexpr int kStep = 128;    // columns per pipeline step (half a super-block)
@@ -94,21 +94,24 @@ __device__ __forceinline__ void expand_float(const uint8_t *__restrict__ row, ui
 // blocks.  A pipeline step covers 128 columns: thread t expands weight row
 // t/2, unit t%2, and splits 32 inputs of token t/4.  The next step's weight
 // and input loads are issued into registers before this step's MFMAs.
-template <uint32_t FMT, int STORE>
+template <uint32_t FMT, int STORE, int MB>
 __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, uint64_t row_bytes,
                                                 const float *__restrict__ X, float *__restrict__ Y, uint32_t n_rows,
                                                 uint32_t n_cols, uint32_t n_tokens) {
+  constexpr int BM = 64 * MB;           // weight rows of this tile (MB 32-row blocks per wave)
   extern __shared__ _Float16 lds[];
-  _Float16 *A = lds;                    // [kBM][kLds]
-  _Float16 *Bh = A + kBM * kLds;        // [kBN][kLds]
+  _Float16 *A = lds;                    // [BM][kLds]
+  _Float16 *Bh = A + BM * kLds;         // [kBN][kLds]
   _Float16 *Bl = Bh + kBN * kLds;       // [kBN][kLds]
   __shared__ float unscale[kBN];        // 2^-k that undoes each token's input scaling in this step
   const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
-  const uint32_t row0 = blockIdx.x * kBM, tok0 = blockIdx.y * kBN;
+  const uint32_t row0 = blockIdx.x * BM, tok0 = blockIdx.y * kBN;
   const int wm = wave / 2, wn = wave % 2;
 
-  // This thread's weight row and unit, and token and quarter.
-  const int ar = tid / 2, aq = tid % 2;
+  // This thread's weight row and unit (threads past 2·BM stage no weights),
+  // and token and quarter.
+  const bool a_thread = tid < 2 * BM;
+  const int ar = a_thread ? tid / 2 : 0, aq = tid % 2;
   const uint8_t *wrow = W + (uint64_t)min(row0 + ar, n_rows - 1) * row_bytes;
   const int bt = tid / 4, bq = tid % 4;
   const bool tok_ok = tok0 + bt < n_tokens;
@@ -117,25 +120,28 @@ __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, u
   RawUnit ra{};
   float4 xv[8];
   auto prefetch = [&](uint32_t k0) {
-    if constexpr (FMT == 12) ra = fetch_q4k(wrow, k0 & ~255u, (int)((k0 & 255u) / 64) + aq);
+    if constexpr (FMT == 12)
+      if (a_thread) ra = fetch_q4k(wrow, k0 & ~255u, (int)((k0 & 255u) / 64) + aq);
     const float4 *src = reinterpret_cast<const float4 *>(xrow + k0);
 #pragma unroll
     for (int i = 0; i < 8; i++) xv[i] = src[i];
   };
 
-  float16_t total[2], acc[2];
+  float16_t total[MB], acc[MB];
 #pragma unroll
-  for (int b = 0; b < 2; b++)
+  for (int b = 0; b < MB; b++)
 #pragma unroll
     for (int i = 0; i < 16; i++) total[b][i] = 0.f;
 
   prefetch(0);
   for (uint32_t k0 = 0; k0 < n_cols; k0 += kStep) {
     // Stage this step: weights to halves, inputs scaled and split.
-    if constexpr (FMT == 12)
-      expand_q4k(ra, (int)((k0 & 255u) / 64) + aq, A + ar * kLds + 64 * aq);
-    else
-      expand_float<FMT>(wrow, k0 + 64 * aq, A + ar * kLds + 64 * aq);
+    if (a_thread) {
+      if constexpr (FMT == 12)
+        expand_q4k(ra, (int)((k0 & 255u) / 64) + aq, A + ar * kLds + 64 * aq);
+      else
+        expand_float<FMT>(wrow, k0 + 64 * aq, A + ar * kLds + 64 * aq);
+    }
     {
       // Each token's 128 inputs are scaled by a power of two that brings
       // their largest magnitude just under 2^14 (half precision cannot
@@ -171,29 +177,29 @@ __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, u
     __syncthreads();
     if (k0 + kStep < n_cols) prefetch(k0 + kStep);
     // 16 k-steps of 8: lane supplies A[row = lane%32][k + 4*(lane/32) .. +4].
-    const _Float16 *arow0 = A + (wm * 64 + lane % 32) * kLds + 4 * (lane / 32);
-    const _Float16 *arow1 = arow0 + 32 * kLds;
+    const _Float16 *arow0 = A + (wm * 32 * MB + lane % 32) * kLds + 4 * (lane / 32);
     const _Float16 *bhrow = Bh + (wn * 32 + lane % 32) * kLds + 4 * (lane / 32);
     const _Float16 *blrow = Bl + (wn * 32 + lane % 32) * kLds + 4 * (lane / 32);
 #pragma unroll
-    for (int b = 0; b < 2; b++)
+    for (int b = 0; b < MB; b++)
 #pragma unroll
       for (int i = 0; i < 16; i++) acc[b][i] = 0.f;
 #pragma unroll 4
     for (int kk = 0; kk < kStep; kk += 8) {
-      const half4_t a0 = *reinterpret_cast<const half4_t *>(arow0 + kk);
-      const half4_t a1 = *reinterpret_cast<const half4_t *>(arow1 + kk);
       const half4_t bh = *reinterpret_cast<const half4_t *>(bhrow + kk);
       const half4_t bl = *reinterpret_cast<const half4_t *>(blrow + kk);
-      acc[0] = __builtin_amdgcn_mfma_f32_32x32x8f16(a0, bh, acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_32x32x8f16(a1, bh, acc[1], 0, 0, 0);
-      acc[0] = __builtin_amdgcn_mfma_f32_32x32x8f16(a0, bl, acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_32x32x8f16(a1, bl, acc[1], 0, 0, 0);
+      half4_t a[MB];
+#pragma unroll
+      for (int b = 0; b < MB; b++) a[b] = *reinterpret_cast<const half4_t *>(arow0 + 32 * b * kLds + kk);
+#pragma unroll
+      for (int b = 0; b < MB; b++) acc[b] = __builtin_amdgcn_mfma_f32_32x32x8f16(a[b], bh, acc[b], 0, 0, 0);
+#pragma unroll
+      for (int b = 0; b < MB; b++) acc[b] = __builtin_amdgcn_mfma_f32_32x32x8f16(a[b], bl, acc[b], 0, 0, 0);
     }
     // Every accumulator of a lane belongs to token column lane%32.
     const float us = unscale[wn * 32 + lane % 32];
 #pragma unroll
-    for (int b = 0; b < 2; b++)
+    for (int b = 0; b < MB; b++)
 #pragma unroll
       for (int i = 0; i < 16; i++) total[b][i] = fmaf(acc[b][i], us, total[b][i]);
     __syncthreads();
@@ -202,10 +208,10 @@ __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, u
   const uint32_t tok = tok0 + wn * 32 + lane % 32;
   if (tok >= n_tokens) return;
 #pragma unroll
-  for (int b = 0; b < 2; b++)
+  for (int b = 0; b < MB; b++)
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const uint32_t row = row0 + wm * 64 + 32 * b + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+      const uint32_t row = row0 + wm * 32 * MB + 32 * b + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
       if (row < n_rows) {
         float *y = Y + (uint64_t)tok * n_rows + row;
         if (STORE == 0)
@@ -218,17 +224,29 @@ __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, u
     }
 }
 
+template <uint32_t FMT, int MB>
+static void matmul_tile(hipStream_t s, const uint8_t *W, uint64_t rb, const float *x, float *y, uint32_t n_rows,
+                        uint32_t n_cols, uint32_t n_tokens, uint32_t store) {
+  dim3 grid(div_ceil(n_rows, 64 * MB), div_ceil(n_tokens, kBN));
+  const size_t lds = (size_t)(64 * MB + 2 * kBN) * kLds * sizeof(_Float16);
+  if (store == 0)
+    k_matmul<FMT, 0, MB><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_tokens);
+  else if (store == 1)
+    k_matmul<FMT, 1, MB><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_tokens);
+  else
+    k_matmul<FMT, 2, MB><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_tokens);
+}
+
+// 128-row tiles when they give the chip at least two workgroups per CU,
+// 64-row tiles (twice the workgroups) otherwise.
 template <uint32_t FMT>
 static void matmul_fmt(hipStream_t s, const uint8_t *W, uint64_t rb, const float *x, float *y, uint32_t n_rows,
                        uint32_t n_cols, uint32_t n_tokens, uint32_t store) {
-  dim3 grid(div_ceil(n_rows, kBM), div_ceil(n_tokens, kBN));
-  const size_t lds = (size_t)(kBM + 2 * kBN) * kLds * sizeof(_Float16);
-  if (store == 0)
-    k_matmul<FMT, 0><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_tokens);
-  else if (store == 1)
-    k_matmul<FMT, 1><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_tokens);
+  const uint64_t big_tiles = (uint64_t)div_ceil(n_rows, 128) * div_ceil(n_tokens, kBN);
+  if (big_tiles >= 512)
+    matmul_tile<FMT, 2>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
   else
-    k_matmul<FMT, 2><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_tokens);
+    matmul_tile<FMT, 1>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
 }
 
 static void set_lds_limits();
@@ -252,7 +270,9 @@ static void set_lds_limits() {
   if (done) return;
   done = true;
   const int lds = (kBM + 2 * kBN) * kLds * sizeof(_Float16);
-#define BCH_SET(F, S) hipFuncSetAttribute((const void *)k_matmul<F, S>, hipFuncAttributeMaxDynamicSharedMemorySize, lds)
+#define BCH_SET(F, S)                                                                                        \
+  hipFuncSetAttribute((const void *)k_matmul<F, S, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);    \
+  hipFuncSetAttribute((const void *)k_matmul<F, S, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, lds)
   BCH_SET(12, 0); BCH_SET(12, 1); BCH_SET(12, 2);
   BCH_SET(1, 0); BCH_SET(1, 1); BCH_SET(1, 2);
   BCH_SET(0, 0); BCH_SET(0, 1); BCH_SET(0, 2);
