@@ -171,6 +171,10 @@ PROTOTYPES = {
     "bch_moe_route": (_int, [_vp, View, C.POINTER(Norm), View, View, View, View, _u32, _u32, _u32, _u32]),
     "bch_matvec_experts_swiglu": (_int, [_vp, _u32, View, View, _u32, _u32, _u32, View, View, _u32, View, _u32]),
     "bch_matvec_experts_down": (_int, [_vp, _u32, View, _u32, _u32, _u32, View, View, _u32, View, _u32]),
+    "bch_moe_group": (_int, [_vp, View, View, View, _u32, _u32, _u32]),
+    "bch_matmul_experts": (_int, [_vp, _u32, View, C.POINTER(View), _u32, _u32, _u32, View, C.c_int, View, View,
+                                  _u32, View, _u32]),
+    "bch_moe_combine": (_int, [_vp, View, View, View, _u32, _u32, _u32]),
     "bch_lfm2_new": (_int, [_vp, C.POINTER(Lfm2Model), _u32, _int, C.POINTER(_vp)]),
     "bch_lfm2_free": (None, [_vp]),
     "bch_lfm2_n_past": (_u32, [_vp]),

@@ -260,6 +260,20 @@ class Hip:
         check(lib().bch_matvec_experts_down(self.handle, int(fmt), _view(weights), n_rows, n_cols, n_experts,
                                             _view(x), _view(route), n_used, _view(y), n_tokens))
 
+    def moe_group(self, route, offsets, entries, n_experts, n_used, n_tokens):
+        check(lib().bch_moe_group(self.handle, _view(route), _view(offsets), _view(entries), n_experts, n_used,
+                                  n_tokens))
+
+    def matmul_experts(self, fmt, weights, up, n_rows, n_cols, n_experts, x, shared_input, offsets, entries,
+                       n_used, y, n_tokens):
+        upv = C.byref(_view(up)) if up is not None else None
+        check(lib().bch_matmul_experts(self.handle, int(fmt), _view(weights), upv, n_rows, n_cols, n_experts,
+                                       _view(x), int(bool(shared_input)), _view(offsets), _view(entries), n_used,
+                                       _view(y), n_tokens))
+
+    def moe_combine(self, x, route, y, n_embd, n_used, n_tokens):
+        check(lib().bch_moe_combine(self.handle, _view(x), _view(route), _view(y), n_embd, n_used, n_tokens))
+
     def sample(self, logits, n_vocab, recent, n_recent, settings, rng_state, out):
         check(lib().bch_sample(self.handle, _view(logits), n_vocab, _view(recent), n_recent, C.byref(settings),
                                _view(rng_state), _view(out)))

@@ -37,6 +37,11 @@ FLAGS = [
 
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
+    if os.environ.get("BCH_INCREMENTAL") == "1" and obj.exists():
+        # Development shortcut: keep an object newer than its source and every header.
+        newest = max(p.stat().st_mtime for p in [src, *CSRC.glob("*.h"), PKG.parent / "include" / "bobcat_hip.h"])
+        if obj.stat().st_mtime > newest:
+            return obj
     cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:

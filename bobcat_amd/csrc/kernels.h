@@ -86,6 +86,15 @@ constexpr uint32_t kMoeMaxExperts = 128;  // MOE_MAX_EXPERTS
 constexpr uint32_t kMoeMaxUsed = 8;       // MOE_MAX_USED
 // Route n_tokens tokens of x; with norm_w, RMS-normalise each token first
 // and store it at `normed`.
+// Batched experts (prefill): grouping, grouped GEMM, weighted combine.
+void run_moe_group(hipStream_t s, const uint32_t *route, uint32_t *offsets, uint32_t *entries, uint32_t n_experts,
+                   uint32_t n_used, uint32_t n_tokens);
+void run_matmul_experts(hipStream_t s, uint32_t format, const uint8_t *W, const uint8_t *up, uint32_t n_rows,
+                        uint32_t n_cols, uint32_t n_experts, const float *x, bool shared_input,
+                        const uint32_t *offsets, const uint32_t *entries, uint32_t n_used, float *y,
+                        uint32_t n_tokens);
+void run_moe_combine(hipStream_t s, const float *x, const uint32_t *route, float *y, uint32_t n_embd,
+                     uint32_t n_used, uint32_t n_tokens);
 void run_moe_route(hipStream_t s, const float *x, const float *norm_w, float eps, float *normed, const float *router,
                    const float *bias, uint32_t *route, uint32_t n_cols, uint32_t n_experts, uint32_t n_used,
                    uint32_t n_tokens);

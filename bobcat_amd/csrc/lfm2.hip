@@ -63,6 +63,10 @@ struct bch_lfm2 : bch::Sequence {
   float *partials = nullptr;
   uint32_t *counters = nullptr;
   uint32_t *route = nullptr;  // expert routes of a batch (route_bytes(n_used, batch))
+  // Batched experts: the batch's entries grouped by expert, each entry's
+  // SwiGLU activations and down projection (Recorder::grouped_moe).
+  uint32_t *moe_offsets = nullptr, *moe_entries = nullptr;
+  float *expert_ffn = nullptr, *expert_out = nullptr;
   bool kv_half = true;
   uint32_t decode_splits = 1, prefill_splits = 1;
 
@@ -269,9 +273,23 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
       // Route the whole batch in one launch, then each token's experts.
       run_moe_route(s, m->normed, nullptr, 0.f, nullptr, reinterpret_cast<const float *>(L.router.data),
                     L.expert_bias, m->route, n, m->n_experts, m->n_used, count);
-      for (uint32_t t = 0; t < count; t++)
-        record_moe_token(m, s, L, m->normed + (uint64_t)t * n, nullptr, nullptr,
-                         m->route + (uint64_t)t * 2 * m->n_used, m->hidden + (uint64_t)t * n);
+      const bool grouped = count > 1 && n % 256 == 0 && m->n_ff_expert % 256 == 0 &&
+                           L.gate_exps.format == L.up_exps.format;
+      if (grouped) {
+        // lfm2_metal.rs:1317-1380: group the entries by expert, one MFMA
+        // GEMM per stacked matrix over all experts, then the weighted sum.
+        run_moe_group(s, m->route, m->moe_offsets, m->moe_entries, m->n_experts, m->n_used, count);
+        run_matmul_experts(s, L.gate_exps.format, L.gate_exps.data, L.up_exps.data, m->n_ff_expert, n,
+                           m->n_experts, m->normed, true, m->moe_offsets, m->moe_entries, m->n_used, m->expert_ffn,
+                           count);
+        run_matmul_experts(s, L.down_exps.format, L.down_exps.data, nullptr, n, m->n_ff_expert, m->n_experts,
+                           m->expert_ffn, false, m->moe_offsets, m->moe_entries, m->n_used, m->expert_out, count);
+        run_moe_combine(s, m->expert_out, m->route, m->hidden, n, m->n_used, count);
+      } else {
+        for (uint32_t t = 0; t < count; t++)
+          record_moe_token(m, s, L, m->normed + (uint64_t)t * n, nullptr, nullptr,
+                           m->route + (uint64_t)t * 2 * m->n_used, m->hidden + (uint64_t)t * n);
+      }
       check_finite(s, "moe", il, m->hidden, (uint64_t)count * n);
     } else {
       run_matmul(s, L.gate.format, L.gate.data, m->n_ff, n, m->normed, m->ffn, count, 0);
@@ -440,7 +458,12 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
            (rc = m->alloc_t(std::max<uint64_t>(rows * m->n_ff, (uint64_t)m->n_used * m->n_ff_expert), &m->ffn)) ||
            (rc = m->alloc_t(partial_floats + 4, &m->partials)) ||
            (rc = m->alloc_t((uint64_t)kAttnQueryBatch * std::max(1u, m->n_heads), &m->counters)) ||
-           (rc = m->alloc_t(2 * (uint64_t)std::max(1u, m->n_used) * rows, &m->route)) || (rc = m->alloc_common()));
+           (rc = m->alloc_t(2 * (uint64_t)std::max(1u, m->n_used) * rows, &m->route)) ||
+           (rc = m->alloc_t((uint64_t)m->n_experts + 1, &m->moe_offsets)) ||
+           (rc = m->alloc_t(std::max(1u, m->n_used) * rows, &m->moe_entries)) ||
+           (rc = m->alloc_t(std::max<uint64_t>(1, (uint64_t)m->n_used * rows * m->n_ff_expert), &m->expert_ffn)) ||
+           (rc = m->alloc_t(std::max<uint64_t>(1, (uint64_t)m->n_used * rows * n), &m->expert_out)) ||
+           (rc = m->alloc_common()));
     if (rc) return cleanup(rc);
   }
   *out = m;

@@ -94,10 +94,20 @@ __device__ __forceinline__ void expand_float(const uint8_t *__restrict__ row, ui
 // blocks.  A pipeline step covers 128 columns: thread t expands weight row
 // t/2, unit t%2, and splits 32 inputs of token t/4.  The next step's weight
 // and input loads are issued into registers before this step's MFMAs.
-template <uint32_t FMT, int STORE, int MB>
+// Expert groups of a grouped launch (Metal::matmul_experts): the entries of
+// expert e are positions offsets[e] .. offsets[e+1] of `entries`, each entry
+// v = token·n_used + slot; entry v reads input row v / x_div and writes
+// output row v.  The token tiles of all experts are numbered one after the
+// other along blockIdx.y.
+struct ExpertGroups {
+  const uint32_t *offsets, *entries;
+  uint32_t n_experts, x_div;
+};
+
+template <uint32_t FMT, int STORE, int MB, bool GROUPED>
 __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, uint64_t row_bytes,
                                                 const float *__restrict__ X, float *__restrict__ Y, uint32_t n_rows,
-                                                uint32_t n_cols, uint32_t n_tokens) {
+                                                uint32_t n_cols, uint32_t n_tokens, ExpertGroups groups) {
   constexpr int BM = 64 * MB;           // weight rows of this tile (MB 32-row blocks per wave)
   extern __shared__ _Float16 lds[];
   _Float16 *A = lds;                    // [BM][kLds]
@@ -105,8 +115,35 @@ __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, u
   _Float16 *Bl = Bh + kBN * kLds;       // [kBN][kLds]
   __shared__ float unscale[kBN];        // 2^-k that undoes each token's input scaling in this step
   const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
-  const uint32_t row0 = blockIdx.x * BM, tok0 = blockIdx.y * kBN;
+  const uint32_t row0 = blockIdx.x * BM;
+  uint32_t tok0 = blockIdx.y * kBN, tok_end = n_tokens;  // positions [tok0, tok_end) of this tile's group
   const int wm = wave / 2, wn = wave % 2;
+  if constexpr (GROUPED) {
+    // Find this tile's expert: the offsets go to LDS, one thread walks them.
+    __shared__ uint32_t off_s[kMoeMaxExperts + 1];
+    __shared__ uint32_t pick[3];
+    for (uint32_t e = tid; e <= groups.n_experts; e += 256) off_s[e] = groups.offsets[e];
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t t = blockIdx.y, e = 0;
+      for (; e < groups.n_experts; e++) {
+        const uint32_t tiles = (off_s[e + 1] - off_s[e] + kBN - 1) / kBN;
+        if (t < tiles) break;
+        t -= tiles;
+      }
+      pick[0] = e;
+      pick[1] = e < groups.n_experts ? off_s[e] + t * kBN : 0;
+      pick[2] = e < groups.n_experts ? off_s[e + 1] : 0;
+    }
+    __syncthreads();
+    if (pick[0] >= groups.n_experts) return;  // past the last tile (the grid is an upper bound)
+    W += (uint64_t)pick[0] * n_rows * row_bytes;
+    tok0 = pick[1];
+    tok_end = pick[2];
+  }
+  // Input and output rows of tile position p.
+  auto x_row = [&](uint32_t p) { return GROUPED ? groups.entries[p] / groups.x_div : p; };
+  auto y_row = [&](uint32_t p) { return GROUPED ? groups.entries[p] : p; };
 
   // This thread's weight row and unit (threads past 2·BM stage no weights),
   // and token and quarter.
@@ -114,8 +151,8 @@ __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, u
   const int ar = a_thread ? tid / 2 : 0, aq = tid % 2;
   const uint8_t *wrow = W + (uint64_t)min(row0 + ar, n_rows - 1) * row_bytes;
   const int bt = tid / 4, bq = tid % 4;
-  const bool tok_ok = tok0 + bt < n_tokens;
-  const float *xrow = X + (uint64_t)min(tok0 + bt, n_tokens - 1) * n_cols + 32 * bq;
+  const bool tok_ok = tok0 + bt < tok_end;
+  const float *xrow = X + (uint64_t)x_row(min(tok0 + bt, tok_end - 1)) * n_cols + 32 * bq;
 
   RawUnit ra{};
   float4 xv[8];
@@ -206,14 +243,15 @@ __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, u
   }
   // total[b][r] holds D[row = 32b + 8*(r/4) + 4*(lane/32) + r%4][token = lane%32].
   const uint32_t tok = tok0 + wn * 32 + lane % 32;
-  if (tok >= n_tokens) return;
+  if (tok >= tok_end) return;
+  const uint64_t yr = y_row(tok);
 #pragma unroll
   for (int b = 0; b < MB; b++)
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const uint32_t row = row0 + wm * 32 * MB + 32 * b + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
       if (row < n_rows) {
-        float *y = Y + (uint64_t)tok * n_rows + row;
+        float *y = Y + yr * n_rows + row;
         if (STORE == 0)
           *y = total[b][r];
         else if (STORE == 1)
@@ -229,12 +267,27 @@ static void matmul_tile(hipStream_t s, const uint8_t *W, uint64_t rb, const floa
                         uint32_t n_cols, uint32_t n_tokens, uint32_t store) {
   dim3 grid(div_ceil(n_rows, 64 * MB), div_ceil(n_tokens, kBN));
   const size_t lds = (size_t)(64 * MB + 2 * kBN) * kLds * sizeof(_Float16);
+  const ExpertGroups none{};
   if (store == 0)
-    k_matmul<FMT, 0, MB><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_tokens);
+    k_matmul<FMT, 0, MB, false><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_tokens, none);
   else if (store == 1)
-    k_matmul<FMT, 1, MB><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_tokens);
+    k_matmul<FMT, 1, MB, false><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_tokens, none);
   else
-    k_matmul<FMT, 2, MB><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_tokens);
+    k_matmul<FMT, 2, MB, false><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_tokens, none);
+}
+
+// Grouped launch over n_entries entries (64-row tiles; an expert's tiles
+// are few).  Store 0 overwrites, 2 applies SiLU(y)·product.
+template <uint32_t FMT>
+static void matmul_experts_fmt(hipStream_t s, const uint8_t *W, uint64_t rb, const float *x, float *y,
+                               uint32_t n_rows, uint32_t n_cols, uint32_t n_entries, uint32_t store,
+                               const ExpertGroups &g) {
+  dim3 grid(div_ceil(n_rows, 64), div_ceil(n_entries, kBN) + g.n_experts);
+  const size_t lds = (size_t)(64 + 2 * kBN) * kLds * sizeof(_Float16);
+  if (store == 2)
+    k_matmul<FMT, 2, 1, true><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_entries, g);
+  else
+    k_matmul<FMT, 0, 1, true><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_entries, g);
 }
 
 // 128-row tiles when they give the chip at least two workgroups per CU,
@@ -265,17 +318,41 @@ void run_matmul(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_row
 
 static bool matmul_format(uint32_t f) { return f == 12 || f == 1 || f == 0; }
 
+void run_matmul_experts(hipStream_t s, uint32_t format, const uint8_t *W, const uint8_t *up, uint32_t n_rows,
+                        uint32_t n_cols, uint32_t n_experts, const float *x, bool shared_input,
+                        const uint32_t *offsets, const uint32_t *entries, uint32_t n_used, float *y,
+                        uint32_t n_tokens) {
+  set_lds_limits();
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  const ExpertGroups g{offsets, entries, n_experts, shared_input ? n_used : 1u};
+  const uint32_t n_entries = n_used * n_tokens;
+  auto one = [&](const uint8_t *w, uint32_t store) {
+    if (format == 12)
+      matmul_experts_fmt<12>(s, w, rb, x, y, n_rows, n_cols, n_entries, store, g);
+    else if (format == 1)
+      matmul_experts_fmt<1>(s, w, rb, x, y, n_rows, n_cols, n_entries, store, g);
+    else
+      matmul_experts_fmt<0>(s, w, rb, x, y, n_rows, n_cols, n_entries, store, g);
+  };
+  one(W, 0);
+  if (up) one(up, 2);  // SwiGLU: the up products times SiLU of the gate products
+}
+
 static void set_lds_limits() {
   static bool done = false;
   if (done) return;
   done = true;
   const int lds = (kBM + 2 * kBN) * kLds * sizeof(_Float16);
-#define BCH_SET(F, S)                                                                                        \
-  hipFuncSetAttribute((const void *)k_matmul<F, S, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);    \
-  hipFuncSetAttribute((const void *)k_matmul<F, S, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, lds)
+#define BCH_SET(F, S)                                                                                          \
+  hipFuncSetAttribute((const void *)k_matmul<F, S, 2, false>, hipFuncAttributeMaxDynamicSharedMemorySize, lds); \
+  hipFuncSetAttribute((const void *)k_matmul<F, S, 1, false>, hipFuncAttributeMaxDynamicSharedMemorySize, lds)
   BCH_SET(12, 0); BCH_SET(12, 1); BCH_SET(12, 2);
   BCH_SET(1, 0); BCH_SET(1, 1); BCH_SET(1, 2);
   BCH_SET(0, 0); BCH_SET(0, 1); BCH_SET(0, 2);
+#undef BCH_SET
+#define BCH_SET(F, S) \
+  hipFuncSetAttribute((const void *)k_matmul<F, S, 1, true>, hipFuncAttributeMaxDynamicSharedMemorySize, lds)
+  BCH_SET(12, 0); BCH_SET(12, 2); BCH_SET(1, 0); BCH_SET(1, 2); BCH_SET(0, 0); BCH_SET(0, 2);
 #undef BCH_SET
 }
 

@@ -207,11 +207,76 @@ bool run_experts_down(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t
   return false;
 }
 
+// --- grouping for the batched experts --------------------------------------
+
+// Entries v = token·n_used + slot grouped by expert (moe.metal:122-175 is
+// the reference's kernel): offsets[e] is where expert e's entries start in
+// `entries`, in token order, and offsets[n_experts] the total.  One
+// workgroup of 16 waves; wave w takes experts w, w + 16, ...: its lanes test
+// 64 consecutive entries at a time and a ballot prefix places the matches.
+constexpr int kGroupWaves = 16;
+
+__global__ __launch_bounds__(kGroupWaves * 64) void k_moe_group(const uint32_t *__restrict__ route,
+                                                                uint32_t *__restrict__ offsets,
+                                                                uint32_t *__restrict__ entries, uint32_t n_experts,
+                                                                uint32_t n_used, uint32_t n_tokens) {
+  __shared__ uint32_t counts[kMoeMaxExperts];
+  const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64, n_entries = n_used * n_tokens;
+  auto expert_of = [&](uint32_t v) { return route[2ull * n_used * (v / n_used) + v % n_used]; };
+  for (uint32_t e = wave; e < n_experts; e += kGroupWaves) {
+    uint32_t c = 0;
+    for (uint32_t v = lane; v < n_entries; v += 64) c += expert_of(v) == e;
+    for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+    if (lane == 0) counts[e] = c;
+  }
+  __syncthreads();
+  for (uint32_t e = wave; e < n_experts; e += kGroupWaves) {
+    uint32_t start = 0;
+    for (uint32_t b = 0; b < e; b++) start += counts[b];
+    if (lane == 0) {
+      offsets[e] = start;
+      if (e == n_experts - 1) offsets[n_experts] = start + counts[e];
+    }
+    for (uint32_t first = 0; first < n_entries; first += 64) {
+      const uint32_t v = first + lane;
+      const bool match = v < n_entries && expert_of(v) == e;
+      const uint64_t mask = __ballot(match);
+      if (match) entries[start + __popcll(mask & ((1ull << lane) - 1))] = v;
+      start += __popcll(mask);
+    }
+  }
+}
+
+// y[t] += Σ_s w_s · x[n_used·t + s], the sum in slot order first
+// (moe.metal:177-200).  One thread per element.
+__global__ void k_moe_combine(const float *__restrict__ x, const uint32_t *__restrict__ route, float *__restrict__ y,
+                              uint32_t n_embd, uint32_t n_used, uint32_t n_tokens) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (uint64_t)n_tokens * n_embd) return;
+  const uint64_t t = i / n_embd, d = i % n_embd;
+  const uint32_t *r = route + 2 * n_used * t;
+  float sum = 0.f;
+  for (uint32_t k = 0; k < n_used; k++) sum += __uint_as_float(r[n_used + k]) * x[(t * n_used + k) * n_embd + d];
+  y[i] += sum;
+}
+
+void run_moe_group(hipStream_t s, const uint32_t *route, uint32_t *offsets, uint32_t *entries, uint32_t n_experts,
+                   uint32_t n_used, uint32_t n_tokens) {
+  k_moe_group<<<1, kGroupWaves * 64, 0, s>>>(route, offsets, entries, n_experts, n_used, n_tokens);
+}
+
+void run_moe_combine(hipStream_t s, const float *x, const uint32_t *route, float *y, uint32_t n_embd,
+                     uint32_t n_used, uint32_t n_tokens) {
+  const uint64_t n = (uint64_t)n_tokens * n_embd;
+  if (n) k_moe_combine<<<(uint32_t)((n + 255) / 256), 256, 0, s>>>(x, route, y, n_embd, n_used, n_tokens);
+}
+
 }  // namespace bch
 
 // ---------------------------------------------------------------------
 // C ABI (Metal::moe_route / matvec_experts_swiglu / matvec_experts_down /
-// route_bytes, crates/bobcat-metal/src/backend.rs:1428-1597, 2724-2734).
+// moe_group / matmul_experts / moe_combine / route_bytes,
+// crates/bobcat-metal/src/backend.rs:1428-1731, 2724-2734).
 // ---------------------------------------------------------------------
 
 using namespace bch;
@@ -315,4 +380,64 @@ extern "C" int bch_matvec_experts_down(bch_ctx *ctx, uint32_t format, bch_view w
   }));
   if (!ok) return fail(BCH_ERR_UNSUPPORTED_FORMAT, "matvec_experts_down: rows of %u columns are too wide", n_cols);
   return BCH_OK;
+}
+
+extern "C" int bch_moe_group(bch_ctx *ctx, bch_view route, bch_view offsets, bch_view entries, uint32_t n_experts,
+                             uint32_t n_used, uint32_t n_tokens) {
+  BCH_TRY(check_experts(n_experts, n_used));
+  const uint32_t *rp;
+  uint32_t *op, *ep;
+  BCH_TRY(view_ptr(ctx, "moe_group", route, bch_route_bytes(n_used, n_tokens), &rp));
+  BCH_TRY(view_ptr(ctx, "moe_group", offsets, (uint64_t)(n_experts + 1) * 4, &op));
+  BCH_TRY(view_ptr(ctx, "moe_group", entries, (uint64_t)n_used * n_tokens * 4, &ep));
+  return launch(ctx, {"moe_group", 0, 0, 0},
+                [&](hipStream_t s) { run_moe_group(s, rp, op, ep, n_experts, n_used, n_tokens); });
+}
+
+extern "C" int bch_matmul_experts(bch_ctx *ctx, uint32_t format, bch_view weights, const bch_view *up,
+                                  uint32_t n_rows, uint32_t n_cols, uint32_t n_experts, bch_view x,
+                                  int shared_input, bch_view offsets, bch_view entries, uint32_t n_used, bch_view y,
+                                  uint32_t n_tokens) {
+  if (!expert_format(format))
+    return fail(BCH_ERR_UNSUPPORTED_FORMAT, "format %u has no expert kernels", format);
+  BCH_TRY(check_experts(n_experts, n_used));
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  if (rb == 0 || n_rows == 0 || n_cols % 256)
+    return fail(BCH_ERR_ARGUMENT, "matmul_experts: %u x %u needs columns in multiples of 256", n_rows, n_cols);
+  const uint64_t entry_count = (uint64_t)n_used * n_tokens;
+  const uint64_t input_rows = shared_input ? n_tokens : entry_count;
+  const uint64_t stacked = rb * n_rows * n_experts;
+  const uint8_t *wp, *upp = nullptr;
+  const float *xp;
+  const uint32_t *op, *ep;
+  float *yp;
+  BCH_TRY(view_ptr(ctx, "matmul_experts", weights, stacked, &wp));
+  if (up) BCH_TRY(view_ptr(ctx, "matmul_experts", *up, stacked, &upp));
+  BCH_TRY(view_ptr(ctx, "matmul_experts", x, input_rows * n_cols * 4, &xp));
+  BCH_TRY(view_ptr(ctx, "matmul_experts", y, entry_count * n_rows * 4, &yp));
+  BCH_TRY(view_ptr(ctx, "matmul_experts", offsets, (uint64_t)(n_experts + 1) * 4, &op));
+  BCH_TRY(view_ptr(ctx, "matmul_experts", entries, entry_count * 4, &ep));
+  if (reinterpret_cast<uintptr_t>(wp) % 16 || reinterpret_cast<uintptr_t>(upp) % 16 ||
+      reinterpret_cast<uintptr_t>(xp) % 16)
+    return fail(BCH_ERR_ARGUMENT, "matmul_experts: operands must be 16-byte aligned");
+  return launch(ctx, {"matmul_experts", n_rows, n_cols, stacked * (up ? 2 : 1)}, [&](hipStream_t s) {
+    if (n_tokens)
+      run_matmul_experts(s, format, wp, upp, n_rows, n_cols, n_experts, xp, shared_input != 0, op, ep, n_used, yp,
+                         n_tokens);
+  });
+}
+
+extern "C" int bch_moe_combine(bch_ctx *ctx, bch_view x, bch_view route, bch_view y, uint32_t n_embd,
+                               uint32_t n_used, uint32_t n_tokens) {
+  if (n_used == 0 || n_used > kMoeMaxUsed)
+    return fail(BCH_ERR_EXPERT_LIMITS, "at most %u experts per token, got %u", kMoeMaxUsed, n_used);
+  const float *xp;
+  const uint32_t *rp;
+  float *yp;
+  const uint64_t n = (uint64_t)n_tokens * n_embd;
+  BCH_TRY(view_ptr(ctx, "moe_combine", x, n * n_used * 4, &xp));
+  BCH_TRY(view_ptr(ctx, "moe_combine", route, bch_route_bytes(n_used, n_tokens), &rp));
+  BCH_TRY(view_ptr(ctx, "moe_combine", y, n * 4, &yp));
+  return launch(ctx, {"moe_combine", 0, 0, 0},
+                [&](hipStream_t s) { run_moe_combine(s, xp, rp, yp, n_embd, n_used, n_tokens); });
 }

@@ -249,6 +249,23 @@ int bch_matvec_experts_swiglu(bch_ctx *ctx, uint32_t format, bch_view gate, bch_
 int bch_matvec_experts_down(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_rows, uint32_t n_cols,
                             uint32_t n_experts, bch_view x, bch_view route, uint32_t n_used, bch_view y,
                             uint32_t n_tokens);
+/* Metal::moe_group (backend.rs:1599-1628): the n_used·n_tokens entries
+ * v = n_used·t + s grouped by expert; expert e's entries are
+ * entries[offsets[e] .. offsets[e+1]) in token order, offsets[n_experts]
+ * the total.  offsets: n_experts + 1 u32, entries: n_used·n_tokens u32. */
+int bch_moe_group(bch_ctx *ctx, bch_view route, bch_view offsets, bch_view entries, uint32_t n_experts,
+                  uint32_t n_used, uint32_t n_tokens);
+/* Metal::matmul_experts (backend.rs:1630-1703): each expert of the stack
+ * times the inputs grouped to it, on MFMA.  Entry v reads row v of x, or
+ * row v / n_used with shared_input, and overwrites row v of y; with `up`
+ * (may be NULL) y = silu(W_e·x) ⊙ Up_e·x.  Columns a multiple of 256. */
+int bch_matmul_experts(bch_ctx *ctx, uint32_t format, bch_view weights, const bch_view *up, uint32_t n_rows,
+                       uint32_t n_cols, uint32_t n_experts, bch_view x, int shared_input, bch_view offsets,
+                       bch_view entries, uint32_t n_used, bch_view y, uint32_t n_tokens);
+/* Metal::moe_combine (backend.rs:1705-1731): y_t += Σ_s w_s · x_{n_used·t+s},
+ * the slots summed in route order before the add. */
+int bch_moe_combine(bch_ctx *ctx, bch_view x, bch_view route, bch_view y, uint32_t n_embd, uint32_t n_used,
+                    uint32_t n_tokens);
 
 /* ------------------------------------------------------------------ */
 /* Sampling                                                            */

@@ -142,3 +142,78 @@ def test_expert_limits(hip):
             hip.moe_route(x.at(0), None, None, router.at(0), x.at(0), route.at(0), 256, n_experts, n_used, 1)
         hip.discard()
         assert e.value.status == EXPERT_LIMITS
+
+
+@pytest.mark.parametrize("n_experts,n_used,n_ff,n_embd,n_tokens", [
+    (32, 4, 1792, 2048, 300), (8, 2, 256, 512, 65), (4, 4, 512, 256, 1), (128, 8, 256, 256, 40)])
+def test_grouped_experts_match_oracle(hip, n_experts, n_used, n_ff, n_embd, n_tokens):
+    """The batched (prefill) path of lfm2_metal.rs:1317-1380: moe_group's
+    grouping (expert by expert, token order within), matmul_experts (SwiGLU
+    with shared token inputs, then down on the entries' rows) and moe_combine
+    (slots summed in route order, then added).  Weights round to half in the
+    MFMA tiles as the reference's expanded half tiles do, so the products are
+    compared with half-rounded dequantised weights in float64, within 1e-5 of
+    each row's term-scale."""
+    rng = np.random.default_rng(n_experts * 7 + n_tokens)
+    gate = expert_case(rng, n_experts, n_ff, n_embd)
+    up = expert_case(rng, n_experts, n_ff, n_embd)
+    down = expert_case(rng, n_experts, n_embd, n_ff)
+    x = rng.standard_normal((n_tokens, n_embd)).astype(np.float32)
+    ids = np.stack([rng.choice(n_experts, n_used, replace=False) for _ in range(n_tokens)]).astype(np.uint32)
+    wts = rng.uniform(0.05, 0.5, (n_tokens, n_used)).astype(np.float32)
+    route_np = np.concatenate([ids, wts.view(np.uint32)], axis=1).reshape(-1)
+    n_entries = n_tokens * n_used
+
+    rtb = hip.buffer_from(route_np)
+    offb, entb = hip.new_buffer((n_experts + 1) * 4), hip.new_buffer(n_entries * 4)
+    run(hip, lambda: hip.moe_group(rtb.at(0), offb.at(0), entb.at(0), n_experts, n_used, n_tokens))
+    offsets = hip.read(offb.at(0), np.empty(n_experts + 1, np.uint32))
+    entries = hip.read(entb.at(0), np.empty(n_entries, np.uint32))
+    flat = ids.reshape(-1)
+    want_entries = np.concatenate([np.nonzero(flat == e)[0] for e in range(n_experts)]).astype(np.uint32)
+    want_offsets = np.concatenate([[0], np.cumsum([(flat == e).sum() for e in range(n_experts)])]).astype(np.uint32)
+    assert (offsets == want_offsets).all() and (entries == want_entries).all()
+
+    gb, ub, db, xb = hip.buffer_from(gate), hip.buffer_from(up), hip.buffer_from(down), hip.buffer_from(x)
+    ffb, outb = hip.new_buffer(n_entries * n_ff * 4), hip.new_buffer(n_entries * n_embd * 4)
+    run(hip, lambda: hip.matmul_experts(Format.Q4K, gb.at(0), ub.at(0), n_ff, n_embd, n_experts, xb.at(0), True,
+                                        offb.at(0), entb.at(0), n_used, ffb.at(0), n_tokens))
+    ffn = hip.read(ffb.at(0), np.empty(n_entries * n_ff, np.float32)).reshape(n_entries, n_ff)
+    rb, rbd = n_embd // 256 * 144, n_ff // 256 * 144
+
+    def half_dense(w, e, rows, cols, row_bytes):
+        return dense(w[e * rows * row_bytes:(e + 1) * rows * row_bytes], rows, cols).astype(np.float16) \
+            .astype(np.float64)
+
+    used = sorted(set(flat.tolist()))
+    for e in used:
+        G, U = half_dense(gate, e, n_ff, n_embd, rb), half_dense(up, e, n_ff, n_embd, rb)
+        for v in np.nonzero(flat == e)[0]:
+            xv = x[v // n_used].astype(np.float64)
+            g, u = G @ xv, U @ xv
+            silu = g / (1 + np.exp(-g))
+            sg, su = np.abs(G) @ np.abs(xv), np.abs(U) @ np.abs(xv)
+            bound = 1e-5 * (1.1 * sg * np.abs(u) + np.abs(silu) * su) + 1e-30
+            assert (np.abs(ffn[v] - silu * u) <= bound).all(), (e, v, (np.abs(ffn[v] - silu * u) / bound).max())
+
+    run(hip, lambda: hip.matmul_experts(Format.Q4K, db.at(0), None, n_embd, n_ff, n_experts, ffb.at(0), False,
+                                        offb.at(0), entb.at(0), n_used, outb.at(0), n_tokens))
+    out = hip.read(outb.at(0), np.empty(n_entries * n_embd, np.float32)).reshape(n_entries, n_embd)
+    for e in used:
+        D = half_dense(down, e, n_embd, n_ff, rbd)
+        for v in np.nonzero(flat == e)[0]:
+            fv = ffn[v].astype(np.float64)
+            want, scale = D @ fv, np.abs(D) @ np.abs(fv)
+            assert np.abs(out[v] - want).max() <= 1e-5 * scale.max() + 1e-30, (e, v)
+
+    resid = rng.standard_normal((n_tokens, n_embd)).astype(np.float32)
+    hb = hip.buffer_from(resid)
+    run(hip, lambda: hip.moe_combine(outb.at(0), rtb.at(0), hb.at(0), n_embd, n_used, n_tokens))
+    got = hip.read(hb.at(0), np.empty(n_tokens * n_embd, np.float32)).reshape(n_tokens, n_embd)
+    want = resid.copy()
+    for t in range(n_tokens):
+        acc = np.zeros(n_embd, np.float32)
+        for s in range(n_used):
+            acc = acc + wts[t, s] * out[t * n_used + s]
+        want[t] = resid[t] + acc
+    assert np.abs(got - want).max() <= 1e-6 * max(1.0, float(np.abs(want).max()))
