@@ -235,7 +235,9 @@ __global__ __launch_bounds__(256) void k_gemv(P p, const float *__restrict__ x, 
   // waiting for x does not wait for the weights.
   constexpr uint32_t kPad = F::kUnit >= 64 ? 4 : 0;  // spreads the fragment reads over the LDS banks
   constexpr uint32_t kSlot = F::kUnit + kPad;
-  constexpr int kPer = 8;  // float4 loads per thread per pass
+  // float4 loads per thread per pass: wide rows (the down projection, 10752
+  // inputs over 192 threads) take one pass, so no second round trip.
+  constexpr int kPer = LPR > 64 && !NORM ? 16 : 8;
   extern __shared__ float4 xs4[];
   float *xs = reinterpret_cast<float *>(xs4);
   const uint32_t n4 = n_cols / 4;

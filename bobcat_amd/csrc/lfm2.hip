@@ -68,7 +68,6 @@ struct bch_lfm2 : bch::Sequence {
   uint32_t *moe_offsets = nullptr, *moe_entries = nullptr;
   float *expert_ffn = nullptr, *expert_out = nullptr;
   bool kv_half = true;
-  uint32_t decode_splits = 1, prefill_splits = 1;
 
   uint64_t cache_elems_per_layer() const { return (uint64_t)n_ctx * kv_dim; }
   void *cache_layer(void *base, uint32_t ci) const {
@@ -444,8 +443,6 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
   {
     const uint64_t rows = m->batch;
     const uint64_t cache = (uint64_t)m->n_attn * n_ctx * m->kv_dim * (m->kv_half ? 2 : 4);
-    m->decode_splits = attention_splits(n_ctx, std::max(1u, m->n_kv_heads), ctx->n_cus);
-    m->prefill_splits = m->decode_splits;
     const uint64_t partial_floats = attention_partial_floats(std::min<uint32_t>(m->batch, kAttnQueryBatch), m->n_heads,
                                                             hd, attn_decode_max_splits(n_ctx, hd, m->kv_half));
     int rc = 0;

@@ -7,7 +7,7 @@
 // straight into LDS instead, so the expanded matrix never touches HBM.
 //
 // Tile: 128 weight rows x 64 tokens, in pipeline steps of 128 columns;
-// v_mfma_f32_32x32x8_f16 on LDS tiles.  Weights go to LDS as fp16 (the
+// v_mfma_f32_32x32x16_f16 on LDS tiles.  Weights go to LDS as fp16 (the
 // reference's expanded half tiles); each token's inputs are scaled by a
 // power of two into fp16 range and split into an fp16 high part and an fp16
 // residual, both multiplied, so the inputs keep ~22 bits whatever their
@@ -26,6 +26,7 @@ constexpr int kPad = 8;       // halves of padding per LDS row (bank spread, 16-
 constexpr int kLds = kStep + kPad;
 
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
@@ -213,25 +214,26 @@ __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, u
     }
     __syncthreads();
     if (k0 + kStep < n_cols) prefetch(k0 + kStep);
-    // 16 k-steps of 8: lane supplies A[row = lane%32][k + 4*(lane/32) .. +4].
-    const _Float16 *arow0 = A + (wm * 32 * MB + lane % 32) * kLds + 4 * (lane / 32);
-    const _Float16 *bhrow = Bh + (wn * 32 + lane % 32) * kLds + 4 * (lane / 32);
-    const _Float16 *blrow = Bl + (wn * 32 + lane % 32) * kLds + 4 * (lane / 32);
+    // 8 k-steps of 16 (gfx950's 32x32x16 f16 MFMA): lane supplies
+    // A[row = lane%32][k + 8*(lane/32) .. +8] and B[k + 8*(lane/32) .. +8][col = lane%32].
+    const _Float16 *arow0 = A + (wm * 32 * MB + lane % 32) * kLds + 8 * (lane / 32);
+    const _Float16 *bhrow = Bh + (wn * 32 + lane % 32) * kLds + 8 * (lane / 32);
+    const _Float16 *blrow = Bl + (wn * 32 + lane % 32) * kLds + 8 * (lane / 32);
 #pragma unroll
     for (int b = 0; b < MB; b++)
 #pragma unroll
       for (int i = 0; i < 16; i++) acc[b][i] = 0.f;
 #pragma unroll 4
-    for (int kk = 0; kk < kStep; kk += 8) {
-      const half4_t bh = *reinterpret_cast<const half4_t *>(bhrow + kk);
-      const half4_t bl = *reinterpret_cast<const half4_t *>(blrow + kk);
-      half4_t a[MB];
+    for (int kk = 0; kk < kStep; kk += 16) {
+      const half8_t bh = *reinterpret_cast<const half8_t *>(bhrow + kk);
+      const half8_t bl = *reinterpret_cast<const half8_t *>(blrow + kk);
+      half8_t a[MB];
 #pragma unroll
-      for (int b = 0; b < MB; b++) a[b] = *reinterpret_cast<const half4_t *>(arow0 + 32 * b * kLds + kk);
+      for (int b = 0; b < MB; b++) a[b] = *reinterpret_cast<const half8_t *>(arow0 + 32 * b * kLds + kk);
 #pragma unroll
-      for (int b = 0; b < MB; b++) acc[b] = __builtin_amdgcn_mfma_f32_32x32x8f16(a[b], bh, acc[b], 0, 0, 0);
+      for (int b = 0; b < MB; b++) acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[b], bh, acc[b], 0, 0, 0);
 #pragma unroll
-      for (int b = 0; b < MB; b++) acc[b] = __builtin_amdgcn_mfma_f32_32x32x8f16(a[b], bl, acc[b], 0, 0, 0);
+      for (int b = 0; b < MB; b++) acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[b], bl, acc[b], 0, 0, 0);
     }
     // Every accumulator of a lane belongs to token column lane%32.
     const float us = unscale[wn * 32 + lane % 32];
