@@ -92,7 +92,7 @@ void run_moe_group(hipStream_t s, const uint32_t *route, uint32_t *offsets, uint
 void run_matmul_experts(hipStream_t s, uint32_t format, const uint8_t *W, const uint8_t *up, uint32_t n_rows,
                         uint32_t n_cols, uint32_t n_experts, const float *x, bool shared_input,
                         const uint32_t *offsets, const uint32_t *entries, uint32_t n_used, float *y,
-                        uint32_t n_tokens);
+                        uint32_t n_tokens, void *split);
 void run_moe_combine(hipStream_t s, const float *x, const uint32_t *route, float *y, uint32_t n_embd,
                      uint32_t n_used, uint32_t n_tokens);
 void run_moe_route(hipStream_t s, const float *x, const float *norm_w, float eps, float *normed, const float *router,
@@ -191,7 +191,10 @@ void run_attention(hipStream_t s, const float *q, const void *k_cache, const voi
 
 // matmul.hip.  Y[t] (store) W·X[t] for n_tokens rows; store 0 overwrite,
 // 1 accumulate, 2 swiglu (y = silu(y) * product).
+// `split` is scratch of matmul_split_bytes(n_tokens, n_cols) bytes (the
+// inputs split into fp16 high and low parts).
+uint64_t matmul_split_bytes(uint32_t n_rows, uint32_t n_cols);
 void run_matmul(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,
-                float *y, uint32_t n_tokens, uint32_t store);
+                float *y, uint32_t n_tokens, uint32_t store, void *split);
 
 }  // namespace bch

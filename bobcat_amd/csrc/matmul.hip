@@ -8,10 +8,11 @@
 //
 // Tile: 128 weight rows x 64 tokens, in pipeline steps of 128 columns;
 // v_mfma_f32_32x32x16_f16 on LDS tiles.  Weights go to LDS as fp16 (the
-// reference's expanded half tiles); each token's inputs are scaled by a
-// power of two into fp16 range and split into an fp16 high part and an fp16
-// residual, both multiplied, so the inputs keep ~22 bits whatever their
-// magnitude.  Accumulation is fp32.
+// reference's expanded half tiles).  Before the GEMM, k_split_rows scales
+// each token's inputs by a power of two into fp16 range and splits them into
+// an fp16 high part and an fp16 residual (once per launch, not once per
+// weight tile); both are multiplied, so the inputs keep ~22 bits whatever
+// their magnitude.  Accumulation is fp32.
 #include "formats.h"
 #include "kernels.h"
 #include "runtime.h"
@@ -90,6 +91,62 @@ __device__ __forceinline__ void expand_float(const uint8_t *__restrict__ row, ui
   }
 }
 
+// Row t of X [n_rows x n_cols] f32 to fp16 high and low parts: with s the
+// power of two that puts max|x_t| in [2^13, 2^14) (half precision cannot
+// overflow in the MFMA operands), hi = fp16(x·s), lo = fp16(x·s − hi), and
+// unscale[t] = 1/s.  Each group of 8 columns is stored as its 8 high halves
+// then its 8 low halves (32 bytes), so a GEMM thread's 32 columns of a step
+// are 128 contiguous bytes.  One workgroup per row.
+__global__ __launch_bounds__(256) void k_split_rows(const float *__restrict__ X, uint32_t n_cols,
+                                                   _Float16 *__restrict__ HL, float *__restrict__ unscale) {
+  const uint32_t t = blockIdx.x, tid = threadIdx.x;
+  const float4 *x4 = reinterpret_cast<const float4 *>(X + (uint64_t)t * n_cols);
+  const uint32_t n4 = n_cols / 4;
+  float mx = 0.f;
+  for (uint32_t i = tid; i < n4; i += 256) {
+    const float4 v = x4[i];
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
+  __shared__ float red[4];
+  mx = wave_max(mx);
+  if (tid % 64 == 0) red[tid / 64] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int ex = 0;
+  if (mx > 0.f) frexpf(mx, &ex);  // mx < 2^ex
+  const int k = max(-100, min(100, 14 - ex));
+  const float scale = ldexpf(1.0f, k);
+  if (tid == 0) unscale[t] = ldexpf(1.0f, -k);
+  _Float16 *row = HL + (uint64_t)t * 2 * n_cols;
+  for (uint32_t i = tid; i < n4; i += 256) {
+    const float4 v4 = x4[i];
+    const float v[4] = {v4.x * scale, v4.y * scale, v4.z * scale, v4.w * scale};
+    half4_t h, l;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      h[j] = (_Float16)v[j];
+      l[j] = (_Float16)(v[j] - (float)h[j]);
+    }
+    _Float16 *g = row + (i / 2) * 16 + (i % 2) * 4;
+    *reinterpret_cast<half4_t *>(g) = h;
+    *reinterpret_cast<half4_t *>(g + 8) = l;
+  }
+}
+
+// The split inputs of a launch: rows of 2·n_cols halves (groups of 8 high
+// then 8 low) and the per-row unscale, carved from one scratch region.
+struct SplitInputs {
+  const _Float16 *hl;
+  const float *unscale;
+};
+
+static SplitInputs split_inputs(hipStream_t s, const float *x, uint32_t n_rows, uint32_t n_cols, void *scratch) {
+  _Float16 *hl = static_cast<_Float16 *>(scratch);
+  float *u = reinterpret_cast<float *>(hl + (uint64_t)n_rows * 2 * n_cols);
+  if (n_rows) k_split_rows<<<n_rows, 256, 0, s>>>(x, n_cols, hl, u);
+  return SplitInputs{hl, u};
+}
+
 // Tile 128 weight rows x 64 tokens; 256 threads = 4 waves in a 2x2
 // arrangement, each wave owning 64 rows x 32 tokens as two 32x32 MFMA
 // blocks.  A pipeline step covers 128 columns: thread t expands weight row
@@ -106,15 +163,14 @@ struct ExpertGroups {
 };
 
 template <uint32_t FMT, int STORE, int MB, bool GROUPED>
-__global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, uint64_t row_bytes,
-                                                const float *__restrict__ X, float *__restrict__ Y, uint32_t n_rows,
-                                                uint32_t n_cols, uint32_t n_tokens, ExpertGroups groups) {
+__global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, uint64_t row_bytes, SplitInputs X,
+                                                float *__restrict__ Y, uint32_t n_rows, uint32_t n_cols,
+                                                uint32_t n_tokens, ExpertGroups groups) {
   constexpr int BM = 64 * MB;           // weight rows of this tile (MB 32-row blocks per wave)
   extern __shared__ _Float16 lds[];
   _Float16 *A = lds;                    // [BM][kLds]
   _Float16 *Bh = A + BM * kLds;         // [kBN][kLds]
   _Float16 *Bl = Bh + kBN * kLds;       // [kBN][kLds]
-  __shared__ float unscale[kBN];        // 2^-k that undoes each token's input scaling in this step
   const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
   const uint32_t row0 = blockIdx.x * BM;
   uint32_t tok0 = blockIdx.y * kBN, tok_end = n_tokens;  // positions [tok0, tok_end) of this tile's group
@@ -152,26 +208,33 @@ __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, u
   const int ar = a_thread ? tid / 2 : 0, aq = tid % 2;
   const uint8_t *wrow = W + (uint64_t)min(row0 + ar, n_rows - 1) * row_bytes;
   const int bt = tid / 4, bq = tid % 4;
-  const bool tok_ok = tok0 + bt < tok_end;
-  const float *xrow = X + (uint64_t)x_row(min(tok0 + bt, tok_end - 1)) * n_cols + 32 * bq;
+  // (Tokens past the tile's end stage a copy of the last row; their output
+  // columns are never stored.)
+  // This thread's 32 columns of a step: 4 groups of (8 high, 8 low) halves.
+  const uint4 *xrow = reinterpret_cast<const uint4 *>(X.hl + (uint64_t)x_row(min(tok0 + bt, tok_end - 1)) * 2 * n_cols +
+                                                      2 * 32 * bq);
 
+  // Loads of a step, issued a step ahead.  (Plain locals rather than an
+  // array captured by a lambda: the compiler kept such an array in scratch
+  // memory, which waited on each load.)
   RawUnit ra{};
-  float4 xv[8];
-  auto prefetch = [&](uint32_t k0) {
-    if constexpr (FMT == 12)
-      if (a_thread) ra = fetch_q4k(wrow, k0 & ~255u, (int)((k0 & 255u) / 64) + aq);
-    const float4 *src = reinterpret_cast<const float4 *>(xrow + k0);
-#pragma unroll
-    for (int i = 0; i < 8; i++) xv[i] = src[i];
-  };
+  uint4 x0, x1, x2, x3, x4, x5, x6, x7;
+#define BCH_PREFETCH(k0)                                                                     \
+  do {                                                                                       \
+    if constexpr (FMT == 12)                                                                 \
+      if (a_thread) ra = fetch_q4k(wrow, (k0) & ~255u, (int)(((k0) & 255u) / 64) + aq);       \
+    const uint4 *src_ = xrow + (k0) / 4;                                                     \
+    x0 = src_[0], x1 = src_[1], x2 = src_[2], x3 = src_[3];                                  \
+    x4 = src_[4], x5 = src_[5], x6 = src_[6], x7 = src_[7];                                  \
+  } while (0)
 
-  float16_t total[MB], acc[MB];
+  float16_t total[MB];
 #pragma unroll
   for (int b = 0; b < MB; b++)
 #pragma unroll
     for (int i = 0; i < 16; i++) total[b][i] = 0.f;
 
-  prefetch(0);
+  BCH_PREFETCH(0u);
   for (uint32_t k0 = 0; k0 < n_cols; k0 += kStep) {
     // Stage this step: weights to halves, inputs scaled and split.
     if (a_thread) {
@@ -181,48 +244,18 @@ __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, u
         expand_float<FMT>(wrow, k0 + 64 * aq, A + ar * kLds + 64 * aq);
     }
     {
-      // Each token's 128 inputs are scaled by a power of two that brings
-      // their largest magnitude just under 2^14 (half precision cannot
-      // overflow), then split into an fp16 high part and an fp16 residual:
-      // ~22 bits whatever their magnitude.  The scaling is undone on the
-      // step's products.
-      float mx = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; i++)
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xv[i].x), fabsf(xv[i].y)), fmaxf(fabsf(xv[i].z), fabsf(xv[i].w))));
-      mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-      if (!tok_ok) mx = 0.f;
-      int ex = 0;
-      if (mx > 0.f) frexpf(mx, &ex);  // mx < 2^ex
-      const int k = max(-100, min(100, 14 - ex));
-      const float scale = tok_ok ? ldexpf(1.0f, k) : 0.f;
-      if (bq == 0) unscale[bt] = ldexpf(1.0f, -k);
-      _Float16 *dh = Bh + bt * kLds + 32 * bq, *dl = Bl + bt * kLds + 32 * bq;
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float v[4] = {xv[i].x * scale, xv[i].y * scale, xv[i].z * scale, xv[i].w * scale};
-        half4_t h, l;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          h[j] = (_Float16)v[j];
-          l[j] = (_Float16)(v[j] - (float)h[j]);
-        }
-        *reinterpret_cast<half4_t *>(dh + 4 * i) = h;
-        *reinterpret_cast<half4_t *>(dl + 4 * i) = l;
-      }
+      uint4 *dh = reinterpret_cast<uint4 *>(Bh + bt * kLds + 32 * bq);
+      uint4 *dl = reinterpret_cast<uint4 *>(Bl + bt * kLds + 32 * bq);
+      dh[0] = x0, dl[0] = x1, dh[1] = x2, dl[1] = x3;
+      dh[2] = x4, dl[2] = x5, dh[3] = x6, dl[3] = x7;
     }
     __syncthreads();
-    if (k0 + kStep < n_cols) prefetch(k0 + kStep);
+    if (k0 + kStep < n_cols) BCH_PREFETCH(k0 + kStep);
     // 8 k-steps of 16 (gfx950's 32x32x16 f16 MFMA): lane supplies
     // A[row = lane%32][k + 8*(lane/32) .. +8] and B[k + 8*(lane/32) .. +8][col = lane%32].
     const _Float16 *arow0 = A + (wm * 32 * MB + lane % 32) * kLds + 8 * (lane / 32);
     const _Float16 *bhrow = Bh + (wn * 32 + lane % 32) * kLds + 8 * (lane / 32);
     const _Float16 *blrow = Bl + (wn * 32 + lane % 32) * kLds + 8 * (lane / 32);
-#pragma unroll
-    for (int b = 0; b < MB; b++)
-#pragma unroll
-      for (int i = 0; i < 16; i++) acc[b][i] = 0.f;
 #pragma unroll 4
     for (int kk = 0; kk < kStep; kk += 16) {
       const half8_t bh = *reinterpret_cast<const half8_t *>(bhrow + kk);
@@ -231,22 +264,17 @@ __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, u
 #pragma unroll
       for (int b = 0; b < MB; b++) a[b] = *reinterpret_cast<const half8_t *>(arow0 + 32 * b * kLds + kk);
 #pragma unroll
-      for (int b = 0; b < MB; b++) acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[b], bh, acc[b], 0, 0, 0);
+      for (int b = 0; b < MB; b++) total[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[b], bh, total[b], 0, 0, 0);
 #pragma unroll
-      for (int b = 0; b < MB; b++) acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[b], bl, acc[b], 0, 0, 0);
+      for (int b = 0; b < MB; b++) total[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[b], bl, total[b], 0, 0, 0);
     }
-    // Every accumulator of a lane belongs to token column lane%32.
-    const float us = unscale[wn * 32 + lane % 32];
-#pragma unroll
-    for (int b = 0; b < MB; b++)
-#pragma unroll
-      for (int i = 0; i < 16; i++) total[b][i] = fmaf(acc[b][i], us, total[b][i]);
     __syncthreads();
   }
   // total[b][r] holds D[row = 32b + 8*(r/4) + 4*(lane/32) + r%4][token = lane%32].
   const uint32_t tok = tok0 + wn * 32 + lane % 32;
   if (tok >= tok_end) return;
   const uint64_t yr = y_row(tok);
+  const float us = X.unscale[x_row(tok)];  // undoes the token's input scaling
 #pragma unroll
   for (int b = 0; b < MB; b++)
 #pragma unroll
@@ -254,18 +282,21 @@ __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, u
       const uint32_t row = row0 + wm * 32 * MB + 32 * b + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
       if (row < n_rows) {
         float *y = Y + yr * n_rows + row;
+        const float v = total[b][r] * us;
         if (STORE == 0)
-          *y = total[b][r];
+          *y = v;
         else if (STORE == 1)
-          *y += total[b][r];
+          *y += v;
         else
-          *y = silu_f(*y) * total[b][r];
+          *y = silu_f(*y) * v;
       }
     }
 }
 
+#undef BCH_PREFETCH
+
 template <uint32_t FMT, int MB>
-static void matmul_tile(hipStream_t s, const uint8_t *W, uint64_t rb, const float *x, float *y, uint32_t n_rows,
+static void matmul_tile(hipStream_t s, const uint8_t *W, uint64_t rb, const SplitInputs &x, float *y, uint32_t n_rows,
                         uint32_t n_cols, uint32_t n_tokens, uint32_t store) {
   dim3 grid(div_ceil(n_rows, 64 * MB), div_ceil(n_tokens, kBN));
   const size_t lds = (size_t)(64 * MB + 2 * kBN) * kLds * sizeof(_Float16);
@@ -281,7 +312,7 @@ static void matmul_tile(hipStream_t s, const uint8_t *W, uint64_t rb, const floa
 // Grouped launch over n_entries entries (64-row tiles; an expert's tiles
 // are few).  Store 0 overwrites, 2 applies SiLU(y)·product.
 template <uint32_t FMT>
-static void matmul_experts_fmt(hipStream_t s, const uint8_t *W, uint64_t rb, const float *x, float *y,
+static void matmul_experts_fmt(hipStream_t s, const uint8_t *W, uint64_t rb, const SplitInputs &x, float *y,
                                uint32_t n_rows, uint32_t n_cols, uint32_t n_entries, uint32_t store,
                                const ExpertGroups &g) {
   dim3 grid(div_ceil(n_rows, 64), div_ceil(n_entries, kBN) + g.n_experts);
@@ -295,7 +326,7 @@ static void matmul_experts_fmt(hipStream_t s, const uint8_t *W, uint64_t rb, con
 // 128-row tiles when they give the chip at least two workgroups per CU,
 // 64-row tiles (twice the workgroups) otherwise.
 template <uint32_t FMT>
-static void matmul_fmt(hipStream_t s, const uint8_t *W, uint64_t rb, const float *x, float *y, uint32_t n_rows,
+static void matmul_fmt(hipStream_t s, const uint8_t *W, uint64_t rb, const SplitInputs &x, float *y, uint32_t n_rows,
                        uint32_t n_cols, uint32_t n_tokens, uint32_t store) {
   const uint64_t big_tiles = (uint64_t)div_ceil(n_rows, 128) * div_ceil(n_tokens, kBN);
   if (big_tiles >= 512)
@@ -306,10 +337,13 @@ static void matmul_fmt(hipStream_t s, const uint8_t *W, uint64_t rb, const float
 
 static void set_lds_limits();
 
-void run_matmul(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,
-                float *y, uint32_t n_tokens, uint32_t store) {
+uint64_t matmul_split_bytes(uint32_t n_rows, uint32_t n_cols) { return (uint64_t)n_rows * (4ull * n_cols + 4); }
+
+void run_matmul(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *xf,
+                float *y, uint32_t n_tokens, uint32_t store, void *split) {
   set_lds_limits();
   const uint64_t rb = bch_row_bytes(format, n_cols);
+  const SplitInputs x = split_inputs(s, xf, n_tokens, n_cols, split);
   if (format == 12)
     matmul_fmt<12>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
   else if (format == 1)
@@ -321,11 +355,12 @@ void run_matmul(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_row
 static bool matmul_format(uint32_t f) { return f == 12 || f == 1 || f == 0; }
 
 void run_matmul_experts(hipStream_t s, uint32_t format, const uint8_t *W, const uint8_t *up, uint32_t n_rows,
-                        uint32_t n_cols, uint32_t n_experts, const float *x, bool shared_input,
+                        uint32_t n_cols, uint32_t n_experts, const float *xf, bool shared_input,
                         const uint32_t *offsets, const uint32_t *entries, uint32_t n_used, float *y,
-                        uint32_t n_tokens) {
+                        uint32_t n_tokens, void *split) {
   set_lds_limits();
   const uint64_t rb = bch_row_bytes(format, n_cols);
+  const SplitInputs x = split_inputs(s, xf, shared_input ? n_tokens : n_used * n_tokens, n_cols, split);
   const ExpertGroups g{offsets, entries, n_experts, shared_input ? n_used : 1u};
   const uint32_t n_entries = n_used * n_tokens;
   auto one = [&](const uint8_t *w, uint32_t store) {
@@ -380,7 +415,9 @@ extern "C" int bch_matmul(bch_ctx *ctx, uint32_t format, bch_view weights, uint3
     return fail(BCH_ERR_ARGUMENT, "matmul: weights and inputs must be 16-byte aligned");
   set_lds_limits();
   const char *name = format == 12 ? "matmul_q4k" : format == 1 ? "matmul_f16" : "matmul_f32";
+  void *split = nullptr;
+  BCH_TRY(ctx_scratch(ctx, matmul_split_bytes(n_tokens, n_cols), &split));
   return launch(ctx, {name, n_rows, n_cols, rb * n_rows}, [&](hipStream_t s) {
-    if (n_tokens) run_matmul(s, format, W, n_rows, n_cols, xp, yp, n_tokens, store);
+    if (n_tokens) run_matmul(s, format, W, n_rows, n_cols, xp, yp, n_tokens, store, split);
   });
 }

@@ -420,10 +420,12 @@ extern "C" int bch_matmul_experts(bch_ctx *ctx, uint32_t format, bch_view weight
   if (reinterpret_cast<uintptr_t>(wp) % 16 || reinterpret_cast<uintptr_t>(upp) % 16 ||
       reinterpret_cast<uintptr_t>(xp) % 16)
     return fail(BCH_ERR_ARGUMENT, "matmul_experts: operands must be 16-byte aligned");
+  void *split = nullptr;
+  BCH_TRY(ctx_scratch(ctx, matmul_split_bytes((uint32_t)input_rows, n_cols), &split));
   return launch(ctx, {"matmul_experts", n_rows, n_cols, stacked * (up ? 2 : 1)}, [&](hipStream_t s) {
     if (n_tokens)
       run_matmul_experts(s, format, wp, upp, n_rows, n_cols, n_experts, xp, shared_input != 0, op, ep, n_used, yp,
-                         n_tokens);
+                         n_tokens, split);
   });
 }
 

@@ -40,6 +40,9 @@ struct bch_ctx {
   bool capturing = false;
   // Zeroed split counters of the op-level attention launcher.
   uint32_t *counters = nullptr;
+  // Scratch of the op-level launchers (ctx_scratch), grown on demand.
+  void *scratch = nullptr;
+  uint64_t scratch_bytes = 0;
 };
 
 namespace bch {
@@ -47,6 +50,9 @@ namespace bch {
 // Record `code` with a formatted message as this thread's last error and
 // return it.
 int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// At least `bytes` of the context's scratch memory; growing it waits for the
+// work in flight (the old region may still be in use).
+int ctx_scratch(bch_ctx *ctx, uint64_t bytes, void **out);
 int ok();
 
 // Check `view` for `bytes` bytes on behalf of `kernel`; on success store the

@@ -118,6 +118,7 @@ void bch_close(bch_ctx *ctx) {
   }
   if (ctx->begin_event) hipEventDestroy(ctx->begin_event);
   if (ctx->counters) hipFree(ctx->counters);
+  if (ctx->scratch) hipFree(ctx->scratch);
   hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -263,3 +264,21 @@ int bch_profile_get(const bch_ctx *ctx, uint32_t index, bch_profile_entry *out) 
 }
 
 }  // extern "C"
+
+int bch::ctx_scratch(bch_ctx *ctx, uint64_t bytes, void **out) {
+  if (bytes > ctx->scratch_bytes) {
+    if (ctx->scratch) {
+      hipStreamSynchronize(ctx->stream);
+      hipFree(ctx->scratch);
+      ctx->scratch = nullptr;
+      ctx->scratch_bytes = 0;
+    }
+    if (hipMalloc(&ctx->scratch, bytes) != hipSuccess) {
+      ctx->scratch = nullptr;
+      return fail(BCH_ERR_ALLOCATION, "cannot allocate %llu bytes of scratch", (unsigned long long)bytes);
+    }
+    ctx->scratch_bytes = bytes;
+  }
+  *out = ctx->scratch;
+  return BCH_OK;
+}
