@@ -143,6 +143,7 @@ PROTOTYPES = {
     "bch_copy": (_int, [_vp, View, View, _u32]),
     "bch_embed": (_int, [_vp, _u32, View, _u32, View, View, _u32, _u32]),
     "bch_attention": (_int, [_vp, View, View, View, _int, View, View, _u32, _u32, _u32, _u32, _u32, _u32]),
+    "bch_attention_prefill": (_int, [_vp, View, View, View, View, _u32, _u32, _u32, _u32, _u32, _u32]),
     "bch_attention_scratch_floats": (_u64, [_u32, _u32, _u32, _u32]),
     "bch_matmul": (_int, [_vp, _u32, View, _u32, _u32, View, View, _u32, _u32]),
     "bch_argmax": (_int, [_vp, View, View, _u32]),

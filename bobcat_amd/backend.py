@@ -239,6 +239,11 @@ class Hip:
                                   _view(scratch), _view(out), n_heads, n_kv_heads, head_dim,
                                   first_pos, n_queries, n_ctx))
 
+    def attention_prefill(self, q, k_cache, v_cache, out, n_heads, n_kv_heads, head_dim, first_pos, n_queries,
+                          n_ctx):
+        check(lib().bch_attention_prefill(self.handle, _view(q), _view(k_cache), _view(v_cache), _view(out),
+                                          n_heads, n_kv_heads, head_dim, first_pos, n_queries, n_ctx))
+
     def matmul(self, fmt, weights, n_rows, n_cols, x, y, n_tokens, store: Store):
         check(lib().bch_matmul(self.handle, int(fmt), _view(weights), n_rows, n_cols, _view(x),
                                _view(y), n_tokens, int(store)))

@@ -189,6 +189,14 @@ void run_attention(hipStream_t s, const float *q, const void *k_cache, const voi
                    float *partials, uint32_t *counters, float *out, uint32_t n_heads, uint32_t n_kv_heads,
                    uint32_t head_dim, uint32_t first_pos, const uint32_t *dpos, uint32_t n_queries, uint32_t splits);
 
+// attn_prefill.hip: causal GQA attention of n_queries queries at positions
+// first_pos.. over the f16 cache (their keys already stored), on MFMA.  q and
+// out rows are q_stride / out_stride floats apart, head h at h·head_dim.
+bool attn_prefill_mfma_supported(uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, bool kv_half);
+void run_attn_prefill_mfma(hipStream_t s, const float *q, const void *k_cache, const void *v_cache, float *out,
+                           uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t first_pos,
+                           uint32_t n_queries, uint32_t q_stride, uint32_t out_stride, float scale);
+
 // matmul.hip.  Y[t] (store) W·X[t] for n_tokens rows; store 0 overwrite,
 // 1 accumulate, 2 swiglu (y = silu(y) * product).
 // `split` is scratch of matmul_split_bytes(n_tokens, n_cols) bytes (the

@@ -243,6 +243,11 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
         run_convert_half(s, m->v, m->cache_slot(m->v_cache, ci, pos), count * m->kv_dim, nullptr, 0);
       else
         run_copy(s, m->v, static_cast<float *>(m->cache_slot(m->v_cache, ci, pos)), count * m->kv_dim, nullptr, 0);
+      if (attn_prefill_mfma_supported(m->n_heads, m->n_kv_heads, m->head_dim, m->kv_half))
+        run_attn_prefill_mfma(s, m->q, m->cache_layer(m->k_cache, ci), m->cache_layer(m->v_cache, ci), m->attn,
+                              m->n_heads, m->n_kv_heads, m->head_dim, pos, count, m->q_dim, m->q_dim,
+                              1.0f / sqrtf((float)m->head_dim));
+      else
       for (uint32_t q0 = 0; q0 < count; q0 += kAttnQueryBatch) {
         const uint32_t nq = std::min(kAttnQueryBatch, count - q0);
         AttnDecodeArgs ad{};

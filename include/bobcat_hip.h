@@ -203,6 +203,16 @@ int bch_embed(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_vocab,
 int bch_attention(bch_ctx *ctx, bch_view q, bch_view k_cache, bch_view v_cache, int kv_half,
                   bch_view scratch, bch_view out, uint32_t n_heads, uint32_t n_kv_heads,
                   uint32_t head_dim, uint32_t first_pos, uint32_t n_queries, uint32_t n_ctx);
+/* MI355X addition (no counterpart in the reference): the prefill form of
+ * Metal::attention (backend.rs:2150-2320, attention_flash attention.metal:
+ * 289-480) on MFMA, for an f16 cache, head_dim 64 or 128 and at most 4 query
+ * heads per KV head (else BCH_ERR_ATTENTION_LIMITS).  Queries and
+ * probabilities enter the products as f16 high + low parts (~22 bits), so
+ * results agree with bch_attention to ~1e-6 of the outputs' scale, not
+ * bit for bit.  No scratch. */
+int bch_attention_prefill(bch_ctx *ctx, bch_view q, bch_view k_cache, bch_view v_cache, bch_view out,
+                          uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t first_pos,
+                          uint32_t n_queries, uint32_t n_ctx);
 /* attention_scratch_floats (backend.rs:2739-2748). */
 uint64_t bch_attention_scratch_floats(uint32_t n_heads, uint32_t head_dim, uint32_t n_ctx,
                                       uint32_t n_queries);
