@@ -9,8 +9,9 @@
 // out_c = Σ_r S[r][c]·q[r]), so the k_dim rows of a column live in the
 // registers of one wave (k_dim/64 per lane) for a whole prefill batch and the
 // two dot products per token are wave reductions.  16 heads of 128 columns
-// make 2048 waves.  The next token's query, key and value are loaded before
-// the current token's update, which does not depend on them.
+// make 2048 waves.  The workgroup stages 32 tokens at a time in LDS (the
+// normalised query and key, its columns' values, the gates), so the
+// sequential token loop reads LDS instead of waiting on memory per token.
 #include <cmath>
 
 #include "device.h"
@@ -25,67 +26,77 @@ __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf
 // transformers' softplus returns its input above 20 (qwen35.rs:775-778).
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 
+constexpr int kGdnChunk = 32;  // tokens staged in LDS at a time
+
 template <int RPL>
 __global__ __launch_bounds__(kGdnCols * 64) void k_gdn_recurrence(GdnArgs a) {
-  const uint32_t lane = threadIdx.x % 64, col = blockIdx.x * kGdnCols + threadIdx.x / 64, head = blockIdx.y;
+  constexpr int KD = RPL * 64;  // k_dim
+  // A chunk of tokens staged by the workgroup: the l2-normalised query
+  // (times q_scale) and key of this head, the four columns' values, and
+  // the gates.  The token loop then waits on LDS, not on memory.
+  __shared__ float qs[kGdnChunk][KD], ks[kGdnChunk][KD], vs[kGdnChunk][kGdnCols], bs[kGdnChunk], ds[kGdnChunk];
+  const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const uint32_t col0 = blockIdx.x * kGdnCols, col = col0 + wave, head = blockIdx.y;
   const uint32_t key_head = head % a.n_k, key_dim = a.n_k * a.k_dim, conv_dim = 2 * key_dim + a.n_v * a.v_dim;
   const uint32_t r0 = lane * RPL;
   float *S = a.state + (uint64_t)head * a.k_dim * a.v_dim;
   float rows[RPL];
 #pragma unroll
   for (int i = 0; i < RPL; i++) rows[i] = S[(uint64_t)(r0 + i) * a.v_dim + col];
-  auto load = [&](uint32_t t, float *q, float *k, float &v, float &b, float &d) {
-    const float *tok = a.y + (uint64_t)t * conv_dim;
+  for (uint32_t t0 = 0; t0 < a.n_tokens; t0 += kGdnChunk) {
+    const uint32_t n = min((uint32_t)kGdnChunk, a.n_tokens - t0);
+    __syncthreads();  // the previous chunk is consumed
+    // Wave w stages tokens w, w + 4, ...: l2_normalize of the query and the
+    // key (qwen35.rs:464-470), each lane holding rows r0 .. r0+RPL-1.
+    for (uint32_t j = wave; j < n; j += kGdnCols) {
+      const float *tok = a.y + (uint64_t)(t0 + j) * conv_dim;
+      float q[RPL], k[RPL], sq = 0.f, sk = 0.f;
 #pragma unroll
-    for (int i = 0; i < RPL; i++) {
-      q[i] = tok[key_head * a.k_dim + r0 + i];
-      k[i] = tok[key_dim + key_head * a.k_dim + r0 + i];
-    }
-    v = tok[2 * key_dim + head * a.v_dim + col];
-    b = a.beta[(uint64_t)t * a.n_v + head];
-    d = a.alpha[(uint64_t)t * a.n_v + head];
-  };
-  float q[RPL], k[RPL], v, b, d;
-  load(0, q, k, v, b, d);
-  for (uint32_t t = 0; t < a.n_tokens; t++) {
-    float nq[RPL], nk[RPL], nv = 0.f, nb = 0.f, nd = 0.f;
-    if (t + 1 < a.n_tokens) load(t + 1, nq, nk, nv, nb, nd);
-    // l2_normalize of the query (times q_scale) and the key (qwen35.rs:464-470).
-    float sq = 0.f, sk = 0.f;
+      for (int i = 0; i < RPL; i++) {
+        q[i] = tok[key_head * a.k_dim + r0 + i];
+        k[i] = tok[key_dim + key_head * a.k_dim + r0 + i];
+      }
 #pragma unroll
-    for (int i = 0; i < RPL; i++) {
-      sq = fmaf(q[i], q[i], sq);
-      sk = fmaf(k[i], k[i], sk);
-    }
-    sq = wave_sum(sq);
-    sk = wave_sum(sk);
-    const float fq = a.q_scale / sqrtf(sq + 1e-6f), fk = 1.0f / sqrtf(sk + 1e-6f);
-    const float beta = a.raw_gates ? sigmoid_f(b) : b;
-    const float decay = a.raw_gates ? expf(a.a[head] * softplus_f(d + a.dt_bias[head])) : d;
-    float rem = 0.f;
+      for (int i = 0; i < RPL; i++) {
+        sq = fmaf(q[i], q[i], sq);
+        sk = fmaf(k[i], k[i], sk);
+      }
+      sq = wave_sum(sq);
+      sk = wave_sum(sk);
+      const float fq = a.q_scale / sqrtf(sq + 1e-6f), fk = 1.0f / sqrtf(sk + 1e-6f);
 #pragma unroll
-    for (int i = 0; i < RPL; i++) {
-      rows[i] *= decay;
-      rem = fmaf(rows[i], k[i] * fk, rem);
+      for (int i = 0; i < RPL; i++) {
+        qs[j][r0 + i] = q[i] * fq;
+        ks[j][r0 + i] = k[i] * fk;
+      }
+      if (lane < kGdnCols) vs[j][lane] = tok[2 * key_dim + head * a.v_dim + col0 + lane];
+      if (lane == 0) {
+        const float b = a.beta[(uint64_t)(t0 + j) * a.n_v + head];
+        const float d = a.alpha[(uint64_t)(t0 + j) * a.n_v + head];
+        bs[j] = a.raw_gates ? sigmoid_f(b) : b;
+        ds[j] = a.raw_gates ? expf(a.a[head] * softplus_f(d + a.dt_bias[head])) : d;
+      }
     }
-    rem = wave_sum(rem);
-    const float delta = (v - rem) * beta;
-    float o = 0.f;
+    __syncthreads();
+    for (uint32_t j = 0; j < n; j++) {
+      const float decay = ds[j], beta = bs[j];
+      float rem = 0.f;
 #pragma unroll
-    for (int i = 0; i < RPL; i++) {
-      rows[i] = fmaf(k[i] * fk, delta, rows[i]);
-      o = fmaf(rows[i], q[i] * fq, o);
-    }
-    o = wave_sum(o);
-    if (lane == 0) a.out[(uint64_t)t * a.n_v * a.v_dim + head * a.v_dim + col] = o;
+      for (int i = 0; i < RPL; i++) {
+        rows[i] *= decay;
+        rem = fmaf(rows[i], ks[j][r0 + i], rem);
+      }
+      rem = wave_sum(rem);
+      const float delta = (vs[j][wave] - rem) * beta;
+      float o = 0.f;
 #pragma unroll
-    for (int i = 0; i < RPL; i++) {
-      q[i] = nq[i];
-      k[i] = nk[i];
+      for (int i = 0; i < RPL; i++) {
+        rows[i] = fmaf(ks[j][r0 + i], delta, rows[i]);
+        o = fmaf(rows[i], qs[j][r0 + i], o);
+      }
+      o = wave_sum(o);
+      if (lane == 0) a.out[(uint64_t)(t0 + j) * a.n_v * a.v_dim + head * a.v_dim + col] = o;
     }
-    v = nv;
-    b = nb;
-    d = nd;
   }
 #pragma unroll
   for (int i = 0; i < RPL; i++) S[(uint64_t)(r0 + i) * a.v_dim + col] = rows[i];
@@ -104,42 +115,45 @@ bool run_gdn_recurrence(hipStream_t s, const GdnArgs &a) {
 }
 
 // The causal convolution with SiLU of gdn_conv / the DeltaNet step
-// (qwen35.rs:448-462): thread c walks the tokens of channel c with its
-// history in registers, then leaves the latest k-1 inputs in `hist`.
-__global__ void k_gdn_conv(const float *__restrict__ x, const float *__restrict__ taps, float *__restrict__ hist,
+// (qwen35.rs:448-462), one thread per (token, channel): input t - past + i
+// comes from the batch or, before it, from `hist`.  The newest term is added
+// first, then the window oldest first, as the reference adds them.  A second
+// launch then leaves the latest k-1 inputs in `hist` (after every read of
+// the old history).
+__global__ void k_gdn_conv(const float *__restrict__ x, const float *__restrict__ taps, const float *__restrict__ hist,
                            float *__restrict__ y, uint32_t channels, uint32_t ksize, uint32_t n_tokens) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (uint64_t)n_tokens * channels) return;
+  const uint32_t t = (uint32_t)(i / channels), c = (uint32_t)(i % channels), past = ksize - 1;
+  const float *tp = taps + (uint64_t)c * ksize;
+  float sum = tp[past] * x[i];
+  for (uint32_t j = 0; j < past; j++) {
+    const int src = (int)t - (int)past + (int)j;  // token of window slot j
+    const float w = src >= 0 ? x[(uint64_t)src * channels + c] : hist[(uint64_t)c * past + (past + src)];
+    sum += tp[j] * w;
+  }
+  y[i] = sum / (1.0f + expf(-sum));
+}
+
+__global__ void k_gdn_conv_history(const float *__restrict__ x, float *__restrict__ hist, uint32_t channels,
+                                   uint32_t ksize, uint32_t n_tokens) {
   const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= channels) return;
   const uint32_t past = ksize - 1;
   float window[kGdnMaxKernel - 1];
-  float tp[kGdnMaxKernel];
-#pragma unroll
-  for (uint32_t i = 0; i < kGdnMaxKernel; i++) tp[i] = i < ksize ? taps[(uint64_t)c * ksize + i] : 0.f;
-#pragma unroll
-  for (uint32_t i = 0; i < kGdnMaxKernel - 1; i++) window[i] = i < past ? hist[(uint64_t)c * past + i] : 0.f;
-  for (uint32_t t = 0; t < n_tokens; t++) {
-    const float input = x[(uint64_t)t * channels + c];
-    // The newest term first, then the history oldest first, as the reference adds them.
-    float sum = tp[past] * input;
-#pragma unroll
-    for (uint32_t i = 0; i < kGdnMaxKernel - 1; i++)
-      if (i < past) sum += tp[i] * window[i];
-    y[(uint64_t)t * channels + c] = sum / (1.0f + expf(-sum));
-#pragma unroll
-    for (uint32_t i = 0; i + 1 < kGdnMaxKernel - 1; i++)
-      if (i + 1 < past) window[i] = window[i + 1];
-#pragma unroll
-    for (uint32_t i = 0; i < kGdnMaxKernel - 1; i++)
-      if (i + 1 == past) window[i] = input;
+  for (uint32_t j = 0; j < past; j++) {
+    const int src = (int)n_tokens - (int)past + (int)j;
+    window[j] = src >= 0 ? x[(uint64_t)src * channels + c] : hist[(uint64_t)c * past + (past + src)];
   }
-#pragma unroll
-  for (uint32_t i = 0; i < kGdnMaxKernel - 1; i++)
-    if (i < past) hist[(uint64_t)c * past + i] = window[i];
+  for (uint32_t j = 0; j < past; j++) hist[(uint64_t)c * past + j] = window[j];
 }
 
 void run_gdn_conv(hipStream_t s, const float *x, const float *taps, float *hist, float *y, uint32_t channels,
                   uint32_t ksize, uint32_t n_tokens) {
-  k_gdn_conv<<<(channels + 255) / 256, 256, 0, s>>>(x, taps, hist, y, channels, ksize, n_tokens);
+  const uint64_t n = (uint64_t)n_tokens * channels;
+  if (!n) return;
+  k_gdn_conv<<<(uint32_t)((n + 255) / 256), 256, 0, s>>>(x, taps, hist, y, channels, ksize, n_tokens);
+  k_gdn_conv_history<<<(channels + 255) / 256, 256, 0, s>>>(x, hist, channels, ksize, n_tokens);
 }
 
 // gdn_gates (gdn.metal:125-149): beta <- sigmoid(beta), alpha <- the decay
