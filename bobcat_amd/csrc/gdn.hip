@@ -102,8 +102,80 @@ __global__ __launch_bounds__(kGdnCols * 64) void k_gdn_recurrence(GdnArgs a) {
   for (int i = 0; i < RPL; i++) S[(uint64_t)(r0 + i) * a.v_dim + col] = rows[i];
 }
 
+// One token (decode): lane c of the workgroup owns column c of a 64-column
+// block of one value head's state and wave w rows [w·KD/4, (w+1)·KD/4), so
+// each row of the block is one coalesced 256-byte access; the two dot
+// products over the rows are per-lane sums, then a sum over the four waves
+// in LDS (in wave order).  (The wave-per-column form above spreads a column
+// over 64 lanes, which touches a cache line per row and per column.)
+template <int KD>
+__global__ __launch_bounds__(256) void k_gdn_step(GdnArgs a) {
+  constexpr int RW = KD / 4;  // rows per wave
+  __shared__ float qn[KD], kn[KD], part[4][64];
+  __shared__ float gate_s[2];
+  const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const uint32_t head = blockIdx.y, col = blockIdx.x * 64 + lane;
+  const uint32_t key_head = head % a.n_k, key_dim = a.n_k * a.k_dim;
+  const float *tok = a.y;
+  float *S = a.state + (uint64_t)head * KD * a.v_dim + col;
+  // The state rows first: their loads overlap the norms below.
+  float rows[RW];
+#pragma unroll
+  for (int i = 0; i < RW; i++) rows[i] = S[(uint64_t)(wave * RW + i) * a.v_dim];
+  const float v = tok[2 * key_dim + head * a.v_dim + col];
+  // Waves 0 and 1 normalise the query and the key (qwen35.rs:464-470).
+  if (wave < 2) {
+    const float *src = tok + (wave == 0 ? 0u : key_dim) + key_head * KD;
+    float e[KD / 64], ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < KD / 64; i++) {
+      e[i] = src[lane * (KD / 64) + i];
+      ss = fmaf(e[i], e[i], ss);
+    }
+    ss = wave_sum(ss);
+    const float f = wave == 0 ? a.q_scale / sqrtf(ss + 1e-6f) : 1.0f / sqrtf(ss + 1e-6f);
+#pragma unroll
+    for (int i = 0; i < KD / 64; i++) (wave == 0 ? qn : kn)[lane * (KD / 64) + i] = e[i] * f;
+  } else if (wave == 2 && lane == 0) {
+    const float b = a.beta[head], d = a.alpha[head];
+    gate_s[0] = a.raw_gates ? sigmoid_f(b) : b;
+    gate_s[1] = a.raw_gates ? expf(a.a[head] * softplus_f(d + a.dt_bias[head])) : d;
+  }
+  __syncthreads();
+  const float beta = gate_s[0], decay = gate_s[1];
+  float rem = 0.f;
+#pragma unroll
+  for (int i = 0; i < RW; i++) {
+    rows[i] *= decay;
+    rem = fmaf(rows[i], kn[wave * RW + i], rem);
+  }
+  part[wave][lane] = rem;
+  __syncthreads();
+  rem = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+  const float delta = (v - rem) * beta;
+  float o = 0.f;
+#pragma unroll
+  for (int i = 0; i < RW; i++) {
+    rows[i] = fmaf(kn[wave * RW + i], delta, rows[i]);
+    o = fmaf(rows[i], qn[wave * RW + i], o);
+    S[(uint64_t)(wave * RW + i) * a.v_dim] = rows[i];
+  }
+  __syncthreads();
+  part[wave][lane] = o;
+  __syncthreads();
+  if (wave == 0) a.out[head * a.v_dim + col] = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+}
+
 bool run_gdn_recurrence(hipStream_t s, const GdnArgs &a) {
   if (a.v_dim % kGdnCols || a.n_tokens == 0) return false;
+  if (a.n_tokens == 1 && a.v_dim % 64 == 0 && (a.k_dim == 64 || a.k_dim == 128)) {
+    const dim3 grid(a.v_dim / 64, a.n_v);
+    if (a.k_dim == 64)
+      k_gdn_step<64><<<grid, 256, 0, s>>>(a);
+    else
+      k_gdn_step<128><<<grid, 256, 0, s>>>(a);
+    return true;
+  }
   const dim3 grid(a.v_dim / kGdnCols, a.n_v);
   if (a.k_dim == 64)
     k_gdn_recurrence<1><<<grid, kGdnCols * 64, 0, s>>>(a);
