@@ -41,21 +41,32 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t index) {
 
 template <bool ACC>
 struct PlainItems {
+  // Accumulating rows read y[item] with the batch's weights (preload), so
+  // the read-modify-write at the end does not wait on memory.
+  static constexpr bool kPre = ACC;
   static constexpr int kRows = 1;
   static constexpr bool kArgmax = false;
   const uint8_t *W;
   uint64_t rb;
   float *y;
+  struct Pre {
+    float y;
+  };
   __device__ const uint8_t *row(uint32_t item, int) const { return W + (uint64_t)item * rb; }
   __device__ void store(uint32_t item, const float *v, float scale) const {
     const float t = v[0] * scale;
     y[item] = ACC ? y[item] + t : t;
+  }
+  __device__ Pre preload(uint32_t item) const { return Pre{y[item]}; }
+  __device__ void store_pre(uint32_t item, const float *v, float scale, const Pre &pre) const {
+    y[item] = pre.y + v[0] * scale;
   }
 };
 
 // Logits: rows stored as PlainItems<false>, plus one argmax partial per
 // workgroup, so the next token needs no pass over the logits.
 struct ArgmaxItems {
+  static constexpr bool kPre = false;
   static constexpr int kRows = 1;
   static constexpr bool kArgmax = true;
   const uint8_t *W;
@@ -67,6 +78,7 @@ struct ArgmaxItems {
 };
 
 struct SwigluItems {
+  static constexpr bool kPre = false;
   static constexpr int kRows = 2;
   static constexpr bool kArgmax = false;
   const uint8_t *Wg, *Wu;
@@ -82,6 +94,7 @@ struct SwigluItems {
 // i % n_ff of the expert in route slot i / n_ff (gate and up stack the
 // experts, n_ff rows each; lfm2.rs:128-142).
 struct ExpertSwigluItems {
+  static constexpr bool kPre = false;
   static constexpr int kRows = 2;
   static constexpr bool kArgmax = false;
   const uint8_t *Wg, *Wu;
@@ -105,6 +118,7 @@ struct ExpertSwigluItems {
 // [channel][k-1], the oldest first), rows [r0, r0+r1) the output gate z,
 // then r2 rows of beta and r2 of alpha (raw; the recurrence gates them).
 struct GdnInItems {
+  static constexpr bool kPre = false;
   static constexpr int kRows = 1;
   static constexpr bool kArgmax = false;
   const uint8_t *Wqkv, *Wz, *Wb, *Wa;
@@ -142,6 +156,7 @@ struct GdnInItems {
 };
 
 struct ThreeItems {
+  static constexpr bool kPre = false;
   static constexpr int kRows = 1;
   static constexpr bool kArgmax = false;
   const uint8_t *W0, *W1, *W2;
@@ -167,6 +182,9 @@ struct ThreeItems {
 // The gated short convolution of one channel (matvec.metal:386-454,
 // lfm2.rs:456-475) on rows ch, n+ch, 2n+ch of the input projection.
 struct ConvItems {
+  // The channel's taps and history are read with the batch's weights.
+  static constexpr bool kPre = true;
+  static constexpr int kMaxTaps = 9;
   static constexpr int kRows = 3;
   static constexpr bool kArgmax = false;
   const uint8_t *W;
@@ -174,7 +192,37 @@ struct ConvItems {
   uint32_t n_embd, ksize;
   const float *taps;
   float *history, *out;
+  struct Pre {
+    float t[kMaxTaps], h[kMaxTaps - 1];
+  };
   __device__ const uint8_t *row(uint32_t ch, int j) const { return W + (uint64_t)(j * n_embd + ch) * rb; }
+  __device__ Pre preload(uint32_t ch) const {
+    Pre pre;
+#pragma unroll
+    for (int k = 0; k < kMaxTaps; k++) pre.t[k] = (uint32_t)k < ksize ? taps[(uint64_t)ch * ksize + k] : 0.f;
+#pragma unroll
+    for (int k = 0; k < kMaxTaps - 1; k++) pre.h[k] = (uint32_t)k + 1 < ksize ? history[k * n_embd + ch] : 0.f;
+    return pre;
+  }
+  // store() with the preloaded taps and history: the same operations in the
+  // same order.
+  __device__ void store_pre(uint32_t ch, const float *v, float scale, const Pre &pre) const {
+    const float b = v[0] * scale, c = v[1] * scale, xin = v[2] * scale;
+    const float bx = b * xin;
+    float last = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMaxTaps; k++)
+      if ((uint32_t)k + 1 == ksize) last = pre.t[k];
+    float sum = last * bx;
+#pragma unroll
+    for (int k = 0; k < kMaxTaps - 1; k++)
+      if ((uint32_t)k + 1 < ksize) sum = fmaf(pre.t[k], pre.h[k], sum);
+#pragma unroll
+    for (int k = 0; k < kMaxTaps - 2; k++)
+      if ((uint32_t)k + 2 < ksize) history[k * n_embd + ch] = pre.h[k + 1];
+    history[(ksize - 2) * n_embd + ch] = bx;
+    out[ch] = c * sum;
+  }
   __device__ void store(uint32_t ch, const float *v, float scale) const {
     const float b = v[0] * scale, c = v[1] * scale, xin = v[2] * scale;
     const float *t = taps + (uint64_t)ch * ksize;
@@ -188,6 +236,16 @@ struct ConvItems {
 };
 
 // --- the kernel ----------------------------------------------------------
+
+// The preloaded values of a policy with kPre, else nothing.
+template <class P, bool = P::kPre>
+struct PreOf {
+  struct type {};
+};
+template <class P>
+struct PreOf<P, true> {
+  using type = typename P::Pre;
+};
 
 template <int LPR>
 __device__ __forceinline__ float group_total(float v, float *lds_scratch, int slot) {
@@ -217,15 +275,24 @@ __global__ __launch_bounds__(256) void k_gemv(P p, const float *__restrict__ x, 
   const uint32_t stride = gridDim.x * G;
   uint32_t b = blockIdx.x * G + g;
 
-  // Weight loads of a batch: issued ahead of the batch's arithmetic.
+  // Weight loads of a batch: issued ahead of the batch's arithmetic.  The
+  // lane that stores item `it` of a batch (lane it, or thread it when a
+  // group spans waves) also preloads what its store reads, when the policy
+  // asks for it and every lane stores at most one item.
+  constexpr bool kPreload = P::kPre && (LPR > 64 || LPR >= RPG);
+  using Pre = typename PreOf<P>::type;
+  const uint32_t my_item = LPR <= 64 ? (uint32_t)li : (uint32_t)tid;
   typename F::Raw ra[N], rb[N];
-  auto fetch = [&](typename F::Raw *dst, uint32_t batch) {
+  Pre pa{}, pb{};
+  auto fetch = [&](typename F::Raw *dst, Pre &pre, uint32_t batch) {
 #pragma unroll
     for (int it = 0; it < RPG; it++) {
       const uint32_t item = min(batch * RPG + it, n_items - 1);
 #pragma unroll
       for (int j = 0; j < R; j++) dst[it * R + j] = F::fetch(p.row(item, j), unit);
     }
+    if constexpr (kPreload)
+      if (my_item < (uint32_t)RPG && batch * RPG + my_item < n_items) pre = p.preload(batch * RPG + my_item);
   };
   // The input (times the norm weights) is staged once per workgroup in LDS
   // with coalesced loads, one padded slot of kSlot floats per unit, and each
@@ -254,7 +321,7 @@ __global__ __launch_bounds__(256) void k_gemv(P p, const float *__restrict__ x, 
         if (NORM) wv[k] = w4[i];
       }
     }
-    if (base == 0 && b < n_batches) fetch(ra, b);
+    if (base == 0 && b < n_batches) fetch(ra, pa, b);
 #pragma unroll
     for (int k = 0; k < kPer; k++) {
       const uint32_t i = base + tid + k * T;
@@ -290,7 +357,7 @@ __global__ __launch_bounds__(256) void k_gemv(P p, const float *__restrict__ x, 
   uint64_t best = 0;  // argmax key of the items this lane stored (P::kArgmax)
 
   // Reduce a batch over the group and store it.
-  auto finish = [&](const typename F::Raw *cur, uint32_t batch) {
+  auto finish = [&](const typename F::Raw *cur, const Pre &pre, uint32_t batch) {
     float acc[N];
 #pragma unroll
     for (int i = 0; i < N; i++) acc[i] = active ? F::compute(cur[i], unit, f) : 0.f;
@@ -304,7 +371,10 @@ __global__ __launch_bounds__(256) void k_gemv(P p, const float *__restrict__ x, 
           float v[R];
 #pragma unroll
           for (int j = 0; j < R; j++) v[j] = acc[it * R + j];
-          p.store(first + it, v, scale);
+          if constexpr (kPreload)
+            p.store_pre(first + it, v, scale, pre);
+          else
+            p.store(first + it, v, scale);
           if constexpr (P::kArgmax) best = max(best, argmax_key(v[0] * scale, first + it));
         }
       }
@@ -324,7 +394,10 @@ __global__ __launch_bounds__(256) void k_gemv(P p, const float *__restrict__ x, 
           for (int w = 0; w < W; w++) t += red[(tid * R + j) * W + w];
           v[j] = t;
         }
-        p.store(first + tid, v, scale);
+        if constexpr (kPreload)
+          p.store_pre(first + tid, v, scale, pre);
+        else
+          p.store(first + tid, v, scale);
         if constexpr (P::kArgmax) best = max(best, argmax_key(v[0] * scale, first + tid));
       }
       __syncthreads();
@@ -335,12 +408,12 @@ __global__ __launch_bounds__(256) void k_gemv(P p, const float *__restrict__ x, 
   // flight while the current batch is reduced.
   while (true) {
     if (b >= n_batches) break;
-    if (b + stride < n_batches) fetch(rb, b + stride);
-    finish(ra, b);
+    if (b + stride < n_batches) fetch(rb, pb, b + stride);
+    finish(ra, pa, b);
     b += stride;
     if (b >= n_batches) break;
-    if (b + stride < n_batches) fetch(ra, b + stride);
-    finish(rb, b);
+    if (b + stride < n_batches) fetch(ra, pa, b + stride);
+    finish(rb, pb, b);
     b += stride;
   }
   if constexpr (P::kArgmax) {
