@@ -172,8 +172,21 @@ __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, u
   _Float16 *Bh = A + BM * kLds;         // [kBN][kLds]
   _Float16 *Bl = Bh + kBN * kLds;       // [kBN][kLds]
   const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
-  const uint32_t row0 = blockIdx.x * BM;
-  uint32_t tok0 = blockIdx.y * kBN, tok_end = n_tokens;  // positions [tok0, tok_end) of this tile's group
+  // Dense launches are one-dimensional and XCD-aware: workgroup L runs on
+  // XCD L % 8 (round-robin dispatch), so logical tile (L % 8)·⌈total/8⌉ + L/8
+  // gives each XCD a contiguous run of tiles in token-tile-major order — the
+  // row tiles sharing a token tile's inputs then share that XCD's L2 instead
+  // of every XCD reading every input tile.
+  uint32_t row_tile = blockIdx.x, tok_tile = blockIdx.y;
+  if constexpr (!GROUPED) {
+    const uint32_t n_rt = (n_rows + BM - 1) / BM, total = n_rt * ((n_tokens + kBN - 1) / kBN);
+    const uint32_t per = (total + 7) / 8, logical = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    if (logical >= total) return;
+    row_tile = logical % n_rt;
+    tok_tile = logical / n_rt;
+  }
+  const uint32_t row0 = row_tile * BM;
+  uint32_t tok0 = tok_tile * kBN, tok_end = n_tokens;  // positions [tok0, tok_end) of this tile's group
   const int wm = wave / 2, wn = wave % 2;
   if constexpr (GROUPED) {
     // Find this tile's expert: the offsets go to LDS, one thread walks them.
@@ -298,7 +311,8 @@ __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, u
 template <uint32_t FMT, int MB>
 static void matmul_tile(hipStream_t s, const uint8_t *W, uint64_t rb, const SplitInputs &x, float *y, uint32_t n_rows,
                         uint32_t n_cols, uint32_t n_tokens, uint32_t store) {
-  dim3 grid(div_ceil(n_rows, 64 * MB), div_ceil(n_tokens, kBN));
+  const uint32_t total = div_ceil(n_rows, 64 * MB) * div_ceil(n_tokens, kBN);
+  const dim3 grid(8 * div_ceil(total, 8));  // XCD-aware tile order (see k_matmul)
   const size_t lds = (size_t)(64 * MB + 2 * kBN) * kLds * sizeof(_Float16);
   const ExpertGroups none{};
   if (store == 0)
