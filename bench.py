@@ -11,6 +11,9 @@ Prints ONE JSON line (the driver's contract).  Legs:
   * gemv  — BASELINE config 1: Q4_K dequant-GEMV, W [8192 x 2048], timed
             over 64 rotating copies of W (604 MB > the 256 MB MALL) with HIP
             events on the backend's own stream: the `roofline` object.
+  * long  — BASELINE configs[3] part 2 (2.6B only): 128 greedy steps after a
+            32,768-token prompt, and a second request that reuses the KV
+            cache of a shared 30,000-token prefix: the `long_context` object.
   * cpu   — the oracle (a C restatement of the reference's scalar Rust path)
             decoding the same model on the host cores, on a bounded sample.
 
@@ -30,6 +33,7 @@ HBM_PEAK_GBS = 8000.0
 GEMV_ROWS, GEMV_COLS = 8192, 2048
 GEMV_BYTES = GEMV_ROWS * GEMV_COLS // 256 * 144 + GEMV_COLS * 4 + GEMV_ROWS * 4  # 9,478,144
 PROMPT, GEN = 512, 128
+LONG_PROMPT, LONG_SHARED = 32768, 30000
 READ_THREADS = 256 * 1024
 COPY_BYTES = 64 << 20
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -135,6 +139,58 @@ def model_leg(hip, weights, steps: int, warmup: int, seed: int = 42):
                 ttft_ms=ttft / n * 1e3, tpot_ms=dec / n / (GEN - 1) * 1e3, tokens=first_tokens)
 
 
+def long_leg(hip, weights, seed: int = 7):
+    """BASELINE configs[3] part 2: 128 greedy steps after a 32,768-token random
+    prompt, then a second request sharing the first 30,000 prompt tokens.
+
+    Request 1 prefills the shared prefix, takes a checkpoint there (as the
+    reference's engine does at a prompt's turn boundary, engine.rs:561-584),
+    prefills the rest and decodes.  Request 2 restores the checkpoint (the KV
+    cache of the prefix stays in HBM, lfm2_metal.rs:86-97), prefills only its
+    own 2,768-token tail and decodes; its tokens are checked against the same
+    request run from scratch."""
+    from bobcat_amd.lfm2 import Lfm2Hip
+
+    cfg = weights.cfg
+    rng = np.random.default_rng(seed)
+    prompt1 = rng.integers(0, cfg.n_vocab, LONG_PROMPT).astype(np.uint32)
+    prompt2 = prompt1.copy()
+    prompt2[LONG_SHARED:] = rng.integers(0, cfg.n_vocab, LONG_PROMPT - LONG_SHARED)
+    m = Lfm2Hip(hip, weights, n_ctx=LONG_PROMPT + GEN, kv_half=True)
+    m.reset()
+    t0 = time.perf_counter()
+    m.prefill(prompt1[:LONG_SHARED], logits=False)
+    ck = m.checkpoint()
+    m.prefill(prompt1[LONG_SHARED:], logits=False)
+    m.greedy_token()
+    t1 = time.perf_counter()
+    m.generate(GEN - 1)
+    t2 = time.perf_counter()
+    gpu_decode = m.last_gpu_seconds
+    # Request 2 with the shared prefix reused.
+    m.restore(ck)
+    t3 = time.perf_counter()
+    m.prefill(prompt2[LONG_SHARED:], logits=False)
+    first = m.greedy_token()
+    t4 = time.perf_counter()
+    reused = [first] + m.generate(GEN - 1).tolist()
+    # Request 2 from scratch, for the reuse check and the TTFT it saves.
+    m.reset()
+    t5 = time.perf_counter()
+    m.prefill(prompt2, logits=False)
+    first = m.greedy_token()
+    t6 = time.perf_counter()
+    fresh = [first] + m.generate(GEN - 1).tolist()
+    m.close()
+    return dict(prompt=LONG_PROMPT, shared_prefix=LONG_SHARED,
+                prefill_tok_s=round(LONG_PROMPT / (t1 - t0), 1),
+                decode_tok_s=round((GEN - 1) / (t2 - t1), 1),
+                decode_tok_s_device=round((GEN - 1) / gpu_decode, 1),
+                reuse_ttft_ms=round((t4 - t3) * 1e3, 2), fresh_ttft_ms=round((t6 - t5) * 1e3, 2),
+                reuse_matches_fresh=reused == fresh,
+                reuse_matching_prefix=next((i for i, (a, b) in enumerate(zip(reused, fresh)) if a != b), GEN))
+
+
 def cpu_leg(weights, budget_s: float, threads: int):
     """Decode steps of the oracle on the host: the reference's scalar path
     (f64-accumulating matvec, lfm2.rs:308-394) restated in C, rows split over
@@ -166,6 +222,7 @@ def main() -> int:
     ap.add_argument("--model", default="lfm2-2.6b")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-long", action="store_true", help="skip the 32K-context leg")
     ap.add_argument("--gemv-only", action="store_true", help="only the config-1 GEMV leg (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -193,6 +250,10 @@ def main() -> int:
         log(f"generated {cfg.name} weights in {time.perf_counter() - t:.1f}s")
         mres = model_leg(hip, weights, args.steps, args.warmup)
         log(f"model: { {k: v for k, v in mres.items() if k != 'tokens'} }")
+        lres = None
+        if not args.skip_long and cfg.name == "lfm2-2.6b":
+            lres = long_leg(hip, weights)
+            log(f"long context: {lres}")
     threads = host_threads()
     cpu = None if args.skip_cpu else cpu_leg(weights, args.cpu_seconds, threads)
     if cpu:
@@ -230,6 +291,7 @@ def main() -> int:
         "decode_bytes_per_token": int(token_bytes),
         "decode_hbm_gbs": round(decode_gbs, 1),
         "decode_roofline_frac": round(decode_gbs / HBM_PEAK_GBS, 4),
+        "long_context": lres,
         "roofline": {"kernel": "matvec_q4k (config 1, 8192x2048)", "bound": "hbm",
                      "achieved": round(g["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
