@@ -223,6 +223,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-long", action="store_true", help="skip the 32K-context leg")
+    ap.add_argument("--long-only", action="store_true", help="only the 32K-context leg (for profiling)")
     ap.add_argument("--gemv-only", action="store_true", help="only the config-1 GEMV leg (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -241,6 +242,10 @@ def main() -> int:
     with Hip() as hip:
         name, cus = hip.device_info()
         log(f"device: {name}, {cus} CUs")
+        if args.long_only:
+            lres = long_leg(hip, Lfm2Weights(cfg, seed=0))
+            log(f"long context: {lres}")
+            return 0
         g = gemv_leg(hip, reps=10)
         log(f"gemv: {g}")
         if args.gemv_only:

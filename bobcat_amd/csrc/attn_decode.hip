@@ -4,7 +4,7 @@
 // attention_chunk + attention_combine (crates/bobcat/src/lfm2_metal.rs:
 // 1094-1160; kernels norm.metal:43-108, attention.metal:25-120, 489-531).
 //
-// Grid (query head, split); a split covers up to kKeys consecutive
+// One workgroup per (query head, split); a split covers up to kKeys consecutive
 // positions (all of them for the contexts of a chat turn, so usually one
 // split).  One workgroup per query head rather than per KV head spreads the
 // arithmetic over four times the CUs; the heads of a group read the same
@@ -40,6 +40,14 @@ constexpr int kDecThreads = 1024;
 constexpr int kChunks = 8;       // 16-byte chunks of K (and of V) per thread
 constexpr int kKeys = 1024;      // positions per split, at most
 constexpr int kHd = 256;         // head size, at most
+constexpr uint32_t kXcds = 8;
+
+// Workgroups of one launch: (head, split) items padded to whole runs of a
+// KV group's heads on every XCD (the kernel's item mapping needs that).
+static uint32_t attn_decode_grid(const AttnDecodeArgs &a) {
+  const uint32_t per = kXcds * (a.n_heads / a.n_kv);
+  return (a.n_heads * a.max_splits + per - 1) / per * per;
+}
 
 template <class T>
 __device__ __forceinline__ void coherent_store(T *p, T v) {
@@ -105,6 +113,49 @@ __device__ __forceinline__ float column_sum(float v) {
   return v;
 }
 
+// Combines the (max, sum, output) partials of one head's n_splits splits
+// (split sp at pp + sp·stride: m, l, o[hd]) and returns output element tid
+// (tid < hd; 0 elsewhere).  The whole workgroup calls it: the split maxima
+// are loaded in parallel, then THREADS / hd groups of threads each sum every
+// groups-th split for all hd elements, and the groups are added through LDS,
+// so the loads of different splits are in flight together instead of one
+// dependent chain per element.
+template <int THREADS>
+__device__ float combine_partials(const float *pp, uint32_t n_splits, uint32_t stride, uint32_t hd) {
+  __shared__ float o_s[THREADS], l_s[THREADS], m_w[THREADS / 64];
+  const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  float M = -INFINITY;
+  for (uint32_t sp = tid; sp < n_splits; sp += THREADS) M = fmaxf(M, coherent_load(pp + (uint64_t)sp * stride));
+  M = wave_max(M);
+  if (lane == 0) m_w[wave] = M;
+  __syncthreads();
+  M = m_w[0];
+#pragma unroll
+  for (int w = 1; w < THREADS / 64; w++) M = fmaxf(M, m_w[w]);
+  const uint32_t groups = THREADS / hd, grp = tid / hd, e = tid % hd;
+  float L = 0.f, O = 0.f;
+  for (uint32_t sp = grp; sp < n_splits; sp += groups) {
+    const float *p = pp + (uint64_t)sp * stride;
+    const float w = expf(coherent_load(p) - M);
+    L = fmaf(coherent_load(p + 1), w, L);
+    O = fmaf(coherent_load(p + 2 + e), w, O);
+  }
+  o_s[tid] = O;
+  l_s[tid] = L;
+  __syncthreads();
+  float out = 0.f;
+  if (tid < hd) {
+    float Os = 0.f, Ls = 0.f;
+    for (uint32_t g = 0; g < groups; g++) {
+      Os += o_s[g * hd + tid];
+      Ls += l_s[g * hd + tid];
+    }
+    out = Os / Ls;
+  }
+  __syncthreads();  // o_s, l_s and m_w are reused by the next call
+  return out;
+}
+
 // CPR: 16-byte chunks per cache row (head_dim * element size / 16).
 // FUSED: one decode query at *dpos with its norm/RoPE and cache store;
 // otherwise query z of a prefill batch at first_pos + z, already normalised
@@ -117,10 +168,19 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
   constexpr uint32_t kRowsPerPass = kDecThreads / CPR;
   constexpr uint32_t kps = kRowsPerPass * kChunks < (uint32_t)kKeys ? kRowsPerPass * kChunks : kKeys;
   constexpr int kWaves = kDecThreads / 64;
-  const uint32_t head = blockIdx.x, split = blockIdx.y, tid = threadIdx.x;
+  const uint32_t tid = threadIdx.x;
   const uint32_t wave = tid / 64, lane = tid % 64;
-  const uint32_t group = a.n_heads / a.n_kv, kvh = head / group, kv_dim = a.n_kv * hd;
-  const uint32_t qz = blockIdx.z;
+  const uint32_t group = a.n_heads / a.n_kv, kv_dim = a.n_kv * hd;
+  // Workgroup L goes to XCD L % 8.  Item t = split · n_heads + head numbers
+  // the work so that the `group` heads reading one KV head's split are
+  // consecutive; runs of `group` items are dealt to the XCDs in turn, so
+  // those heads run back to back on one XCD and share its L2 instead of
+  // each fetching the split's keys and values from HBM.
+  const uint32_t L = blockIdx.x, xcd = L % kXcds, k = L / kXcds;
+  const uint32_t t = ((k / group) * kXcds + xcd) * group + k % group;
+  if (t >= a.n_heads * a.max_splits) return;
+  const uint32_t head = t % a.n_heads, split = t / a.n_heads, kvh = head / group;
+  const uint32_t qz = blockIdx.y;
   const uint32_t pos = FUSED ? *a.dpos : a.first_pos + qz;
   const uint32_t n_keys = pos + 1;
   const uint32_t n_splits = (n_keys + kps - 1) / kps;
@@ -325,18 +385,9 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
   }
   __syncthreads();
   if (!last_s) return;
-  if (tid < hd) {
-    const float *pp = a.partials + (uint64_t)slot * a.max_splits * stride;
-    float M = -INFINITY;
-    for (uint32_t sp = 0; sp < n_splits; sp++) M = fmaxf(M, coherent_load(pp + sp * stride));
-    float L = 0.f, O = 0.f;
-    for (uint32_t sp = 0; sp < n_splits; sp++) {
-      const float w = expf(coherent_load(pp + sp * stride) - M);
-      L = fmaf(coherent_load(pp + sp * stride + 1), w, L);
-      O = fmaf(coherent_load(pp + sp * stride + 2 + tid), w, O);
-    }
-    outp[tid] = O / L * gate;
-  }
+  const float o_all = combine_partials<kDecThreads>(a.partials + (uint64_t)slot * a.max_splits * stride, n_splits,
+                                                   stride, hd);
+  if (tid < hd) outp[tid] = o_all * gate;
   if (tid == 0) coherent_store(&a.counters[slot], 0u);
 }
 
@@ -370,7 +421,7 @@ static void launch_attn_decode(hipStream_t s, const AttnDecodeArgs &a, dim3 grid
 }
 
 void run_attn_decode(hipStream_t s, const AttnDecodeArgs &a, bool kv_half) {
-  dim3 grid(a.n_heads, a.max_splits);
+  dim3 grid(attn_decode_grid(a));
   if (kv_half)
     launch_attn_decode<true, true>(s, a, grid);
   else
@@ -378,7 +429,7 @@ void run_attn_decode(hipStream_t s, const AttnDecodeArgs &a, bool kv_half) {
 }
 
 void run_attn_prefill(hipStream_t s, const AttnDecodeArgs &a, bool kv_half, uint32_t n_queries) {
-  dim3 grid(a.n_heads, a.max_splits, n_queries);
+  dim3 grid(attn_decode_grid(a), n_queries);
   if (kv_half)
     launch_attn_decode<true, false>(s, a, grid);
   else

@@ -166,6 +166,31 @@ def test_decode_across_attention_splits(hip, kv_half):
     gpu.close()
 
 
+@pytest.mark.parametrize("kv_half", [False, True])
+def test_long_context_decode(hip, kv_half):
+    """A driver sized for a long context (n_ctx 8192: 16 splits of 512 f32 or
+    8 of 1024 f16 positions, four query heads per KV head) launches a grid of
+    that many splits, dealt to the XCDs by KV group; steps at positions
+    1020-1027 run with one to three live splits and the parallel split
+    combine, against the oracle, and against a driver sized for 1100."""
+    w = Lfm2Weights(LFM2_TINY_F16, seed=12)
+    toks = prompt(LFM2_TINY_F16, 1028, seed=9)
+    big = Lfm2Hip(hip, w, n_ctx=8192, kv_half=kv_half)
+    small = Lfm2Hip(hip, w, n_ctx=1100, kv_half=kv_half)
+    cpu = oracle.Lfm2State(w, n_ctx=1100)
+    big.prefill(toks[:1020], logits=False)
+    small.prefill(toks[:1020], logits=False)
+    for t in toks[:1020]:
+        cpu.step(t, logits=False)
+    tol = HALF_TOLERANCE if kv_half else TOLERANCE
+    for t in toks[1020:]:
+        got, per_head, want = big.step(t), small.step(t), cpu.step(t)
+        assert rel(got, want) < tol, (t, rel(got, want))
+        assert rel(got, per_head) < 1e-5, (t, rel(got, per_head))
+    big.close()
+    small.close()
+
+
 def test_reset_matches_fresh_state(hip, weights):
     cfg = weights.cfg
     toks = prompt(cfg, 10, seed=5)

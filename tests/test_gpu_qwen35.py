@@ -21,7 +21,7 @@ import pytest
 
 import oracle
 from bobcat_amd._lib import DeltaShape
-from bobcat_amd.qwen35 import QWEN35_TINY, QWEN35_TINY_64, Qwen35Hip, Qwen35Weights
+from bobcat_amd.qwen35 import QWEN35_TINY, QWEN35_TINY_64, Qwen35Config, Qwen35Hip, Qwen35Weights
 
 pytestmark = pytest.mark.gpu
 
@@ -245,3 +245,26 @@ def test_attention_gate_matches_float64(hip):
     got = hip.read(ab.at(0), np.empty_like(attn))
     gate = qg.reshape(n_tokens, heads, 2, hd)[:, :, 1, :].reshape(n_tokens, q_dim).astype(np.float64)
     assert rel(got, attn * (1 / (1 + np.exp(-gate)))) < 1e-6
+
+
+@pytest.mark.parametrize("kv_half", [False, True])
+def test_long_context_gated_decode(hip, kv_half):
+    """Four query heads per KV head in a driver sized for 8192 positions: the
+    gated decode kernel over a grid of many splits; steps at positions
+    1020-1027 (one to three live splits, combined in parallel) against the
+    oracle."""
+    cfg = Qwen35Config("qwen3.5-group4", n_embd=256, n_ff=512, n_vocab=500, n_layers=4, n_heads=4,
+                       n_kv_heads=1, head_dim=64, n_rot=32, n_k_heads=2, n_v_heads=4, k_head_dim=64,
+                       v_head_dim=64)
+    w = Qwen35Weights(cfg, seed=13)
+    toks = prompt(cfg, 1028, seed=10)
+    gpu = Qwen35Hip(hip, w, n_ctx=8192, kv_half=kv_half)
+    cpu = oracle.Qwen35State(w, n_ctx=1100)
+    gpu.prefill(toks[:1020], logits=False)
+    for t in toks[:1020]:
+        cpu.step(t, logits=False)
+    tol = HALF_TOLERANCE if kv_half else TOLERANCE
+    for t in toks[1020:]:
+        got, want = gpu.step(t), cpu.step(t)
+        assert rel(got, want) < tol, (t, rel(got, want))
+    gpu.close()
