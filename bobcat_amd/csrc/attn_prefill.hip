@@ -14,6 +14,7 @@
 // probabilities are split into f16 high and low parts (~22 bits) and both
 // are multiplied; K and V are the cache's f16 values, so the products are
 // exact and accumulate in f32.
+#include <algorithm>
 #include <cmath>
 
 #include "device.h"
@@ -35,7 +36,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *__restrict__ 
                                                       const _Float16 *__restrict__ vc, float *__restrict__ out,
                                                       uint32_t n_heads, uint32_t n_kv, uint32_t first_pos,
                                                       uint32_t n_queries, uint32_t q_stride, uint32_t out_stride,
-                                                      float scale) {
+                                                      float scale, float *__restrict__ partials) {
   constexpr int KS = HD / 16;  // k-steps of the score product
   constexpr int OB = HD / 32;  // 32-row blocks of the output
   __shared__ _Float16 vt[HD * kVtStride];  // V^T of the current key block: [d][key]
@@ -49,6 +50,12 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *__restrict__ 
   const uint32_t qpos = first_pos + q0 + col;
   const uint32_t kend = first_pos + min(q0 + kPrefQ, n_queries);  // keys of the block's last query, exclusive
   const uint64_t row_elems = (uint64_t)n_kv * HD;                 // cache elements per position
+  // Key split blockIdx.z of gridDim.z: a contiguous run of whole 32-key
+  // blocks.  The host gives every split at least two blocks, so each split
+  // starts at or before the tile's first query and every query sees a key
+  // of every split.
+  const uint32_t n_blocks = (kend + kPrefKeys - 1) / kPrefKeys, n_split = gridDim.z, split = blockIdx.z;
+  const uint32_t kb_lo = split * n_blocks / n_split * kPrefKeys, kb_hi = (split + 1) * n_blocks / n_split * kPrefKeys;
 
   // The query's k-step fragments as the B operand: Q[z][16·s + 8·half .. +8].
   ph8_t qh[KS], ql[KS];
@@ -74,7 +81,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *__restrict__ 
     for (int i = 0; i < 16; i++) o[b][i] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  for (uint32_t kb = 0; kb < kend; kb += kPrefKeys) {
+  for (uint32_t kb = kb_lo; kb < kb_hi && kb < kend; kb += kPrefKeys) {
     // Stage V^T of keys kb .. kb+31 (zeros past kend).
     __syncthreads();
     for (uint32_t c = tid; c < (uint32_t)(kPrefKeys * HD / 8); c += 256) {
@@ -145,36 +152,96 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *__restrict__ 
       }
     }
   }
-  if (!active || q0 + col >= n_queries) return;
-  const float inv = 1.f / (l_run + __shfl_xor(l_run, 32, 64));
+  if (!active) return;
+  const float l_all = l_run + __shfl_xor(l_run, 32, 64);
+  if (q0 + col >= n_queries) return;
+  float inv = 1.f / l_all;
   float *orow = out + (uint64_t)(q0 + col) * out_stride + (uint64_t)head * HD;
+  if (n_split > 1) {
+    // Unnormalised partial (max, sum, output) of this split, combined by
+    // k_attn_prefill_combine.
+    float *pp = partials + (((uint64_t)(q0 + col) * n_heads + head) * n_split + split) * (HD + 2);
+    if (half_id == 0) {
+      pp[0] = m_run;
+      pp[1] = l_all;
+    }
+    orow = pp + 2;
+    inv = 1.f;
+  }
 #pragma unroll
   for (int b = 0; b < OB; b++)
 #pragma unroll
     for (int g = 0; g < 4; g++) {
       const uint32_t d = 32 * b + 8 * g + 4 * half_id;
-      *reinterpret_cast<float4 *>(orow + d) =
-          float4{o[b][4 * g] * inv, o[b][4 * g + 1] * inv, o[b][4 * g + 2] * inv, o[b][4 * g + 3] * inv};
+      if (n_split > 1) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) orow[d + i] = o[b][4 * g + i];
+      } else {
+        *reinterpret_cast<float4 *>(orow + d) =
+            float4{o[b][4 * g] * inv, o[b][4 * g + 1] * inv, o[b][4 * g + 2] * inv, o[b][4 * g + 3] * inv};
+      }
     }
+}
+
+// Output of each (query, head) from its key splits' partials: one workgroup
+// of HD threads per (query, head).
+template <int HD>
+__global__ __launch_bounds__(HD) void k_attn_prefill_combine(const float *__restrict__ partials, float *__restrict__ out,
+                                                              uint32_t n_heads, uint32_t n_split, uint32_t out_stride) {
+  const uint32_t slot = blockIdx.x, z = slot / n_heads, head = slot % n_heads, d = threadIdx.x;
+  const float *pp = partials + (uint64_t)slot * n_split * (HD + 2);
+  float M = -INFINITY;
+  for (uint32_t sp = 0; sp < n_split; sp++) M = fmaxf(M, pp[sp * (HD + 2)]);
+  float L = 0.f, O = 0.f;
+  for (uint32_t sp = 0; sp < n_split; sp++) {
+    const float w = expf(pp[sp * (HD + 2)] - M);
+    L = fmaf(pp[sp * (HD + 2) + 1], w, L);
+    O = fmaf(pp[sp * (HD + 2) + 2 + d], w, O);
+  }
+  out[(uint64_t)z * out_stride + (uint64_t)head * HD + d] = O / L;
 }
 
 bool attn_prefill_mfma_supported(uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, bool kv_half) {
   return kv_half && n_kv && n_heads % n_kv == 0 && n_heads / n_kv <= 4 && (head_dim == 64 || head_dim == 128);
 }
 
+uint32_t attn_prefill_splits(uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t first_pos,
+                             uint32_t n_queries, uint64_t partial_floats) {
+  if (!n_queries) return 1;
+  // Enough workgroups for two per CU, each split at least kMinSplitKeys keys
+  // of the batch's first tile (so at least two 32-key blocks of every tile),
+  // and no more partials than the scratch holds.
+  constexpr uint32_t kTargetGroups = 512, kMinSplitKeys = 1024, kMaxSplits = 16;
+  const uint32_t tiles = (n_queries + kPrefQ - 1) / kPrefQ;
+  uint32_t want = (kTargetGroups + tiles * n_kv - 1) / (tiles * n_kv);
+  want = std::min(want, (first_pos + std::min<uint32_t>(kPrefQ, n_queries)) / kMinSplitKeys);
+  want = std::min<uint32_t>(want, kMaxSplits);
+  const uint64_t per_split = (uint64_t)n_queries * n_heads * (head_dim + 2);
+  want = (uint32_t)std::min<uint64_t>(want, partial_floats / per_split);
+  return std::max<uint32_t>(want, 1);
+}
+
 void run_attn_prefill_mfma(hipStream_t s, const float *q, const void *k_cache, const void *v_cache, float *out,
                            uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t first_pos,
-                           uint32_t n_queries, uint32_t q_stride, uint32_t out_stride, float scale) {
+                           uint32_t n_queries, uint32_t q_stride, uint32_t out_stride, float scale, float *partials,
+                           uint64_t partial_floats) {
   if (!n_queries) return;
-  const dim3 grid((n_queries + kPrefQ - 1) / kPrefQ, n_kv);
+  const uint32_t n_split =
+      partials ? attn_prefill_splits(n_heads, n_kv, head_dim, first_pos, n_queries, partial_floats) : 1;
+  const dim3 grid((n_queries + kPrefQ - 1) / kPrefQ, n_kv, n_split);
   const _Float16 *kc = static_cast<const _Float16 *>(k_cache);
   const _Float16 *vc = static_cast<const _Float16 *>(v_cache);
-  if (head_dim == 64)
+  if (head_dim == 64) {
     k_attn_prefill<64><<<grid, 256, 0, s>>>(q, kc, vc, out, n_heads, n_kv, first_pos, n_queries, q_stride,
-                                            out_stride, scale);
-  else
+                                            out_stride, scale, partials);
+    if (n_split > 1)
+      k_attn_prefill_combine<64><<<n_queries * n_heads, 64, 0, s>>>(partials, out, n_heads, n_split, out_stride);
+  } else {
     k_attn_prefill<128><<<grid, 256, 0, s>>>(q, kc, vc, out, n_heads, n_kv, first_pos, n_queries, q_stride,
-                                             out_stride, scale);
+                                             out_stride, scale, partials);
+    if (n_split > 1)
+      k_attn_prefill_combine<128><<<n_queries * n_heads, 128, 0, s>>>(partials, out, n_heads, n_split, out_stride);
+  }
 }
 
 }  // namespace bch
@@ -204,6 +271,6 @@ extern "C" int bch_attention_prefill(bch_ctx *ctx, bch_view q, bch_view k_cache,
     return fail(BCH_ERR_ARGUMENT, "attention_prefill: operands must be 16-byte aligned");
   return launch(ctx, {"attention_prefill", 0, 0, 0}, [&](hipStream_t s) {
     run_attn_prefill_mfma(s, qp, kp, vp, op, n_heads, n_kv_heads, head_dim, first_pos, n_queries,
-                          n_heads * head_dim, n_heads * head_dim, 1.0f / sqrtf((float)head_dim));
+                          n_heads * head_dim, n_heads * head_dim, 1.0f / sqrtf((float)head_dim), nullptr, 0);
   });
 }

@@ -192,10 +192,17 @@ void run_attention(hipStream_t s, const float *q, const void *k_cache, const voi
 // attn_prefill.hip: causal GQA attention of n_queries queries at positions
 // first_pos.. over the f16 cache (their keys already stored), on MFMA.  q and
 // out rows are q_stride / out_stride floats apart, head h at h·head_dim.
+// `partials` (nullable) is scratch for key splits.
 bool attn_prefill_mfma_supported(uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, bool kv_half);
 void run_attn_prefill_mfma(hipStream_t s, const float *q, const void *k_cache, const void *v_cache, float *out,
                            uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t first_pos,
-                           uint32_t n_queries, uint32_t q_stride, uint32_t out_stride, float scale);
+                           uint32_t n_queries, uint32_t q_stride, uint32_t out_stride, float scale,
+                           float *partials, uint64_t partial_floats);
+// Key splits run_attn_prefill_mfma uses for a batch (1 without scratch):
+// long contexts split the keys so the launch fills the chip, each split's
+// (max, sum, output) partials going to `partials` (partial_floats floats).
+uint32_t attn_prefill_splits(uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t first_pos,
+                             uint32_t n_queries, uint64_t partial_floats);
 
 // matmul.hip.  Y[t] (store) W·X[t] for n_tokens rows; store 0 overwrite,
 // 1 accumulate, 2 swiglu (y = silu(y) * product).

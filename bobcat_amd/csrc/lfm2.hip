@@ -61,6 +61,7 @@ struct bch_lfm2 : bch::Sequence {
   float *conv_state = nullptr, *hidden = nullptr, *normed = nullptr, *bcx = nullptr, *conv_out = nullptr;
   float *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *ffn = nullptr;
   float *partials = nullptr;
+  uint64_t partial_floats = 0;  // floats of `partials`
   uint32_t *counters = nullptr;
   uint32_t *route = nullptr;  // expert routes of a batch (route_bytes(n_used, batch))
   // Batched experts: the batch's entries grouped by expert, each entry's
@@ -246,7 +247,7 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
       if (attn_prefill_mfma_supported(m->n_heads, m->n_kv_heads, m->head_dim, m->kv_half))
         run_attn_prefill_mfma(s, m->q, m->cache_layer(m->k_cache, ci), m->cache_layer(m->v_cache, ci), m->attn,
                               m->n_heads, m->n_kv_heads, m->head_dim, pos, count, m->q_dim, m->q_dim,
-                              1.0f / sqrtf((float)m->head_dim));
+                              1.0f / sqrtf((float)m->head_dim), m->partials, m->partial_floats);
       else
       for (uint32_t q0 = 0; q0 < count; q0 += kAttnQueryBatch) {
         const uint32_t nq = std::min(kAttnQueryBatch, count - q0);
@@ -452,6 +453,7 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
     const uint64_t cache = (uint64_t)m->n_attn * n_ctx * m->kv_dim * (m->kv_half ? 2 : 4);
     const uint64_t partial_floats = attention_partial_floats(std::min<uint32_t>(m->batch, kAttnQueryBatch), m->n_heads,
                                                             hd, attn_decode_max_splits(n_ctx, hd, m->kv_half));
+    m->partial_floats = partial_floats;
     const uint32_t widest = std::max({n, m->q_dim, m->n_ff});
     const uint64_t split_bytes =
         std::max(matmul_split_bytes((uint32_t)rows, widest),

@@ -191,6 +191,26 @@ def test_long_context_decode(hip, kv_half):
     small.close()
 
 
+def test_long_context_prefill_key_splits(hip):
+    """A 40-token prefill after 2,900 cached positions (f16 cache, n_ctx 8192)
+    splits the keys of the MFMA prefill attention in two, each split's
+    partials combined afterwards; its logits and the next steps against the
+    oracle."""
+    w = Lfm2Weights(LFM2_TINY_F16, seed=14)
+    toks = prompt(LFM2_TINY_F16, 2944, seed=15)
+    gpu = Lfm2Hip(hip, w, n_ctx=8192, kv_half=True)
+    cpu = oracle.Lfm2State(w, n_ctx=3000)
+    gpu.prefill(toks[:2900], logits=False)
+    for t in toks[:2939]:
+        cpu.step(t, logits=False)
+    got, want = gpu.prefill(toks[2900:2940]), cpu.step(toks[2939])
+    assert rel(got, want) < HALF_TOLERANCE, rel(got, want)
+    for t in toks[2940:]:
+        got, want = gpu.step(t), cpu.step(t)
+        assert rel(got, want) < HALF_TOLERANCE, (t, rel(got, want))
+    gpu.close()
+
+
 def test_reset_matches_fresh_state(hip, weights):
     cfg = weights.cfg
     toks = prompt(cfg, 10, seed=5)
