@@ -49,14 +49,6 @@ static uint32_t attn_decode_grid(const AttnDecodeArgs &a) {
   return (a.n_heads * a.max_splits + per - 1) / per * per;
 }
 
-template <class T>
-__device__ __forceinline__ void coherent_store(T *p, T v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <class T>
-__device__ __forceinline__ T coherent_load(const T *p) {
-  return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // RMS-normalise one head of `hd` floats at src (scaled by w) and rotate its
 // first n_rot elements NeoX-style for `position`, into dst (LDS).  Called by

@@ -117,4 +117,15 @@ __device__ __forceinline__ uint32_t q4k_pair_scales(uint32_t h1, uint32_t h2, ui
   return p < 2 ? low : high;
 }
 
+// Device-scope relaxed accesses for data one workgroup hands to another on
+// any XCD (they go past the non-coherent L2 of the writer's XCD).
+template <class T>
+__device__ __forceinline__ void coherent_store(T *p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ T coherent_load(const T *p) {
+  return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace bch

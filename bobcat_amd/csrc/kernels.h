@@ -95,9 +95,13 @@ void run_matmul_experts(hipStream_t s, uint32_t format, const uint8_t *W, const 
                         uint32_t n_tokens, void *split);
 void run_moe_combine(hipStream_t s, const float *x, const uint32_t *route, float *y, uint32_t n_embd,
                      uint32_t n_used, uint32_t n_tokens);
+// With `scores` (n_tokens · n_experts floats of scratch) and `counters`
+// (n_tokens zeroed u32, left zeroed) the scores are spread over (token,
+// 4-expert) workgroups and the last of a token's picks its route; without,
+// one workgroup per token does both.
 void run_moe_route(hipStream_t s, const float *x, const float *norm_w, float eps, float *normed, const float *router,
                    const float *bias, uint32_t *route, uint32_t n_cols, uint32_t n_experts, uint32_t n_used,
-                   uint32_t n_tokens);
+                   uint32_t n_tokens, float *scores, uint32_t *counters);
 // y[slot][r] = silu(G_e·x)[r] · (U_e·x)[r] for the n_used experts e of `ids`.
 bool fast_matvec_experts_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const uint8_t *Wu, uint32_t n_ff,
                                 uint32_t n_cols, const uint32_t *ids, uint32_t n_used, const float *x, float *y,

@@ -64,6 +64,8 @@ struct bch_lfm2 : bch::Sequence {
   uint64_t partial_floats = 0;  // floats of `partials`
   uint32_t *counters = nullptr;
   uint32_t *route = nullptr;  // expert routes of a batch (route_bytes(n_used, batch))
+  float *route_scores = nullptr;  // router scores of a batch [batch][n_experts]
+  uint32_t *route_counters = nullptr;  // [batch], zeroed
   // Batched experts: the batch's entries grouped by expert, each entry's
   // SwiGLU activations and down projection (Recorder::grouped_moe).
   uint32_t *moe_offsets = nullptr, *moe_entries = nullptr;
@@ -102,7 +104,7 @@ static void record_moe_token(bch_lfm2 *m, hipStream_t s, const Layer &L, const f
   const uint32_t n = m->n_embd, cus = m->ctx->n_cus;
   if (norm)
     run_moe_route(s, x, norm, m->norm_eps, normed, reinterpret_cast<const float *>(L.router.data), L.expert_bias,
-                  route, n, m->n_experts, m->n_used, 1);
+                  route, n, m->n_experts, m->n_used, 1, m->route_scores, m->route_counters);
   const float *in = norm ? normed : x;
   fast_matvec_experts_swiglu(s, L.gate_exps.format, L.gate_exps.data, L.up_exps.data, m->n_ff_expert, n, route,
                              m->n_used, in, m->ffn, cus);
@@ -278,7 +280,7 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
     if (L.moe) {
       // Route the whole batch in one launch, then each token's experts.
       run_moe_route(s, m->normed, nullptr, 0.f, nullptr, reinterpret_cast<const float *>(L.router.data),
-                    L.expert_bias, m->route, n, m->n_experts, m->n_used, count);
+                    L.expert_bias, m->route, n, m->n_experts, m->n_used, count, m->route_scores, m->route_counters);
       const bool grouped = count > 1 && n % 256 == 0 && m->n_ff_expert % 256 == 0 &&
                            L.gate_exps.format == L.up_exps.format;
       if (grouped) {
@@ -469,6 +471,8 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
            (rc = m->alloc_t(partial_floats + 4, &m->partials)) ||
            (rc = m->alloc_t((uint64_t)kAttnQueryBatch * std::max(1u, m->n_heads), &m->counters)) ||
            (rc = m->alloc_t(2 * (uint64_t)std::max(1u, m->n_used) * rows, &m->route)) ||
+           (rc = m->alloc_t((uint64_t)std::max(1u, m->n_experts) * rows, &m->route_scores)) ||
+           (rc = m->alloc_t(rows, &m->route_counters)) ||
            (rc = m->alloc_t((uint64_t)m->n_experts + 1, &m->moe_offsets)) ||
            (rc = m->alloc_t(std::max(1u, m->n_used) * rows, &m->moe_entries)) ||
            (rc = m->alloc_t(std::max<uint64_t>(1, (uint64_t)m->n_used * rows * m->n_ff_expert), &m->expert_ffn)) ||

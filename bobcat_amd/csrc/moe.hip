@@ -31,53 +31,15 @@ __device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
   return k;
 }
 
-// One workgroup per token.  The token (RMS-normalised when norm_w is given,
-// as rms_norm does: w·(x·scale)) is staged in LDS; wave w scores experts
-// w, w+16, ... with the F32 router rows; wave 0 then picks the n_used experts
-// of largest sigmoid score + bias and writes their ids and normalised weights.
-__global__ __launch_bounds__(1024) void k_moe_route(const float *__restrict__ x, const float *__restrict__ norm_w,
-                                                    float eps, float *__restrict__ normed,
-                                                    const float *__restrict__ router, const float *__restrict__ bias,
-                                                    uint32_t *__restrict__ route, uint32_t n_cols, uint32_t n_experts,
-                                                    uint32_t n_used) {
-  extern __shared__ float xs[];
-  __shared__ float red[16];
-  __shared__ float score[kMoeMaxExperts];
-  const uint32_t t = blockIdx.x, tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
-  const float *row = x + (uint64_t)t * n_cols;
-  float ss = 0.f;
-  for (uint32_t i = tid; i < n_cols; i += 1024) {
-    const float v = row[i];
-    xs[i] = v;
-    ss = fmaf(v, v, ss);
-  }
-  if (norm_w) {
-    ss = block_sum<1024>(ss, red);
-    const float scale = (float)(1.0 / sqrt((double)ss / (double)n_cols + (double)eps));
-    for (uint32_t i = tid; i < n_cols; i += 1024) {
-      const float v = norm_w[i] * (xs[i] * scale);
-      xs[i] = v;
-      normed[(uint64_t)t * n_cols + i] = v;
-    }
-  }
-  __syncthreads();
-  for (uint32_t e = wave; e < n_experts; e += 16) {
-    const float4 *r4 = reinterpret_cast<const float4 *>(router + (uint64_t)e * n_cols);
-    float acc = 0.f;
-    for (uint32_t i = lane; i < n_cols / 4; i += 64) {
-      const float4 w = r4[i];
-      const float4 v = reinterpret_cast<const float4 *>(xs)[i];
-      acc = fmaf(w.x, v.x, fmaf(w.y, v.y, fmaf(w.z, v.z, fmaf(w.w, v.w, acc))));
-    }
-    acc = wave_sum(acc);
-    if (lane == 0) score[e] = 1.0f / (1.0f + expf(-acc));
-  }
-  __syncthreads();
-  if (wave != 0) return;
+// Wave 0 of a workgroup: the n_used experts of largest score + bias, ties to
+// the lower expert, and their normalised weights, into out (ids, then
+// weights as float bits).
+__device__ void pick_route(const float *score, const float *__restrict__ bias, uint32_t *__restrict__ out,
+                           uint32_t n_experts, uint32_t n_used) {
+  const uint32_t lane = threadIdx.x % 64;
   // Lane l holds experts l and l + 64.
   uint64_t k0 = lane < n_experts ? route_key(score[lane] + bias[lane], lane) : 0;
   uint64_t k1 = lane + 64 < n_experts ? route_key(score[lane + 64] + bias[lane + 64], lane + 64) : 0;
-  uint32_t *out = route + (uint64_t)t * 2 * n_used;
   float sum = 0.f;
   uint32_t picked[kMoeMaxUsed];
   for (uint32_t k = 0; k < n_used; k++) {
@@ -95,6 +57,178 @@ __global__ __launch_bounds__(1024) void k_moe_route(const float *__restrict__ x,
       out[n_used + k] = __float_as_uint(score[picked[k]] / norm);
     }
   }
+}
+
+// One workgroup per token.  The token (RMS-normalised when norm_w is given,
+// as rms_norm does: w·(x·scale)) is staged in LDS; wave w scores experts
+// w, w+16, ... with the F32 router rows, their loads issued ahead; wave 0 then picks the n_used experts
+// of largest sigmoid score + bias and writes their ids and normalised weights.
+__global__ __launch_bounds__(1024) void k_moe_route(const float *__restrict__ x, const float *__restrict__ norm_w,
+                                                    float eps, float *__restrict__ normed,
+                                                    const float *__restrict__ router, const float *__restrict__ bias,
+                                                    uint32_t *__restrict__ route, uint32_t n_cols, uint32_t n_experts,
+                                                    uint32_t n_used) {
+  extern __shared__ float xs[];
+  __shared__ float red[16];
+  __shared__ float score[kMoeMaxExperts];
+  const uint32_t t = blockIdx.x, tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+  const float *row = x + (uint64_t)t * n_cols;
+  // Router rows of this wave's experts (e0 + 16k), kU float4 per lane per
+  // pass; the first pass is issued before the input is read, so its latency
+  // overlaps the staging and the norm, and every pass issues all its loads
+  // before the first multiply.
+  constexpr int kU = 8, kE = 2;
+  const uint32_t n4 = n_cols / 4;
+  float4 w[kE][kU];
+#define BCH_ROUTER_LOAD(e0, base)                                                                   \
+  _Pragma("unroll") for (int k = 0; k < kE; k++) {                                                   \
+    const uint32_t e_ = (e0) + 16 * k;                                                               \
+    const float4 *r4_ = reinterpret_cast<const float4 *>(router + (uint64_t)min(e_, n_experts - 1) * n_cols); \
+    _Pragma("unroll") for (int u = 0; u < kU; u++) {                                                 \
+      const uint32_t i_ = (base) + lane + 64 * u;                                                    \
+      w[k][u] = (e_ < n_experts && i_ < n4) ? r4_[i_] : make_float4(0.f, 0.f, 0.f, 0.f);             \
+    }                                                                                                \
+  }
+  BCH_ROUTER_LOAD(wave, 0u)
+  float ss = 0.f;
+  for (uint32_t i = tid; i < n_cols; i += 1024) {
+    const float v = row[i];
+    xs[i] = v;
+    ss = fmaf(v, v, ss);
+  }
+  if (norm_w) {
+    ss = block_sum<1024>(ss, red);
+    const float scale = (float)(1.0 / sqrt((double)ss / (double)n_cols + (double)eps));
+    for (uint32_t i = tid; i < n_cols; i += 1024) {
+      const float v = norm_w[i] * (xs[i] * scale);
+      xs[i] = v;
+      normed[(uint64_t)t * n_cols + i] = v;
+    }
+  }
+  __syncthreads();
+  // Each lane sums its columns in increasing order, then the wave sums.
+  for (uint32_t e0 = wave; e0 < n_experts; e0 += 16 * kE) {
+    float acc[kE];
+#pragma unroll
+    for (int k = 0; k < kE; k++) acc[k] = 0.f;
+    for (uint32_t base = 0; base < n4; base += 64 * kU) {
+      if (e0 != wave || base != 0) {
+        BCH_ROUTER_LOAD(e0, base)
+      }
+#pragma unroll
+      for (int u = 0; u < kU; u++) {
+        const uint32_t i = base + lane + 64 * u;
+        if (i < n4) {
+          const float4 v = reinterpret_cast<const float4 *>(xs)[i];
+#pragma unroll
+          for (int k = 0; k < kE; k++)
+            acc[k] = fmaf(w[k][u].x, v.x, fmaf(w[k][u].y, v.y, fmaf(w[k][u].z, v.z, fmaf(w[k][u].w, v.w, acc[k]))));
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kE; k++) {
+      acc[k] = wave_sum(acc[k]);
+      if (lane == 0 && e0 + 16 * k < n_experts) score[e0 + 16 * k] = 1.0f / (1.0f + expf(-acc[k]));
+    }
+  }
+#undef BCH_ROUTER_LOAD
+  __syncthreads();
+  if (wave != 0) return;
+  pick_route(score, bias, route + (uint64_t)t * 2 * n_used, n_experts, n_used);
+}
+
+// Routes of decode and prefill tokens with the router spread over the chip:
+// one workgroup per (token, 4 experts), wave w scoring expert
+// 4·blockIdx.y + w.  A workgroup issues its router row loads, the norm
+// weights and the token's inputs at once, normalises the token for itself
+// (as k_moe_route does; the first workgroup also stores it in `normed`) and
+// hands its scores to the token's other workgroups through
+// scores[token][expert] with device-scope stores.  The last to arrive, by
+// counters[token] (left zeroed), picks the route.
+__global__ __launch_bounds__(256) void k_moe_scores(const float *__restrict__ x, const float *__restrict__ norm_w,
+                                                    float eps, float *__restrict__ normed,
+                                                    const float *__restrict__ router, const float *__restrict__ bias,
+                                                    float *__restrict__ scores, uint32_t *__restrict__ counters,
+                                                    uint32_t *__restrict__ route, uint32_t n_cols, uint32_t n_experts,
+                                                    uint32_t n_used) {
+  extern __shared__ float xs[];
+  __shared__ float red[4];
+  __shared__ float score_s[kMoeMaxExperts];
+  __shared__ uint32_t last_s;
+  const uint32_t t = blockIdx.x, tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+  const uint32_t e = 4 * blockIdx.y + wave, n4 = n_cols / 4;
+  constexpr int kU = 8, kX = 8;  // router float4 per lane per pass; input elements per thread held
+  const float4 *r4 = reinterpret_cast<const float4 *>(router + (uint64_t)min(e, n_experts - 1) * n_cols);
+  float4 w[kU];
+#pragma unroll
+  for (int u = 0; u < kU; u++) {
+    const uint32_t i = lane + 64 * u;
+    w[u] = (e < n_experts && i < n4) ? r4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  const float *row = x + (uint64_t)t * n_cols;
+  float xv[kX], nv[kX];
+#pragma unroll
+  for (int j = 0; j < kX; j++) {
+    const uint32_t i = tid + 256 * j;
+    xv[j] = i < n_cols ? row[i] : 0.f;
+    nv[j] = (norm_w && i < n_cols) ? norm_w[i] : 0.f;
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kX; j++) ss = fmaf(xv[j], xv[j], ss);
+  for (uint32_t i = tid + 256 * kX; i < n_cols; i += 256) ss = fmaf(row[i], row[i], ss);
+  float scale = 1.f;
+  if (norm_w) {
+    ss = block_sum<256>(ss, red);
+    scale = (float)(1.0 / sqrt((double)ss / (double)n_cols + (double)eps));
+  }
+  // Staged as rms_norm computes it: w·(x·scale).
+#pragma unroll
+  for (int j = 0; j < kX; j++) {
+    const uint32_t i = tid + 256 * j;
+    if (i < n_cols) xs[i] = norm_w ? nv[j] * (xv[j] * scale) : xv[j];
+  }
+  for (uint32_t i = tid + 256 * kX; i < n_cols; i += 256) xs[i] = norm_w ? norm_w[i] * (row[i] * scale) : row[i];
+  if (norm_w && blockIdx.y == 0)
+    for (uint32_t i = tid; i < n_cols; i += 256) normed[(uint64_t)t * n_cols + i] = xs[i];  // own elements only
+  __syncthreads();
+  // Each lane sums its columns in increasing order, then the wave sums (the
+  // order k_moe_route uses).
+  if (e < n_experts) {
+    float acc = 0.f;
+    for (uint32_t base = 0; base < n4; base += 64 * kU) {
+      if (base != 0) {
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+          const uint32_t i = base + lane + 64 * u;
+          w[u] = i < n4 ? r4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kU; u++) {
+        const uint32_t i = base + lane + 64 * u;
+        if (i < n4) {
+          const float4 v = reinterpret_cast<const float4 *>(xs)[i];
+          acc = fmaf(w[u].x, v.x, fmaf(w[u].y, v.y, fmaf(w[u].z, v.z, fmaf(w[u].w, v.w, acc))));
+        }
+      }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) coherent_store(scores + (uint64_t)t * n_experts + e, 1.0f / (1.0f + expf(-acc)));
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&counters[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_s = prev == gridDim.y - 1;
+  }
+  __syncthreads();
+  if (!last_s || wave != 0) return;
+  for (uint32_t i = lane; i < n_experts; i += 64) score_s[i] = coherent_load(scores + (uint64_t)t * n_experts + i);
+  __builtin_amdgcn_wave_barrier();
+  pick_route(score_s, bias, route + (uint64_t)t * 2 * n_used, n_experts, n_used);
+  if (lane == 0) coherent_store(&counters[t], 0u);
 }
 
 // y[r] += Σ_slot w_slot · (W_{e_slot} row r) · x_slot for one token.  The
@@ -150,12 +284,20 @@ __global__ __launch_bounds__(256) void k_experts_down(const uint8_t *__restrict_
 
 void run_moe_route(hipStream_t s, const float *x, const float *norm_w, float eps, float *normed, const float *router,
                    const float *bias, uint32_t *route, uint32_t n_cols, uint32_t n_experts, uint32_t n_used,
-                   uint32_t n_tokens) {
+                   uint32_t n_tokens, float *scores, uint32_t *counters) {
   const size_t lds = (size_t)n_cols * 4;
   static const bool lds_limit_set =
       hipFuncSetAttribute(reinterpret_cast<const void *>(k_moe_route), hipFuncAttributeMaxDynamicSharedMemorySize,
                           131072) == hipSuccess;
   (void)lds_limit_set;
+  if (scores) {
+    static const bool set = hipFuncSetAttribute(reinterpret_cast<const void *>(k_moe_scores),
+                                                hipFuncAttributeMaxDynamicSharedMemorySize, 131072) == hipSuccess;
+    (void)set;
+    k_moe_scores<<<dim3(n_tokens, (n_experts + 3) / 4), 256, lds, s>>>(x, norm_w, eps, normed, router, bias, scores,
+                                                                      counters, route, n_cols, n_experts, n_used);
+    return;
+  }
   k_moe_route<<<n_tokens, 1024, lds, s>>>(x, norm_w, eps, normed, router, bias, route, n_cols, n_experts, n_used);
 }
 
@@ -317,7 +459,7 @@ extern "C" int bch_moe_route(bch_ctx *ctx, bch_view x, const bch_norm *norm, bch
     return fail(BCH_ERR_ARGUMENT, "moe_route: the router is not 16-byte aligned");
   const float eps = norm ? norm->eps : 0.f;
   return launch(ctx, {"moe_route", n_experts, n_cols, (uint64_t)n_experts * n_cols * 4}, [&](hipStream_t s) {
-    run_moe_route(s, xp, nw, eps, np, rp, bp, route_p, n_cols, n_experts, n_used, n_tokens);
+    run_moe_route(s, xp, nw, eps, np, rp, bp, route_p, n_cols, n_experts, n_used, n_tokens, nullptr, nullptr);
   });
 }
 
