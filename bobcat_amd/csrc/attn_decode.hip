@@ -168,11 +168,18 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
   // consecutive; runs of `group` items are dealt to the XCDs in turn, so
   // those heads run back to back on one XCD and share its L2 instead of
   // each fetching the split's keys and values from HBM.
-  const uint32_t L = blockIdx.x, xcd = L % kXcds, k = L / kXcds;
-  const uint32_t t = ((k / group) * kXcds + xcd) * group + k % group;
-  if (t >= a.n_heads * a.max_splits) return;
-  const uint32_t head = t % a.n_heads, split = t / a.n_heads, kvh = head / group;
-  const uint32_t qz = blockIdx.y;
+  // (The prefill form keeps the plain grid (head, split, query): its many
+  // queries fill the chip, and the padded mapping measured slower there.)
+  uint32_t head = blockIdx.x, split = blockIdx.y;
+  if constexpr (FUSED) {
+    const uint32_t L = blockIdx.x, xcd = L % kXcds, k = L / kXcds;
+    const uint32_t t = ((k / group) * kXcds + xcd) * group + k % group;
+    if (t >= a.n_heads * a.max_splits) return;
+    head = t % a.n_heads;
+    split = t / a.n_heads;
+  }
+  const uint32_t kvh = head / group;
+  const uint32_t qz = FUSED ? 0u : blockIdx.z;
   const uint32_t pos = FUSED ? *a.dpos : a.first_pos + qz;
   const uint32_t n_keys = pos + 1;
   const uint32_t n_splits = (n_keys + kps - 1) / kps;
@@ -377,9 +384,22 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
   }
   __syncthreads();
   if (!last_s) return;
-  const float o_all = combine_partials<kDecThreads>(a.partials + (uint64_t)slot * a.max_splits * stride, n_splits,
-                                                   stride, hd);
-  if (tid < hd) outp[tid] = o_all * gate;
+  const float *pp = a.partials + (uint64_t)slot * a.max_splits * stride;
+  if constexpr (FUSED) {
+    const float o_all = combine_partials<kDecThreads>(pp, n_splits, stride, hd);
+    if (tid < hd) outp[tid] = o_all * gate;
+  } else if (tid < hd) {
+    // A prefill query spans a few splits at most: one thread per element.
+    float M = -INFINITY;
+    for (uint32_t sp = 0; sp < n_splits; sp++) M = fmaxf(M, coherent_load(pp + sp * stride));
+    float L = 0.f, O = 0.f;
+    for (uint32_t sp = 0; sp < n_splits; sp++) {
+      const float w = expf(coherent_load(pp + sp * stride) - M);
+      L = fmaf(coherent_load(pp + sp * stride + 1), w, L);
+      O = fmaf(coherent_load(pp + sp * stride + 2 + tid), w, O);
+    }
+    outp[tid] = O / L * gate;
+  }
   if (tid == 0) coherent_store(&a.counters[slot], 0u);
 }
 
@@ -421,7 +441,7 @@ void run_attn_decode(hipStream_t s, const AttnDecodeArgs &a, bool kv_half) {
 }
 
 void run_attn_prefill(hipStream_t s, const AttnDecodeArgs &a, bool kv_half, uint32_t n_queries) {
-  dim3 grid(attn_decode_grid(a), n_queries);
+  dim3 grid(a.n_heads, a.max_splits, n_queries);
   if (kv_half)
     launch_attn_decode<true, false>(s, a, grid);
   else

@@ -163,12 +163,54 @@ __global__ __launch_bounds__(256) void k_gdn_step(GdnArgs a) {
   __syncthreads();
   part[wave][lane] = o;
   __syncthreads();
-  if (wave == 0) a.out[head * a.v_dim + col] = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+  o = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+  float *orow = a.out + (uint64_t)head * a.v_dim;
+  if (!a.norm_w) {
+    if (wave == 0) orow[col] = o;
+    return;
+  }
+  // The gated norm of the head (k_gdn_gated_norm's arithmetic and order):
+  // with several column blocks per head, each block hands its outputs over
+  // with device-scope stores and the last to arrive normalises the head.
+  if (wave != 0) return;
+  if (gridDim.x > 1) {
+    coherent_store(orow + col, o);
+    __builtin_amdgcn_s_waitcnt(0);
+    uint32_t prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(&a.counters[head], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (__shfl(prev, 0, 64) != gridDim.x - 1) return;
+  }
+  constexpr int kMaxPer = 4;  // v_dim ≤ 256
+  float e[kMaxPer];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMaxPer; j++) {
+    const uint32_t i = lane + 64 * j;
+    e[j] = i < a.v_dim ? (gridDim.x > 1 ? coherent_load(orow + i) : o) : 0.f;
+    if (i < a.v_dim) ss = fmaf(e[j], e[j], ss);
+  }
+  ss = wave_sum(ss);
+  const float scale = (float)(1.0 / sqrt((double)ss / (double)a.v_dim + (double)a.norm_eps));
+  const float *gz = a.gate_z + (uint64_t)head * a.v_dim;
+#pragma unroll
+  for (int j = 0; j < kMaxPer; j++) {
+    const uint32_t i = lane + 64 * j;
+    if (i < a.v_dim) {
+      const float gi = gz[i];
+      orow[i] = a.norm_w[i] * (e[j] * scale) * (gi / (1.0f + expf(-gi)));
+    }
+  }
+  if (gridDim.x > 1 && lane == 0) coherent_store(&a.counters[head], 0u);
+}
+
+bool gdn_step_supported(const GdnArgs &a) {
+  return a.n_tokens == 1 && a.v_dim % kGdnCols == 0 && a.v_dim % 64 == 0 && a.v_dim <= 256 &&
+         (a.k_dim == 64 || a.k_dim == 128);
 }
 
 bool run_gdn_recurrence(hipStream_t s, const GdnArgs &a) {
   if (a.v_dim % kGdnCols || a.n_tokens == 0) return false;
-  if (a.n_tokens == 1 && a.v_dim % 64 == 0 && (a.k_dim == 64 || a.k_dim == 128)) {
+  if (gdn_step_supported(a)) {
     const dim3 grid(a.v_dim / 64, a.n_v);
     if (a.k_dim == 64)
       k_gdn_step<64><<<grid, 256, 0, s>>>(a);

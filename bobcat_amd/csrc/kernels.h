@@ -129,7 +129,15 @@ struct GdnArgs {
   uint32_t n_k, n_v, k_dim, v_dim, n_tokens;
   float q_scale;
   bool raw_gates;
+  // Decode only (gdn_step_supported): with norm_w, out of each value head
+  // becomes norm_w ⊙ rmsnorm(out) ⊙ silu(gate_z[head]) in the same launch;
+  // counters holds n_v zeroed u32 (left zeroed).
+  const float *norm_w, *gate_z;
+  float norm_eps;
+  uint32_t *counters;
 };
+// Whether a one-token recurrence runs k_gdn_step (which fuses the gated norm).
+bool gdn_step_supported(const GdnArgs &a);
 // false when k_dim is not 64 or 128 (or v_dim not a multiple of the columns per workgroup).
 bool run_gdn_recurrence(hipStream_t s, const GdnArgs &a);
 void run_gdn_conv(hipStream_t s, const float *x, const float *taps, float *hist, float *y, uint32_t channels,

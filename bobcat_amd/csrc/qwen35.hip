@@ -61,6 +61,7 @@ struct bch_qwen35 : bch::Sequence {
         *attn = nullptr, *proj = nullptr, *conv_out = nullptr, *z = nullptr, *beta = nullptr, *alpha = nullptr,
         *delta_out = nullptr, *ffn = nullptr, *partials = nullptr;
   uint32_t *counters = nullptr;
+  uint32_t *gdn_counters = nullptr;  // [n_v], zeroed: the decode step's fused gated norm
 
   void *cache_layer(void *base, uint32_t ci) const {
     return static_cast<char *>(base) + (uint64_t)n_ctx * kv_dim * ci * (kv_half ? 2 : 4);
@@ -141,8 +142,15 @@ void bch_qwen35::record_step(hipStream_t st, bool greedy_input, bool trace) {
       g.n_tokens = 1;
       g.q_scale = 1.0f / sqrtf((float)k_dim);
       g.raw_gates = true;
+      const bool fused = gdn_step_supported(g);
+      if (fused) {
+        g.norm_w = L.ssm_norm;
+        g.gate_z = z;
+        g.norm_eps = norm_eps;
+        g.counters = gdn_counters;
+      }
       run_gdn_recurrence(st, g);
-      run_gdn_gated_norm(st, delta_out, L.ssm_norm, z, v_dim, n_v, norm_eps);
+      if (!fused) run_gdn_gated_norm(st, delta_out, L.ssm_norm, z, v_dim, n_v, norm_eps);
       run_matvec(st, L.out.format, L.out.data, n, value_dim, delta_out, hidden, nullptr, 0.f, true, cus);
     }
     run_matvec_swiglu(st, L.gate.format, L.gate.data, L.up.data, n_ff, n, hidden, ffn, L.ffn_norm, norm_eps, cus);
@@ -370,6 +378,7 @@ int bch_qwen35_new(bch_ctx *ctx, const bch_qwen35_model *md, uint32_t n_ctx, int
            (rc = m->alloc(matmul_split_bytes((uint32_t)rows, std::max({n, m->q_dim, m->value_dim, m->n_ff})),
                           &m->split)) || (rc = m->alloc_t(partial_floats + 4, &m->partials)) ||
            (rc = m->alloc_t((uint64_t)kQwenAttnQueryBatch * std::max(1u, m->n_heads), &m->counters)) ||
+           (rc = m->alloc_t(std::max(1u, m->n_v), &m->gdn_counters)) ||
            (rc = m->alloc_common()));
     if (rc) return cleanup(rc);
   }
