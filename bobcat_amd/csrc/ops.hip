@@ -279,8 +279,18 @@ __global__ __launch_bounds__(256) void k_embed_next(uint32_t format, const uint8
   __shared__ uint64_t best_s[4];
   __shared__ uint32_t token_s;
   const uint32_t p = *dpos;
+  // The first kP keys of each thread are loaded together (one round trip).
+  constexpr int kP = 4;
+  uint64_t keys[kP];
+#pragma unroll
+  for (int j = 0; j < kP; j++) {
+    const uint32_t i = threadIdx.x + 256 * j;
+    keys[j] = i < n_partials ? partials[i] : 0;
+  }
   uint64_t best = 0;
-  for (uint32_t i = threadIdx.x; i < n_partials; i += 256) best = max_key(best, partials[i]);
+#pragma unroll
+  for (int j = 0; j < kP; j++) best = max_key(best, keys[j]);
+  for (uint32_t i = threadIdx.x + 256 * kP; i < n_partials; i += 256) best = max_key(best, partials[i]);
   for (int off = 32; off > 0; off >>= 1) {
     const uint64_t o = ((uint64_t)__shfl_xor((uint32_t)(best >> 32), off, 64) << 32) |
                        (uint64_t)__shfl_xor((uint32_t)best, off, 64);
@@ -295,7 +305,20 @@ __global__ __launch_bounds__(256) void k_embed_next(uint32_t format, const uint8
   __syncthreads();
   const uint32_t tok = token_s;
   const uint8_t *row = W + (uint64_t)tok * row_bytes;
-  for (uint32_t i = threadIdx.x; i < n_embd; i += 256) out[i] = dequant_elem(format, row, i);
+  // The thread's first kE elements are read before any is stored.
+  constexpr int kE = 8;
+  float v[kE];
+#pragma unroll
+  for (int j = 0; j < kE; j++) {
+    const uint32_t i = threadIdx.x + 256 * j;
+    v[j] = i < n_embd ? dequant_elem(format, row, i) : 0.f;
+  }
+#pragma unroll
+  for (int j = 0; j < kE; j++) {
+    const uint32_t i = threadIdx.x + 256 * j;
+    if (i < n_embd) out[i] = v[j];
+  }
+  for (uint32_t i = threadIdx.x + 256 * kE; i < n_embd; i += 256) out[i] = dequant_elem(format, row, i);
   if (threadIdx.x == 0) {
     tokens[p + 1] = tok;
     *dpos = p + 1;  // every thread read p above, before this store
