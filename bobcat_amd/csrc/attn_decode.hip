@@ -5,12 +5,12 @@
 // 1094-1160; kernels norm.metal:43-108, attention.metal:25-120, 489-531).
 //
 // One workgroup per (query head, split); a split covers up to kKeys consecutive
-// positions (all of them for the contexts of a chat turn, so usually one
-// split).  One workgroup per query head rather than per KV head spreads the
+// positions (256 f16 positions of a 64-wide head, so a few splits for the
+// contexts of a chat turn).  One workgroup per query head rather than per KV head spreads the
 // arithmetic over four times the CUs; the heads of a group read the same
 // K/V rows, mostly from L2.  The position comes from the device counter, so
 // the launch replays in a graph; splits past the last position exit at once.
-// Each 1024-lane workgroup
+// Each 256-lane workgroup
 //   1. issues all its key and value loads at once: coalesced 16-byte chunks,
 //      a cache row shared by consecutive lanes, eight chunks of K and eight
 //      of V per lane held in registers;
@@ -36,7 +36,7 @@
 
 namespace bch {
 
-constexpr int kDecThreads = 1024;
+constexpr int kDecThreads = 256;  // 1024 ran 32K-context decode at 779 tok/s, 256 at 805
 constexpr int kChunks = 8;       // 16-byte chunks of K (and of V) per thread
 constexpr int kKeys = 1024;      // positions per split, at most
 constexpr int kHd = 256;         // head size, at most

@@ -150,8 +150,9 @@ def test_prefill_in_batches_matches_one_batch(hip):
 @pytest.mark.parametrize("kv_half", [False, True])
 def test_decode_across_attention_splits(hip, kv_half):
     """Decode steps at positions 1020-1027 cross the split boundary at 1024
-    (a split holds 512 f32 or 1024 f16 positions of a 64-wide head), so they
-    run with one, two and three splits and the cross-workgroup combine."""
+    (a split holds 128 f32 or 256 f16 positions of a 64-wide head), so the
+    number of splits, and with it the cross-workgroup combine, changes
+    between steps (8 to 9 f32 splits, 4 to 5 f16)."""
     w = Lfm2Weights(LFM2_TINY, seed=11)
     toks = prompt(LFM2_TINY, 1028, seed=6)
     gpu = Lfm2Hip(hip, w, n_ctx=1100, kv_half=kv_half)
@@ -168,11 +169,11 @@ def test_decode_across_attention_splits(hip, kv_half):
 
 @pytest.mark.parametrize("kv_half", [False, True])
 def test_long_context_decode(hip, kv_half):
-    """A driver sized for a long context (n_ctx 8192: 16 splits of 512 f32 or
-    8 of 1024 f16 positions, four query heads per KV head) launches a grid of
+    """A driver sized for a long context (n_ctx 8192: 64 splits of 128 f32 or
+    32 of 256 f16 positions, four query heads per KV head) launches a grid of
     that many splits, dealt to the XCDs by KV group; steps at positions
-    1020-1027 run with one to three live splits and the parallel split
-    combine, against the oracle, and against a driver sized for 1100."""
+    1020-1027 run with 4 to 9 live splits and the parallel split combine,
+    against the oracle, and against a driver sized for 1100."""
     w = Lfm2Weights(LFM2_TINY_F16, seed=12)
     toks = prompt(LFM2_TINY_F16, 1028, seed=9)
     big = Lfm2Hip(hip, w, n_ctx=8192, kv_half=kv_half)

@@ -251,7 +251,7 @@ def test_attention_gate_matches_float64(hip):
 def test_long_context_gated_decode(hip, kv_half):
     """Four query heads per KV head in a driver sized for 8192 positions: the
     gated decode kernel over a grid of many splits; steps at positions
-    1020-1027 (one to three live splits, combined in parallel) against the
+    1020-1027 (4 to 9 live splits, combined in parallel) against the
     oracle."""
     cfg = Qwen35Config("qwen3.5-group4", n_embd=256, n_ff=512, n_vocab=500, n_layers=4, n_heads=4,
                        n_kv_heads=1, head_dim=64, n_rot=32, n_k_heads=2, n_v_heads=4, k_head_dim=64,
