@@ -102,27 +102,32 @@ __global__ __launch_bounds__(kGdnCols * 64) void k_gdn_recurrence(GdnArgs a) {
   for (int i = 0; i < RPL; i++) S[(uint64_t)(r0 + i) * a.v_dim + col] = rows[i];
 }
 
-// One token (decode): lane c of the workgroup owns column c of a 64-column
-// block of one value head's state and wave w rows [w·KD/4, (w+1)·KD/4), so
-// each row of the block is one coalesced 256-byte access; the two dot
-// products over the rows are per-lane sums, then a sum over the four waves
-// in LDS (in wave order).  (The wave-per-column form above spreads a column
-// over 64 lanes, which touches a cache line per row and per column.)
-template <int KD>
-__global__ __launch_bounds__(256) void k_gdn_step(GdnArgs a) {
+// One token (decode): a workgroup per value head, CB blocks of 64 columns;
+// in block cb lane c owns column 64·cb + c of the head's state and wave w of
+// the block rows [w·KD/4, (w+1)·KD/4), so each row of a block is one
+// coalesced 256-byte access; the two dot products over the rows are per-lane
+// sums, then a sum over the block's four waves in LDS (in wave order).  (The
+// wave-per-column form above spreads a column over 64 lanes, which touches a
+// cache line per row and per column.)  With norm_w the head's output gets
+// the gated norm of k_gdn_gated_norm in the same workgroup.
+template <int KD, int CB>
+__global__ __launch_bounds__(256 * CB) void k_gdn_step(GdnArgs a) {
   constexpr int RW = KD / 4;  // rows per wave
-  __shared__ float qn[KD], kn[KD], part[4][64];
-  __shared__ float gate_s[2];
+  __shared__ float qn[KD], kn[KD], part[CB][4][64];
+  __shared__ float gate_s[2], ss_s[CB];
   const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const uint32_t head = blockIdx.y, col = blockIdx.x * 64 + lane;
+  const uint32_t cb = wave / 4, wq = wave % 4;
+  const uint32_t head = blockIdx.y, col = cb * 64 + lane;
   const uint32_t key_head = head % a.n_k, key_dim = a.n_k * a.k_dim;
   const float *tok = a.y;
   float *S = a.state + (uint64_t)head * KD * a.v_dim + col;
   // The state rows first: their loads overlap the norms below.
   float rows[RW];
 #pragma unroll
-  for (int i = 0; i < RW; i++) rows[i] = S[(uint64_t)(wave * RW + i) * a.v_dim];
+  for (int i = 0; i < RW; i++) rows[i] = S[(uint64_t)(wq * RW + i) * a.v_dim];
   const float v = tok[2 * key_dim + head * a.v_dim + col];
+  const float gz = a.norm_w ? a.gate_z[(uint64_t)head * a.v_dim + col] : 0.f;
+  const float nw = a.norm_w ? a.norm_w[col] : 0.f;
   // Waves 0 and 1 normalise the query and the key (qwen35.rs:464-470).
   if (wave < 2) {
     const float *src = tok + (wave == 0 ? 0u : key_dim) + key_head * KD;
@@ -147,60 +152,41 @@ __global__ __launch_bounds__(256) void k_gdn_step(GdnArgs a) {
 #pragma unroll
   for (int i = 0; i < RW; i++) {
     rows[i] *= decay;
-    rem = fmaf(rows[i], kn[wave * RW + i], rem);
+    rem = fmaf(rows[i], kn[wq * RW + i], rem);
   }
-  part[wave][lane] = rem;
+  part[cb][wq][lane] = rem;
   __syncthreads();
-  rem = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+  rem = (part[cb][0][lane] + part[cb][1][lane]) + (part[cb][2][lane] + part[cb][3][lane]);
   const float delta = (v - rem) * beta;
   float o = 0.f;
 #pragma unroll
   for (int i = 0; i < RW; i++) {
-    rows[i] = fmaf(kn[wave * RW + i], delta, rows[i]);
-    o = fmaf(rows[i], qn[wave * RW + i], o);
-    S[(uint64_t)(wave * RW + i) * a.v_dim] = rows[i];
+    rows[i] = fmaf(kn[wq * RW + i], delta, rows[i]);
+    o = fmaf(rows[i], qn[wq * RW + i], o);
+    S[(uint64_t)(wq * RW + i) * a.v_dim] = rows[i];
   }
   __syncthreads();
-  part[wave][lane] = o;
+  part[cb][wq][lane] = o;
   __syncthreads();
-  o = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+  o = (part[cb][0][lane] + part[cb][1][lane]) + (part[cb][2][lane] + part[cb][3][lane]);
   float *orow = a.out + (uint64_t)head * a.v_dim;
   if (!a.norm_w) {
-    if (wave == 0) orow[col] = o;
+    if (wq == 0) orow[col] = o;
     return;
   }
-  // The gated norm of the head (k_gdn_gated_norm's arithmetic and order):
-  // with several column blocks per head, each block hands its outputs over
-  // with device-scope stores and the last to arrive normalises the head.
-  if (wave != 0) return;
-  if (gridDim.x > 1) {
-    coherent_store(orow + col, o);
-    __builtin_amdgcn_s_waitcnt(0);
-    uint32_t prev = 0;
-    if (lane == 0) prev = __hip_atomic_fetch_add(&a.counters[head], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (__shfl(prev, 0, 64) != gridDim.x - 1) return;
+  // The gated norm of the head: RMS over its v_dim outputs (block sums in
+  // block order), then w ⊙ (o·scale) ⊙ silu(z).
+  if (wq == 0) {
+    const float ss = wave_sum(o * o);
+    if (lane == 0) ss_s[cb] = ss;
   }
-  constexpr int kMaxPer = 4;  // v_dim ≤ 256
-  float e[kMaxPer];
+  __syncthreads();
+  if (wq != 0) return;
   float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < kMaxPer; j++) {
-    const uint32_t i = lane + 64 * j;
-    e[j] = i < a.v_dim ? (gridDim.x > 1 ? coherent_load(orow + i) : o) : 0.f;
-    if (i < a.v_dim) ss = fmaf(e[j], e[j], ss);
-  }
-  ss = wave_sum(ss);
+  for (int b = 0; b < CB; b++) ss += ss_s[b];
   const float scale = (float)(1.0 / sqrt((double)ss / (double)a.v_dim + (double)a.norm_eps));
-  const float *gz = a.gate_z + (uint64_t)head * a.v_dim;
-#pragma unroll
-  for (int j = 0; j < kMaxPer; j++) {
-    const uint32_t i = lane + 64 * j;
-    if (i < a.v_dim) {
-      const float gi = gz[i];
-      orow[i] = a.norm_w[i] * (e[j] * scale) * (gi / (1.0f + expf(-gi)));
-    }
-  }
-  if (gridDim.x > 1 && lane == 0) coherent_store(&a.counters[head], 0u);
+  orow[col] = nw * (o * scale) * (gz / (1.0f + expf(-gz)));
 }
 
 bool gdn_step_supported(const GdnArgs &a) {
@@ -211,11 +197,15 @@ bool gdn_step_supported(const GdnArgs &a) {
 bool run_gdn_recurrence(hipStream_t s, const GdnArgs &a) {
   if (a.v_dim % kGdnCols || a.n_tokens == 0) return false;
   if (gdn_step_supported(a)) {
-    const dim3 grid(a.v_dim / 64, a.n_v);
-    if (a.k_dim == 64)
-      k_gdn_step<64><<<grid, 256, 0, s>>>(a);
-    else
-      k_gdn_step<128><<<grid, 256, 0, s>>>(a);
+    const uint32_t cb = a.v_dim / 64;
+    const dim3 grid(1, a.n_v);
+#define BCH_STEP(KD, CB) k_gdn_step<KD, CB><<<grid, 256 * CB, 0, s>>>(a)
+    if (a.k_dim == 64) {
+      if (cb == 1) BCH_STEP(64, 1); else if (cb == 2) BCH_STEP(64, 2); else if (cb == 3) BCH_STEP(64, 3); else BCH_STEP(64, 4);
+    } else {
+      if (cb == 1) BCH_STEP(128, 1); else if (cb == 2) BCH_STEP(128, 2); else if (cb == 3) BCH_STEP(128, 3); else BCH_STEP(128, 4);
+    }
+#undef BCH_STEP
     return true;
   }
   const dim3 grid(a.v_dim / kGdnCols, a.n_v);

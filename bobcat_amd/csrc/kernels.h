@@ -130,11 +130,9 @@ struct GdnArgs {
   float q_scale;
   bool raw_gates;
   // Decode only (gdn_step_supported): with norm_w, out of each value head
-  // becomes norm_w ⊙ rmsnorm(out) ⊙ silu(gate_z[head]) in the same launch;
-  // counters holds n_v zeroed u32 (left zeroed).
+  // becomes norm_w ⊙ rmsnorm(out) ⊙ silu(gate_z[head]) in the same launch.
   const float *norm_w, *gate_z;
   float norm_eps;
-  uint32_t *counters;
 };
 // Whether a one-token recurrence runs k_gdn_step (which fuses the gated norm).
 bool gdn_step_supported(const GdnArgs &a);

@@ -61,7 +61,6 @@ struct bch_qwen35 : bch::Sequence {
         *attn = nullptr, *proj = nullptr, *conv_out = nullptr, *z = nullptr, *beta = nullptr, *alpha = nullptr,
         *delta_out = nullptr, *ffn = nullptr, *partials = nullptr;
   uint32_t *counters = nullptr;
-  uint32_t *gdn_counters = nullptr;  // [n_v], zeroed: the decode step's fused gated norm
 
   void *cache_layer(void *base, uint32_t ci) const {
     return static_cast<char *>(base) + (uint64_t)n_ctx * kv_dim * ci * (kv_half ? 2 : 4);
@@ -147,7 +146,6 @@ void bch_qwen35::record_step(hipStream_t st, bool greedy_input, bool trace) {
         g.norm_w = L.ssm_norm;
         g.gate_z = z;
         g.norm_eps = norm_eps;
-        g.counters = gdn_counters;
       }
       run_gdn_recurrence(st, g);
       if (!fused) run_gdn_gated_norm(st, delta_out, L.ssm_norm, z, v_dim, n_v, norm_eps);
@@ -378,7 +376,6 @@ int bch_qwen35_new(bch_ctx *ctx, const bch_qwen35_model *md, uint32_t n_ctx, int
            (rc = m->alloc(matmul_split_bytes((uint32_t)rows, std::max({n, m->q_dim, m->value_dim, m->n_ff})),
                           &m->split)) || (rc = m->alloc_t(partial_floats + 4, &m->partials)) ||
            (rc = m->alloc_t((uint64_t)kQwenAttnQueryBatch * std::max(1u, m->n_heads), &m->counters)) ||
-           (rc = m->alloc_t(std::max(1u, m->n_v), &m->gdn_counters)) ||
            (rc = m->alloc_common()));
     if (rc) return cleanup(rc);
   }
