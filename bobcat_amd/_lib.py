@@ -57,6 +57,8 @@ class Matrix(C.Structure):
 
 
 _FP = C.POINTER(C.c_float)
+# bch_emit_fn: int (*)(uint32_t token, void *user)
+EMIT_FN = C.CFUNCTYPE(C.c_int, C.c_uint32, C.c_void_p)
 
 
 class Lfm2Layer(C.Structure):
@@ -162,6 +164,8 @@ PROTOTYPES = {
     "bch_qwen35_prefill": (_int, [_vp, C.POINTER(C.c_uint32), _u32, _FP, _FP, _FP, _FP]),
     "bch_qwen35_greedy_token": (_int, [_vp, C.POINTER(C.c_uint32)]),
     "bch_qwen35_generate": (_int, [_vp, C.POINTER(C.c_uint32), _u32]),
+    "bch_qwen35_generate_next": (_int, [_vp, C.POINTER(C.c_uint32), _u32]),
+    "bch_qwen35_generate_stream": (_int, [_vp, _u32, EMIT_FN, _vp, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
     "bch_qwen35_generate_sampled": (_int, [_vp, C.POINTER(C.c_uint32), _u32, C.POINTER(Sampling), _u64]),
     "bch_qwen35_checkpoint_bytes": (_u64, [_vp]),
     "bch_qwen35_checkpoint": (_int, [_vp, _vp, _u64]),
@@ -184,6 +188,8 @@ PROTOTYPES = {
     "bch_lfm2_prefill": (_int, [_vp, C.POINTER(_u32), _u32, _FP, _FP, _FP, _FP]),
     "bch_lfm2_greedy_token": (_int, [_vp, C.POINTER(_u32)]),
     "bch_lfm2_generate": (_int, [_vp, C.POINTER(_u32), _u32]),
+    "bch_lfm2_generate_next": (_int, [_vp, C.POINTER(_u32), _u32]),
+    "bch_lfm2_generate_stream": (_int, [_vp, _u32, EMIT_FN, _vp, C.POINTER(_u32), C.POINTER(_u32)]),
     "bch_lfm2_checkpoint_bytes": (_u64, [_vp]),
     "bch_lfm2_checkpoint": (_int, [_vp, _vp, _u64]),
     "bch_lfm2_restore": (_int, [_vp, _vp, _u64]),

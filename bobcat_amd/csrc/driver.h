@@ -72,6 +72,11 @@ struct Sequence {
   // Host staging of the small asynchronous uploads (they must outlive the call).
   uint32_t dpos_host = 0, token_host = 0;
   uint64_t rng_host = 0;
+  // generate_stream: the token each in-flight step selected, per slot, on
+  // the device and in pinned host memory, with the event of its copy.
+  static constexpr int kStreamInFlight = 3;  // GENERATE_IN_FLIGHT (lfm2_metal.rs:36)
+  uint32_t *stream_dev = nullptr, *stream_host = nullptr;
+  hipEvent_t stream_ev[kStreamInFlight] = {};
 
   // --- the model's part ------------------------------------------------
   // One decode step at position *dpos.  With greedy_input the step first
@@ -107,6 +112,8 @@ struct Sequence {
   int greedy_token(uint32_t *token);
   int generate(uint32_t *out, uint32_t n);
   int generate_sampled(uint32_t *out, uint32_t n, const bch_sampling *settings, uint64_t seed);
+  int generate_next(uint32_t *out, uint32_t n);
+  int generate_stream(uint32_t max_tokens, bch_emit_fn emit, void *user, uint32_t *gained, uint32_t *n_gained);
   uint64_t checkpoint_bytes() const;
   int checkpoint(void *blob, uint64_t bytes);
   int restore(const void *blob, uint64_t bytes);

@@ -68,6 +68,9 @@ Sequence::~Sequence() {
   if (sample_graph) hipGraphExecDestroy(sample_graph);
   if (ev0) hipEventDestroy(ev0);
   if (ev1) hipEventDestroy(ev1);
+  for (auto &e : stream_ev)
+    if (e) hipEventDestroy(e);
+  if (stream_host) hipHostFree(stream_host);
   for (void *p : allocations) hipFree(p);
 }
 
@@ -277,6 +280,32 @@ int Sequence::generate(uint32_t *out, uint32_t n) {
   return BCH_OK;
 }
 
+// Lfm2Metal::generate_next (lfm2_metal.rs:413-420): consume the current
+// greedy selection and n - 1 more, returning the selection after each of the
+// n steps; the last stays unconsumed (it is the next greedy_token).
+int Sequence::generate_next(uint32_t *out, uint32_t n) {
+  BCH_TRY(busy_check());
+  if (n_past == 0 || !have_logits) return fail(BCH_ERR_ARGUMENT, "generation needs a prompt first");
+  if (n > n_ctx - n_past) return fail(BCH_ERR_CONTEXT_FULL, "%u tokens exceed the %u free positions", n, n_ctx - n_past);
+  if (n == 0) return BCH_OK;
+  BCH_TRY(set_dpos(n_past - 1));
+  hipEventRecord(ev0, s);
+  run_argmax_partials(s, logits, n_vocab, argmax_partials, kArgmaxPartials);
+  if (use_graphs()) {
+    if (!gen_graph) BCH_TRY(capture(true, nullptr, &gen_graph));
+    for (uint32_t i = 0; i < n; i++) BCH_TRY(check_hip(hipGraphLaunch(gen_graph, s), "launch decode graph"));
+  } else {
+    for (uint32_t i = 0; i < n; i++) record_step(s, true, false);
+  }
+  // The selection after the last step goes one past the consumed tokens
+  // (the ring holds n_ctx + 2 entries).
+  run_argmax_pick(s, argmax_partials, kArgmaxPartials, tokens + n_past + n);
+  BCH_TRY(finish());
+  BCH_TRY(check_hip(hipMemcpy(out, tokens + n_past + 1, (uint64_t)n * 4, hipMemcpyDeviceToHost), "read tokens"));
+  n_past += n;
+  return BCH_OK;
+}
+
 int Sequence::generate_sampled(uint32_t *out, uint32_t n, const bch_sampling *settings, uint64_t seed) {
   BCH_TRY(busy_check());
   if (!settings) return fail(BCH_ERR_ARGUMENT, "no sampling settings");
@@ -320,6 +349,87 @@ int Sequence::generate_sampled(uint32_t *out, uint32_t n, const bch_sampling *se
   BCH_TRY(finish());
   BCH_TRY(check_hip(hipMemcpy(out, tokens + n_past, (uint64_t)n * 4, hipMemcpyDeviceToHost), "read tokens"));
   n_past += n;
+  return BCH_OK;
+}
+
+// Lfm2Metal::generate_stream (lfm2_metal.rs:425-560).  The first token is
+// the argmax of the current logits and needs no step; each step then runs
+// the token at the next position (the decode graph reduces the previous
+// logits' argmax keys into it) and a small kernel picks the token it
+// selects into a slot that is copied to pinned host memory.  Up to
+// kStreamInFlight steps are queued ahead of the host, so the GPU does not
+// wait for `emit`; once emit returns 0 no further step is queued, but the
+// queued ones still run.  `gained` (room for max_tokens) receives the tokens
+// the sequence consumed, n_gained of them: every emitted token but the last,
+// possibly followed by tokens selected after the last emitted one.
+int Sequence::generate_stream(uint32_t max_tokens, bch_emit_fn emit, void *user, uint32_t *gained,
+                              uint32_t *n_gained) {
+  BCH_TRY(busy_check());
+  if (!emit || !n_gained) return fail(BCH_ERR_ARGUMENT, "generate_stream needs an emit callback and n_gained");
+  *n_gained = 0;
+  if (max_tokens == 0) return BCH_OK;
+  if (!gained) return fail(BCH_ERR_ARGUMENT, "generate_stream needs room for the gained tokens");
+  uint32_t first;
+  BCH_TRY(greedy_token(&first));
+  if (!emit(first, user)) return BCH_OK;
+  const uint32_t steps = std::min(max_tokens - 1, n_ctx - n_past);
+  if (steps == 0) return BCH_OK;
+  if (!stream_dev) {
+    BCH_TRY(alloc_t(kStreamInFlight, &stream_dev));
+    BCH_TRY(check_hip(hipHostMalloc(reinterpret_cast<void **>(&stream_host), kStreamInFlight * 4, hipHostMallocDefault),
+                      "allocate pinned slots"));
+    for (auto &e : stream_ev) BCH_TRY(check_hip(hipEventCreateWithFlags(&e, hipEventDisableTiming), "create event"));
+  }
+  const uint32_t start = n_past;
+  BCH_TRY(set_dpos(n_past - 1));
+  hipEventRecord(ev0, s);
+  run_argmax_partials(s, logits, n_vocab, argmax_partials, kArgmaxPartials);
+  if (use_graphs() && !gen_graph) BCH_TRY(capture(true, nullptr, &gen_graph));
+  bool pending[kStreamInFlight] = {};
+  bool emitting = true;
+  uint32_t committed = 0;
+  int rc = BCH_OK;
+  auto drain = [&](int slot) -> int {
+    pending[slot] = false;
+    BCH_TRY(check_hip(hipEventSynchronize(stream_ev[slot]), "the GPU failed to run a decode step"));
+    if (emitting) emitting = emit(stream_host[slot], user) != 0;
+    return BCH_OK;
+  };
+  for (uint32_t step = 0; step < steps; step++) {
+    const int slot = (int)(step % kStreamInFlight);
+    if (pending[slot] && (rc = drain(slot)) != BCH_OK) break;
+    if (!emitting) break;
+    if (use_graphs()) {
+      if ((rc = check_hip(hipGraphLaunch(gen_graph, s), "launch decode graph")) != BCH_OK) break;
+    } else {
+      record_step(s, true, false);
+    }
+    run_argmax_pick(s, argmax_partials, kArgmaxPartials, stream_dev + slot);
+    if ((rc = check_hip(hipMemcpyAsync(stream_host + slot, stream_dev + slot, 4, hipMemcpyDeviceToHost, s),
+                        "read a selected token")) != BCH_OK)
+      break;
+    hipEventRecord(stream_ev[slot], s);
+    pending[slot] = true;
+    committed++;
+  }
+  // The steps still in flight finish in submission order, their tokens' order.
+  for (int k = 0; k < kStreamInFlight; k++) {
+    const int slot = (int)((committed + k) % kStreamInFlight);
+    if (pending[slot]) {
+      const int r = drain(slot);
+      if (rc == BCH_OK) rc = r;
+    }
+  }
+  hipEventRecord(ev1, s);
+  hipEventSynchronize(ev1);
+  float ms = 0.f;
+  hipEventElapsedTime(&ms, ev0, ev1);
+  last_gpu_seconds = ms * 1e-3;
+  n_past += committed;
+  BCH_TRY(rc);
+  BCH_TRY(check_hip(hipGetLastError(), "launch"));
+  BCH_TRY(check_hip(hipMemcpy(gained, tokens + start, (uint64_t)committed * 4, hipMemcpyDeviceToHost), "read tokens"));
+  *n_gained = committed;
   return BCH_OK;
 }
 

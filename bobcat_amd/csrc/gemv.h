@@ -16,6 +16,7 @@
 // LPR is a power of two up to 64 (several groups per wave) or a multiple
 // of 64 up to 256 (one group over several waves); rows wider than 256 units
 // use the older per-unit kernel in matvec.hip.
+#pragma once
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -438,7 +439,7 @@ __global__ __launch_bounds__(256) void k_gemv(P p, const float *__restrict__ x, 
 // --- host side -------------------------------------------------------------
 
 // Lanes per row for n_units units (0 when the x-stationary path does not apply).
-static int lanes_for(uint32_t n_units) {
+inline int lanes_for(uint32_t n_units) {
   if (n_units > 256) return 0;
   if (n_units <= 64) {
     int l = 4;
@@ -529,58 +530,6 @@ static bool gemv_any(hipStream_t s, uint32_t format, const P &p, const float *x,
                 : gemv_dispatch<F16, false>(s, p, x, nw, eps, n_items, n_cols, n_cus);
   return norm ? gemv_dispatch<F32, true>(s, p, x, nw, eps, n_items, n_cols, n_cus)
               : gemv_dispatch<F32, false>(s, p, x, nw, eps, n_items, n_cols, n_cus);
-}
-
-bool fast_matvec(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,
-                 float *y, const float *nw, float eps, bool accumulate, uint32_t n_cus) {
-  const uint64_t rb = bch_row_bytes(format, n_cols);
-  if (accumulate) return gemv_any(s, format, PlainItems<true>{W, rb, y}, x, nw, eps, n_rows, n_cols, n_cus);
-  return gemv_any(s, format, PlainItems<false>{W, rb, y}, x, nw, eps, n_rows, n_cols, n_cus);
-}
-
-bool fast_matvec_argmax(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols,
-                        const float *x, float *y, const float *nw, float eps, uint64_t *partials, uint32_t n_cus) {
-  const uint64_t rb = bch_row_bytes(format, n_cols);
-  return gemv_any(s, format, ArgmaxItems{W, rb, y, partials}, x, nw, eps, n_rows, n_cols, n_cus);
-}
-
-bool fast_matvec_experts_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const uint8_t *Wu, uint32_t n_ff,
-                                uint32_t n_cols, const uint32_t *ids, uint32_t n_used, const float *x, float *y,
-                                uint32_t n_cus) {
-  const uint64_t rb = bch_row_bytes(format, n_cols);
-  return gemv_any(s, format, ExpertSwigluItems{Wg, Wu, rb, ids, n_ff, y}, x, nullptr, 0.f, n_used * n_ff, n_cols,
-                  n_cus);
-}
-
-bool fast_matvec_gdn_in(hipStream_t s, uint32_t format, const uint8_t *Wqkv, const uint8_t *Wz, const uint8_t *Wb,
-                        const uint8_t *Wa, uint32_t conv_dim, uint32_t value_dim, uint32_t n_v, uint32_t n_cols,
-                        const float *x, const float *nw, float eps, const float *taps, float *hist, uint32_t ksize,
-                        float *conv_out, float *z, float *beta, float *alpha, uint32_t n_cus) {
-  const uint64_t rb = bch_row_bytes(format, n_cols);
-  return gemv_any(s, format,
-                  GdnInItems{Wqkv, Wz, Wb, Wa, conv_dim, value_dim, n_v, rb, taps, hist, ksize, conv_out, z, beta, alpha},
-                  x, nw, eps, conv_dim + value_dim + 2 * n_v, n_cols, n_cus);
-}
-
-bool fast_matvec_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const uint8_t *Wu, uint32_t n_rows,
-                        uint32_t n_cols, const float *x, float *y, const float *nw, float eps, uint32_t n_cus) {
-  const uint64_t rb = bch_row_bytes(format, n_cols);
-  return gemv_any(s, format, SwigluItems{Wg, Wu, rb, y}, x, nw, eps, n_rows, n_cols, n_cus);
-}
-
-bool fast_matvec3(hipStream_t s, uint32_t format, const uint8_t *W0, const uint8_t *W1, const uint8_t *W2, uint32_t r0,
-                  uint32_t r1, uint32_t r2, uint32_t n_cols, const float *x, float *y0, float *y1, float *y2,
-                  const float *nw, float eps, uint32_t n_cus) {
-  const uint64_t rb = bch_row_bytes(format, n_cols);
-  return gemv_any(s, format, ThreeItems{W0, W1, W2, r0, r1, rb, y0, y1, y2}, x, nw, eps, r0 + r1 + r2, n_cols,
-                  n_cus);
-}
-
-bool fast_matvec_conv(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_cols, const float *x,
-                      const float *nw, float eps, const float *taps, float *history, float *out, uint32_t n_embd,
-                      uint32_t ksize, uint32_t n_cus) {
-  const uint64_t rb = bch_row_bytes(format, n_cols);
-  return gemv_any(s, format, ConvItems{W, rb, n_embd, ksize, taps, history, out}, x, nw, eps, n_embd, n_cols, n_cus);
 }
 
 }  // namespace bch

@@ -169,6 +169,8 @@ void run_sample(hipStream_t s, const SampleArgs &a);
 // ops.hip
 // argmax of n logits as partials[0] (an argmax key), with partials[1..n_partials) zeroed.
 void run_argmax_partials(hipStream_t s, const float *logits, uint32_t n, uint64_t *partials, uint32_t n_partials);
+// The token the argmax keys select, stored at *out.
+void run_argmax_pick(hipStream_t s, const uint64_t *partials, uint32_t n_partials, uint32_t *out);
 // The next decode step's first launch: reduce the argmax partials to the
 // greedy token, store it at tokens[*dpos + 1], advance *dpos, and embed it.
 void run_embed_next(hipStream_t s, uint32_t format, const uint8_t *W, uint64_t row_bytes, uint32_t *tokens,

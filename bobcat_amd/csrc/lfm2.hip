@@ -503,6 +503,11 @@ int bch_lfm2_prefill(bch_lfm2 *m, const uint32_t *tokens, uint32_t n_tokens, flo
 
 int bch_lfm2_greedy_token(bch_lfm2 *m, uint32_t *token) { return m->greedy_token(token); }
 int bch_lfm2_generate(bch_lfm2 *m, uint32_t *out, uint32_t n) { return m->generate(out, n); }
+int bch_lfm2_generate_next(bch_lfm2 *m, uint32_t *out, uint32_t n) { return m->generate_next(out, n); }
+int bch_lfm2_generate_stream(bch_lfm2 *m, uint32_t max_tokens, bch_emit_fn emit, void *user, uint32_t *gained,
+                             uint32_t *n_gained) {
+  return m->generate_stream(max_tokens, emit, user, gained, n_gained);
+}
 int bch_lfm2_generate_sampled(bch_lfm2 *m, uint32_t *out, uint32_t n, const bch_sampling *settings, uint64_t seed) {
   return m->generate_sampled(out, n, settings, seed);
 }

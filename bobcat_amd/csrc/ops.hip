@@ -272,6 +272,25 @@ __global__ __launch_bounds__(1024) void k_argmax_partials(const float *__restric
   }
 }
 
+// The token the argmax keys select (generate_stream's per-step readback).
+__global__ __launch_bounds__(256) void k_argmax_pick(const uint64_t *__restrict__ partials, uint32_t n_partials,
+                                                     uint32_t *out) {
+  __shared__ uint64_t best_s[4];
+  uint64_t best = 0;
+  for (uint32_t i = threadIdx.x; i < n_partials; i += 256) best = max_key(best, partials[i]);
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint64_t o = ((uint64_t)__shfl_xor((uint32_t)(best >> 32), off, 64) << 32) |
+                       (uint64_t)__shfl_xor((uint32_t)best, off, 64);
+    best = max_key(best, o);
+  }
+  if (threadIdx.x % 64 == 0) best_s[threadIdx.x / 64] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; w++) best = max_key(best, best_s[w]);
+    *out = 0xffffffffu - (uint32_t)best;
+  }
+}
+
 __global__ __launch_bounds__(256) void k_embed_next(uint32_t format, const uint8_t *__restrict__ W, uint64_t row_bytes,
                                                     uint32_t *tokens, float *__restrict__ out, uint32_t n_embd,
                                                     uint32_t *dpos, const uint64_t *__restrict__ partials,
@@ -364,6 +383,10 @@ void run_embed(hipStream_t s, uint32_t format, const uint8_t *W, uint64_t row_by
 
 void run_argmax(hipStream_t s, const float *x, uint32_t *out, uint32_t n, uint32_t *dpos, bool advance) {
   k_argmax<<<1, 1024, 0, s>>>(x, out, n, dpos, advance ? 1 : 0);
+}
+
+void run_argmax_pick(hipStream_t s, const uint64_t *partials, uint32_t n_partials, uint32_t *out) {
+  k_argmax_pick<<<1, 256, 0, s>>>(partials, n_partials, out);
 }
 
 void run_argmax_partials(hipStream_t s, const float *logits, uint32_t n, uint64_t *partials, uint32_t n_partials) {

@@ -400,6 +400,11 @@ int bch_qwen35_prefill(bch_qwen35 *m, const uint32_t *tokens, uint32_t n_tokens,
 
 int bch_qwen35_greedy_token(bch_qwen35 *m, uint32_t *token) { return m->greedy_token(token); }
 int bch_qwen35_generate(bch_qwen35 *m, uint32_t *out, uint32_t n) { return m->generate(out, n); }
+int bch_qwen35_generate_next(bch_qwen35 *m, uint32_t *out, uint32_t n) { return m->generate_next(out, n); }
+int bch_qwen35_generate_stream(bch_qwen35 *m, uint32_t max_tokens, bch_emit_fn emit, void *user, uint32_t *gained,
+                               uint32_t *n_gained) {
+  return m->generate_stream(max_tokens, emit, user, gained, n_gained);
+}
 int bch_qwen35_generate_sampled(bch_qwen35 *m, uint32_t *out, uint32_t n, const bch_sampling *settings, uint64_t seed) {
   return m->generate_sampled(out, n, settings, seed);
 }

@@ -14,7 +14,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from ._lib import Lfm2Layer, Lfm2Model, Matrix, check, lib
+from ._lib import EMIT_FN, Lfm2Layer, Lfm2Model, Matrix, check, lib
 from .backend import Format, Hip
 from .synth import q4k_matrix
 
@@ -242,6 +242,35 @@ class SequenceHip:
         out = np.empty(n, np.uint32)
         check(self._fn("generate")(self.handle, out.ctypes.data_as(C.POINTER(C.c_uint32)), n))
         return out
+
+    def generate_next(self, n: int) -> np.ndarray:
+        """Lfm2Metal::generate_next: consume the current selection and n - 1 more; the
+        selection after each of the n steps."""
+        out = np.empty(max(n, 1), np.uint32)
+        check(self._fn("generate_next")(self.handle, out.ctypes.data_as(C.POINTER(C.c_uint32)), n))
+        return out[:n]
+
+    def generate_stream(self, max_tokens: int, emit) -> list:
+        """Lfm2Metal::generate_stream: emit(token) -> bool per selected token; returns the
+        tokens the sequence gained (every emitted token but the last, and possibly tokens
+        selected after it)."""
+        errors = []
+
+        def cb(token, _user):
+            try:
+                return 1 if emit(int(token)) else 0
+            except Exception as e:  # an exception in emit stops the stream and is re-raised
+                errors.append(e)
+                return 0
+
+        fn = EMIT_FN(cb)
+        gained = np.empty(max(max_tokens, 1), np.uint32)
+        n = C.c_uint32()
+        check(self._fn("generate_stream")(self.handle, max_tokens, fn, None,
+                                          gained.ctypes.data_as(C.POINTER(C.c_uint32)), C.byref(n)))
+        if errors:
+            raise errors[0]
+        return gained[:n.value].tolist()
 
     def generate_sampled(self, n: int, settings, seed: int) -> np.ndarray:
         """n tokens drawn by the GPU sampler (settings: a bch_sampling)."""

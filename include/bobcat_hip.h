@@ -290,6 +290,10 @@ typedef struct bch_sampling {
   float repeat_penalty; /* 1 turns the penalty off */
 } bch_sampling;
 
+/* The per-token callback of generate_stream (the `emit` closure of
+ * lfm2_metal.rs:425-431): return nonzero to keep generating. */
+typedef int (*bch_emit_fn)(uint32_t token, void *user);
+
 /* Sampler::sample (crates/bobcat-cli/src/sampler.rs:45-112) on the GPU:
  * penalty over the distinct tokens of the last 64 of `recent` (applied to
  * `logits` in place), top-k, top-p, min-p, temperature, then a draw from the
@@ -425,6 +429,22 @@ int bch_lfm2_greedy_token(bch_lfm2 *lfm2, uint32_t *token);
  * the argmax of the current logits; each step runs on the GPU with no host
  * round trip (a captured HIP graph replayed per token). */
 int bch_lfm2_generate(bch_lfm2 *lfm2, uint32_t *out, uint32_t n);
+/* Lfm2Metal::generate_next (lfm2_metal.rs:413-420): consume the current
+ * greedy selection (greedy_token) and n - 1 more, storing the selection after
+ * each of the n steps; the last stays unconsumed.  n = 0 changes nothing. */
+int bch_lfm2_generate_next(bch_lfm2 *lfm2, uint32_t *out, uint32_t n);
+/* Lfm2Metal::generate_stream (lfm2_metal.rs:425-560; called by enum Gpu,
+ * crates/bobcat-cli/src/backend.rs:128-137).  Emits the argmax of the
+ * current logits, then runs up to max_tokens - 1 greedy steps (bounded by the
+ * free context), passing each selected token to emit(token, user) as soon as
+ * its step finishes; up to three steps are queued ahead of the host.  When
+ * emit returns 0 no further step is queued (queued steps still run).
+ * `gained` (room for max_tokens) receives the tokens the sequence consumed,
+ * *n_gained of them: every emitted token but the last, possibly followed by
+ * tokens selected after the last emitted one — the Vec the reference
+ * returns. */
+int bch_lfm2_generate_stream(bch_lfm2 *lfm2, uint32_t max_tokens, bch_emit_fn emit, void *user, uint32_t *gained,
+                             uint32_t *n_gained);
 /* Lfm2Metal::checkpoint / restore (lfm2_metal.rs:250-288).  The blob holds
  * the reset count, n_past, the convolution history and the logits;
  * bch_lfm2_checkpoint_bytes gives its size. */
@@ -513,6 +533,12 @@ int bch_qwen35_prefill(bch_qwen35 *qwen, const uint32_t *tokens, uint32_t n_toke
                        float *trace_embedding, float *trace_layers, float *trace_final);
 int bch_qwen35_greedy_token(bch_qwen35 *qwen, uint32_t *token);
 int bch_qwen35_generate(bch_qwen35 *qwen, uint32_t *out, uint32_t n);
+/* Qwen35Metal's generate_next (same protocol as bch_lfm2_generate_next). */
+int bch_qwen35_generate_next(bch_qwen35 *qwen, uint32_t *out, uint32_t n);
+/* Qwen35Metal's generate_stream (qwen35_metal.rs, same protocol as
+ * bch_lfm2_generate_stream). */
+int bch_qwen35_generate_stream(bch_qwen35 *qwen, uint32_t max_tokens, bch_emit_fn emit, void *user,
+                               uint32_t *gained, uint32_t *n_gained);
 int bch_qwen35_generate_sampled(bch_qwen35 *qwen, uint32_t *out, uint32_t n, const bch_sampling *settings,
                                 uint64_t seed);
 /* Qwen35Metal::checkpoint / restore (qwen35::Checkpoint): resets, n_past,

@@ -282,3 +282,108 @@ def test_error_paths(hip):
         m.step(5)
     assert e.value.status == 15
     m.close()
+
+
+def test_restore_continues_against_oracle(hip, weights):
+    """lfm2_reference.rs:190-238: a restored state continues as the checkpointed
+    one did, straight into generation and through more prompt after later
+    tokens changed the histories, logits and cache positions; the continuation
+    is checked against the oracle stepping prefix + suffix."""
+    cfg = weights.cfg
+    prefix, suffix = prompt(cfg, 12, seed=21), prompt(cfg, 5, seed=22)
+    gpu = Lfm2Hip(hip, weights, n_ctx=64, kv_half=False)
+    gpu.prefill(prefix, logits=False)
+    ck = gpu.checkpoint()
+    first = gpu.generate(8)
+    gpu.prefill(prompt(cfg, 3, seed=23), logits=False)
+    gpu.restore(ck)
+    assert gpu.n_past == len(prefix)
+    assert np.array_equal(gpu.generate(8), first), "generation after a restore"
+    gpu.restore(ck)
+    got = gpu.prefill(suffix)
+    cpu = oracle.Lfm2State(weights, n_ctx=64)
+    for t in prefix + suffix:
+        want = cpu.step(t)
+    # The suffix runs as a prefill batch, whose GEMM rounds weights to f16.
+    assert rel(got, want) < HALF_TOLERANCE, rel(got, want)
+    # ...and the next steps after the restored prompt.
+    for t in prompt(cfg, 4, seed=24):
+        assert rel(gpu.step(t), cpu.step(t)) < HALF_TOLERANCE
+    gpu.reset()
+    with pytest.raises(BobcatError):
+        gpu.restore(ck)
+    gpu.close()
+
+
+def test_streaming_matches_generate(hip, weights):
+    """lfm2_reference.rs:240-292: the stream emits what generate picks, stops
+    where the caller stops it, and reports every token its steps ran,
+    including those past the stop and at the end of the context."""
+    cfg = weights.cfg
+    toks = prompt(cfg, 4, seed=25)
+    gpu = Lfm2Hip(hip, weights, n_ctx=20)
+    gpu.prefill(toks, logits=False)
+    ck = gpu.checkpoint()
+    expected = gpu.generate(16).tolist()
+    after = gpu.greedy_token()
+
+    gpu.restore(ck)
+    emitted = []
+    gained = gpu.generate_stream(17, lambda t: emitted.append(t) or True)
+    assert emitted[:16] == expected, "streamed tokens"
+    assert emitted[16] == after, "the selection after the last position"
+    assert gained == expected, "tokens a full stream ran"
+    assert gpu.n_past == 20
+
+    gpu.restore(ck)
+    emitted = []
+    gained = gpu.generate_stream(17, lambda t: emitted.append(t) or len(emitted) < 5)
+    assert emitted == expected[:5], "tokens up to the stop"
+    assert len(gained) >= 4, "a stopped stream ran the tokens before its last"
+    assert gained == expected[:len(gained)], "tokens a stopped stream ran"
+    assert gpu.n_past == 4 + len(gained)
+    # The sequence goes on from where the stream left it.
+    nxt = gpu.generate(20 - gpu.n_past).tolist()
+    assert gained + nxt == expected
+
+    gpu.restore(ck)
+    assert gpu.generate_stream(0, lambda t: True) == []
+    emitted = []
+    assert gpu.generate_stream(1, lambda t: emitted.append(t) or True) == []
+    assert emitted == expected[:1] and gpu.n_past == 4
+    assert gpu.generate_stream(5, lambda t: False) == []
+    assert gpu.n_past == 4
+    gpu.close()
+
+
+def test_greedy_selection_preserves_sequence_state(hip, weights):
+    """lfm2_reference.rs:296-350: greedy_token consumes nothing, and
+    generate_next continues from it in chunks as generate would."""
+    cfg = weights.cfg
+    toks = prompt(cfg, 4, seed=26)
+    for kv_half in (True, False):
+        gpu = Lfm2Hip(hip, weights, n_ctx=20, kv_half=kv_half)
+        with pytest.raises(BobcatError):
+            gpu.greedy_token()
+        gpu.prefill(toks, logits=False)
+        ck = gpu.checkpoint()
+        expected = gpu.generate(16).tolist()
+        nxt = gpu.greedy_token()
+        with pytest.raises(BobcatError):
+            gpu.generate(1)  # full context
+        assert gpu.greedy_token() == nxt
+        for chunk in (1, 3, 8):
+            gpu.restore(ck)
+            streamed = [gpu.greedy_token()]
+            assert gpu.greedy_token() == streamed[0], "repeated selection"
+            assert gpu.generate_next(0).size == 0
+            assert gpu.greedy_token() == streamed[0], "empty continuation"
+            while len(streamed) < 16:
+                streamed += gpu.generate_next(min(chunk, 16 - len(streamed))).tolist()
+            assert streamed == expected, "early selection changes generation"
+            assert gpu.generate(1).tolist() == [expected[15]]
+            assert gpu.greedy_token() == nxt, "selection advances the sequence"
+        gpu.reset()
+        with pytest.raises(BobcatError):
+            gpu.greedy_token()
+        gpu.close()

@@ -142,6 +142,54 @@ def test_checkpoint_restore_and_reset(hip, weights):
     fresh.close()
 
 
+def test_restore_continues_against_oracle(hip, weights):
+    """A restored DeltaNet/conv state continues through more prompt as the
+    oracle stepping prefix + suffix does (lfm2_reference.rs:190-238's check on
+    the Qwen3.5 driver)."""
+    cfg = weights.cfg
+    prefix, suffix = prompt(cfg, 10, seed=31), prompt(cfg, 6, seed=32)
+    m = Qwen35Hip(hip, weights, n_ctx=64, kv_half=False)
+    m.prefill(prefix, logits=False)
+    ck = m.checkpoint()
+    first = m.generate(6)
+    m.prefill(prompt(cfg, 3, seed=33), logits=False)
+    m.restore(ck)
+    assert np.array_equal(m.generate(6), first)
+    m.restore(ck)
+    got = m.prefill(suffix)
+    cpu = oracle.Qwen35State(weights, n_ctx=64)
+    for t in prefix + suffix:
+        want = cpu.step(t)
+    # The suffix runs as a prefill batch, whose GEMM rounds weights to f16.
+    assert rel(got, want) < HALF_TOLERANCE, rel(got, want)
+    for t in prompt(cfg, 3, seed=34):
+        assert rel(m.step(t), cpu.step(t)) < HALF_TOLERANCE
+    m.close()
+
+
+def test_streaming_matches_generate(hip, weights):
+    cfg = weights.cfg
+    m = Qwen35Hip(hip, weights, n_ctx=24)
+    m.prefill(prompt(cfg, 6, seed=35), logits=False)
+    ck = m.checkpoint()
+    expected = m.generate(18).tolist()
+    after = m.greedy_token()
+    m.restore(ck)
+    emitted = []
+    assert m.generate_stream(40, lambda t: emitted.append(t) or True) == expected
+    assert emitted == expected + [after]
+    m.restore(ck)
+    emitted = []
+    gained = m.generate_stream(40, lambda t: emitted.append(t) or len(emitted) < 7)
+    assert emitted == expected[:7] and gained == expected[:len(gained)] and len(gained) >= 6
+    m.restore(ck)
+    streamed = [m.greedy_token()]
+    while len(streamed) < 18:
+        streamed += m.generate_next(min(4, 18 - len(streamed))).tolist()
+    assert streamed == expected
+    m.close()
+
+
 # ---------------------------------------------------------------- kernels
 
 def run(hip, fn):
