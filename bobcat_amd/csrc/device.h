@@ -70,6 +70,23 @@ __device__ __forceinline__ float block_sum(float v, float *scratch) {
   return v;
 }
 
+// Maximum over a workgroup of `threads` threads (scratch as block_sum).
+template <int threads>
+__device__ __forceinline__ float block_max(float v, float *scratch) {
+  v = wave_max(v);
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  if (threads > kWave) {
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    float t = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < threads / kWave; w++) t = fmaxf(t, scratch[w]);
+    __syncthreads();
+    return t;
+  }
+  return v;
+}
+
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
   return __half2float(__ushort_as_half((unsigned short)bits16));
 }

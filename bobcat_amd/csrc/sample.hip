@@ -11,6 +11,11 @@
 //   4. the candidates are sorted by logit (bitonic sort in LDS), then
 //      softmax at temperature 1, the top-p prefix, the min-p floor, log and
 //      softmax at the temperature, and a draw walking the sorted candidates.
+// When more than kMaxCandidates candidates survive top-k (top_k = 0 keeps
+// the whole vocabulary), nothing is sorted: every step that walks the
+// sorted list (the top-p prefix and the draw) instead finds the rank where
+// the cumulative mass crosses its target by a radix descent over the logits'
+// ordered keys with mass histograms (sample_large below).
 // The draw comes from a wyrand generator whose 64-bit state lives in device
 // memory, so graph replays continue the stream.  Sums run as tree
 // reductions/scans instead of the reference's sequential loops, so draws
@@ -72,6 +77,187 @@ __device__ T block_scan(T v, T *lds16, T *total) {
   return base + incl - v;
 }
 
+// --- candidates beyond kMaxCandidates ------------------------------------
+//
+// Candidates are ranked by key descending, then id ascending (the sorted
+// order of the reference, whose unstable sort leaves equal logits in an
+// unspecified order).  A "cut" (key K, id I) keeps the candidates ranked at
+// or before (K, I): key > K, or key == K and id <= I.
+struct Cut {
+  uint32_t key, id;
+};
+
+__device__ __forceinline__ bool before_cut(uint32_t key, uint32_t id, Cut c) {
+  return key > c.key || (key == c.key && id <= c.id);
+}
+
+// The id of the j-th (0-based) element, in id order, among those with key K
+// that pass `pred`; 0xffffffff when there are fewer.  Each thread scans a
+// contiguous range, so the order is the id order.
+template <class Pred>
+__device__ uint32_t nth_tied_id(const float *logits, uint32_t n, uint32_t K, uint32_t j, Pred pred, uint32_t *u16,
+                                uint32_t *result) {
+  const uint32_t per = (n + kSampleThreads - 1) / kSampleThreads;
+  const uint32_t lo = threadIdx.x * per, hi = min(n, lo + per);
+  uint32_t cnt = 0;
+  for (uint32_t i = lo; i < hi; i++) cnt += ord_key(logits[i]) == K && pred(i);
+  if (threadIdx.x == 0) *result = 0xffffffffu;
+  uint32_t total;
+  const uint32_t base = block_scan<uint32_t>(cnt, u16, &total);
+  if (j >= base && j < base + cnt) {
+    uint32_t seen = base;
+    for (uint32_t i = lo; i < hi; i++)
+      if (ord_key(logits[i]) == K && pred(i)) {
+        if (seen == j) {
+          *result = i;
+          break;
+        }
+        seen++;
+      }
+  }
+  __syncthreads();
+  const uint32_t r = *result;
+  __syncthreads();
+  return r;
+}
+
+// A float from its ordered key (the inverse of ord_key).
+__device__ __forceinline__ float ord_value(uint32_t key) {
+  return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
+}
+
+// The first rank whose cumulative weight reaches `target` (>= when
+// `inclusive`, > otherwise), among the elements passing `pred`, as a cut.
+// When the total weight never gets there (rounding), the cut is the last
+// such element and `found` is false.  A radix descent over the 32-bit keys,
+// 8 bits a pass, with weight histograms; the elements tied at the final key
+// weigh the same, so the id of the crossing one follows by division.
+template <class Pred, class Weight>
+__device__ Cut mass_cut(const float *logits, uint32_t n, float target, bool inclusive, Pred pred, Weight weight,
+                        float *bins, uint32_t *u16, uint32_t *sel_s, float *above_s, bool *found) {
+  constexpr uint32_t kNone = 0xffffffffu;
+  const uint32_t tid = threadIdx.x;
+  uint32_t prefix = 0;
+  float above = 0.f;  // weight of the keys above the current prefix
+  bool reached = true;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (uint32_t i = tid; i < 256; i += kSampleThreads) bins[i] = 0.f;
+    __syncthreads();
+    const uint32_t hi_mask = shift == 24 ? 0u : ~0u << (shift + 8);
+    for (uint32_t i = tid; i < n; i += kSampleThreads) {
+      const float v = logits[i];
+      const uint32_t key = ord_key(v);
+      if ((key & hi_mask) == (prefix & hi_mask) && pred(i)) atomicAdd(&bins[(key >> shift) & 255u], weight(v));
+    }
+    __syncthreads();
+    if (tid == 0) {
+      float acc = above;
+      uint32_t bin = kNone, last = kNone;
+      for (int b = 255; b >= 0; b--) {
+        if (bins[b] <= 0.f) continue;
+        const float next = acc + bins[b];
+        if (inclusive ? next >= target : next > target) {
+          bin = (uint32_t)b;
+          break;
+        }
+        acc = next;
+        last = (uint32_t)b;
+      }
+      if (bin == kNone) {
+        // Not reached: descend into the last bin with weight, if any.
+        sel_s[0] = last;
+        sel_s[1] = 0;
+        *above_s = last == kNone ? acc : acc - bins[last];
+      } else {
+        sel_s[0] = bin;
+        sel_s[1] = 1;
+        *above_s = acc;
+      }
+    }
+    __syncthreads();
+    const uint32_t bin = sel_s[0];
+    reached = reached && sel_s[1] != 0;
+    above = *above_s;
+    __syncthreads();
+    if (bin == kNone) {  // nothing passes the predicate
+      *found = false;
+      return Cut{0u, 0u};
+    }
+    prefix |= bin << shift;
+  }
+  uint32_t c = 0;
+  for (uint32_t i = tid; i < n; i += kSampleThreads) c += ord_key(logits[i]) == prefix && pred(i);
+  uint32_t n_tied;
+  block_scan<uint32_t>(c, u16, &n_tied);
+  uint32_t j = n_tied - 1;
+  if (reached) {
+    const float wk = weight(ord_value(prefix));
+    const float need = wk > 0.f ? (target - above) / wk : 0.f;  // ties before the crossing, as a real
+    float f = inclusive ? ceilf(need) - 1.f : floorf(need);
+    if (!(f >= 0.f)) f = 0.f;
+    if (f < (float)j) j = (uint32_t)f;
+  }
+  *found = reached;
+  const uint32_t id = nth_tied_id(logits, n, prefix, j, pred, u16, sel_s);
+  return Cut{prefix, id};
+}
+
+__device__ void sample_large(const SampleArgs &a, uint32_t k, float *bins, uint32_t *u16, float *f16s, uint32_t *sel_s,
+                             float *above_s, uint32_t *token_s) {
+  const uint32_t tid = threadIdx.x, n = a.n;
+  const float *logits = a.logits;
+  // 1. The top-k set as a cut (top_k = 0 or >= n keeps everything).
+  Cut topk{0u, 0xffffffffu};
+  if (k < n) {
+    bool f;
+    topk = mass_cut(
+        logits, n, (float)k, true, [](uint32_t) { return true; }, [](float) { return 1.0f; }, bins, u16, sel_s,
+        above_s, &f);
+  }
+  auto in_topk = [&](uint32_t i) { return before_cut(ord_key(logits[i]), i, topk); };
+  // 2. Softmax at temperature 1 over the candidates.
+  float mx = -INFINITY;
+  for (uint32_t i = tid; i < n; i += kSampleThreads)
+    if (in_topk(i)) mx = fmaxf(mx, logits[i]);
+  mx = block_max<kSampleThreads>(mx, f16s);
+  float part = 0.f;
+  for (uint32_t i = tid; i < n; i += kSampleThreads)
+    if (in_topk(i)) part += expf(logits[i] - mx);
+  const float S = block_sum<kSampleThreads>(part, f16s);
+  auto prob = [=](float v) { return expf(v - mx) / S; };
+  // 3. Top-p: the shortest prefix reaching top_p (all candidates when none does).
+  bool reached = false;
+  Cut topp = mass_cut(logits, n, a.top_p, true, in_topk, prob, bins, u16, sel_s, above_s, &reached);
+  if (!reached) topp = topk;
+  // 4. Min-p: drop candidates below the first one's probability times min_p.
+  const float floor_p = (1.0f / S) * a.min_p;
+  auto kept = [&](uint32_t i) {
+    const float v = logits[i];
+    return in_topk(i) && before_cut(ord_key(v), i, topp) && prob(v) >= floor_p;
+  };
+  // 5. Temperature over the kept log-probabilities, then the draw.
+  const float l0 = logf(1.0f / S);
+  const float T = a.temperature;
+  auto tq = [=](float v) { return expf((logf(expf(v - mx) / S) - l0) / T); };
+  float qp = 0.f;
+  for (uint32_t i = tid; i < n; i += kSampleThreads)
+    if (kept(i)) qp += tq(logits[i]);
+  const float Sq = block_sum<kSampleThreads>(qp, f16s);
+  __shared__ float draw_s;
+  if (tid == 0) {
+    uint64_t st = *a.rng;
+    draw_s = wyrand_f32(&st);
+    *a.rng = st;
+  }
+  __syncthreads();
+  const float u = draw_s;
+  bool got = false;
+  const Cut c = mass_cut(logits, n, u, false, kept, [=](float v) { return tq(v) / Sq; }, bins, u16, sel_s,
+                         above_s, &got);
+  if (tid == 0) *token_s = c.id;
+  __syncthreads();
+}
+
 __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   __shared__ float cval[kMaxCandidates];
   __shared__ uint32_t cidx[kMaxCandidates];
@@ -80,6 +266,9 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   __shared__ float f16s[16];
   __shared__ uint64_t k16[16];
   __shared__ uint32_t prefix_s, remain_s, keep_s, token_s;
+  __shared__ float large_bins[256];
+  __shared__ uint32_t large_sel[2];
+  __shared__ float large_above;
   const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
   const uint32_t n = a.n;
   float *logits = a.logits;
@@ -124,6 +313,10 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   } else {
     // 3. Candidates: the kc largest logits (radix select of the kc-th).
     const uint32_t k = (a.top_k > 0 && a.top_k < n) ? a.top_k : n;
+    if (k > kMaxCandidates) {
+      sample_large(a, k, large_bins, u16, f16s, large_sel, &large_above, &token_s);
+      goto store;
+    }
     const uint32_t kc = k < kMaxCandidates ? k : kMaxCandidates;
     uint32_t prefix = 0, need = kc;  // the threshold's key bits so far, and how many of its bucket to take
     if (kc < n) {
@@ -278,6 +471,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     __syncthreads();
   }
 
+store:
   if (tid == 0) {
     const uint32_t tok = token_s;
     if (a.dpos) {
