@@ -154,6 +154,9 @@ PROTOTYPES = {
     "bch_gdn_conv": (_int, [_vp, View, View, View, View, _u32, _u32, _u32]),
     "bch_gdn_gates": (_int, [_vp, View, View, View, View, _u32, _u32]),
     "bch_gdn_recurrence": (_int, [_vp, View, View, View, View, View, C.POINTER(DeltaShape), _u32, C.c_float]),
+    "bch_gdn_chunk_scratch_floats": (_u64, [C.POINTER(DeltaShape), _u32]),
+    "bch_gdn_recurrence_chunked": (_int, [_vp, View, View, View, View, View, C.POINTER(DeltaShape), _u32, C.c_float,
+                                          View]),
     "bch_gdn_gated_norm": (_int, [_vp, View, View, View, _u32, _u32, C.c_float]),
     "bch_attention_gate": (_int, [_vp, View, View, _u32, _u32, _u32]),
     "bch_qwen35_new": (_int, [_vp, C.POINTER(Qwen35Model), _u32, _int, C.POINTER(_vp)]),

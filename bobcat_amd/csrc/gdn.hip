@@ -218,6 +218,283 @@ bool run_gdn_recurrence(hipStream_t s, const GdnArgs &a) {
   return true;
 }
 
+// --- chunked prefill ------------------------------------------------------
+//
+// The gated delta rule over a chunk of C tokens from the state S0 at its
+// start, with gamma_t the product of the decays up to token t (from the
+// chunk's start), reads (the WY/UT form of the delta rule):
+//   A[t][s] = beta_t (gamma_t / gamma_s) k_t.k_s          s < t
+//   (I + A) D = diag(beta) (V - diag(gamma) K S0)         D = the chunk's deltas
+//   D = U - W S0,  U = (I + A)^-1 diag(beta) V,  W = (I + A)^-1 diag(beta gamma) K
+//   O = diag(gamma) Q S0 + P D,  P[t][s] = (gamma_t / gamma_s) q_t.k_s   s <= t
+//   S_C = gamma_C S0 + Kt^T D,   Kt[s] = (gamma_C / gamma_s) k_s
+// which unrolls the per-token recurrence of qwen35.rs:475-511 exactly (in
+// exact arithmetic).  k_gdn_chunk_prep computes W, U, P, diag(gamma) Q, Kt
+// and gamma_C for every (chunk, head) at once: U and W by forward
+// substitution, one thread per column; the decays as differences of a
+// float64 running sum of log-decays.  k_gdn_chunk_scan then carries the
+// state through the chunks: each column of S evolves on its own, so a
+// workgroup owns NC columns of one head and walks the chunks in order.
+
+constexpr int kGdnC = 64;  // tokens per chunk
+
+__host__ __device__ constexpr uint64_t gdn_chunk_floats(uint32_t kd, uint32_t vd) {
+  return 64ull * (3ull * kd + vd) + 64ull * 64ull + 64ull;
+}
+
+template <int KD>
+__global__ __launch_bounds__(256) void k_gdn_chunk_prep(GdnArgs a, float *__restrict__ scratch, uint32_t n_chunks) {
+  constexpr int C = kGdnC, KP = KD + 1, R = KD / 64;
+  __shared__ float qs[C][KP], ks[C][KP], am[C][C + 1];
+  __shared__ float bs[C], wgam[C];
+  __shared__ double lg[C];
+  const uint32_t tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+  const uint32_t chunk = blockIdx.x, head = blockIdx.y;
+  const uint32_t vd = a.v_dim;
+  const uint32_t t0 = chunk * C, L = min((uint32_t)C, a.n_tokens - t0);
+  const uint32_t key_head = head % a.n_k, key_dim = a.n_k * KD, conv_dim = 2 * key_dim + a.n_v * vd;
+  float *base = scratch + ((uint64_t)head * n_chunks + chunk) * gdn_chunk_floats(KD, vd);
+  float *Wg = base, *Ug = Wg + C * KD, *Qg = Ug + (uint64_t)C * vd, *Kt = Qg + C * KD, *Pg = Kt + C * KD;
+  float *gC = Pg + C * C;
+  // The l2-normalised query (times q_scale) and key of each token
+  // (qwen35.rs:464-470); rows past the chunk's end are zero.
+  for (uint32_t j = wave; j < (uint32_t)C; j += 4) {
+    float q[R], k[R], sq = 0.f, sk = 0.f;
+    if (j < L) {
+      const float *tok = a.y + (uint64_t)(t0 + j) * conv_dim;
+#pragma unroll
+      for (int i = 0; i < R; i++) {
+        q[i] = tok[key_head * KD + lane * R + i];
+        k[i] = tok[key_dim + key_head * KD + lane * R + i];
+      }
+#pragma unroll
+      for (int i = 0; i < R; i++) {
+        sq = fmaf(q[i], q[i], sq);
+        sk = fmaf(k[i], k[i], sk);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < R; i++) q[i] = k[i] = 0.f;
+    }
+    sq = wave_sum(sq);
+    sk = wave_sum(sk);
+    const float fq = a.q_scale / sqrtf(sq + 1e-6f), fk = 1.0f / sqrtf(sk + 1e-6f);
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+      qs[j][lane * R + i] = q[i] * fq;
+      ks[j][lane * R + i] = k[i] * fk;
+    }
+  }
+  // Gates: beta, and the running sum of the log-decays in float64.
+  if (wave == 0) {
+    float b = 0.f, l = 0.f;
+    if (lane < L) {
+      const float rb = a.beta[(uint64_t)(t0 + lane) * a.n_v + head];
+      const float rd = a.alpha[(uint64_t)(t0 + lane) * a.n_v + head];
+      b = a.raw_gates ? sigmoid_f(rb) : rb;
+      l = a.raw_gates ? a.a[head] * softplus_f(rd + a.dt_bias[head]) : logf(rd);
+    }
+    double v = l;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const double o = __shfl_up(v, off, 64);
+      if (lane >= (uint32_t)off) v += o;
+    }
+    bs[lane] = b;
+    lg[lane] = v;
+    wgam[lane] = lane < L ? b * expf((float)v) : 0.f;
+  }
+  __syncthreads();
+  const double lC = lg[L - 1];
+  // A (strictly lower) and P (lower with the diagonal): 4x4 blocks per thread.
+  {
+    const uint32_t ti = tid / 16, si = tid % 16;
+    float kk[4][4] = {}, qk[4][4] = {};
+    for (int r = 0; r < KD; r++) {
+      float kt[4], qt[4], kv[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        kt[i] = ks[4 * ti + i][r];
+        qt[i] = qs[4 * ti + i][r];
+        kv[i] = ks[4 * si + i][r];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          kk[i][j] = fmaf(kt[i], kv[j], kk[i][j]);
+          qk[i][j] = fmaf(qt[i], kv[j], qk[i][j]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t t = 4 * ti + i, u = 4 * si + j;
+        const float dec = (u <= t && t < L) ? expf((float)(lg[t] - lg[u])) : 0.f;
+        am[t][u] = u < t ? bs[t] * dec * kk[i][j] : 0.f;
+        Pg[t * C + u] = dec * qk[i][j];
+      }
+  }
+  // diag(gamma) Q and Kt, and gamma_C.
+  for (uint32_t e = tid; e < (uint32_t)(C * KD); e += 256) {
+    const uint32_t t = e / KD, r = e % KD;
+    const float gt = t < L ? expf((float)lg[t]) : 0.f;
+    const float kc = t < L ? expf((float)(lC - lg[t])) : 0.f;
+    Qg[e] = gt * qs[t][r];
+    Kt[e] = kc * ks[t][r];
+  }
+  if (tid == 0) gC[0] = expf((float)lC);
+  __syncthreads();
+  // W and U by forward substitution, x_t = rhs_t - sum_{s<t} A[t][s] x_s,
+  // one thread per column of [W | U].
+  for (uint32_t col = tid; col < KD + vd; col += 256) {
+    float x[C];
+    if (col < KD) {
+#pragma unroll
+      for (int t = 0; t < C; t++) x[t] = wgam[t] * ks[t][col];
+    } else {
+      const float *v = a.y + (uint64_t)t0 * conv_dim + 2 * key_dim + head * vd + (col - KD);
+#pragma unroll
+      for (int t = 0; t < C; t++) x[t] = (uint32_t)t < L ? bs[t] * v[(uint64_t)t * conv_dim] : 0.f;
+    }
+#pragma unroll
+    for (int t = 1; t < C; t++) {
+      float acc = x[t];
+#pragma unroll
+      for (int u = 0; u < t; u++) acc = fmaf(-am[t][u], x[u], acc);
+      x[t] = acc;
+    }
+    if (col < KD) {
+#pragma unroll
+      for (int t = 0; t < C; t++) Wg[t * KD + col] = x[t];
+    } else {
+#pragma unroll
+      for (int t = 0; t < C; t++) Ug[(uint64_t)t * vd + (col - KD)] = x[t];
+    }
+  }
+}
+
+template <int KD, int NC>
+__global__ __launch_bounds__(256) void k_gdn_chunk_scan(GdnArgs a, const float *__restrict__ scratch,
+                                                        uint32_t n_chunks) {
+  constexpr int C = kGdnC, KP = KD + 4;
+  static_assert(NC == 8, "the thread layout below assumes 8 columns");
+  __shared__ __align__(16) float w_s[C][KP], q_s[C][KP], k_s[C][KP];
+  __shared__ float p_s[C][C + 1], s_s[KD][NC], d_s[C][NC];
+  const uint32_t tid = threadIdx.x, vd = a.v_dim;
+  // Blocks are numbered so that the column blocks of one head run on one
+  // XCD (workgroup i goes to XCD i % 8) and share its L2.
+  const uint32_t n_cb = vd / NC, total = n_cb * a.n_v;
+  uint32_t v = blockIdx.x;
+  if (total % 8 == 0) v = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;
+  const uint32_t head = v / n_cb, col0 = (v % n_cb) * NC;
+  float *S = a.state + (uint64_t)head * KD * vd + col0;
+  // This thread's state entries: row r = tid / 2, columns c0 .. c0 + 3.
+  const uint32_t sr = tid / 2, sc = (tid % 2) * 4;
+  float srow[4];
+  if (sr < (uint32_t)KD) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) srow[j] = s_s[sr][sc + j] = S[(uint64_t)sr * vd + sc + j];
+  }
+  // Delta / output entries: token t = tid / 4, columns dc, dc + 1.
+  const uint32_t dt = tid / 4, dc = (tid % 4) * 2;
+  for (uint32_t c = 0; c < n_chunks; c++) {
+    const float *base = scratch + ((uint64_t)head * n_chunks + c) * gdn_chunk_floats(KD, vd);
+    const float *Wg = base, *Ug = Wg + C * KD, *Qg = Ug + (uint64_t)C * vd, *Kt = Qg + C * KD, *Pg = Kt + C * KD;
+    const float gC = Pg[C * C];
+    const uint32_t t0 = c * C, L = min((uint32_t)C, a.n_tokens - t0);
+    // Stage W, diag(gamma) Q, Kt and P.
+    for (uint32_t e = tid; e < (uint32_t)(C * KD / 4); e += 256) {
+      const uint32_t t = e / (KD / 4), r4 = e % (KD / 4);
+      const float4 w = reinterpret_cast<const float4 *>(Wg)[e];
+      const float4 q = reinterpret_cast<const float4 *>(Qg)[e];
+      const float4 k = reinterpret_cast<const float4 *>(Kt)[e];
+      *reinterpret_cast<float4 *>(&w_s[t][4 * r4]) = w;
+      *reinterpret_cast<float4 *>(&q_s[t][4 * r4]) = q;
+      *reinterpret_cast<float4 *>(&k_s[t][4 * r4]) = k;
+    }
+    for (uint32_t e = tid; e < (uint32_t)(C * C); e += 256) p_s[e / C][e % C] = Pg[e];
+    const float u0 = Ug[(uint64_t)dt * vd + col0 + dc], u1 = Ug[(uint64_t)dt * vd + col0 + dc + 1];
+    __syncthreads();
+    // D = U - W S0.
+    float d0 = u0, d1 = u1;
+    for (int r = 0; r < KD; r++) {
+      const float w = w_s[dt][r];
+      d0 = fmaf(-w, s_s[r][dc], d0);
+      d1 = fmaf(-w, s_s[r][dc + 1], d1);
+    }
+    d_s[dt][dc] = d0;
+    d_s[dt][dc + 1] = d1;
+    __syncthreads();
+    // O = diag(gamma) Q S0 + P D.
+    float o0 = 0.f, o1 = 0.f;
+    for (int r = 0; r < KD; r++) {
+      const float q = q_s[dt][r];
+      o0 = fmaf(q, s_s[r][dc], o0);
+      o1 = fmaf(q, s_s[r][dc + 1], o1);
+    }
+    for (uint32_t u = 0; u <= dt; u++) {
+      const float pv = p_s[dt][u];
+      o0 = fmaf(pv, d_s[u][dc], o0);
+      o1 = fmaf(pv, d_s[u][dc + 1], o1);
+    }
+    if (dt < L) {
+      float *orow = a.out + (uint64_t)(t0 + dt) * a.n_v * vd + head * vd + col0;
+      orow[dc] = o0;
+      orow[dc + 1] = o1;
+    }
+    // S_C = gamma_C S0 + Kt^T D.
+    if (sr < (uint32_t)KD) {
+      float acc[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[j] = gC * srow[j];
+      for (int u = 0; u < C; u++) {
+        const float kv = k_s[u][sr];
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[j] = fmaf(kv, d_s[u][sc + j], acc[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) srow[j] = acc[j];
+    }
+    __syncthreads();  // every read of s_s and of the staged chunk is done
+    if (sr < (uint32_t)KD) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) s_s[sr][sc + j] = srow[j];
+    }
+  }
+  if (sr < (uint32_t)KD) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) S[(uint64_t)sr * vd + sc + j] = srow[j];
+  }
+}
+
+constexpr int kGdnScanCols = 8;
+
+bool gdn_chunked_supported(const GdnArgs &a) {
+  return (a.k_dim == 64 || a.k_dim == 128) && a.v_dim % kGdnScanCols == 0 && a.v_dim <= 256 && a.n_tokens > 0;
+}
+
+uint64_t gdn_chunk_scratch_floats(uint32_t n_v, uint32_t k_dim, uint32_t v_dim, uint32_t n_tokens) {
+  const uint64_t chunks = (n_tokens + kGdnC - 1) / kGdnC;
+  return (uint64_t)n_v * chunks * gdn_chunk_floats(k_dim, v_dim);
+}
+
+bool run_gdn_chunked(hipStream_t s, const GdnArgs &a, float *scratch) {
+  if (!gdn_chunked_supported(a)) return false;
+  const uint32_t n_chunks = (a.n_tokens + kGdnC - 1) / kGdnC;
+  const dim3 prep(n_chunks, a.n_v);
+  const uint32_t scan = a.n_v * (a.v_dim / kGdnScanCols);
+  if (a.k_dim == 64) {
+    k_gdn_chunk_prep<64><<<prep, 256, 0, s>>>(a, scratch, n_chunks);
+    k_gdn_chunk_scan<64, kGdnScanCols><<<scan, 256, 0, s>>>(a, scratch, n_chunks);
+  } else {
+    k_gdn_chunk_prep<128><<<prep, 256, 0, s>>>(a, scratch, n_chunks);
+    k_gdn_chunk_scan<128, kGdnScanCols><<<scan, 256, 0, s>>>(a, scratch, n_chunks);
+  }
+  return true;
+}
+
 // The causal convolution with SiLU of gdn_conv / the DeltaNet step
 // (qwen35.rs:448-462), one thread per (token, channel): input t - past + i
 // comes from the batch or, before it, from `hist`.  The newest term is added
@@ -372,6 +649,43 @@ extern "C" int bch_gdn_recurrence(bch_ctx *ctx, bch_view y, bch_view beta, bch_v
   if (n_tokens == 0) return BCH_OK;
   return launch(ctx, {"gdn_recurrence", nv, dv, (uint64_t)nv * dk * dv * 8},
                 [&](hipStream_t s) { run_gdn_recurrence(s, a); });
+}
+
+extern "C" uint64_t bch_gdn_chunk_scratch_floats(const bch_delta_shape *shape, uint32_t n_tokens) {
+  if (!shape) return 0;
+  return gdn_chunk_scratch_floats(shape->n_v_heads, shape->k_dim, shape->v_dim, n_tokens);
+}
+
+extern "C" int bch_gdn_recurrence_chunked(bch_ctx *ctx, bch_view y, bch_view beta, bch_view decay, bch_view state,
+                                          bch_view out, const bch_delta_shape *shape, uint32_t n_tokens,
+                                          float q_scale, bch_view scratch) {
+  if (!shape) return fail(BCH_ERR_ARGUMENT, "gdn_recurrence_chunked: no shape");
+  const uint32_t nk = shape->n_k_heads, nv = shape->n_v_heads, dk = shape->k_dim, dv = shape->v_dim;
+  if (nk == 0 || nv % nk || (dk != 64 && dk != 128) || dv == 0 || dv % kGdnScanCols || dv > 256)
+    return fail(BCH_ERR_DELTANET_LIMITS,
+                "gdn_recurrence_chunked: key heads of 64 or 128, value heads of at most 256 and a multiple of %d, "
+                "value heads a multiple of the key heads (got %u/%u heads of %u/%u)",
+                kGdnScanCols, nk, nv, dk, dv);
+  GdnArgs a{};
+  const uint64_t conv_dim = 2ull * nk * dk + (uint64_t)nv * dv;
+  BCH_TRY(view_ptr(ctx, "gdn_recurrence_chunked", y, (uint64_t)n_tokens * conv_dim * 4, &a.y));
+  BCH_TRY(view_ptr(ctx, "gdn_recurrence_chunked", beta, (uint64_t)n_tokens * nv * 4, &a.beta));
+  BCH_TRY(view_ptr(ctx, "gdn_recurrence_chunked", decay, (uint64_t)n_tokens * nv * 4, &a.alpha));
+  BCH_TRY(view_ptr(ctx, "gdn_recurrence_chunked", state, (uint64_t)nv * dk * dv * 4, &a.state));
+  BCH_TRY(view_ptr(ctx, "gdn_recurrence_chunked", out, (uint64_t)n_tokens * nv * dv * 4, &a.out));
+  float *sp;
+  BCH_TRY(view_ptr(ctx, "gdn_recurrence_chunked", scratch, gdn_chunk_scratch_floats(nv, dk, dv, n_tokens) * 4, &sp));
+  if (reinterpret_cast<uintptr_t>(sp) % 16) return fail(BCH_ERR_ARGUMENT, "gdn_recurrence_chunked: scratch not 16-byte aligned");
+  a.n_k = nk;
+  a.n_v = nv;
+  a.k_dim = dk;
+  a.v_dim = dv;
+  a.n_tokens = n_tokens;
+  a.q_scale = q_scale;
+  a.raw_gates = false;
+  if (n_tokens == 0) return BCH_OK;
+  return launch(ctx, {"gdn_recurrence_chunked", nv, dv, (uint64_t)nv * dk * dv * 8},
+                [&](hipStream_t s) { run_gdn_chunked(s, a, sp); });
 }
 
 extern "C" int bch_gdn_gated_norm(bch_ctx *ctx, bch_view x, bch_view weight, bch_view z, uint32_t v_dim, uint32_t n_rows,

@@ -138,6 +138,11 @@ struct GdnArgs {
 bool gdn_step_supported(const GdnArgs &a);
 // false when k_dim is not 64 or 128 (or v_dim not a multiple of the columns per workgroup).
 bool run_gdn_recurrence(hipStream_t s, const GdnArgs &a);
+// The chunked (WY) form of the same recurrence for prefill batches, in 64-token
+// chunks; `scratch` holds gdn_chunk_scratch_floats() floats (16-byte aligned).
+bool gdn_chunked_supported(const GdnArgs &a);
+uint64_t gdn_chunk_scratch_floats(uint32_t n_v, uint32_t k_dim, uint32_t v_dim, uint32_t n_tokens);
+bool run_gdn_chunked(hipStream_t s, const GdnArgs &a, float *scratch);
 void run_gdn_conv(hipStream_t s, const float *x, const float *taps, float *hist, float *y, uint32_t channels,
                   uint32_t ksize, uint32_t n_tokens);
 void run_gdn_gates(hipStream_t s, float *beta, float *alpha, const float *a, const float *dt_bias, uint32_t n_v,

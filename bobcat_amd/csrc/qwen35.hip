@@ -60,6 +60,7 @@ struct bch_qwen35 : bch::Sequence {
   float *hidden = nullptr, *normed = nullptr, *q_gate = nullptr, *q = nullptr, *k = nullptr, *v = nullptr,
         *attn = nullptr, *proj = nullptr, *conv_out = nullptr, *z = nullptr, *beta = nullptr, *alpha = nullptr,
         *delta_out = nullptr, *ffn = nullptr, *partials = nullptr;
+  float *chunk_scratch = nullptr;  // the chunked DeltaNet form's per-chunk matrices (prefill)
   uint32_t *counters = nullptr;
 
   void *cache_layer(void *base, uint32_t ci) const {
@@ -233,7 +234,8 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
       g.n_tokens = count;
       g.q_scale = 1.0f / sqrtf((float)k_dim);
       g.raw_gates = true;
-      run_gdn_recurrence(st, g);
+      // Batches of more than one token take the chunked (WY) form.
+      if (count == 1 || !chunk_scratch || !run_gdn_chunked(st, g, chunk_scratch)) run_gdn_recurrence(st, g);
       run_gdn_gated_norm(st, delta_out, L.ssm_norm, z, v_dim, count * n_v, norm_eps);
       run_matmul(st, L.out.format, L.out.data, n, value_dim, delta_out, hidden, count, 1, split);
     }
@@ -376,6 +378,7 @@ int bch_qwen35_new(bch_ctx *ctx, const bch_qwen35_model *md, uint32_t n_ctx, int
            (rc = m->alloc(matmul_split_bytes((uint32_t)rows, std::max({n, m->q_dim, m->value_dim, m->n_ff})),
                           &m->split)) || (rc = m->alloc_t(partial_floats + 4, &m->partials)) ||
            (rc = m->alloc_t((uint64_t)kQwenAttnQueryBatch * std::max(1u, m->n_heads), &m->counters)) ||
+           (rc = m->alloc_t(gdn_chunk_scratch_floats(m->n_v, m->k_dim, m->v_dim, (uint32_t)rows), &m->chunk_scratch)) ||
            (rc = m->alloc_common()));
     if (rc) return cleanup(rc);
   }

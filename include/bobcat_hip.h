@@ -334,6 +334,18 @@ int bch_gdn_gates(bch_ctx *ctx, bch_view beta, bch_view alpha, bch_view a, bch_v
  * Key heads of 64 or 128. */
 int bch_gdn_recurrence(bch_ctx *ctx, bch_view y, bch_view beta, bch_view decay, bch_view state, bch_view out,
                        const bch_delta_shape *shape, uint32_t n_tokens, float q_scale);
+/* The recurrence of bch_gdn_recurrence in its chunked (WY) form, for
+ * prefill: 64-token chunks, each chunk's deltas from a triangular solve
+ * (I + A) D = diag(beta)(V - diag(gamma) K S0) and the state carried from
+ * chunk to chunk; same arguments and result (to rounding) as
+ * bch_gdn_recurrence, whose reference form is gdn.metal:204-290 and
+ * qwen35.rs:430-516 (the reference has no chunked form).  `scratch` holds
+ * bch_gdn_chunk_scratch_floats(shape, n_tokens) floats.  Value heads of at
+ * most 256, a multiple of 8. */
+uint64_t bch_gdn_chunk_scratch_floats(const bch_delta_shape *shape, uint32_t n_tokens);
+int bch_gdn_recurrence_chunked(bch_ctx *ctx, bch_view y, bch_view beta, bch_view decay, bch_view state,
+                               bch_view out, const bch_delta_shape *shape, uint32_t n_tokens, float q_scale,
+                               bch_view scratch);
 /* Metal::gdn_gated_norm (gdn.metal:100-123): each row of v_dim floats of x
  * <- weight ⊙ rmsnorm(row) ⊙ silu(z row), in place. */
 int bch_gdn_gated_norm(bch_ctx *ctx, bch_view x, bch_view weight, bch_view z, uint32_t v_dim, uint32_t n_rows,
