@@ -37,16 +37,21 @@ int Uploader::mat(const bch_matrix &src, uint32_t rows, uint32_t cols, DevMatrix
   return BCH_OK;
 }
 
-bool gemv_format(uint32_t f) { return f == BCH_Q4K || f == BCH_F16 || f == BCH_F32; }
+bool gemv_format(uint32_t f) {
+  return f == BCH_Q4K || f == BCH_F16 || f == BCH_F32 || f == BCH_Q5K || f == BCH_Q6K || f == BCH_Q8_0 || f == BCH_Q4_0;
+}
 
 int check_matrix(const bch_matrix &mat, uint32_t rows, uint32_t cols, const char *name) {
   if (!mat.data) return fail(BCH_ERR_ARGUMENT, "missing tensor %s", name);
   if (mat.n_rows != rows || mat.n_cols != cols)
     return fail(BCH_ERR_ARGUMENT, "tensor %s is %u x %u, expected %u x %u", name, mat.n_rows, mat.n_cols, rows, cols);
   if (!gemv_format(mat.format))
-    return fail(BCH_ERR_UNSUPPORTED_FORMAT, "tensor %s: format %u is not supported (Q4_K, F16 or F32)", name,
-                mat.format);
-  if (mat.format == BCH_Q4K && cols % 256) return fail(BCH_ERR_ARGUMENT, "tensor %s: columns not a multiple of 256", name);
+    return fail(BCH_ERR_UNSUPPORTED_FORMAT, "tensor %s: format %u is not supported (Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, F16 or F32)",
+                name, mat.format);
+  if ((mat.format == BCH_Q4K || mat.format == BCH_Q5K || mat.format == BCH_Q6K) && cols % 256)
+    return fail(BCH_ERR_ARGUMENT, "tensor %s: columns not a multiple of 256", name);
+  if ((mat.format == BCH_Q8_0 || mat.format == BCH_Q4_0) && cols % 64)
+    return fail(BCH_ERR_ARGUMENT, "tensor %s: columns not a multiple of 64", name);
   return BCH_OK;
 }
 

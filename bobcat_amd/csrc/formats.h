@@ -251,4 +251,269 @@ struct F32 {
   }
 };
 
+// --- the other GGUF formats of real Q4_K_M / Q4_0 / Q8_0 files ------------
+//
+// A 64-weight unit of these formats is not 16-byte aligned (Q8_0 blocks are
+// 34 bytes, Q4_0 18, Q6_K super-blocks 210), so a unit is read as dwords
+// from the dword at or below its first byte and realigned with alignbyte.
+
+// n dwords starting at byte address p (2-byte aligned), via aligned loads;
+// the dword past the last one is read only when p is not dword aligned (its
+// first two bytes are then still the caller's), so nothing past p + 4n + 1
+// is touched.
+template <int N>
+__device__ __forceinline__ void load_dwords(const uint8_t *p, uint32_t *out) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t *w = reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
+  const uint32_t sh = (uint32_t)(a & 3);
+  uint32_t raw[N + 1];
+#pragma unroll
+  for (int i = 0; i < N; i++) raw[i] = w[i];
+  raw[N] = sh ? w[N] : 0u;
+#pragma unroll
+  for (int i = 0; i < N; i++) out[i] = sh ? __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], sh) : raw[i];
+}
+
+// The inputs of a 64-weight unit: the values and the sums of its four
+// 16-element groups.
+struct Frag64 {
+  float x[64];
+  float gs[4];
+};
+
+__device__ __forceinline__ void frag64_from_lds(const float *p, Frag64 &f) {
+  const float4 *p4 = reinterpret_cast<const float4 *>(p);
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const float4 a = p4[i];
+    f.x[4 * i] = a.x, f.x[4 * i + 1] = a.y, f.x[4 * i + 2] = a.z, f.x[4 * i + 3] = a.w;
+  }
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) t += f.x[16 * g + i];
+    f.gs[g] = t;
+  }
+}
+
+template <bool NORM>
+__device__ __forceinline__ void frag64_load(const float *x, const float *nw, uint32_t u, Frag64 &f) {
+  load_inputs<NORM>(x, nw, u * 64, f.x, 16);
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) t += f.x[16 * g + i];
+    f.gs[g] = t;
+  }
+}
+
+// Σ over 4 bytes of dword w (unsigned) times x[0..3].
+__device__ __forceinline__ float dot4u(uint32_t w, const float *x, float acc) {
+  acc = fmaf(ubyte0(w), x[0], acc);
+  acc = fmaf(ubyte1(w), x[1], acc);
+  acc = fmaf(ubyte2(w), x[2], acc);
+  return fmaf(ubyte3(w), x[3], acc);
+}
+
+// Q8_0 (scalar.rs:106-113): 32-weight blocks of fp16 d and 32 int8; a unit
+// is two blocks (68 bytes).  Σ d·q·x = d·(Σ (q+128)·x − 128·Σx): the bytes
+// flipped to unsigned feed v_cvt_f32_ubyte directly.
+struct Q8_0 {
+  static constexpr uint32_t kFormat = 8;
+  static constexpr uint32_t kUnit = 64;
+  using Frag = Frag64;
+  template <bool NORM>
+  __device__ __forceinline__ static void load(const float *x, const float *nw, uint32_t u, Frag &f) {
+    frag64_load<NORM>(x, nw, u, f);
+  }
+  __device__ __forceinline__ static void from_lds(const float *p, Frag &f) { frag64_from_lds(p, f); }
+  struct Raw {
+    uint32_t w[17];
+  };
+  __device__ __forceinline__ static Raw fetch(const uint8_t *__restrict__ row, uint32_t u) {
+    Raw r;
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(row + 68 * u);
+#pragma unroll
+    for (int i = 0; i < 17; i++) r.w[i] = p[i];
+    return r;
+  }
+  __device__ __forceinline__ static float compute(const Raw &r, uint32_t, const Frag &f) {
+    float tot = 0.f;
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      // Block b: d at byte 34b, quants at bytes 34b+2 .. 34b+33.
+      const float d = half_bits_to_float(b == 0 ? (r.w[0] & 0xffffu) : (r.w[8] >> 16));
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const uint32_t q = b == 0 ? __builtin_amdgcn_alignbyte(r.w[i + 1], r.w[i], 2) : r.w[9 + i];
+        const float *x = f.x + 32 * b + 4 * i;
+        if (i & 1)
+          s1 = dot4u(q ^ 0x80808080u, x, s1);
+        else
+          s0 = dot4u(q ^ 0x80808080u, x, s0);
+      }
+      tot = fmaf(d, (s0 + s1) - 128.f * (f.gs[2 * b] + f.gs[2 * b + 1]), tot);
+    }
+    return tot;
+  }
+  __device__ __forceinline__ static float dot(const uint8_t *__restrict__ row, uint32_t u, const Frag &f) {
+    return compute(fetch(row, u), u, f);
+  }
+};
+
+// Q4_0 (scalar.rs:95-104): 32-weight blocks of fp16 d and 16 bytes, low
+// nibbles elements 0..15 and high nibbles 16..31, value (q − 8)·d; a unit is
+// two blocks (36 bytes).
+struct Q4_0 {
+  static constexpr uint32_t kFormat = 2;
+  static constexpr uint32_t kUnit = 64;
+  using Frag = Frag64;
+  template <bool NORM>
+  __device__ __forceinline__ static void load(const float *x, const float *nw, uint32_t u, Frag &f) {
+    frag64_load<NORM>(x, nw, u, f);
+  }
+  __device__ __forceinline__ static void from_lds(const float *p, Frag &f) { frag64_from_lds(p, f); }
+  struct Raw {
+    uint32_t w[9];
+  };
+  __device__ __forceinline__ static Raw fetch(const uint8_t *__restrict__ row, uint32_t u) {
+    Raw r;
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(row + 36 * u);
+#pragma unroll
+    for (int i = 0; i < 9; i++) r.w[i] = p[i];
+    return r;
+  }
+  __device__ __forceinline__ static float compute(const Raw &r, uint32_t, const Frag &f) {
+    float tot = 0.f;
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      const float d = half_bits_to_float(b == 0 ? (r.w[0] & 0xffffu) : (r.w[4] >> 16));
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t q = b == 0 ? __builtin_amdgcn_alignbyte(r.w[i + 1], r.w[i], 2) : r.w[5 + i];
+        s0 = dot4u(q & 0x0f0f0f0fu, f.x + 32 * b + 4 * i, s0);
+        s1 = dot4u((q >> 4) & 0x0f0f0f0fu, f.x + 32 * b + 16 + 4 * i, s1);
+      }
+      tot = fmaf(d, (s0 + s1) - 8.f * (f.gs[2 * b] + f.gs[2 * b + 1]), tot);
+    }
+    return tot;
+  }
+  __device__ __forceinline__ static float dot(const uint8_t *__restrict__ row, uint32_t u, const Frag &f) {
+    return compute(fetch(row, u), u, f);
+  }
+};
+
+// Q6_K (scalar.rs:181-202): 256-weight super-blocks of 210 bytes, ql[128]
+// (low nibbles), qh[64] (2-bit highs), 16 int8 scales, fp16 d at 208.  Unit
+// u is weights 64·(u%4) .. +63 of super-block u/4: half h = (u%4)/2 and
+// p = u%2; weight j of the unit has its low nibble in ql[64h + j] (high
+// nibble when p = 1), its top bits at 2·(2p + j/32) in qh[32h + j%32], and
+// scale s[8h + 4p + j/16]; q = (low | top << 4) − 32.
+struct Q6K {
+  static constexpr uint32_t kFormat = 14;
+  static constexpr uint32_t kUnit = 64;
+  using Frag = Frag64;
+  template <bool NORM>
+  __device__ __forceinline__ static void load(const float *x, const float *nw, uint32_t u, Frag &f) {
+    frag64_load<NORM>(x, nw, u, f);
+  }
+  __device__ __forceinline__ static void from_lds(const float *p, Frag &f) { frag64_from_lds(p, f); }
+  struct Raw {
+    uint32_t ql[16], qh[8], sc, d;
+  };
+  __device__ __forceinline__ static Raw fetch(const uint8_t *__restrict__ row, uint32_t u) {
+    Raw r;
+    const uint8_t *blk = row + (uint64_t)(u >> 2) * 210;
+    const uint32_t h = (u >> 1) & 1, p = u & 1;
+    load_dwords<16>(blk + 64 * h, r.ql);
+    load_dwords<8>(blk + 128 + 32 * h, r.qh);
+    load_dwords<1>(blk + 192 + 8 * h + 4 * p, &r.sc);
+    // d: two bytes inside one aligned dword.
+    const uintptr_t da = reinterpret_cast<uintptr_t>(blk + 208);
+    r.d = *reinterpret_cast<const uint32_t *>(da & ~uintptr_t(3)) >> (8 * (da & 3));
+    return r;
+  }
+  __device__ __forceinline__ static float compute(const Raw &r, uint32_t u, const Frag &f) {
+    const uint32_t p = u & 1;
+    float tot = 0.f;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int i = 4 * g + k;  // dword of ql: weights 4i .. 4i+3
+        const uint32_t lo = p ? (r.ql[i] >> 4) & 0x0f0f0f0fu : r.ql[i] & 0x0f0f0f0fu;
+        const uint32_t top = (r.qh[i & 7] >> (2 * (2 * p + (i >> 3)))) & 0x03030303u;
+        const uint32_t q = lo | (top << 4);
+        if (k & 1)
+          s1 = dot4u(q, f.x + 4 * i, s1);
+        else
+          s0 = dot4u(q, f.x + 4 * i, s0);
+      }
+      const float sc = (float)(int8_t)((r.sc >> (8 * g)) & 0xffu);
+      tot = fmaf(sc, (s0 + s1) - 32.f * f.gs[g], tot);
+    }
+    return half_bits_to_float(r.d & 0xffffu) * tot;
+  }
+  __device__ __forceinline__ static float dot(const uint8_t *__restrict__ row, uint32_t u, const Frag &f) {
+    return compute(fetch(row, u), u, f);
+  }
+};
+
+// Q5_K (scalar.rs:157-176): 176-byte super-blocks of fp16 d and dmin, the
+// 12 scale bytes of Q4_K, qh[32] (bit j of byte l is the fifth bit of
+// element 32j + l) and qs[128] as Q4_K's nibbles.  A unit is the pair of
+// 32-element blocks 2p, 2p+1 (the layout of the Q4K unit plus qh).
+struct Q5K {
+  static constexpr uint32_t kFormat = 13;
+  static constexpr uint32_t kUnit = 64;
+  using Frag = Q4K::Frag;
+  template <bool NORM>
+  __device__ __forceinline__ static void load(const float *x, const float *nw, uint32_t u, Frag &f) {
+    Q4K::load<NORM>(x, nw, u, f);
+  }
+  __device__ __forceinline__ static void from_lds(const float *p, Frag &f) { Q4K::from_lds(p, f); }
+  struct Raw {
+    uint4 h, qh0, qh1, q0, q1;
+  };
+  __device__ __forceinline__ static Raw fetch(const uint8_t *__restrict__ row, uint32_t u) {
+    const uint8_t *blk = row + (uint64_t)(u >> 2) * 176;
+    const uint4 *hp = reinterpret_cast<const uint4 *>(blk);
+    const uint4 *qp = reinterpret_cast<const uint4 *>(blk + 48 + 32 * (u & 3));
+    return Raw{hp[0], hp[1], hp[2], qp[0], qp[1]};
+  }
+  __device__ __forceinline__ static float compute(const Raw &raw, uint32_t u, const Frag &f) {
+    const int p = u & 3;
+    const uint32_t qw[8] = {raw.q0.x, raw.q0.y, raw.q0.z, raw.q0.w, raw.q1.x, raw.q1.y, raw.q1.z, raw.q1.w};
+    const uint32_t hw[8] = {raw.qh0.x, raw.qh0.y, raw.qh0.z, raw.qh0.w, raw.qh1.x, raw.qh1.y, raw.qh1.z, raw.qh1.w};
+    float s_lo0 = 0.f, s_lo1 = 0.f, s_hi0 = 0.f, s_hi1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const uint32_t lo = (qw[k] & 0x0f0f0f0fu) | (((hw[k] >> (2 * p)) & 0x01010101u) << 4);
+      const uint32_t hi = ((qw[k] >> 4) & 0x0f0f0f0fu) | (((hw[k] >> (2 * p + 1)) & 0x01010101u) << 4);
+      s_lo0 = fmaf(ubyte0(lo), f.lo[4 * k + 0], s_lo0);
+      s_lo1 = fmaf(ubyte1(lo), f.lo[4 * k + 1], s_lo1);
+      s_lo0 = fmaf(ubyte2(lo), f.lo[4 * k + 2], s_lo0);
+      s_lo1 = fmaf(ubyte3(lo), f.lo[4 * k + 3], s_lo1);
+      s_hi0 = fmaf(ubyte0(hi), f.hi[4 * k + 0], s_hi0);
+      s_hi1 = fmaf(ubyte1(hi), f.hi[4 * k + 1], s_hi1);
+      s_hi0 = fmaf(ubyte2(hi), f.hi[4 * k + 2], s_hi0);
+      s_hi1 = fmaf(ubyte3(hi), f.hi[4 * k + 3], s_hi1);
+    }
+    const uint32_t sc = q4k_pair_scales(raw.h.y, raw.h.z, raw.h.w, p);
+    const float d = half_bits_to_float(raw.h.x & 0xffffu);
+    const float dmin = half_bits_to_float(raw.h.x >> 16);
+    const float qs = ubyte0(sc) * (s_lo0 + s_lo1) + ubyte1(sc) * (s_hi0 + s_hi1);
+    const float ms = ubyte2(sc) * f.sum_lo + ubyte3(sc) * f.sum_hi;
+    return d * qs - dmin * ms;
+  }
+  __device__ __forceinline__ static float dot(const uint8_t *__restrict__ row, uint32_t u, const Frag &f) {
+    return compute(fetch(row, u), u, f);
+  }
+};
+
 }  // namespace bch

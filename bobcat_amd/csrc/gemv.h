@@ -485,14 +485,27 @@ static void launch_gemv(hipStream_t s, const P &p, const float *x, const float *
   k_gemv<F, LPR, RPG, NORM, P><<<grid, threads, lds, s>>>(p, x, nw, eps, n_items, n_units, n_cols);
 }
 
+// Formats outside the headline path (Q8_0, Q4_0, Q5_K, Q6_K) are built for one and
+// two items per group only, which keeps the number of kernels down.
+template <class F>
+constexpr bool kFewBatches = F::kFormat == 8 || F::kFormat == 2 || F::kFormat == 14 || F::kFormat == 13;
+
 template <class F, int LPR, bool NORM, class P>
 static void gemv_rpg(hipStream_t s, int rpg, const P &p, const float *x, const float *nw, float eps,
                      uint32_t n_items, uint32_t n_units, uint32_t n_cols) {
-  switch (rpg) {
-    case 8: launch_gemv<F, LPR, 8, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols); break;
-    case 4: launch_gemv<F, LPR, 4, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols); break;
-    case 2: launch_gemv<F, LPR, 2, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols); break;
-    default: launch_gemv<F, LPR, 1, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols); break;
+  if constexpr (kFewBatches<F>) {
+    if (rpg >= 2)
+      launch_gemv<F, LPR, 2, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols);
+    else
+      launch_gemv<F, LPR, 1, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols);
+    return;
+  } else {
+    switch (rpg) {
+      case 8: launch_gemv<F, LPR, 8, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols); break;
+      case 4: launch_gemv<F, LPR, 4, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols); break;
+      case 2: launch_gemv<F, LPR, 2, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols); break;
+      default: launch_gemv<F, LPR, 1, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols); break;
+    }
   }
 }
 
@@ -528,6 +541,19 @@ static bool gemv_any(hipStream_t s, uint32_t format, const P &p, const float *x,
   if (format == F16::kFormat)
     return norm ? gemv_dispatch<F16, true>(s, p, x, nw, eps, n_items, n_cols, n_cus)
                 : gemv_dispatch<F16, false>(s, p, x, nw, eps, n_items, n_cols, n_cus);
+  if (format == Q6K::kFormat)
+    return norm ? gemv_dispatch<Q6K, true>(s, p, x, nw, eps, n_items, n_cols, n_cus)
+                : gemv_dispatch<Q6K, false>(s, p, x, nw, eps, n_items, n_cols, n_cus);
+  if (format == Q5K::kFormat)
+    return norm ? gemv_dispatch<Q5K, true>(s, p, x, nw, eps, n_items, n_cols, n_cus)
+                : gemv_dispatch<Q5K, false>(s, p, x, nw, eps, n_items, n_cols, n_cus);
+  if (format == Q8_0::kFormat)
+    return norm ? gemv_dispatch<Q8_0, true>(s, p, x, nw, eps, n_items, n_cols, n_cus)
+                : gemv_dispatch<Q8_0, false>(s, p, x, nw, eps, n_items, n_cols, n_cus);
+  if (format == Q4_0::kFormat)
+    return norm ? gemv_dispatch<Q4_0, true>(s, p, x, nw, eps, n_items, n_cols, n_cus)
+                : gemv_dispatch<Q4_0, false>(s, p, x, nw, eps, n_items, n_cols, n_cus);
+  if (format != F32::kFormat) return false;
   return norm ? gemv_dispatch<F32, true>(s, p, x, nw, eps, n_items, n_cols, n_cus)
               : gemv_dispatch<F32, false>(s, p, x, nw, eps, n_items, n_cols, n_cus);
 }

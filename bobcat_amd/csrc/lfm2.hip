@@ -138,8 +138,14 @@ static void lfm2_step(bch_lfm2 *m, hipStream_t s, bool greedy_input, bool trace)
       run_matvec(s, L.out_proj.format, L.out_proj.data, n, n, m->conv_out, m->hidden, nullptr, 0.f, true, cus);
     } else {
       const uint32_t ci = L.cache_index;
-      run_matvec3(s, L.wq.format, L.wq.data, L.wk.data, L.wv.data, m->q_dim, m->kv_dim, m->kv_dim, n, m->hidden,
-                  m->q, m->k, m->v, L.attn_norm, m->norm_eps, cus);
+      if (L.wq.format == L.wk.format && L.wq.format == L.wv.format) {
+        run_matvec3(s, L.wq.format, L.wq.data, L.wk.data, L.wv.data, m->q_dim, m->kv_dim, m->kv_dim, n, m->hidden,
+                    m->q, m->k, m->v, L.attn_norm, m->norm_eps, cus);
+      } else {  // mixed formats (Q4_K_M files keep attn_v in Q6_K): one launch each
+        run_matvec(s, L.wq.format, L.wq.data, m->q_dim, n, m->hidden, m->q, L.attn_norm, m->norm_eps, false, cus);
+        run_matvec(s, L.wk.format, L.wk.data, m->kv_dim, n, m->hidden, m->k, L.attn_norm, m->norm_eps, false, cus);
+        run_matvec(s, L.wv.format, L.wv.data, m->kv_dim, n, m->hidden, m->v, L.attn_norm, m->norm_eps, false, cus);
+      }
       AttnDecodeArgs ad;
       ad.q = m->q;
       ad.k = m->k;
@@ -406,15 +412,15 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
           (rc = mat(S.wv, m->kv_dim, n, &L.wv, "attn_v")) || (rc = mat(S.wo, n, m->q_dim, &L.wo, "attn_output")) ||
           (rc = vec(S.q_norm, hd, &L.q_norm, "attn_q_norm")) || (rc = vec(S.k_norm, hd, &L.k_norm, "attn_k_norm")))
         return cleanup(rc);
-      if (S.wq.format != S.wk.format || S.wq.format != S.wv.format)
-        return cleanup(fail(BCH_ERR_UNSUPPORTED_FORMAT, "layer %u: q, k and v matrices of one format", il));
     } else {
       L.cache_index = m->n_conv++;
       if ((rc = mat(S.in_proj, 3 * n, n, &L.in_proj, "shortconv.in_proj")) ||
           (rc = mat(S.out_proj, n, n, &L.out_proj, "shortconv.out_proj")) ||
           (rc = vec(S.conv_taps, (uint64_t)n * md->conv_kernel, &L.taps, "shortconv.conv")))
         return cleanup(rc);
-      if (S.in_proj.format != BCH_Q4K)
+      // The fused conv projection takes every GEMV format up to 16384 columns
+      // (the x-stationary kernel); wider rows only as Q4_K.
+      if (S.in_proj.format != BCH_Q4K && n > 16384)
         return cleanup(fail(BCH_ERR_UNSUPPORTED_FORMAT, "layer %u: the fused conv projection needs Q4_K", il));
     }
     L.moe = S.is_moe != 0;

@@ -91,6 +91,21 @@ __device__ __forceinline__ void expand_float(const uint8_t *__restrict__ row, ui
   }
 }
 
+// Q8_0 / Q4_0 / Q5_K / Q6_K rows: 64 consecutive weights from column k, each
+// dequantised exactly as the scalar path does (formats.h dequant_elem), then
+// rounded to half.  (These formats appear in a few tensors of real Q4_K_M
+// files; the byte-wise reads are not tuned.)
+template <uint32_t FMT>
+__device__ __forceinline__ void expand_generic(const uint8_t *__restrict__ row, uint32_t k, _Float16 *dst) {
+#pragma unroll 8
+  for (int i = 0; i < 64; i += 4) {
+    half4_t h;
+#pragma unroll
+    for (int j = 0; j < 4; j++) h[j] = (_Float16)dequant_elem(FMT, row, k + i + j);
+    *reinterpret_cast<half4_t *>(dst + i) = h;
+  }
+}
+
 // Row t of X [n_rows x n_cols] f32 to fp16 high and low parts: with s the
 // power of two that puts max|x_t| in [2^13, 2^14) (half precision cannot
 // overflow in the MFMA operands), hi = fp16(x·s), lo = fp16(x·s − hi), and
@@ -253,6 +268,8 @@ __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, u
     if (a_thread) {
       if constexpr (FMT == 12)
         expand_q4k(ra, (int)((k0 & 255u) / 64) + aq, A + ar * kLds + 64 * aq);
+      else if constexpr (FMT == 2 || FMT == 8 || FMT == 13 || FMT == 14)
+        expand_generic<FMT>(wrow, k0 + 64 * aq, A + ar * kLds + 64 * aq);
       else
         expand_float<FMT>(wrow, k0 + 64 * aq, A + ar * kLds + 64 * aq);
     }
@@ -362,11 +379,21 @@ void run_matmul(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_row
     matmul_fmt<12>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
   else if (format == 1)
     matmul_fmt<1>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
+  else if (format == 14)
+    matmul_fmt<14>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
+  else if (format == 13)
+    matmul_fmt<13>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
+  else if (format == 8)
+    matmul_fmt<8>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
+  else if (format == 2)
+    matmul_fmt<2>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
   else
     matmul_fmt<0>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
 }
 
-static bool matmul_format(uint32_t f) { return f == 12 || f == 1 || f == 0; }
+static bool matmul_format(uint32_t f) {
+  return f == 12 || f == 1 || f == 0 || f == 13 || f == 14 || f == 8 || f == 2;
+}
 
 void run_matmul_experts(hipStream_t s, uint32_t format, const uint8_t *W, const uint8_t *up, uint32_t n_rows,
                         uint32_t n_cols, uint32_t n_experts, const float *xf, bool shared_input,
@@ -400,6 +427,10 @@ static void set_lds_limits() {
   BCH_SET(12, 0); BCH_SET(12, 1); BCH_SET(12, 2);
   BCH_SET(1, 0); BCH_SET(1, 1); BCH_SET(1, 2);
   BCH_SET(0, 0); BCH_SET(0, 1); BCH_SET(0, 2);
+  BCH_SET(14, 0); BCH_SET(14, 1); BCH_SET(14, 2);
+  BCH_SET(13, 0); BCH_SET(13, 1); BCH_SET(13, 2);
+  BCH_SET(8, 0); BCH_SET(8, 1); BCH_SET(8, 2);
+  BCH_SET(2, 0); BCH_SET(2, 1); BCH_SET(2, 2);
 #undef BCH_SET
 #define BCH_SET(F, S) \
   hipFuncSetAttribute((const void *)k_matmul<F, S, 1, true>, hipFuncAttributeMaxDynamicSharedMemorySize, lds)
@@ -428,7 +459,13 @@ extern "C" int bch_matmul(bch_ctx *ctx, uint32_t format, bch_view weights, uint3
   if (reinterpret_cast<uintptr_t>(W) % 16 || reinterpret_cast<uintptr_t>(xp) % 16)
     return fail(BCH_ERR_ARGUMENT, "matmul: weights and inputs must be 16-byte aligned");
   set_lds_limits();
-  const char *name = format == 12 ? "matmul_q4k" : format == 1 ? "matmul_f16" : "matmul_f32";
+  const char *name = format == 12 ? "matmul_q4k"
+                     : format == 14 ? "matmul_q6k"
+                     : format == 13 ? "matmul_q5k"
+                     : format == 8  ? "matmul_q8_0"
+                     : format == 2  ? "matmul_q4_0"
+                     : format == 1  ? "matmul_f16"
+                                    : "matmul_f32";
   void *split = nullptr;
   BCH_TRY(ctx_scratch(ctx, matmul_split_bytes(n_tokens, n_cols), &split));
   return launch(ctx, {name, n_rows, n_cols, rb * n_rows}, [&](hipStream_t s) {

@@ -13,6 +13,7 @@
 // and R are picked per shape so that every lane has whole units and the
 // grid holds enough waves to cover all 256 CUs.
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 
 #include "formats.h"
@@ -332,10 +333,32 @@ static void swiglu_f(hipStream_t s, Geometry g, const uint8_t *Wg, const uint8_t
   });
 }
 
-static bool is_gemv_format(uint32_t f) { return f == Q4K::kFormat || f == F16::kFormat || f == F32::kFormat; }
+static bool is_gemv_format(uint32_t f) {
+  return f == Q4K::kFormat || f == F16::kFormat || f == F32::kFormat || f == Q6K::kFormat || f == Q5K::kFormat ||
+         f == Q8_0::kFormat || f == Q4_0::kFormat;
+}
 
+// Weights per unit (formats.h).
 static uint32_t unit_of(uint32_t f) {
-  return f == Q4K::kFormat ? Q4K::kUnit : f == F16::kFormat ? F16::kUnit : F32::kUnit;
+  if (f == Q4K::kFormat || f == Q5K::kFormat || f == Q6K::kFormat || f == Q8_0::kFormat || f == Q4_0::kFormat) return 64;
+  return f == F16::kFormat ? F16::kUnit : F32::kUnit;
+}
+
+// Columns a row of format f must be a multiple of (whole super-blocks).
+static uint32_t cols_of(uint32_t f) {
+  return f == Q4K::kFormat || f == Q5K::kFormat || f == Q6K::kFormat ? 256 : unit_of(f);
+}
+
+static const char *format_name(uint32_t f) {
+  switch (f) {
+    case 12: return "q4k";
+    case 14: return "q6k";
+    case 13: return "q5k";
+    case 8: return "q8_0";
+    case 2: return "q4_0";
+    case 1: return "f16";
+    default: return "f32";
+  }
 }
 
 // Call f.template operator()<Format>() for a runtime format id.
@@ -345,6 +368,14 @@ static void dispatch_format(uint32_t format, Fn &&f) {
     f.template operator()<Q4K>();
   else if (format == F16::kFormat)
     f.template operator()<F16>();
+  else if (format == Q6K::kFormat)
+    f.template operator()<Q6K>();
+  else if (format == Q5K::kFormat)
+    f.template operator()<Q5K>();
+  else if (format == Q8_0::kFormat)
+    f.template operator()<Q8_0>();
+  else if (format == Q4_0::kFormat)
+    f.template operator()<Q4_0>();
   else
     f.template operator()<F32>();
 }
@@ -408,7 +439,7 @@ void run_matvec_conv(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t 
 static int check_shape(const char *name, uint32_t format, uint32_t n_rows, uint32_t n_cols) {
   if (!is_gemv_format(format))
     return fail(BCH_ERR_UNSUPPORTED_FORMAT, "%s: format %u has no matrix-vector kernel", name, format);
-  if (n_rows == 0 || n_cols == 0 || n_cols % unit_of(format) || (format == Q4K::kFormat && n_cols % 256))
+  if (n_rows == 0 || n_cols == 0 || n_cols % cols_of(format))
     return fail(BCH_ERR_ARGUMENT, "%s: %u x %u does not tile format %u", name, n_rows, n_cols, format);
   return BCH_OK;
 }
@@ -454,7 +485,8 @@ int bch_matvec(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_rows,
   BCH_TRY(check_align("matvec", xp, 16));
   if (nw) BCH_TRY(check_align("matvec", nw, 16));
   const float eps = norm ? norm->eps : 0.f;
-  const char *name = format == Q4K::kFormat ? "matvec_q4k" : format == F16::kFormat ? "matvec_f16" : "matvec_f32";
+  char name[32];
+  snprintf(name, sizeof name, "matvec_%s", format_name(format));
   return launch(ctx, {name, n_rows, n_cols, rb * n_rows}, [&](hipStream_t s) {
     run_matvec(s, format, W, n_rows, n_cols, xp, yp, nw, eps, accumulate != 0, ctx->n_cus);
   });
@@ -476,8 +508,8 @@ int bch_matvec_swiglu(bch_ctx *ctx, uint32_t format, bch_view gate, bch_view up,
   BCH_TRY(check_align("matvec_swiglu", Wu, 16));
   BCH_TRY(check_align("matvec_swiglu", xp, 16));
   BCH_TRY(check_align("matvec_swiglu", nw, 16));
-  const char *name = format == Q4K::kFormat ? "matvec_swiglu_q4k" : format == F16::kFormat ? "matvec_swiglu_f16"
-                                                                                          : "matvec_swiglu_f32";
+  char name[32];
+  snprintf(name, sizeof name, "matvec_swiglu_%s", format_name(format));
   return launch(ctx, {name, n_rows, n_cols, 2 * rb * n_rows}, [&](hipStream_t s) {
     run_matvec_swiglu(s, format, Wg, Wu, n_rows, n_cols, xp, yp, nw, norm.eps, ctx->n_cus);
   });

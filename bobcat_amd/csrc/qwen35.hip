@@ -95,8 +95,14 @@ void bch_qwen35::record_step(hipStream_t st, bool greedy_input, bool trace) {
     const QwenLayer &L = layers[il];
     if (L.attention) {
       const uint32_t ci = L.cache_index;
-      run_matvec3(st, L.wq.format, L.wq.data, L.wk.data, L.wv.data, 2 * q_dim, kv_dim, kv_dim, n, hidden, q_gate, k, v,
-                  L.attn_norm, norm_eps, cus);
+      if (L.wq.format == L.wk.format && L.wq.format == L.wv.format) {
+        run_matvec3(st, L.wq.format, L.wq.data, L.wk.data, L.wv.data, 2 * q_dim, kv_dim, kv_dim, n, hidden, q_gate, k,
+                    v, L.attn_norm, norm_eps, cus);
+      } else {  // mixed formats: one launch each
+        run_matvec(st, L.wq.format, L.wq.data, 2 * q_dim, n, hidden, q_gate, L.attn_norm, norm_eps, false, cus);
+        run_matvec(st, L.wk.format, L.wk.data, kv_dim, n, hidden, k, L.attn_norm, norm_eps, false, cus);
+        run_matvec(st, L.wv.format, L.wv.data, kv_dim, n, hidden, v, L.attn_norm, norm_eps, false, cus);
+      }
       AttnDecodeArgs ad{};
       ad.q = q_gate;
       ad.k = k;
@@ -328,8 +334,6 @@ int bch_qwen35_new(bch_ctx *ctx, const bch_qwen35_model *md, uint32_t n_ctx, int
           (rc = up.mat(S.wv, m->kv_dim, n, &L.wv, "attn_v")) || (rc = up.mat(S.wo, n, m->q_dim, &L.wo, "attn_output")) ||
           (rc = up.vec(S.q_norm, hd, &L.q_norm, "attn_q_norm")) || (rc = up.vec(S.k_norm, hd, &L.k_norm, "attn_k_norm")))
         return cleanup(rc);
-      if (S.wq.format != S.wk.format || S.wq.format != S.wv.format)
-        return cleanup(fail(BCH_ERR_UNSUPPORTED_FORMAT, "layer %u: q, k and v matrices of one format", il));
     } else {
       L.cache_index = m->n_delta++;
       if ((rc = up.mat(S.qkv, m->conv_dim, n, &L.qkv, "attn_qkv")) ||

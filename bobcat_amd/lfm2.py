@@ -16,7 +16,7 @@ import numpy as np
 
 from ._lib import EMIT_FN, Lfm2Layer, Lfm2Model, Matrix, check, lib
 from .backend import Format, Hip
-from .synth import q4k_matrix
+from .synth import block_matrix, q4k_matrix
 
 
 @dataclass
@@ -42,6 +42,13 @@ class Lfm2Config:
     n_experts_used: int = 0
     n_ff_expert: int = 0
     n_dense_layers: int = 0
+    # Per-tensor formats overriding layer_format/embd_format, keyed by tensor
+    # name ("wv") or layer and name ("3.down"), as real Q4_K_M files mix
+    # formats (lfm2_reference.rs:45-49).
+    tensor_formats: dict = field(default_factory=dict)
+
+    def format_of(self, key: str, default: int) -> int:
+        return self.tensor_formats.get(key, self.tensor_formats.get(key.split(".", 1)[-1], default))
 
     def is_moe(self, il: int) -> bool:
         return self.n_experts > 0 and il >= self.n_dense_layers
@@ -92,12 +99,23 @@ LFM2_8B_A1B = Lfm2Config("lfm2-8b-a1b", n_embd=2048, n_ff=7168, n_heads=32, n_kv
 LFM2_TINY_MOE = Lfm2Config("lfm2-tiny-moe", n_embd=256, n_ff=512, n_heads=4, n_kv_heads=2, n_vocab=1000,
                            attention_layers=[1, 3], n_layers=4, n_experts=8, n_experts_used=2, n_ff_expert=256,
                            n_dense_layers=1)
-CONFIGS = {c.name: c for c in (LFM2_350M, LFM2_2_6B, LFM2_TINY, LFM2_TINY_F16, LFM2_8B_A1B, LFM2_TINY_MOE)}
+# A tiny model whose tensors mix the formats of real files: attn_v and the
+# tied embedding in Q6_K (as Q4_K_M files keep them), Q8_0, Q4_0 and Q5_K
+# matrices elsewhere.
+LFM2_TINY_MIXED = Lfm2Config("lfm2-tiny-mixed", n_embd=256, n_ff=512, n_heads=4, n_kv_heads=2, n_vocab=1000,
+                             attention_layers=[1, 3], n_layers=4,
+                             tensor_formats={"wv": Format.Q6K, "token_embd": Format.Q6K, "0.out_proj": Format.Q8_0,
+                                             "1.wo": Format.Q4_0, "2.down": Format.Q6K, "3.up": Format.Q5K,
+                                             "3.gate": Format.Q5K, "0.in_proj": Format.Q8_0})
+CONFIGS = {c.name: c for c in (LFM2_350M, LFM2_2_6B, LFM2_TINY, LFM2_TINY_F16, LFM2_8B_A1B, LFM2_TINY_MOE,
+                               LFM2_TINY_MIXED)}
 
 
 def _matrix(fmt: int, rows: int, cols: int, rng: np.random.Generator) -> np.ndarray:
     if fmt == Format.Q4K:
         return q4k_matrix(rng, rows, cols)
+    if fmt in (Format.Q4_0, Format.Q8_0, Format.Q5K, Format.Q6K):
+        return block_matrix(rng, int(fmt), rows, cols)
     if fmt == Format.F16:
         return rng.standard_normal(rows * cols, dtype=np.float32).astype(np.float16).view(np.uint8)
     return rng.standard_normal(rows * cols, dtype=np.float32).view(np.uint8)
@@ -119,6 +137,7 @@ class Lfm2Weights:
         fp = lambda arr: arr.ctypes.data_as(C.POINTER(C.c_float))
 
         def mat(key, fmt, rows, cols):
+            fmt = cfg.format_of(key, fmt)
             a[key] = _matrix(fmt, rows, cols, rng)
             return Matrix(int(fmt), rows, cols, a[key].ctypes.data)
 

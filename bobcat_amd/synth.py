@@ -64,3 +64,28 @@ def gemv_case(seed: int = 0x9E3779B97F4A7C15, n_rows: int = 8192, n_cols: int = 
     w = q4k_matrix(rng, n_rows, n_cols)
     x = rng.standard_normal(n_cols).astype(np.float32)
     return w, x
+
+
+# Block layouts of the other GGUF formats: (weights per block, bytes per
+# block, byte offsets of the fp16 scales, their range).
+BLOCK_FORMATS = {
+    2: (32, 18, [0], (2e-3, 2e-2)),            # Q4_0: d, 16 bytes of nibbles
+    8: (32, 34, [0], (1e-3, 1e-2)),            # Q8_0: d, 32 int8
+    13: (256, 176, [0, 2], (1e-3, 1e-2)),      # Q5_K: d, dmin, 12 scale bytes, qh[32], qs[128]
+    14: (256, 210, [208], (1e-3, 1e-2)),       # Q6_K: ql[128], qh[64], 16 int8 scales, d
+}
+
+
+def block_matrix(rng: np.random.Generator, fmt: int, n_rows: int, n_cols: int) -> np.ndarray:
+    """A random matrix of a GGUF block format as flat bytes: every byte
+    uniform, then each fp16 scale field set to U(range) (for Q6_K the int8
+    sub-block scales stay uniform bytes)."""
+    if fmt == 12:
+        return q4k_matrix(rng, n_rows, n_cols)
+    ne, nb, scales, (lo, hi) = BLOCK_FORMATS[fmt]
+    assert n_cols % ne == 0
+    n_blocks = n_rows * n_cols // ne
+    w = rng.integers(0, 256, n_blocks * nb, dtype=np.uint8).reshape(n_blocks, nb)
+    for at in scales:
+        w[:, at:at + 2] = rng.uniform(lo, hi, n_blocks).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    return w.reshape(-1)

@@ -19,7 +19,7 @@ import pytest
 
 import oracle
 from bobcat_amd import BobcatError
-from bobcat_amd.lfm2 import LFM2_TINY, LFM2_TINY_F16, LFM2_TINY_MOE, Lfm2Hip, Lfm2Weights
+from bobcat_amd.lfm2 import LFM2_TINY, LFM2_TINY_F16, LFM2_TINY_MIXED, LFM2_TINY_MOE, Lfm2Hip, Lfm2Weights
 
 pytestmark = pytest.mark.gpu
 
@@ -35,7 +35,7 @@ def rel(got, want):
     return float(d.max() / max(np.abs(want).max(), 1e-30))
 
 
-@pytest.fixture(scope="module", params=[LFM2_TINY, LFM2_TINY_F16, LFM2_TINY_MOE], ids=lambda c: c.name)
+@pytest.fixture(scope="module", params=[LFM2_TINY, LFM2_TINY_F16, LFM2_TINY_MOE, LFM2_TINY_MIXED], ids=lambda c: c.name)
 def weights(request):
     return Lfm2Weights(request.param, seed=7)
 
@@ -79,7 +79,14 @@ def test_prefill_trace_matches_oracle(hip, weights, kv_half):
         errs += [rel(layers[i, t], wlayers[i * cfg.n_embd:(i + 1) * cfg.n_embd]) for i in range(cfg.n_layers)]
         errs += [rel(final[t], wfinal), rel(lg, wl) if t + 1 == len(toks) else 0.0]
         worst = np.maximum(worst, errs)
-    assert worst.max() < HALF_TOLERANCE, worst
+    print(cfg.name, kv_half, "worst per layer", np.array2string(worst, formatter={'float_kind': lambda v: f'{v:.1e}'}))
+    # The prefill GEMM equals the product with half-rounded weights to 1e-5
+    # (test_gpu_ops.py::test_matmul_other_formats); on the mixed-format
+    # model, whose random Q8_0/Q6_K layers amplify that rounding, the layer
+    # outputs stay within 1e-2 (the other models within the 5e-3 of
+    # lfm2_reference.rs:21-25).
+    bound = 1e-2 if cfg.tensor_formats else HALF_TOLERANCE
+    assert worst.max() < bound, worst
     gpu.close()
 
 

@@ -21,21 +21,26 @@ TOLERANCE = 1e-5
 NORM_EPS = 1e-5
 SHAPES = [(1, 32), (7, 64), (7, 256), (1000, 1024), (1024, 1024), (3072, 1024), (4608, 1024),
           (1024, 4608), (65536, 1024)]
-BLOCK = {Format.Q4K: (256, 144, [0, 2]), Format.F16: (1, 2, []), Format.F32: (1, 4, [])}
+BLOCK = {Format.Q4K: (256, 144, [0, 2]), Format.F16: (1, 2, []), Format.F32: (1, 4, []),
+         Format.Q8_0: (32, 34, [0]), Format.Q4_0: (32, 18, [0]), Format.Q5K: (256, 176, [0, 2]),
+         Format.Q6K: (256, 210, [208])}
+# Columns a row must be a multiple of on the GPU (Q8_0/Q4_0 units are two blocks).
+COLS = {Format.Q4K: 256, Format.Q5K: 256, Format.Q6K: 256, Format.Q8_0: 64, Format.Q4_0: 64}
 
 
 def make_weights(rnd: Random, fmt: Format, rows: int, cols: int, big_rng) -> np.ndarray:
     n_el, n_b, scales = BLOCK[fmt]
     nbytes = rows * cols // n_el * n_b
-    if fmt == Format.Q4K:
+    if fmt in COLS:
         if nbytes <= 1 << 20:
             return rnd.blocks(nbytes, n_b, scales)
         # Large shapes: the same distribution from numpy (the xorshift in
         # Python would take minutes).
-        w = big_rng.integers(0, 256, nbytes, dtype=np.uint8).reshape(-1, 144)
-        exp = big_rng.integers(5, 9, (w.shape[0], 2)).astype(np.uint16)
-        man = big_rng.integers(0, 1024, (w.shape[0], 2)).astype(np.uint16)
-        w[:, 0:4] = ((exp << 10) | man).view(np.uint8)
+        w = big_rng.integers(0, 256, nbytes, dtype=np.uint8).reshape(-1, n_b)
+        for at in scales:
+            exp = big_rng.integers(5, 9, w.shape[0]).astype(np.uint16)
+            man = big_rng.integers(0, 1024, w.shape[0]).astype(np.uint16)
+            w[:, at:at + 2] = ((exp << 10) | man).view(np.uint8).reshape(-1, 2)
         return w.reshape(-1)
     vals = rnd.units(rows * cols) if rows * cols <= 1 << 18 else \
         big_rng.uniform(-1, 1, rows * cols).astype(np.float32)
@@ -100,14 +105,15 @@ def launch_error(hip, rnd, fmt, mode, rows, cols, big_rng):
     return float(diff.max() / scale)
 
 
-@pytest.mark.parametrize("fmt", [Format.Q4K])
+@pytest.mark.parametrize("fmt", [Format.Q4K, Format.Q8_0, Format.Q4_0, Format.Q5K, Format.Q6K])
 def test_matvec_kernels_match_scalar(hip, fmt):
+    """metal_matvec.rs:39-45's five block formats over its shapes and modes."""
     rnd = Random(0x9E3779B97F4A7C15)
     big = np.random.default_rng(11)
     failures = []
     for mode in ("plain", "norm", "accumulate", "swiglu"):
         for rows, cols in SHAPES:
-            if cols % 256:
+            if cols % COLS[fmt]:
                 continue
             print(f"matvec {fmt.name} {mode} {rows}x{cols}", flush=True)
             err = launch_error(hip, rnd, fmt, mode, rows, cols, big)

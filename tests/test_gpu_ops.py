@@ -232,6 +232,30 @@ def test_matmul_random_q4k(hip):
     matmul_check(hip, Format.Q4K, w, n_rows, n_cols, n_tokens, Store.OVERWRITE, 5e-3, inputs=x)
 
 
+@pytest.mark.parametrize("fmt", [Format.Q4K, Format.Q6K, Format.Q8_0, Format.Q4_0, Format.Q5K])
+def test_matmul_other_formats(hip, fmt):
+    """The prefill GEMM on every block format of real files: each weight is
+    the scalar path's dequantised value rounded to half (as the reference's
+    expanded half tiles, lfm2_metal.rs:936-985), inputs keep ~22 bits; so
+    the result equals X times the half-rounded dense matrix within 1e-5, and
+    the exact product within the 5e-3 half tolerance."""
+    from bobcat_amd.synth import block_matrix
+
+    rng = np.random.default_rng(int(fmt))
+    n_rows, n_cols, n_tokens = 200, 512, 45
+    w = block_matrix(rng, int(fmt), n_rows, n_cols)
+    x = rng.standard_normal((n_tokens, n_cols)).astype(np.float32)
+    dense = oracle.dequantize(int(fmt), w, n_rows * n_cols).reshape(n_rows, n_cols)
+    exact = x.astype(np.float64) @ dense.astype(np.float64).T
+    halves = x.astype(np.float64) @ dense.astype(np.float16).astype(np.float64).T
+    wb, xb, yb = hip.buffer_from(w), hip.buffer_from(x), hip.new_buffer(n_tokens * n_rows * 4)
+    run(hip, lambda: hip.matmul(fmt, wb.at(0), n_rows, n_cols, xb.at(0), yb.at(0), n_tokens, Store.OVERWRITE))
+    got = hip.read(yb.at(0), np.empty((n_tokens, n_rows), np.float32))
+    scale = np.abs(exact).max()
+    assert np.abs(got - halves).max() / scale < 1e-5
+    assert np.abs(got - exact).max() / scale < 5e-3
+
+
 def test_matmul_f16(hip):
     rng = np.random.default_rng(10)
     n_rows, n_cols, n_tokens = 96, 512, 40
