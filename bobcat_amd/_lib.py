@@ -148,6 +148,8 @@ PROTOTYPES = {
     "bch_attention_prefill": (_int, [_vp, View, View, View, View, _u32, _u32, _u32, _u32, _u32, _u32]),
     "bch_attention_scratch_floats": (_u64, [_u32, _u32, _u32, _u32]),
     "bch_matmul": (_int, [_vp, _u32, View, _u32, _u32, View, View, _u32, _u32]),
+    "bch_matmul_noalloc": (_int, [_vp, _u32, View, _u32, _u32, View, View, _u32, _u32]),
+    "bch_matmul_noalloc_max_bytes": (_u64, []),
     "bch_argmax": (_int, [_vp, View, View, _u32]),
     "bch_read_sum": (_int, [_vp, View, _u64, View, _u32]),
     "bch_route_bytes": (_u64, [_u32, _u32]),

@@ -13,6 +13,7 @@
 // an fp16 high part and an fp16 residual (once per launch, not once per
 // weight tile); both are multiplied, so the inputs keep ~22 bits whatever
 // their magnitude.  Accumulation is fp32.
+#include <mutex>
 #include "formats.h"
 #include "kernels.h"
 #include "runtime.h"
@@ -438,9 +439,83 @@ static void set_lds_limits() {
 #undef BCH_SET
 }
 
+// --- bch_matmul_noalloc: the split inputs in a static device array ---------
+//
+// For callers that cannot allocate (code under graph capture, serving loops
+// that forbid hipMalloc): the per-launch input split lives in `scratch`, a
+// file-scope device array that every GPU the library runs on holds until the
+// process ends.  Its device address on each GPU comes from
+// hipGetSymbolAddress, once per device, when bch_open runs there; host code
+// never passes the array's name itself to a kernel.  All calls on one GPU
+// share the array: calls that overlap on one GPU (two streams, two threads)
+// race on it.  Nothing in it needs clearing (each launch writes every byte it
+// reads).
+
+constexpr uint64_t kNoAllocScratchBytes = 16ull << 20;
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kMaxDevices] = {};
+
+int matmul_noalloc_setup(int device) {
+  if (device < 0 || device >= kMaxDevices) return fail(BCH_ERR_NO_DEVICE, "device %d beyond %d", device, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device]) return BCH_OK;
+  void *p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p)
+    return fail(BCH_ERR_EXECUTION, "cannot find the no-allocation scratch on device %d: %s", device,
+                hipGetErrorString(e));
+  g_scratch_ptr[device] = p;
+  return BCH_OK;
+}
+
+static void *noalloc_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return g_scratch_ptr[device];
+}
+
 }  // namespace bch
 
 using namespace bch;
+
+extern "C" uint64_t bch_matmul_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int bch_matmul_noalloc(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_rows, uint32_t n_cols,
+                                  bch_view x, bch_view y, uint32_t n_tokens, uint32_t store) {
+  if (!matmul_format(format))
+    return fail(BCH_ERR_UNSUPPORTED_FORMAT, "format %u matrices have no matrix-matrix kernel", format);
+  if (store > 2) return fail(BCH_ERR_ARGUMENT, "matmul_noalloc: unknown store mode %u", store);
+  if (n_rows == 0 || n_cols == 0 || n_cols % kBK)
+    return fail(BCH_ERR_ARGUMENT, "matmul_noalloc: %u x %u needs columns in multiples of %d", n_rows, n_cols, kBK);
+  const uint64_t need = matmul_split_bytes(n_tokens, n_cols);
+  if (need > kNoAllocScratchBytes)
+    return fail(BCH_ERR_ARGUMENT,
+                "matmul_noalloc: %u tokens of %u columns need %llu bytes of scratch, more than its %llu "
+                "(use bch_matmul)",
+                n_tokens, n_cols, (unsigned long long)need, (unsigned long long)kNoAllocScratchBytes);
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  const uint8_t *W;
+  const float *xp;
+  float *yp;
+  BCH_TRY(view_ptr(ctx, "matmul_noalloc", weights, rb * n_rows, &W));
+  BCH_TRY(view_ptr(ctx, "matmul_noalloc", x, (uint64_t)n_tokens * n_cols * 4, &xp));
+  BCH_TRY(view_ptr(ctx, "matmul_noalloc", y, (uint64_t)n_tokens * n_rows * 4, &yp));
+  if (reinterpret_cast<uintptr_t>(W) % 16 || reinterpret_cast<uintptr_t>(xp) % 16)
+    return fail(BCH_ERR_ARGUMENT, "matmul_noalloc: weights and inputs must be 16-byte aligned");
+  void *split = noalloc_scratch(ctx->device);
+  if (!split) return fail(BCH_ERR_NO_DEVICE, "matmul_noalloc: the scratch of device %d is not set up", ctx->device);
+  if (!ctx->recording && !ctx->capturing) return fail(BCH_ERR_NOT_RECORDING, "no recording is open");
+  set_lds_limits();
+  // No profiling events here (creating them allocates): the launch only.
+  if (n_tokens) run_matmul(ctx->stream, format, W, n_rows, n_cols, xp, yp, n_tokens, store, split);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(BCH_ERR_EXECUTION, "matmul_noalloc launch: %s", hipGetErrorString(e));
+  return BCH_OK;
+}
 
 extern "C" int bch_matmul(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_rows, uint32_t n_cols,
                           bch_view x, bch_view y, uint32_t n_tokens, uint32_t store) {

@@ -53,6 +53,8 @@ int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 // At least `bytes` of the context's scratch memory; growing it waits for the
 // work in flight (the old region may still be in use).
 int ctx_scratch(bch_ctx *ctx, uint64_t bytes, void **out);
+// Finds bch_matmul_noalloc's static scratch on `device` (current); bch_open calls it.
+int matmul_noalloc_setup(int device);
 int ok();
 
 // Check `view` for `bytes` bytes on behalf of `kernel`; on success store the

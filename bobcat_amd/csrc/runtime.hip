@@ -105,6 +105,12 @@ int bch_open(bch_ctx **out) {
   }
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, 0) == hipSuccess) ctx->n_cus = prop.multiProcessorCount;
+  // The device address of bch_matmul_noalloc's static scratch on this device.
+  if (int rc = matmul_noalloc_setup(ctx->device)) {
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return rc;
+  }
   *out = ctx;
   return BCH_OK;
 }

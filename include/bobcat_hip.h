@@ -217,6 +217,18 @@ int bch_attention_prefill(bch_ctx *ctx, bch_view q, bch_view k_cache, bch_view v
 uint64_t bch_attention_scratch_floats(uint32_t n_heads, uint32_t head_dim, uint32_t n_ctx,
                                       uint32_t n_queries);
 
+/* bch_matmul without any allocation: the same kernels and results as
+ * bch_matmul, with the per-launch input split (n_tokens·(4·n_cols + 4)
+ * bytes) in a static device array of bch_matmul_noalloc_max_bytes() (16 MiB)
+ * that each GPU holds for the life of the process, instead of context
+ * scratch that may grow with hipMalloc.  No counterpart in the reference: it
+ * is for callers that cannot allocate (code under HIP graph capture, serving
+ * loops that forbid allocation).  Larger launches fail with
+ * BCH_ERR_ARGUMENT.  All calls on one GPU share the array, so calls that
+ * overlap on one GPU (other streams or threads) race. */
+int bch_matmul_noalloc(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_rows, uint32_t n_cols,
+                       bch_view x, bch_view y, uint32_t n_tokens, uint32_t store);
+uint64_t bch_matmul_noalloc_max_bytes(void);
 /* Metal::matmul (backend.rs:2470-2516): Y[t] (store) W·X[t] for n_tokens
  * rows of n_cols floats at x; store as bobcat_metal::Store
  * (backend.rs:360-370). */
