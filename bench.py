@@ -14,8 +14,15 @@ Prints ONE JSON line (the driver's contract).  Legs:
   * long  — BASELINE configs[3] part 2 (2.6B only): 128 greedy steps after a
             32,768-token prompt, and a second request that reuses the KV
             cache of a shared 30,000-token prefix: the `long_context` object.
+  * models — the other BASELINE model configs (Qwen3.5-0.8B with a 16K-token
+            prefill, LFM2-8B-A1B, LFM2-350M): pp512/tg128 each, in `models`.
   * cpu   — the oracle (a C restatement of the reference's scalar Rust path)
-            decoding the same model on the host cores, on a bounded sample.
+            decoding the same model on the host, on a bounded sample: one
+            core (the reference's scalar path is single-threaded; `value`)
+            and the host share of 16 threads, plus the config-1 GEMV.
+Every model's greedy tokens are compared with the oracle's run of the same
+seeded model and prompt (tests/golden/greedy_<model>.npz):
+`greedy_matches_oracle`.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--model lfm2-2.6b]
 """
@@ -106,13 +113,38 @@ def gemv_leg(hip, reps: int, copies: int = 64):
                 hot_us=hot * 1e6, hot_gbs=GEMV_BYTES / hot / 1e9)
 
 
+def oracle_tokens(name: str):
+    """The oracle's 128 greedy tokens (and top-2 gaps) for the same seeded model
+    and prompt, from the committed fixture tests/golden/greedy_<name>.npz
+    (written on the CPU by tests/golden/make_greedy.py), or None."""
+    path = os.path.join(ROOT, "tests", "golden", f"greedy_{name}.npz")
+    if not os.path.exists(path):
+        return None
+    f = np.load(path)
+    return f["tokens"].tolist(), f["gaps"].tolist()
+
+
+def greedy_match(got, name: str):
+    """(matches, identical_prefix): matches when the GPU's greedy tokens equal
+    the oracle's, or first differ where the oracle's top-2 logits are within
+    1e-3 (the north-star rule)."""
+    ref = oracle_tokens(name)
+    if ref is None:
+        return None, None
+    want, gaps = ref
+    for i, (a, b) in enumerate(zip(got, want)):
+        if a != b:
+            return gaps[i] < 1e-3, i
+    return True, min(len(got), len(want))
+
+
 def model_leg(hip, weights, steps: int, warmup: int, seed: int = 42):
     from bobcat_amd.lfm2 import Lfm2Hip
     from bobcat_amd.qwen35 import Qwen35Hip, Qwen35Weights
 
     cfg = weights.cfg
     Lfm2Hip = Qwen35Hip if isinstance(weights, Qwen35Weights) else Lfm2Hip
-    rng = np.random.default_rng(seed)
+    rng = np.random.default_rng(seed)  # the prompt of tests/golden/make_greedy.py
     prompt = rng.integers(0, cfg.n_vocab, PROMPT).astype(np.uint32)
     m = Lfm2Hip(hip, weights, n_ctx=PROMPT + GEN, kv_half=True)
     rounds = []
@@ -128,7 +160,10 @@ def model_leg(hip, weights, steps: int, warmup: int, seed: int = 42):
         gpu_decode = m.last_gpu_seconds
         if r >= warmup:
             rounds.append(dict(ttft=t1 - t0, decode=t2 - t1, gpu_decode=gpu_decode))
-        first_tokens = [first] + toks.tolist()
+        # generate() starts from the selection greedy_token() made; the 128th
+        # token is the selection after the last step.
+        assert toks[0] == first
+        first_tokens = toks.tolist() + [m.greedy_token()]
     m.close()
     ttft = sum(x["ttft"] for x in rounds)
     dec = sum(x["decode"] for x in rounds)
@@ -191,10 +226,27 @@ def long_leg(hip, weights, seed: int = 7):
                 reuse_matching_prefix=next((i for i, (a, b) in enumerate(zip(reused, fresh)) if a != b), GEN))
 
 
-def cpu_leg(weights, budget_s: float, threads: int):
+def long_prefill(hip, weights, n: int, seed: int = 9) -> float:
+    """Prefill rate of an n-token random prompt (f16 KV cache), after a warm-up."""
+    from bobcat_amd.qwen35 import Qwen35Hip
+
+    prompt = np.random.default_rng(seed).integers(0, weights.cfg.n_vocab, n).astype(np.uint32)
+    m = Qwen35Hip(hip, weights, n_ctx=n + 8, kv_half=True)
+    m.prefill(prompt[:1024], logits=False)
+    m.reset()
+    t0 = time.perf_counter()
+    m.prefill(prompt, logits=False)
+    m.greedy_token()
+    dt = time.perf_counter() - t0
+    m.close()
+    return n / dt
+
+
+def cpu_model_rate(weights, budget_s: float, threads: int):
     """Decode steps of the oracle on the host: the reference's scalar path
-    (f64-accumulating matvec, lfm2.rs:308-394) restated in C, rows split over
-    `threads` threads.  Bounded: a short prompt, then steps until the budget."""
+    (f64-accumulating matvec, lfm2.rs:308-394 / qwen35.rs:280-516) restated in
+    C, rows split over `threads` threads.  Bounded: a short prompt, then steps
+    until the budget (at least one)."""
     import oracle
 
     oracle.set_threads(threads)
@@ -214,15 +266,81 @@ def cpu_leg(weights, budget_s: float, threads: int):
     return dict(tok_s=n / dt, steps=n, seconds=dt)
 
 
+def cpu_gemv_us(w, x, threads: int, budget_s: float = 2.0):
+    """The oracle's config-1 Q4_K matvec (scalar.rs:213-220) on `threads` threads."""
+    import oracle
+
+    oracle.set_threads(threads)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oracle.matvec(12, w, GEMV_ROWS, GEMV_COLS, x)
+        n += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    return (time.perf_counter() - t0) / n * 1e6
+
+
+def host_cpu():
+    """(online cores, model name) of the host."""
+    cores = os.sysconf("SC_NPROCESSORS_ONLN") if hasattr(os, "sysconf") else (os.cpu_count() or 1)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return int(cores), model
+
+
+def cpu_baseline(weights, gemv_case, budget_s: float):
+    """The reference's CPU path (the oracle) on the host, in the same run: the
+    model's decode rate single-threaded (the reference's scalar path runs on
+    one core) and over the GPU's host share, and the config-1 GEMV time."""
+    online, model = host_cpu()
+    threads = host_threads()
+    one = cpu_model_rate(weights, budget_s / 2, 1)
+    many = cpu_model_rate(weights, budget_s / 2, threads)
+    w, x = gemv_case
+    return dict(one_core=one, all_cores=many, threads=threads, online_cores=online, cpu_model=model,
+                gemv_us_1=cpu_gemv_us(w, x, 1), gemv_us_all=cpu_gemv_us(w, x, threads))
+
+
+def model_summary(cfg, mres, name: str):
+    wb = cfg.weight_bytes()
+    mean_ctx = PROMPT + GEN / 2
+    n_attn = (len(cfg.attention_layers) if hasattr(cfg, "attention_layers")
+              else sum(cfg.is_attention(i) for i in range(cfg.n_layers)))
+    kv_bytes = n_attn * mean_ctx * 2 * cfg.n_kv_heads * cfg.head_dim * 2
+    token_bytes = wb["total"] + kv_bytes
+    decode_gbs = mres["decode_tok_s_device"] * token_bytes / 1e9
+    match, prefix = greedy_match(mres["tokens"], name)
+    return token_bytes, decode_gbs, dict(
+        prefill_tok_s=round(mres["prefill_tok_s"], 1), decode_tok_s=round(mres["decode_tok_s"], 1),
+        decode_tok_s_device=round(mres["decode_tok_s_device"], 1), ttft_ms=round(mres["ttft_ms"], 3),
+        tpot_ms=round(mres["tpot_ms"], 4), decode_bytes_per_token=int(token_bytes),
+        decode_hbm_gbs=round(decode_gbs, 1), decode_roofline_frac=round(decode_gbs / HBM_PEAK_GBS, 4),
+        greedy_matches_oracle=match, greedy_identical_prefix=prefix)
+
+
+# The seeded random-init weights of tests/golden/make_greedy.py, so the
+# generated tokens can be checked against the oracle's fixtures.
+WEIGHT_SEED = 3
+SIDE_MODELS = ("qwen3.5-0.8b", "lfm2-8b-a1b", "lfm2-350m")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3, help="timed pp512/tg128 rounds")
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--model", default="lfm2-2.6b")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-long", action="store_true", help="skip the 32K-context leg")
+    ap.add_argument("--skip-side", action="store_true", help="skip the other model configs")
     ap.add_argument("--long-only", action="store_true", help="only the 32K-context leg (for profiling)")
     ap.add_argument("--gemv-only", action="store_true", help="only the config-1 GEMV leg (for profiling)")
     args = ap.parse_args()
@@ -234,16 +352,19 @@ def main() -> int:
     from bobcat_amd.backend import Hip
     from bobcat_amd.lfm2 import CONFIGS, Lfm2Weights
     from bobcat_amd.qwen35 import CONFIGS as QWEN_CONFIGS, Qwen35Weights
+    from bobcat_amd.synth import gemv_case
 
-    if args.model in QWEN_CONFIGS:
-        cfg, Lfm2Weights = QWEN_CONFIGS[args.model], Qwen35Weights
-    else:
-        cfg = CONFIGS[args.model]
+    def weights_of(name):
+        if name in QWEN_CONFIGS:
+            return Qwen35Weights(QWEN_CONFIGS[name], seed=WEIGHT_SEED)
+        return Lfm2Weights(CONFIGS[name], seed=WEIGHT_SEED)
+
+    side = {}
     with Hip() as hip:
         name, cus = hip.device_info()
         log(f"device: {name}, {cus} CUs")
         if args.long_only:
-            lres = long_leg(hip, Lfm2Weights(cfg, seed=0))
+            lres = long_leg(hip, weights_of(args.model))
             log(f"long context: {lres}")
             return 0
         g = gemv_leg(hip, reps=10)
@@ -251,7 +372,8 @@ def main() -> int:
         if args.gemv_only:
             return 0
         t = time.perf_counter()
-        weights = Lfm2Weights(cfg, seed=0)
+        weights = weights_of(args.model)
+        cfg = weights.cfg
         log(f"generated {cfg.name} weights in {time.perf_counter() - t:.1f}s")
         mres = model_leg(hip, weights, args.steps, args.warmup)
         log(f"model: { {k: v for k, v in mres.items() if k != 'tokens'} }")
@@ -259,20 +381,22 @@ def main() -> int:
         if not args.skip_long and cfg.name == "lfm2-2.6b":
             lres = long_leg(hip, weights)
             log(f"long context: {lres}")
-    threads = host_threads()
-    cpu = None if args.skip_cpu else cpu_leg(weights, args.cpu_seconds, threads)
+        if not args.skip_side:
+            for sname in SIDE_MODELS:
+                if sname == cfg.name:
+                    continue
+                sw = weights_of(sname)
+                sres = model_leg(hip, sw, steps=2, warmup=1)
+                side[sname] = model_summary(sw.cfg, sres, sname)[2]
+                if sname.startswith("qwen"):
+                    side[sname]["prefill_16k_tok_s"] = round(long_prefill(hip, sw, 16384), 1)
+                log(f"{sname}: {side[sname]}")
+                del sw
+    cpu = None if args.skip_cpu else cpu_baseline(weights, gemv_case(), args.cpu_seconds)
     if cpu:
-        log(f"cpu: {cpu} ({threads} threads)")
+        log(f"cpu: {cpu}")
 
-    wb = cfg.weight_bytes()
-    # Bytes a decode token streams: all layer matrices + the output matrix
-    # + the KV cache read at the mean context of tg128 after pp512.
-    mean_ctx = PROMPT + GEN / 2
-    n_attn = (len(cfg.attention_layers) if hasattr(cfg, "attention_layers")
-              else sum(cfg.is_attention(i) for i in range(cfg.n_layers)))
-    kv_bytes = n_attn * mean_ctx * 2 * cfg.n_kv_heads * cfg.head_dim * 2
-    token_bytes = wb["total"] + kv_bytes
-    decode_gbs = mres["decode_tok_s_device"] * token_bytes / 1e9
+    token_bytes, decode_gbs, summary = model_summary(cfg, mres, cfg.name)
     line = {
         "metric": "decode tok/s (pp512/tg128, 1 GPU)",
         "value": round(mres["decode_tok_s"], 1),
@@ -285,26 +409,26 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "q4k-f32",
-        "data": "synthetic (random-init weights of the config's shapes, 512 random prompt ids)",
+        "data": "synthetic (random-init weights of the config's shapes, seed 3; 512 random prompt ids, seed 42)",
         "config": {"workload": f"{cfg.name} pp512/tg128 (BASELINE configs[3])" if cfg.name == "lfm2-2.6b"
                    else f"{cfg.name} pp512/tg128", "prompt": PROMPT, "generated": GEN, "kv_cache": "f16",
                    "parallelism": "none"},
-        "prefill_tok_s": round(mres["prefill_tok_s"], 1),
-        "decode_tok_s_device": round(mres["decode_tok_s_device"], 1),
-        "ttft_ms": round(mres["ttft_ms"], 3),
-        "tpot_ms": round(mres["tpot_ms"], 4),
-        "decode_bytes_per_token": int(token_bytes),
-        "decode_hbm_gbs": round(decode_gbs, 1),
-        "decode_roofline_frac": round(decode_gbs / HBM_PEAK_GBS, 4),
+        **{k: v for k, v in summary.items() if k != "decode_tok_s"},
         "long_context": lres,
+        "models": side or None,
         "roofline": {"kernel": "matvec_q4k (config 1, 8192x2048)", "bound": "hbm",
                      "achieved": round(g["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "us_per_launch": round(g["us"], 3)},
         "cpu_baseline": None if cpu is None else {
-            "value": round(cpu["tok_s"], 4), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{cpu['steps']} decode steps of {cfg.name} by the oracle (C restatement of the "
-                      f"reference's scalar path, f64 accumulate, rows over {threads} threads)"},
+            "value": round(cpu["one_core"]["tok_s"], 4), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"{cpu['one_core']['steps']} decode steps of {cfg.name} by the oracle (C restatement of "
+                      f"the reference's scalar path, f64 accumulate) on one core",
+            "all_cores": {"value": round(cpu["all_cores"]["tok_s"], 4), "cores": cpu["threads"],
+                          "sample": f"{cpu['all_cores']['steps']} decode steps, rows over {cpu['threads']} threads"},
+            "host": {"online_cores": cpu["online_cores"], "cpu_model": cpu["cpu_model"]},
+            "gemv_config1_us": {"1_core": round(cpu["gemv_us_1"], 1),
+                                f"{cpu['threads']}_cores": round(cpu["gemv_us_all"], 1)}},
     }
     print(json.dumps(line), flush=True)
     return 0

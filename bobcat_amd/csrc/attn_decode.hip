@@ -41,6 +41,8 @@ constexpr int kChunks = 8;       // 16-byte chunks of K (and of V) per thread
 constexpr int kKeys = 1024;      // positions per split, at most
 constexpr int kHd = 256;         // head size, at most
 constexpr uint32_t kXcds = 8;
+// Splits up to which the prefill form combines with one thread per element.
+constexpr uint32_t kSerialCombine = 8;
 
 // Workgroups of one launch: (head, split) items padded to whole runs of a
 // KV group's heads on every XCD (the kernel's item mapping needs that).
@@ -376,6 +378,17 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
       coherent_store(pp + 1, l_s);
     }
   }
+  // Hand-off to the last workgroup of this (query, head), by the hardware's
+  // ordering rather than release/acquire fences (an agent-scope release
+  // writes back the XCD's whole L2: 32K-context decode fell from 805 to 434
+  // tok/s with it).  The partials are agent-scope atomic stores, which
+  // gfx950 performs write-through at the device coherence point (sc1); the
+  // signal fence stops the compiler from sinking them below the wait, and
+  // s_waitcnt(0) holds each thread until its stores are acknowledged there.
+  // Only then does the barrier let thread 0 count in with a device atomic,
+  // and the last workgroup reads the partials with agent-scope atomic loads
+  // (sc1, from the coherence point) issued after that atomic returned.
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) {
@@ -385,11 +398,12 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
   __syncthreads();
   if (!last_s) return;
   const float *pp = a.partials + (uint64_t)slot * a.max_splits * stride;
-  if constexpr (FUSED) {
+  if (FUSED || n_splits > kSerialCombine) {
     const float o_all = combine_partials<kDecThreads>(pp, n_splits, stride, hd);
     if (tid < hd) outp[tid] = o_all * gate;
   } else if (tid < hd) {
-    // A prefill query spans a few splits at most: one thread per element.
+    // A prefill query over a short context spans a few splits: one thread
+    // per element walks them (long contexts take the workgroup-wide combine).
     float M = -INFINITY;
     for (uint32_t sp = 0; sp < n_splits; sp++) M = fmaxf(M, coherent_load(pp + sp * stride));
     float L = 0.f, O = 0.f;

@@ -196,11 +196,16 @@ int Sequence::step(uint32_t token, float *out_logits, float *trace_embedding, fl
   const uint64_t tstride = (uint64_t)trace_rows * n;
   if (out_logits)
     BCH_TRY(check_hip(hipMemcpy(out_logits, logits, (uint64_t)n_vocab * 4, hipMemcpyDeviceToHost), "read logits"));
-  if (trace_embedding) hipMemcpy(trace_embedding, trace, (uint64_t)n * 4, hipMemcpyDeviceToHost);
+  if (trace_embedding)
+    BCH_TRY(check_hip(hipMemcpy(trace_embedding, trace, (uint64_t)n * 4, hipMemcpyDeviceToHost), "read trace"));
   if (trace_layers)
     for (uint32_t il = 0; il < n_layers; il++)
-      hipMemcpy(trace_layers + (uint64_t)il * n, trace + (1 + il) * tstride, (uint64_t)n * 4, hipMemcpyDeviceToHost);
-  if (trace_final) hipMemcpy(trace_final, trace + (1 + n_layers) * tstride, (uint64_t)n * 4, hipMemcpyDeviceToHost);
+      BCH_TRY(check_hip(hipMemcpy(trace_layers + (uint64_t)il * n, trace + (1 + il) * tstride, (uint64_t)n * 4,
+                                  hipMemcpyDeviceToHost),
+                        "read trace"));
+  if (trace_final)
+    BCH_TRY(check_hip(hipMemcpy(trace_final, trace + (1 + n_layers) * tstride, (uint64_t)n * 4, hipMemcpyDeviceToHost),
+                      "read trace"));
   n_past++;
   have_logits = true;
   return BCH_OK;
@@ -235,13 +240,18 @@ int Sequence::prefill(const uint32_t *toks, uint32_t n_tokens, float *out_logits
     }
     if (traced) {
       const uint64_t rows = (uint64_t)count * n * 4;
-      if (trace_embedding) hipMemcpy(trace_embedding + (uint64_t)done * n, trace, rows, hipMemcpyDeviceToHost);
+      if (trace_embedding)
+        BCH_TRY(check_hip(hipMemcpy(trace_embedding + (uint64_t)done * n, trace, rows, hipMemcpyDeviceToHost),
+                          "read trace"));
       if (trace_final)
-        hipMemcpy(trace_final + (uint64_t)done * n, trace + (1 + n_layers) * tstride, rows, hipMemcpyDeviceToHost);
+        BCH_TRY(check_hip(hipMemcpy(trace_final + (uint64_t)done * n, trace + (1 + n_layers) * tstride, rows,
+                                    hipMemcpyDeviceToHost),
+                          "read trace"));
       if (trace_layers)
         for (uint32_t il = 0; il < n_layers; il++)
-          hipMemcpy(trace_layers + ((uint64_t)il * n_tokens + done) * n, trace + (1 + il) * tstride, rows,
-                    hipMemcpyDeviceToHost);
+          BCH_TRY(check_hip(hipMemcpy(trace_layers + ((uint64_t)il * n_tokens + done) * n, trace + (1 + il) * tstride,
+                                      rows, hipMemcpyDeviceToHost),
+                            "read trace"));
     }
   }
   last_gpu_seconds = gpu;

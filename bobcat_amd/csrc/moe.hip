@@ -217,6 +217,14 @@ __global__ __launch_bounds__(256) void k_moe_scores(const float *__restrict__ x,
     acc = wave_sum(acc);
     if (lane == 0) coherent_store(scores + (uint64_t)t * n_experts + e, 1.0f / (1.0f + expf(-acc)));
   }
+  // Hand-off to the token's last workgroup, by the hardware's ordering (as
+  // in attn_decode.hip; an agent-scope release would write back the whole
+  // L2): the scores are agent-scope atomic stores written through to the
+  // coherence point, acknowledged before the barrier (s_waitcnt(0); the
+  // signal fence keeps the compiler from sinking them), then counted in by
+  // a device atomic, and the last workgroup reads them with agent-scope
+  // atomic loads issued after its atomic returned.
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) {

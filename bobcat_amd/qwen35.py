@@ -89,7 +89,15 @@ QWEN35_TINY = Qwen35Config("qwen3.5-tiny", n_embd=256, n_ff=512, n_vocab=1000, n
 QWEN35_TINY_64 = Qwen35Config("qwen3.5-tiny-64", n_embd=256, n_ff=768, n_vocab=777, n_layers=4, n_heads=4,
                               n_kv_heads=2, head_dim=64, n_rot=32, n_k_heads=2, n_v_heads=4, k_head_dim=64,
                               v_head_dim=64)
-CONFIGS = {c.name: c for c in (QWEN35_0_8B, QWEN35_TINY, QWEN35_TINY_64)}
+# Value heads of 256 with key heads of 64, and of 192 with 128: the decode
+# step's 1024- and 768-lane workgroups with the fused gated norm.
+QWEN35_TINY_V256 = Qwen35Config("qwen3.5-tiny-v256", n_embd=256, n_ff=512, n_vocab=500, n_layers=4, n_heads=2,
+                                n_kv_heads=1, head_dim=128, n_rot=64, n_k_heads=1, n_v_heads=2, k_head_dim=64,
+                                v_head_dim=256)
+QWEN35_TINY_V192 = Qwen35Config("qwen3.5-tiny-v192", n_embd=256, n_ff=512, n_vocab=500, n_layers=4, n_heads=2,
+                                n_kv_heads=1, head_dim=128, n_rot=32, n_k_heads=2, n_v_heads=4, k_head_dim=128,
+                                v_head_dim=192)
+CONFIGS = {c.name: c for c in (QWEN35_0_8B, QWEN35_TINY, QWEN35_TINY_64, QWEN35_TINY_V256, QWEN35_TINY_V192)}
 
 
 @dataclass
