@@ -24,7 +24,7 @@ STATUS_NAMES = {
     0: "OK", 1: "NoDevice", 2: "Allocation", 3: "NotRecording", 4: "AlreadyRecording",
     5: "OutOfBounds", 6: "ForeignBuffer", 7: "Busy", 8: "Access", 9: "AttentionLimits",
     10: "UnsupportedFormat", 11: "DeltaNetLimits", 12: "ExpertLimits", 13: "Execution",
-    14: "Argument", 15: "ContextFull", 16: "Token", 17: "GateShape",
+    14: "Argument", 15: "ContextFull", 16: "Token", 17: "GateShape", 18: "Gguf", 19: "Model",
 }
 STATUS = {v: k for k, v in STATUS_NAMES.items()}
 
@@ -54,6 +54,11 @@ class ProfileEntry(C.Structure):
 class Matrix(C.Structure):
     _fields_ = [("format", C.c_uint32), ("n_rows", C.c_uint32), ("n_cols", C.c_uint32),
                 ("data", C.c_void_p)]
+
+
+class GgufTensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("n_dims", C.c_uint32), ("ne", C.c_uint64 * 4), ("type", C.c_uint32),
+                ("data", C.c_void_p), ("offset", C.c_uint64), ("bytes", C.c_uint64)]
 
 
 _FP = C.POINTER(C.c_float)
@@ -195,6 +200,22 @@ PROTOTYPES = {
     "bch_lfm2_generate": (_int, [_vp, C.POINTER(_u32), _u32]),
     "bch_lfm2_generate_next": (_int, [_vp, C.POINTER(_u32), _u32]),
     "bch_lfm2_generate_stream": (_int, [_vp, _u32, EMIT_FN, _vp, C.POINTER(_u32), C.POINTER(_u32)]),
+    "bch_gguf_parse": (_int, [_vp, _u64, C.POINTER(_vp)]),
+    "bch_gguf_open": (_int, [C.c_char_p, C.POINTER(_vp)]),
+    "bch_gguf_free": (None, [_vp]),
+    "bch_gguf_bytes": (_vp, [_vp, C.POINTER(_u64)]),
+    "bch_gguf_u32": (_int, [_vp, C.c_char_p, C.POINTER(_u32)]),
+    "bch_gguf_f32": (_int, [_vp, C.c_char_p, C.POINTER(C.c_float)]),
+    "bch_gguf_bool": (_int, [_vp, C.c_char_p, C.POINTER(_int)]),
+    "bch_gguf_string": (_int, [_vp, C.c_char_p, C.POINTER(_vp), C.POINTER(_u64)]),
+    "bch_gguf_array_len": (_int, [_vp, C.c_char_p, C.POINTER(_u64)]),
+    "bch_gguf_array_u32": (_int, [_vp, C.c_char_p, _u64, C.POINTER(_u32)]),
+    "bch_gguf_array_string": (_int, [_vp, C.c_char_p, _u64, C.POINTER(_vp), C.POINTER(_u64)]),
+    "bch_gguf_tensor": (_int, [_vp, C.c_char_p, C.POINTER(GgufTensor)]),
+    "bch_gguf_n_tensors": (_u64, [_vp]),
+    "bch_gguf_tensor_at": (_int, [_vp, _u64, C.POINTER(GgufTensor)]),
+    "bch_lfm2_model_from_gguf": (_int, [_vp, C.POINTER(Lfm2Model), C.POINTER(Lfm2Layer), _u32]),
+    "bch_qwen35_model_from_gguf": (_int, [_vp, C.POINTER(Qwen35Model), C.POINTER(Qwen35Layer), _u32]),
     "bch_lfm2_checkpoint_bytes": (_u64, [_vp]),
     "bch_lfm2_checkpoint": (_int, [_vp, _vp, _u64]),
     "bch_lfm2_restore": (_int, [_vp, _vp, _u64]),

@@ -50,6 +50,9 @@ typedef enum bch_status {
   BCH_ERR_CONTEXT_FULL = 15,    /* bobcat::Error::ContextFull */
   BCH_ERR_TOKEN = 16,           /* bobcat::Error::Token */
   BCH_ERR_GATE_SHAPE = 17,      /* Error::GateShape */
+  BCH_ERR_GGUF = 18,            /* bobcat_gguf::Error (crates/bobcat-gguf/src/lib.rs:27-95) */
+  BCH_ERR_MODEL = 19,           /* bobcat::Error::{Metadata, Architecture, Hyperparameters, MissingTensor,
+                                   TensorShape, TensorType, KvHeads, OddHeadDim} of a model file */
 } bch_status;
 
 /* Return the message of the last failed call on this thread ("" if none). */
@@ -571,6 +574,58 @@ uint64_t bch_qwen35_checkpoint_bytes(const bch_qwen35 *qwen);
 int bch_qwen35_checkpoint(bch_qwen35 *qwen, void *blob, uint64_t bytes);
 int bch_qwen35_restore(bch_qwen35 *qwen, const void *blob, uint64_t bytes);
 double bch_qwen35_last_gpu_seconds(const bch_qwen35 *qwen);
+
+/* ------------------------------------------------------------------ */
+/* GGUF files (crates/bobcat-gguf/src/lib.rs) and model loading         */
+/* ------------------------------------------------------------------ */
+
+typedef struct bch_gguf bch_gguf;
+
+/* One tensor of a GGUF file (bobcat_gguf::Tensor, lib.rs:265-296). */
+typedef struct bch_gguf_tensor_info {
+  const char *name;    /* valid while the file is open */
+  uint32_t n_dims;
+  uint64_t ne[4];      /* innermost first; 1 past n_dims */
+  uint32_t type;       /* ggml type id = bch_format */
+  const void *data;    /* the tensor's bytes in the file */
+  uint64_t offset;     /* of the data from the file's start */
+  uint64_t bytes;
+} bch_gguf_tensor_info;
+
+/* Gguf::parse (lib.rs:310-345): parse `size` bytes the caller keeps alive
+ * until bch_gguf_free.  Every read is checked against the end and every size
+ * against overflow; a malformed file fails with BCH_ERR_GGUF and the
+ * reference's message (bch_last_error). */
+int bch_gguf_parse(const void *bytes, uint64_t size, bch_gguf **out);
+/* The same over a read-only mapping of the file at `path` (Storage::open). */
+int bch_gguf_open(const char *path, bch_gguf **out);
+void bch_gguf_free(bch_gguf *gguf);
+/* Gguf::bytes (lib.rs:348-351). */
+const void *bch_gguf_bytes(const bch_gguf *gguf, uint64_t *size);
+/* Gguf::u32 / f32 / bool / string / array_len / array_u32 / string_array
+ * (lib.rs:358-455): BCH_ERR_ARGUMENT when the key is absent or of another
+ * type (u32: any integer that fits; f32: F32 or F64). */
+int bch_gguf_u32(const bch_gguf *gguf, const char *key, uint32_t *out);
+int bch_gguf_f32(const bch_gguf *gguf, const char *key, float *out);
+int bch_gguf_bool(const bch_gguf *gguf, const char *key, int *out);
+int bch_gguf_string(const bch_gguf *gguf, const char *key, const char **ptr, uint64_t *len);
+int bch_gguf_array_len(const bch_gguf *gguf, const char *key, uint64_t *count);
+int bch_gguf_array_u32(const bch_gguf *gguf, const char *key, uint64_t index, uint32_t *out);
+int bch_gguf_array_string(const bch_gguf *gguf, const char *key, uint64_t index, const char **ptr, uint64_t *len);
+/* Gguf::tensor / tensor_data (lib.rs:458-466), and the tensors in file order. */
+int bch_gguf_tensor(const bch_gguf *gguf, const char *name, bch_gguf_tensor_info *out);
+uint64_t bch_gguf_n_tensors(const bch_gguf *gguf);
+int bch_gguf_tensor_at(const bch_gguf *gguf, uint64_t index, bch_gguf_tensor_info *out);
+
+/* lfm2::Model::load (lfm2.rs:186-232, 737-1004) for "lfm2" and "lfm2moe"
+ * files: fills `model` and layers[0..n_layers) (room for max_layers) with
+ * the hyperparameters and pointers into the file, ready for bch_lfm2_new;
+ * the file stays open while they are used.  Errors: BCH_ERR_MODEL. */
+int bch_lfm2_model_from_gguf(const bch_gguf *gguf, bch_lfm2_model *model, bch_lfm2_layer *layers,
+                             uint32_t max_layers);
+/* qwen35::Model::load (qwen35.rs:186-230, 630-745) for "qwen35" files. */
+int bch_qwen35_model_from_gguf(const bch_gguf *gguf, bch_qwen35_model *model, bch_qwen35_layer *layers,
+                               uint32_t max_layers);
 
 #ifdef __cplusplus
 }

@@ -108,3 +108,29 @@ def test_greedy_128_matches_oracle(hip, model):
     same = next((i for i, (a, b) in enumerate(zip(got_h, want)) if a != b), N_GEN)
     print(f"{name}: f16 cache agrees with the oracle on the first {same} tokens")
     half.close()
+
+
+@pytest.mark.timeout(600)
+def test_350m_from_gguf_file(hip, tmp_path):
+    """configs[1] written as a GGUF file with real LFM2 tensor names, opened
+    with bch_gguf_open and loaded by bch_lfm2_model_from_gguf: its 128 greedy
+    tokens after the 512-token prompt equal the oracle's."""
+    from bobcat_amd.gguf import GgufWeights, lfm2_to_gguf
+
+    name = "lfm2-350m"
+    path = fixture_path(name)
+    if not path.exists():
+        pytest.skip(f"{path.name} not generated")
+    cfg, wcls, _ = MODELS[name]
+    weights = wcls(cfg, seed=WEIGHT_SEED)
+    fix = np.load(path)
+    file = tmp_path / "lfm2-350m.gguf"
+    lfm2_to_gguf(weights, file)
+    del weights
+    gw = GgufWeights(file, cfg)
+    prompt = fix["prompt"].tolist()
+    gpu = Lfm2Hip(hip, gw, n_ctx=len(prompt) + N_GEN + 8, kv_half=False)
+    lg = gpu.prefill(prompt)
+    assert rel(lg, fix["logits0"]) < HALF_TOLERANCE
+    assert first_divergence(gpu.generate(N_GEN).tolist(), fix["tokens"].tolist(), fix["gaps"]) is None
+    gpu.close()

@@ -394,3 +394,22 @@ def test_greedy_selection_preserves_sequence_state(hip, weights):
         with pytest.raises(BobcatError):
             gpu.greedy_token()
         gpu.close()
+
+
+def test_gguf_model_matches_direct_upload(hip, weights, tmp_path):
+    """The model written as an LFM2 GGUF file (tensor names and metadata of
+    real files) and loaded through bch_gguf_open + bch_lfm2_model_from_gguf
+    decodes bit-identically to the same weights uploaded directly."""
+    from bobcat_amd.gguf import GgufWeights, lfm2_to_gguf
+
+    cfg = weights.cfg
+    path = tmp_path / "m.gguf"
+    lfm2_to_gguf(weights, path)
+    gw = GgufWeights(path, cfg)
+    toks = prompt(cfg, 9, seed=41)
+    a = Lfm2Hip(hip, weights, n_ctx=32)
+    b = Lfm2Hip(hip, gw, n_ctx=32)
+    assert np.array_equal(a.prefill(toks), b.prefill(toks))
+    assert np.array_equal(a.generate(6), b.generate(6))
+    a.close()
+    b.close()

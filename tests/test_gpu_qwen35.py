@@ -391,3 +391,21 @@ def test_gdn_chunked_matches_float64(hip, n_k, n_v, dk, dv, n_tokens):
     assert rel(got, want) < 1e-5
     assert rel(got_state, want_state) < 1e-5
     assert rel(got, seq) < 1e-5
+
+
+def test_gguf_model_matches_direct_upload(hip, weights, tmp_path):
+    """The model written as a qwen35 GGUF file and loaded through
+    bch_qwen35_model_from_gguf decodes bit-identically to the direct upload."""
+    from bobcat_amd.gguf import GgufWeights, qwen35_to_gguf
+
+    cfg = weights.cfg
+    path = tmp_path / "q.gguf"
+    qwen35_to_gguf(weights, path)
+    gw = GgufWeights(path, cfg)
+    toks = prompt(cfg, 9, seed=41)
+    a = Qwen35Hip(hip, weights, n_ctx=32)
+    b = Qwen35Hip(hip, gw, n_ctx=32)
+    assert np.array_equal(a.prefill(toks), b.prefill(toks))
+    assert np.array_equal(a.generate(6), b.generate(6))
+    a.close()
+    b.close()
