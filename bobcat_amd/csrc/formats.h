@@ -516,4 +516,147 @@ struct Q5K {
   }
 };
 
+// --- Q4_K with integer activations --------------------------------------
+//
+// The decode GEMV's Q4_K path.  The staged input is turned, once per
+// workgroup, into exact integers per 32-element block: with E the exponent
+// of the block's largest |x| (|x| < 2^E), x_int = rint(x · 2^(21−E)) (22
+// bits, error ≤ 2^(E−22), below the rounding of the block's largest
+// element), split into three signed bytes x_int = d0 + 2^8·d1 + 2^16·d2
+// (d0, d1 in [−128, 127], d2 in [−32, 32]).  Then Σ q·x_int over a block is
+// three v_dot4_i32_i8 per four nibbles on the raw nibble bytes, exact in
+// int32 (|Σ| ≤ 32·15·2^21 < 2^31), instead of a conversion and an FMA per
+// weight; the block's scale 2^(E−21) is folded into the (d·sc) multiply.
+// The minimum term uses the block sums of the unquantised inputs.
+constexpr uint32_t kDigitUnitBytes = 208;  // 3 planes × 2 blocks × 32 bytes, then xs[2], sum[2]
+
+struct Q4K8 {
+  static constexpr uint32_t kFormat = 12;
+  static constexpr uint32_t kUnit = 64;
+  static constexpr bool kDigits = true;
+  struct Frag {
+    uint32_t d[3][2][8];  // [digit][block of the pair][4 elements each]
+    float xs[2], sum[2];
+  };
+  // The unit's digits and block constants from its slot in LDS.
+  __device__ __forceinline__ static void from_lds(const float *p, Frag &f) {
+    const uint4 *p4 = reinterpret_cast<const uint4 *>(p);
+#pragma unroll
+    for (int dg = 0; dg < 3; dg++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const uint4 a = p4[(dg * 2 + h) * 2], b = p4[(dg * 2 + h) * 2 + 1];
+        f.d[dg][h][0] = a.x, f.d[dg][h][1] = a.y, f.d[dg][h][2] = a.z, f.d[dg][h][3] = a.w;
+        f.d[dg][h][4] = b.x, f.d[dg][h][5] = b.y, f.d[dg][h][6] = b.z, f.d[dg][h][7] = b.w;
+      }
+    const float4 m = reinterpret_cast<const float4 *>(p)[12];
+    f.xs[0] = m.x, f.xs[1] = m.y, f.sum[0] = m.z, f.sum[1] = m.w;
+  }
+  using Raw = Q4K::Raw;
+  __device__ __forceinline__ static Raw fetch(const uint8_t *__restrict__ row, uint32_t u) { return Q4K::fetch(row, u); }
+  __device__ __forceinline__ static float compute(const Raw &raw, uint32_t u, const Frag &f) {
+    const int p = u & 3;
+    const uint4 q0 = raw.q0, q1 = raw.q1;
+    const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int lo = (int)(qw[k] & 0x0f0f0f0fu), hi = (int)((qw[k] >> 4) & 0x0f0f0f0fu);
+      a0 = __builtin_amdgcn_sdot4(lo, (int)f.d[0][0][k], a0, false);
+      a1 = __builtin_amdgcn_sdot4(lo, (int)f.d[1][0][k], a1, false);
+      a2 = __builtin_amdgcn_sdot4(lo, (int)f.d[2][0][k], a2, false);
+      b0 = __builtin_amdgcn_sdot4(hi, (int)f.d[0][1][k], b0, false);
+      b1 = __builtin_amdgcn_sdot4(hi, (int)f.d[1][1][k], b1, false);
+      b2 = __builtin_amdgcn_sdot4(hi, (int)f.d[2][1][k], b2, false);
+    }
+    const float v_lo = (float)(a0 + a1 * 256 + a2 * 65536);
+    const float v_hi = (float)(b0 + b1 * 256 + b2 * 65536);
+    const uint4 h = raw.h;
+    const uint32_t sc = q4k_pair_scales(h.y, h.z, h.w, p);
+    const float d = half_bits_to_float(h.x & 0xffffu);
+    const float dmin = half_bits_to_float(h.x >> 16);
+    const float qs = ubyte0(sc) * (f.xs[0] * v_lo) + ubyte1(sc) * (f.xs[1] * v_hi);
+    const float ms = ubyte2(sc) * f.sum[0] + ubyte3(sc) * f.sum[1];
+    return d * qs - dmin * ms;
+  }
+};
+
+// Convert the staged inputs of a workgroup (n_units slots of kSlot floats,
+// unit u's 64 inputs at slot u) into Q4K8's digit form, in place.  T
+// threads; thread t takes chunks of 8 inputs c = t, t + T, ... (chunk c is
+// inputs 8·(c % 8) .. +7 of unit c / 8); the four chunks of a 32-element
+// block sit in four consecutive lanes of one wave.  Reads everything, waits
+// for the whole workgroup, then writes.
+template <int T, int kSlot, int kMaxChunks>
+__device__ __forceinline__ void digitize_units(float *xs, uint32_t n_units) {
+  const uint32_t tid = threadIdx.x, n_chunks = n_units * 8;
+  float v[kMaxChunks][8];
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; i++) {
+    const uint32_t c = tid + (uint32_t)i * T;
+    if (c < n_chunks) {
+      const float4 *src = reinterpret_cast<const float4 *>(xs + (c / 8) * kSlot + (c % 8) * 8);
+      const float4 a = src[0], b = src[1];
+      v[i][0] = a.x, v[i][1] = a.y, v[i][2] = a.z, v[i][3] = a.w;
+      v[i][4] = b.x, v[i][5] = b.y, v[i][6] = b.z, v[i][7] = b.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[i][j] = 0.f;
+    }
+  }
+  uint32_t planes[kMaxChunks][3][2];
+  float inv[kMaxChunks], sums[kMaxChunks];
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; i++) {
+    float mx = 0.f, sm = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      mx = fmaxf(mx, fabsf(v[i][j]));
+      sm += v[i][j];
+    }
+    // The block's four chunks: consecutive lanes (T and the chunk numbering
+    // keep c % 4 == lane % 4).
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+    sm += __shfl_xor(sm, 1, 64);
+    sm += __shfl_xor(sm, 2, 64);
+    int e = 0;
+    if (mx > 0.f) frexpf(mx, &e);  // mx < 2^e
+    const float scale = ldexpf(1.0f, 21 - e);
+    inv[i] = ldexpf(1.0f, e - 21);
+    sums[i] = sm;
+    uint32_t pk[3][2] = {};
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int xi = (int)rintf(v[i][j] * scale);
+      const int d0 = (int)(int8_t)(xi & 0xff);
+      const int r = (xi - d0) >> 8;
+      const int d1 = (int)(int8_t)(r & 0xff);
+      const int d2 = (r - d1) >> 8;
+      const int sh = 8 * (j % 4);
+      pk[0][j / 4] |= ((uint32_t)d0 & 0xffu) << sh;
+      pk[1][j / 4] |= ((uint32_t)d1 & 0xffu) << sh;
+      pk[2][j / 4] |= ((uint32_t)d2 & 0xffu) << sh;
+    }
+#pragma unroll
+    for (int dg = 0; dg < 3; dg++) planes[i][dg][0] = pk[dg][0], planes[i][dg][1] = pk[dg][1];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; i++) {
+    const uint32_t c = tid + (uint32_t)i * T;
+    if (c < n_chunks) {
+      uint8_t *slot = reinterpret_cast<uint8_t *>(xs + (c / 8) * kSlot);
+      const uint32_t h = (c % 8) / 4, j0 = (c % 4) * 8;
+#pragma unroll
+      for (int dg = 0; dg < 3; dg++)
+        *reinterpret_cast<uint2 *>(slot + (dg * 2 + h) * 32 + j0) = make_uint2(planes[i][dg][0], planes[i][dg][1]);
+      if (c % 4 == 0) {
+        reinterpret_cast<float *>(slot + 192)[h] = inv[i];
+        reinterpret_cast<float *>(slot + 200)[h] = sums[i];
+      }
+    }
+  }
+}
+
 }  // namespace bch

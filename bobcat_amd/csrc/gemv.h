@@ -248,6 +248,10 @@ struct PreOf<P, true> {
   using type = typename P::Pre;
 };
 
+
+template <class F>
+constexpr bool kDigitsOf = requires { F::kDigits; };
+
 template <int LPR>
 __device__ __forceinline__ float group_total(float v, float *lds_scratch, int slot) {
   if constexpr (LPR <= 64) {
@@ -343,6 +347,11 @@ __global__ __launch_bounds__(256) void k_gemv(P p, const float *__restrict__ x, 
     if (tid % 64 == 0) ss_s[tid / 64] = ss;
   }
   __syncthreads();
+  if constexpr (kDigitsOf<F>) {
+    // Integer activations (Q4K8): the staged inputs become digit planes in place.
+    digitize_units<T, kSlot, (8 * LPR + T - 1) / T>(xs, n_units);
+    __syncthreads();
+  }
   typename F::Frag f;
   F::from_lds(xs + unit * kSlot, f);
   float scale = 1.f;
@@ -455,8 +464,6 @@ template <class P>
 static int rpg_for(uint32_t n_items, int lpr, uint32_t n_cus) {
   constexpr int R = P::kRows;
   const int groups_per_block = lpr <= 64 ? 256 / lpr : 1;
-  static const int forced = getenv("BCH_GEMV_RPG") ? atoi(getenv("BCH_GEMV_RPG")) : 0;
-  if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced;
   // The argmax key costs the registers that keep 4 rows at 2 waves per SIMD.
   int rpg = R == 1 ? (P::kArgmax ? 2 : 4) : R == 2 ? 2 : 1;
   const uint32_t want_blocks = 2 * (n_cus ? n_cus : 256);
@@ -471,7 +478,7 @@ static void launch_gemv(hipStream_t s, const P &p, const float *x, const float *
   constexpr int G = threads / LPR;
   // Persistent groups: enough workgroups for `per_cu` per CU, each group
   // walking batches at a stride of the whole grid.
-  static const uint32_t per_cu = getenv("BCH_GEMV_WG_PER_CU") ? atoi(getenv("BCH_GEMV_WG_PER_CU")) : 2;
+  constexpr uint32_t per_cu = 2;
   const uint32_t n_batches = div_ceil(n_items, RPG);
   uint32_t grid = std::max(1u, std::min(div_ceil(n_batches, G), per_cu * 256));
   if constexpr (P::kArgmax) grid = std::min(grid, kArgmaxPartials);
@@ -535,6 +542,12 @@ template <class P>
 static bool gemv_any(hipStream_t s, uint32_t format, const P &p, const float *x, const float *nw, float eps,
                      uint32_t n_items, uint32_t n_cols, uint32_t n_cus) {
   const bool norm = nw != nullptr;
+  // Integer activations where a workgroup serves many rows (rows of at most
+  // 64 units); for wide rows (the down projection: a few rows per
+  // workgroup) converting the staged input costs more than it saves.
+  if (format == Q4K::kFormat && n_cols <= 64 * 64)
+    return norm ? gemv_dispatch<Q4K8, true>(s, p, x, nw, eps, n_items, n_cols, n_cus)
+                : gemv_dispatch<Q4K8, false>(s, p, x, nw, eps, n_items, n_cols, n_cus);
   if (format == Q4K::kFormat)
     return norm ? gemv_dispatch<Q4K, true>(s, p, x, nw, eps, n_items, n_cols, n_cus)
                 : gemv_dispatch<Q4K, false>(s, p, x, nw, eps, n_items, n_cols, n_cus);

@@ -234,26 +234,19 @@ struct Geometry {
   int r;
 };
 
-static int env_int(const char *name) {
-  const char *v = getenv(name);
-  return v ? atoi(v) : 0;
-}
-
 // Pick lanes per row and rows per group: every lane should own the same
 // number of units (no idle tail), and the grid should hold at least
 // ~8 waves per CU; among equals prefer more rows per group, which loads
 // each input once for more rows.
 static Geometry choose(uint32_t n_rows, uint32_t n_units, uint32_t n_cus, int max_r) {
-  const int forced_lpr = env_int("BCH_MATVEC_LPR"), forced_r = env_int("BCH_MATVEC_R");
   Geometry best{64, 1};
   double best_score = -1.0;
   const double want_waves = (double)(n_cus ? n_cus : 256) * 8.0;
   for (int lpr : {64, 32, 16, 8, 4}) {
-    if (forced_lpr && lpr != forced_lpr) continue;
     const uint32_t iters = (n_units + lpr - 1) / lpr;
     const double util = (double)n_units / ((double)lpr * iters);
     for (int r : {8, 4, 2, 1}) {
-      if (r > max_r || (forced_r && r != forced_r)) continue;
+      if (r > max_r) continue;
       const double rows_per_wave = (double)(kWave / lpr) * r;
       const double waves = std::ceil(n_rows / rows_per_wave);
       const double occ = std::min(1.0, waves / want_waves);
@@ -382,7 +375,7 @@ static void dispatch_format(uint32_t format, Fn &&f) {
 
 void run_matvec(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,
                 float *y, const float *norm_w, float eps, bool accumulate, uint32_t n_cus) {
-  if (!getenv("BCH_SLOW_GEMV") && fast_matvec(s, format, W, n_rows, n_cols, x, y, norm_w, eps, accumulate, n_cus)) return;
+  if (fast_matvec(s, format, W, n_rows, n_cols, x, y, norm_w, eps, accumulate, n_cus)) return;
   const uint32_t n_units = n_cols / unit_of(format);
   const uint64_t rb = bch_row_bytes(format, n_cols);
   const Geometry g = choose(n_rows, n_units, n_cus, 8);
@@ -394,8 +387,7 @@ void run_matvec(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_row
 void run_matvec3(hipStream_t s, uint32_t format, const uint8_t *W0, const uint8_t *W1, const uint8_t *W2, uint32_t r0,
                  uint32_t r1, uint32_t r2, uint32_t n_cols, const float *x, float *y0, float *y1, float *y2,
                  const float *norm_w, float eps, uint32_t n_cus) {
-  if (!getenv("BCH_SLOW_GEMV") &&
-      fast_matvec3(s, format, W0, W1, W2, r0, r1, r2, n_cols, x, y0, y1, y2, norm_w, eps, n_cus))
+  if (fast_matvec3(s, format, W0, W1, W2, r0, r1, r2, n_cols, x, y0, y1, y2, norm_w, eps, n_cus))
     return;
   const uint32_t n_units = n_cols / unit_of(format);
   const uint64_t rb = bch_row_bytes(format, n_cols);
@@ -408,7 +400,7 @@ void run_matvec3(hipStream_t s, uint32_t format, const uint8_t *W0, const uint8_
 
 void run_matvec_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const uint8_t *Wu, uint32_t n_rows,
                        uint32_t n_cols, const float *x, float *y, const float *norm_w, float eps, uint32_t n_cus) {
-  if (!getenv("BCH_SLOW_GEMV") && fast_matvec_swiglu(s, format, Wg, Wu, n_rows, n_cols, x, y, norm_w, eps, n_cus))
+  if (fast_matvec_swiglu(s, format, Wg, Wu, n_rows, n_cols, x, y, norm_w, eps, n_cus))
     return;
   const uint32_t n_units = n_cols / unit_of(format);
   const uint64_t rb = bch_row_bytes(format, n_cols);
@@ -419,8 +411,7 @@ void run_matvec_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const 
 void run_matvec_conv(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_cols, const float *x,
                      const float *norm_w, float eps, const float *taps, float *history, float *out, uint32_t n_embd,
                      uint32_t ksize, uint32_t n_cus) {
-  if (!getenv("BCH_SLOW_GEMV") &&
-      fast_matvec_conv(s, format, W, n_cols, x, norm_w, eps, taps, history, out, n_embd, ksize, n_cus))
+  if (fast_matvec_conv(s, format, W, n_cols, x, norm_w, eps, taps, history, out, n_embd, ksize, n_cus))
     return;
   const uint32_t n_units = n_cols / Q4K::kUnit;
   const uint64_t rb = bch_row_bytes(format, n_cols);
