@@ -223,10 +223,14 @@ uint32_t attn_prefill_splits(uint32_t n_heads, uint32_t n_kv, uint32_t head_dim,
 
 // matmul.hip.  Y[t] (store) W·X[t] for n_tokens rows; store 0 overwrite,
 // 1 accumulate, 2 swiglu (y = silu(y) * product).
-// `split` is scratch of matmul_split_bytes(n_tokens, n_cols) bytes (the
-// inputs split into fp16 high and low parts).
+// `scratch` holds the inputs split into fp16 high and low parts
+// (matmul_split_bytes(n_tokens, n_cols) bytes) and, after them, the
+// split-K partial products: scratch_bytes bounds how many column splits a
+// launch may use (matmul_scratch_bytes(n_tokens, n_cols, n_rows) allows
+// all; matmul_split_bytes alone allows none).
 uint64_t matmul_split_bytes(uint32_t n_rows, uint32_t n_cols);
+uint64_t matmul_scratch_bytes(uint32_t n_tokens, uint32_t n_cols, uint32_t n_rows);
 void run_matmul(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,
-                float *y, uint32_t n_tokens, uint32_t store, void *split);
+                float *y, uint32_t n_tokens, uint32_t store, void *scratch, uint64_t scratch_bytes);
 
 }  // namespace bch

@@ -70,7 +70,8 @@ struct bch_lfm2 : bch::Sequence {
   // SwiGLU activations and down projection (Recorder::grouped_moe).
   uint32_t *moe_offsets = nullptr, *moe_entries = nullptr;
   float *expert_ffn = nullptr, *expert_out = nullptr;
-  void *split = nullptr;  // prefill GEMM inputs split into fp16 halves (matmul_split_bytes)
+  void *split = nullptr;  // prefill GEMM scratch: split inputs and split-K partials (matmul_scratch_bytes)
+  uint64_t split_bytes = 0;
   bool kv_half = true;
 
   uint64_t cache_elems_per_layer() const { return (uint64_t)n_ctx * kv_dim; }
@@ -229,17 +230,17 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
     check_finite(s, "attn_norm", il, m->normed, (uint64_t)count * n);
     if (!L.attention) {
       float *hist = m->conv_state + (uint64_t)L.cache_index * (m->conv_kernel - 1) * n;
-      run_matmul(s, L.in_proj.format, L.in_proj.data, 3 * n, n, m->normed, m->bcx, count, 0, m->split);
+      run_matmul(s, L.in_proj.format, L.in_proj.data, 3 * n, n, m->normed, m->bcx, count, 0, m->split, m->split_bytes);
       check_finite(s, "in_proj", il, m->bcx, (uint64_t)count * 3 * n);
       run_short_conv_batch(s, m->bcx, L.taps, hist, m->conv_out, n, m->conv_kernel, count);
       check_finite(s, "short_conv", il, m->conv_out, (uint64_t)count * n);
-      run_matmul(s, L.out_proj.format, L.out_proj.data, n, n, m->conv_out, m->hidden, count, 1, m->split);
+      run_matmul(s, L.out_proj.format, L.out_proj.data, n, n, m->conv_out, m->hidden, count, 1, m->split, m->split_bytes);
       check_finite(s, "out_proj", il, m->hidden, (uint64_t)count * n);
     } else {
       const uint32_t ci = L.cache_index;
-      run_matmul(s, L.wq.format, L.wq.data, m->q_dim, n, m->normed, m->q, count, 0, m->split);
-      run_matmul(s, L.wk.format, L.wk.data, m->kv_dim, n, m->normed, m->k, count, 0, m->split);
-      run_matmul(s, L.wv.format, L.wv.data, m->kv_dim, n, m->normed, m->v, count, 0, m->split);
+      run_matmul(s, L.wq.format, L.wq.data, m->q_dim, n, m->normed, m->q, count, 0, m->split, m->split_bytes);
+      run_matmul(s, L.wk.format, L.wk.data, m->kv_dim, n, m->normed, m->k, count, 0, m->split, m->split_bytes);
+      run_matmul(s, L.wv.format, L.wv.data, m->kv_dim, n, m->normed, m->v, count, 0, m->split, m->split_bytes);
       check_finite(s, "q", il, m->q, (uint64_t)count * m->q_dim);
       check_finite(s, "k", il, m->k, (uint64_t)count * m->kv_dim);
       check_finite(s, "v", il, m->v, (uint64_t)count * m->kv_dim);
@@ -278,7 +279,7 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
         run_attn_prefill(s, ad, m->kv_half, nq);
       }
       check_finite(s, "attention", il, m->attn, (uint64_t)count * m->q_dim);
-      run_matmul(s, L.wo.format, L.wo.data, n, m->q_dim, m->attn, m->hidden, count, 1, m->split);
+      run_matmul(s, L.wo.format, L.wo.data, n, m->q_dim, m->attn, m->hidden, count, 1, m->split, m->split_bytes);
       check_finite(s, "attn_output", il, m->hidden, (uint64_t)count * n);
     }
     run_rms_norm(s, m->hidden, L.ffn_norm, m->normed, n, count, m->norm_eps);
@@ -307,11 +308,11 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
       }
       check_finite(s, "moe", il, m->hidden, (uint64_t)count * n);
     } else {
-      run_matmul(s, L.gate.format, L.gate.data, m->n_ff, n, m->normed, m->ffn, count, 0, m->split);
+      run_matmul(s, L.gate.format, L.gate.data, m->n_ff, n, m->normed, m->ffn, count, 0, m->split, m->split_bytes);
       check_finite(s, "gate", il, m->ffn, (uint64_t)count * m->n_ff);
-      run_matmul(s, L.up.format, L.up.data, m->n_ff, n, m->normed, m->ffn, count, 2, m->split);
+      run_matmul(s, L.up.format, L.up.data, m->n_ff, n, m->normed, m->ffn, count, 2, m->split, m->split_bytes);
       check_finite(s, "up", il, m->ffn, (uint64_t)count * m->n_ff);
-      run_matmul(s, L.down.format, L.down.data, n, m->n_ff, m->ffn, m->hidden, count, 1, m->split);
+      run_matmul(s, L.down.format, L.down.data, n, m->n_ff, m->ffn, m->hidden, count, 1, m->split, m->split_bytes);
       check_finite(s, "down", il, m->hidden, (uint64_t)count * n);
     }
     if (trace) run_copy(s, m->hidden, m->trace + (1 + il) * tstride, count * n, nullptr, 0);
@@ -463,8 +464,8 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
                                                             hd, attn_decode_max_splits(n_ctx, hd, m->kv_half));
     m->partial_floats = partial_floats;
     const uint32_t widest = std::max({n, m->q_dim, m->n_ff});
-    const uint64_t split_bytes =
-        std::max(matmul_split_bytes((uint32_t)rows, widest),
+    const uint64_t split_bytes = m->split_bytes =
+        std::max(matmul_scratch_bytes((uint32_t)rows, widest, n),
                  matmul_split_bytes((uint32_t)(std::max(1u, m->n_used) * rows), std::max(1u, m->n_ff_expert)));
     int rc = 0;
     (void)((rc = m->alloc(cache, &m->k_cache)) || (rc = m->alloc(cache, &m->v_cache)) ||

@@ -6,13 +6,14 @@
 // a full 512-token batch; here each workgroup dequantises its weight tile
 // straight into LDS instead, so the expanded matrix never touches HBM.
 //
-// Tile: 128 weight rows x 64 tokens, in pipeline steps of 128 columns;
-// v_mfma_f32_32x32x16_f16 on LDS tiles.  Weights go to LDS as fp16 (the
-// reference's expanded half tiles).  Before the GEMM, k_split_rows scales
-// each token's inputs by a power of two into fp16 range and splits them into
-// an fp16 high part and an fp16 residual (once per launch, not once per
-// weight tile); both are multiplied, so the inputs keep ~22 bits whatever
-// their magnitude.  Accumulation is fp32.
+// Two kernels: k_gemm for dense matrices (described at its definition
+// below) and k_matmul for the expert-grouped launches of the MoE layers.
+// k_matmul's tile is 128 weight rows x 64 tokens in pipeline steps of 128
+// columns; before it, k_split_rows scales each token's inputs by a power of
+// two into fp16 range and splits them into an fp16 high part and an fp16
+// residual, and both are multiplied, so those inputs keep ~22 bits.
+// Weights go to LDS as fp16 (the reference's expanded half tiles);
+// accumulation is fp32.
 #include <mutex>
 #include "formats.h"
 #include "kernels.h"
@@ -326,6 +327,472 @@ __global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, u
 
 #undef BCH_PREFETCH
 
+// --- the dense prefill GEMM -------------------------------------------------
+//
+// Tile RB weight rows x 32·NB·NW tokens with NW waves (64·NW threads),
+// wave w owning NB blocks of 32 tokens from 32·NB·w against all RB rows:
+// MB·NB blocks (MB = RB/32) of v_mfma_f32_32x32x16_f16.  (NB = 2 halves
+// the LDS reads per MFMA but needs more registers than two waves per SIMD
+// allow; the launches use NB = 1.)  Three shapes: 128 x 256 with 8 waves (two
+// per SIMD) for batches of more than 128 tokens, 128 x 128 with 4 waves,
+// and 64 x 128 for matrices of at most 64 rows.  Stages of 64 columns (one
+// Q4_K pair of 32-element blocks).
+//
+// Per stage the workgroup dequantises its RB x 64 weights once into LDS
+// (each thread 32 or 16 of them, fp16 as the reference's expanded half
+// tiles), and each lane loads its own token's fp16 inputs straight into
+// MFMA operand registers.  The inputs are those of k_split_hi: each token
+// scaled by the power of two that puts its largest magnitude in
+// [2^13, 2^14) (half precision cannot overflow) and rounded to fp16 — 11
+// significant bits, finer than bf16 — the scale undone in the epilogue.
+// The inputs are the M operand, so the result D[token][row] has rows
+// along the lanes and stores of 32 consecutive rows are contiguous.
+//
+// Budget per MFMA (measured on gfx950: 16 ns per 32x32x16 MFMA per SIMD,
+// ~2.2 ns per wave64 VALU instruction, ~11 ns per ds_read_b128 per SIMD
+// with four SIMDs reading): one LDS read of a weight fragment and, at 256
+// tokens per tile, ~3 VALU instructions of dequantisation.  The VALU work
+// overlaps the matrix core only if it sits between MFMAs in each wave's
+// instruction stream: the next stage's dequantisation is split into parts
+// placed between the MFMAs, held there by scheduling fences.
+//
+// Column order inside a stage.  The k-step of an MFMA sums over 16 columns
+// in any order as long as both operands agree.  Lane half h (lanes 32h ..
+// 32h+31) of k-step s takes the 8 columns base(s) + 16h + 0..7, base =
+// {0, 8, 32, 40}: 16 contiguous bytes of the token's row and of the LDS
+// weight row, and in Q4_K the low (s < 2) or high (s >= 2) nibbles of
+// quant bytes 16h + 8(s%2) .. +7.
+//
+// Software pipeline, three stages deep: step st issues the input loads of
+// stage st+2 and the raw weight loads of stage st+3, runs stage st's MFMAs
+// while the lanes dequantise stage st+1 into the next LDS buffer, then one
+// barrier; every load has two steps to arrive.
+//
+// Split K.  With few tiles (outputs of a 2048-wide residual stream) the
+// column range is split over up to kMaxSplitK workgroups; each writes its
+// partial product to scratch and k_gemm_reduce adds them in a fixed order
+// and applies the store, so the result does not depend on timing.
+constexpr int kGk = 64;             // columns per stage
+constexpr int kGA = kGk + 8;        // halves per LDS weight row (padded)
+constexpr uint32_t kMaxSplitK = 8;
+
+__device__ __forceinline__ int gemm_base(int s) { return (s & 1) * 8 + (s >> 1) * 32; }
+
+// Row t of X to fp16 with the power of two that puts max|x_t| in
+// [2^13, 2^14): H[t][c] = fp16(x·s), unscale[t] = 1/s.  One workgroup per
+// row.
+__global__ __launch_bounds__(256) void k_split_hi(const float *__restrict__ X, uint32_t n_cols,
+                                                 _Float16 *__restrict__ H, float *__restrict__ unscale) {
+  const uint32_t t = blockIdx.x, tid = threadIdx.x;
+  const float4 *x4 = reinterpret_cast<const float4 *>(X + (uint64_t)t * n_cols);
+  const uint32_t n4 = n_cols / 4;
+  float mx = 0.f;
+  for (uint32_t i = tid; i < n4; i += 256) {
+    const float4 v = x4[i];
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
+  __shared__ float red[4];
+  mx = wave_max(mx);
+  if (tid % 64 == 0) red[tid / 64] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int ex = 0;
+  if (mx > 0.f) frexpf(mx, &ex);  // mx < 2^ex
+  const int k = max(-100, min(100, 14 - ex));
+  const float scale = ldexpf(1.0f, k);
+  if (tid == 0) unscale[t] = ldexpf(1.0f, -k);
+  half4_t *row = reinterpret_cast<half4_t *>(H + (uint64_t)t * n_cols);
+  for (uint32_t i = tid; i < n4; i += 256) {
+    const float4 v = x4[i];
+    half4_t o;
+    o[0] = (_Float16)(v.x * scale), o[1] = (_Float16)(v.y * scale);
+    o[2] = (_Float16)(v.z * scale), o[3] = (_Float16)(v.w * scale);
+    row[i] = o;
+  }
+}
+
+struct HiInputs {
+  const _Float16 *h;
+  const float *unscale;
+};
+
+// (Clang vector types rather than uint4: copies of uint4 become memcpy
+// calls that kept these registers in scratch memory.)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Raw bytes of one thread's weights of a stage: for Q4_K the super-block
+// header and the quant bytes of its columns (16 or 8 bytes).
+struct GemmRaw {
+  u32x4 h, q;
+};
+
+// Thread's weights of stage k0 for row `row`: with WPT = 32, columns
+// 16c .. 16c+15 and 32+16c .. 32+16c+15 (c = 0, 1); with WPT = 16, columns
+// 8c .. 8c+7 and 32+8c .. 32+8c+7 (c = 0..3) — in Q4_K the low and high
+// nibbles of quant bytes [WPT/2·c, WPT/2·(c+1)) of the pair.
+template <uint32_t FMT, int WPT>
+__device__ __forceinline__ void gemm_fetch(const uint8_t *__restrict__ row, uint32_t k0, int c, GemmRaw &r) {
+  if constexpr (FMT == 12) {
+    const uint8_t *blk = row + (k0 / 256) * 144;
+    r.h = *reinterpret_cast<const u32x4 *>(blk);
+    const uint8_t *q = blk + 16 + 32 * ((k0 & 255u) / 64) + (WPT / 2) * c;
+    if constexpr (WPT == 32) {
+      r.q = *reinterpret_cast<const u32x4 *>(q);
+    } else {
+      const uint2 v = *reinterpret_cast<const uint2 *>(q);
+      r.q = u32x4{v.x, v.y, 0u, 0u};
+    }
+  }
+}
+
+// The thread's weights of stage k0 for the formats other than Q4_K, read
+// and converted directly (F16, F32, and the block formats through
+// dequant_elem).
+template <uint32_t FMT, int WPT>
+__device__ __forceinline__ void gemm_dequant_direct(const uint8_t *__restrict__ row, uint32_t k0, int c, bool valid,
+                                                    _Float16 *__restrict__ dst) {
+  constexpr int H = WPT / 2;  // weights per nibble half
+  _Float16 *lo = dst + H * c, *hi = dst + 32 + H * c;
+  const uint32_t kl = k0 + H * c, kh = k0 + 32 + H * c;
+#pragma unroll
+  for (int w = 0; w < H / 4; w++) {
+    half4_t l4, h4;
+    if constexpr (FMT == 1) {
+      const _Float16 *f = reinterpret_cast<const _Float16 *>(row);
+      l4 = *reinterpret_cast<const half4_t *>(f + kl + 4 * w);
+      h4 = *reinterpret_cast<const half4_t *>(f + kh + 4 * w);
+    } else if constexpr (FMT == 0) {
+      const float *f = reinterpret_cast<const float *>(row);
+      const float4 u = *reinterpret_cast<const float4 *>(f + kl + 4 * w);
+      const float4 v = *reinterpret_cast<const float4 *>(f + kh + 4 * w);
+      l4[0] = (_Float16)u.x, l4[1] = (_Float16)u.y, l4[2] = (_Float16)u.z, l4[3] = (_Float16)u.w;
+      h4[0] = (_Float16)v.x, h4[1] = (_Float16)v.y, h4[2] = (_Float16)v.z, h4[3] = (_Float16)v.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        l4[i] = (_Float16)dequant_elem(FMT, row, kl + 4 * w + i);
+        h4[i] = (_Float16)dequant_elem(FMT, row, kh + 4 * w + i);
+      }
+    }
+    if (!valid) l4 = half4_t{}, h4 = half4_t{};
+    *reinterpret_cast<half4_t *>(lo + 4 * w) = l4;
+    *reinterpret_cast<half4_t *>(hi + 4 * w) = h4;
+  }
+}
+
+// Q4_K dequantisation of a thread's stage in parts, so that the parts can
+// be interleaved with MFMAs: q4k_scales once, then part J (one quant dword:
+// 4 low-nibble and 4 high-nibble weights, (d·sc)·q − dmin·m each, rounded
+// to fp16) per call.
+struct Q4kScales {
+  float a_lo, b_lo, a_hi, b_hi;
+};
+
+// (valid false: all four zero, so the part writes zeros.)
+__device__ __forceinline__ Q4kScales q4k_scales(const GemmRaw &r, uint32_t k0, bool valid) {
+  const uint32_t sc = q4k_pair_scales(r.h.y, r.h.z, r.h.w, (int)((k0 & 255u) / 64));
+  const float d = valid ? half_bits_to_float(r.h.x & 0xffffu) : 0.f;
+  const float dmin = valid ? half_bits_to_float(r.h.x >> 16) : 0.f;
+  return {d * ubyte0(sc), dmin * ubyte2(sc), d * ubyte1(sc), dmin * ubyte3(sc)};
+}
+
+template <int WPT, int J>
+__device__ __forceinline__ void q4k_part(const GemmRaw &r, const Q4kScales &f, int c, _Float16 *__restrict__ dst) {
+  constexpr int H = WPT / 2;
+  const uint32_t v = J == 0 ? r.q.x : J == 1 ? r.q.y : J == 2 ? r.q.z : r.q.w;
+  const uint32_t ql = v & 0x0f0f0f0fu, qh = (v >> 4) & 0x0f0f0f0fu;
+  half4_t l4, h4;
+  l4[0] = (_Float16)(f.a_lo * ubyte0(ql) - f.b_lo);
+  l4[1] = (_Float16)(f.a_lo * ubyte1(ql) - f.b_lo);
+  l4[2] = (_Float16)(f.a_lo * ubyte2(ql) - f.b_lo);
+  l4[3] = (_Float16)(f.a_lo * ubyte3(ql) - f.b_lo);
+  h4[0] = (_Float16)(f.a_hi * ubyte0(qh) - f.b_hi);
+  h4[1] = (_Float16)(f.a_hi * ubyte1(qh) - f.b_hi);
+  h4[2] = (_Float16)(f.a_hi * ubyte2(qh) - f.b_hi);
+  h4[3] = (_Float16)(f.a_hi * ubyte3(qh) - f.b_hi);
+  *reinterpret_cast<half4_t *>(dst + H * c + 4 * J) = l4;
+  *reinterpret_cast<half4_t *>(dst + 32 + H * c + 4 * J) = h4;
+}
+
+template <uint32_t FMT, int WPT>
+__device__ __forceinline__ void gemm_dequant_all(const uint8_t *__restrict__ row, uint32_t k0, int c,
+                                                 const GemmRaw &r, _Float16 *__restrict__ dst) {
+  if constexpr (FMT == 12) {
+    const Q4kScales f = q4k_scales(r, k0, true);
+    q4k_part<WPT, 0>(r, f, c, dst);
+    q4k_part<WPT, 1>(r, f, c, dst);
+    if constexpr (WPT == 32) {
+      q4k_part<WPT, 2>(r, f, c, dst);
+      q4k_part<WPT, 3>(r, f, c, dst);
+    }
+  } else {
+    gemm_dequant_direct<FMT, WPT>(row, k0, c, true, dst);
+  }
+}
+
+// Y (store) or partials: D[token][row] of the launch.  Splits > 1 write
+// partial products to P[split] (k_gemm_reduce applies the store).
+template <uint32_t FMT, int STORE, int RB, int NW, int NB>
+__global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W, uint64_t row_bytes, HiInputs X,
+                                                  float *__restrict__ Y, float *__restrict__ P, uint32_t n_rows,
+                                                  uint32_t n_cols, uint32_t n_tokens, uint32_t splits) {
+  constexpr int NT = 64 * NW;          // threads
+  constexpr int MB = RB / 32;          // row blocks
+  constexpr int BT = 32 * NB * NW;     // tokens per tile
+  constexpr int WPT = RB * kGk / NT;   // weights a thread dequantises per stage (32 or 16)
+  constexpr int TPR = NT / RB;         // threads per weight row
+  static_assert(WPT == 32 || WPT == 16, "a thread dequantises 16 or 32 weights per stage");
+  constexpr int PARTS = WPT / 8;       // Q4_K dequantisation parts per stage (4 or 2)
+  constexpr int MFMAS = MB * NB * 4;   // MFMAs per wave per stage
+  constexpr int GAP = MFMAS / PARTS;   // MFMAs between dequantisation parts
+  __shared__ __align__(16) _Float16 A[3][RB * kGA];
+  __shared__ float us_s[BT];           // the tile's token scales
+  const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64, h = lane / 32;
+  const uint32_t n_rt = (n_rows + RB - 1) / RB, n_tt = (n_tokens + BT - 1) / BT;
+  const uint32_t total = n_rt * n_tt * splits;
+  // XCD-aware order: workgroup L runs on XCD L % 8, so logical tile
+  // (L % 8)·⌈total/8⌉ + L/8 hands each XCD a contiguous run, split-major
+  // then token-tile-major: the row tiles sharing a token tile's inputs share
+  // that XCD's L2.
+  const uint32_t per = (total + 7) / 8, logical = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  if (logical >= total) return;
+  const uint32_t rt = logical % n_rt, tt = (logical / n_rt) % n_tt, sp = logical / (n_rt * n_tt);
+  const uint32_t row0 = rt * RB, tok0 = tt * BT;
+  const uint32_t n_stages = n_cols / kGk;
+  const uint32_t st0 = (uint32_t)((uint64_t)sp * n_stages / splits);
+  const uint32_t st1 = (uint32_t)((uint64_t)(sp + 1) * n_stages / splits);
+  const uint32_t last = st1 - 1;
+
+  // Dequantising role: weight row ar, part ac.  (Rows past the end are
+  // clamped; their outputs are never stored.)
+  const int ar = tid / TPR, ac = tid % TPR;
+  const uint8_t *wrow = W + (uint64_t)min(row0 + ar, n_rows - 1) * row_bytes;
+  // MFMA role: tokens tok0 + 32·NB·wave + 32j + lane%32 (clamped), lane half h.
+  const u32x4 *xrow[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++)
+    xrow[j] = reinterpret_cast<const u32x4 *>(
+        X.h + (uint64_t)min(tok0 + 32 * NB * wave + 32 * j + lane % 32, n_tokens - 1) * n_cols + 16 * h);
+  static_assert(BT <= NT, "one thread per token scale");
+  if (tid < BT) us_s[tid] = X.unscale[min(tok0 + tid, n_tokens - 1)];
+
+  // The lane's inputs of a stage: token block j, k-step s at v[4j + s].
+  struct BRegs {
+    u32x4 v[4 * NB];
+  };
+  auto load_b = [&](uint32_t st, BRegs &b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+      for (int s = 0; s < 4; s++) b.v[4 * j + s] = xrow[j][(st * kGk + gemm_base(s)) / 8];
+  };
+
+  float16_t acc[MB][NB];
+#pragma unroll
+  for (int i = 0; i < MB; i++)
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+
+  // Three sets of everything, stage x in set (x - st0) % 3: raw weights
+  // r, inputs b, LDS weight buffer A.  Step st (set q) waits for the loads
+  // of step st-2 only, issues the inputs of stage st+2 (set q+2) and the
+  // raw weights of stage st+3 (set q), dequantises stage st+1 (set q+1)
+  // into LDS between the MFMAs of stage st (set q), then one barrier.
+  // Loads thus have two steps to arrive.  The loop runs whole triples of
+  // steps; stages past the split's last are dummies whose loads re-read
+  // the last stage and whose weights dequantise to zeros, adding nothing.
+  GemmRaw r0{}, r1{}, r2{};
+  BRegs b0{}, b1{}, b2{};
+  constexpr int NL = (FMT == 12 ? 2 : 0) + 4 * NB;  // loads a step issues
+  gemm_fetch<FMT, WPT>(wrow, st0 * kGk, ac, r0);
+  load_b(st0, b0);
+  gemm_fetch<FMT, WPT>(wrow, min(st0 + 1, last) * kGk, ac, r1);
+  gemm_dequant_all<FMT, WPT>(wrow, st0 * kGk, ac, r0, &A[0][ar * kGA]);
+  gemm_fetch<FMT, WPT>(wrow, min(st0 + 2, last) * kGk, ac, r2);
+  load_b(min(st0 + 1, last), b1);
+  __syncthreads();
+
+  auto step = [&](uint32_t st, GemmRaw &rq, const GemmRaw &rn, BRegs &b2n, const BRegs &bq, const _Float16 *ab,
+                  _Float16 *anext) __attribute__((always_inline)) {
+    // Wait for the loads of step st-2 (the most recent NL, of step st-1,
+    // may stay in flight).  (Left to itself the compiler counts loads
+    // across the loop's back edge conservatively and stalls the MFMAs on
+    // loads issued just above them.)
+    __builtin_amdgcn_s_waitcnt((NL & 15) | ((NL >> 4) << 14) | 0x0f70);  // vmcnt(NL)
+    load_b(min(st + 2, last), b2n);
+    gemm_fetch<FMT, WPT>(wrow, min(st + 3, last) * kGk, ac, rq);
+    const bool valid = st + 1 <= last;
+    const uint32_t kn = min(st + 1, last) * kGk;
+    Q4kScales f{};
+    if constexpr (FMT == 12)
+      f = q4k_scales(rn, kn, valid);
+    else
+      gemm_dequant_direct<FMT, WPT>(wrow, kn, ac, valid, anext);
+    // MFMAs k-step by k-step, each k-step's weight fragments read from LDS
+    // one k-step ahead, a part of the next stage's dequantisation after
+    // every GAP MFMAs, fenced so the scheduler keeps that order.
+    const _Float16 *ap = ab + (lane % 32) * kGA + 16 * h;
+    half8_t wf[2][MB];
+#pragma unroll
+    for (int i = 0; i < MB; i++) wf[0][i] = *reinterpret_cast<const half8_t *>(ap + 32 * i * kGA + gemm_base(0));
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      if (s < 3) {
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+          wf[(s + 1) & 1][i] = *reinterpret_cast<const half8_t *>(ap + 32 * i * kGA + gemm_base(s + 1));
+      }
+#pragma unroll
+      for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, bq.v[4 * j + s]),
+                                                             wf[s & 1][i], acc[i][j], 0, 0, 0);
+          if constexpr (FMT == 12) {
+            const int m = (s * MB + i) * NB + j;  // MFMA index in the stage
+            if (m % GAP == GAP - 1) {
+              switch (m / GAP) {
+                case 0: q4k_part<WPT, 0>(rn, f, ac, anext); break;
+                case 1: q4k_part<WPT, 1>(rn, f, ac, anext); break;
+                case 2: if constexpr (PARTS > 2) q4k_part<WPT, 2>(rn, f, ac, anext); break;
+                case 3: if constexpr (PARTS > 3) q4k_part<WPT, 3>(rn, f, ac, anext); break;
+              }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+    }
+    __syncthreads();
+  };
+  _Float16 *a0 = &A[0][ar * kGA], *a1 = &A[1][ar * kGA], *a2 = &A[2][ar * kGA];
+  for (uint32_t st = st0; st <= last; st += 3) {
+    step(st, r0, r1, b2, b0, A[0], a1);
+    step(st + 1, r1, r2, b0, b1, A[1], a2);
+    step(st + 2, r2, r0, b1, b2, A[2], a0);
+  }
+
+  // acc[i][j][e]: token 32·NB·wave + 32j + 8(e/4) + 4h + e%4 of the tile,
+  // row 32i + lane%32.  The epilogue's loads (prior outputs, with clamped
+  // addresses) are unconditional so that they issue together; only the
+  // stores test bounds.
+#pragma unroll
+  for (int i = 0; i < MB; i++) {
+    const uint32_t row = row0 + 32 * i + lane % 32;
+    const uint32_t rowc = min(row, n_rows - 1);
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      const int tw = 32 * NB * wave + 32 * j;  // first token of the block in the tile
+      const uint32_t tb = tok0 + tw;
+      float v[16], prior[16];
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int tl = tw + 8 * (e / 4) + 4 * h + e % 4;
+        v[e] = acc[i][j][e] * us_s[tl];
+        if (STORE != 0 && splits == 1) prior[e] = Y[(uint64_t)min(tok0 + tl, n_tokens - 1) * n_rows + rowc];
+      }
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        if (splits > 1)
+          ;
+        else if (STORE == 1)
+          v[e] += prior[e];
+        else if (STORE == 2)
+          v[e] *= silu_f(prior[e]);
+      }
+      float *dst = splits > 1 ? P + (uint64_t)sp * n_tokens * n_rows : Y;
+      if (row >= n_rows) continue;
+      if (tb + 32 <= n_tokens) {
+#pragma unroll
+        for (int e = 0; e < 16; e++) dst[(uint64_t)(tb + 8 * (e / 4) + 4 * h + e % 4) * n_rows + row] = v[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const uint32_t tok = tb + 8 * (e / 4) + 4 * h + e % 4;
+          if (tok < n_tokens) dst[(uint64_t)tok * n_rows + row] = v[e];
+        }
+      }
+    }
+  }
+}
+
+// Y (store) Σ_split P[split], the splits added in order.
+template <int STORE>
+__global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ P, uint32_t splits, uint64_t n,
+                                                     float *__restrict__ Y) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float v = P[i];
+  for (uint32_t sp = 1; sp < splits; sp++) v += P[sp * n + i];
+  if (STORE == 0)
+    Y[i] = v;
+  else if (STORE == 1)
+    Y[i] += v;
+  else
+    Y[i] = silu_f(Y[i]) * v;
+}
+
+template <uint32_t FMT, int RB, int NW, int NB>
+static void gemm_launch(hipStream_t s, const uint8_t *W, uint64_t rb, const HiInputs &x, float *y, float *part,
+                        uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens, uint32_t store, uint32_t splits) {
+  const uint32_t total = div_ceil(n_rows, RB) * div_ceil(n_tokens, 32 * NB * NW) * splits;
+  const dim3 grid(8 * div_ceil(total, 8));
+  if (splits > 1 || store == 0)
+    k_gemm<FMT, 0, RB, NW, NB><<<grid, 64 * NW, 0, s>>>(W, rb, x, y, part, n_rows, n_cols, n_tokens, splits);
+  else if (store == 1)
+    k_gemm<FMT, 1, RB, NW, NB><<<grid, 64 * NW, 0, s>>>(W, rb, x, y, part, n_rows, n_cols, n_tokens, splits);
+  else
+    k_gemm<FMT, 2, RB, NW, NB><<<grid, 64 * NW, 0, s>>>(W, rb, x, y, part, n_rows, n_cols, n_tokens, splits);
+  if (splits > 1) {
+    const uint64_t n = (uint64_t)n_tokens * n_rows;
+    const dim3 g((uint32_t)((n + 255) / 256));
+    if (store == 0)
+      k_gemm_reduce<0><<<g, 256, 0, s>>>(part, splits, n, y);
+    else if (store == 1)
+      k_gemm_reduce<1><<<g, 256, 0, s>>>(part, splits, n, y);
+    else
+      k_gemm_reduce<2><<<g, 256, 0, s>>>(part, splits, n, y);
+  }
+}
+
+// Tile and column split of a launch: 256-token tiles for batches of more
+// than 128 tokens (128 otherwise), 128-row tiles (64 for matrices of at
+// most 64 rows), then split K (at least 4 stages per split, partials
+// within `part_floats`) until the tiles cover the CUs.
+struct GemmShape {
+  uint32_t cfg, splits;  // cfg 0: 128 rows x 256 tokens, 8 waves; 1: 128 x 128, 4 waves; 2: 64 x 128, 4 waves
+};
+
+static GemmShape gemm_shape(uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens, uint64_t part_floats, uint32_t cus) {
+  const uint32_t cfg = n_rows <= 64 ? 2 : n_tokens > 128 ? 0 : 1;
+  const uint32_t bt = cfg == 0 ? 256 : 128, br = cfg == 2 ? 64 : 128;
+  const uint64_t tiles = (uint64_t)div_ceil(n_rows, br) * div_ceil(n_tokens, bt);
+  // Doubling the splits while the workgroups still fit the CUs: at 512
+  // tokens a 10752 x 2048 matrix (168 tiles) runs best unsplit (51 us; 73
+  // with two splits and their reduction), 2048 x 10752 (32 tiles) with 8
+  // (49 us; 220 unsplit), 6144 x 2048 (96 tiles) with 2.
+  uint32_t splits = 1;
+  const uint32_t n_stages = n_cols / kGk;
+  while (splits < kMaxSplitK && tiles * splits * 2 <= cus && n_stages / (2 * splits) >= 4 &&
+         (uint64_t)2 * splits * n_tokens * n_rows <= part_floats)
+    splits *= 2;
+  return {cfg, splits};
+}
+
+template <uint32_t FMT>
+static void gemm_fmt(hipStream_t s, const uint8_t *W, uint64_t rb, const HiInputs &x, float *y, float *part,
+                     uint64_t part_floats, uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens, uint32_t store,
+                     uint32_t cus) {
+  GemmShape g = gemm_shape(n_rows, n_cols, n_tokens, part_floats, cus);
+  if (g.cfg == 0)
+    gemm_launch<FMT, 128, 8, 1>(s, W, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits);
+  else if (g.cfg == 1)
+    gemm_launch<FMT, 128, 4, 1>(s, W, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits);
+  else
+    gemm_launch<FMT, 64, 4, 1>(s, W, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits);
+}
+
 template <uint32_t FMT, int MB>
 static void matmul_tile(hipStream_t s, const uint8_t *W, uint64_t rb, const SplitInputs &x, float *y, uint32_t n_rows,
                         uint32_t n_cols, uint32_t n_tokens, uint32_t store) {
@@ -371,25 +838,45 @@ static void set_lds_limits();
 
 uint64_t matmul_split_bytes(uint32_t n_rows, uint32_t n_cols) { return (uint64_t)n_rows * (4ull * n_cols + 4); }
 
+uint64_t matmul_scratch_bytes(uint32_t n_tokens, uint32_t n_cols, uint32_t n_rows) {
+  return (matmul_split_bytes(n_tokens, n_cols) + 255) / 256 * 256 + 4ull * kMaxSplitK * n_tokens * n_rows;
+}
+
+static uint32_t device_cus() {
+  static uint32_t cus = 0;
+  if (!cus) {
+    int dev = 0;
+    hipDeviceProp_t prop;
+    cus = (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
+              ? (uint32_t)prop.multiProcessorCount
+              : 256u;
+  }
+  return cus;
+}
+
 void run_matmul(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *xf,
-                float *y, uint32_t n_tokens, uint32_t store, void *split) {
-  set_lds_limits();
+                float *y, uint32_t n_tokens, uint32_t store, void *scratch, uint64_t scratch_bytes) {
+  if (!n_tokens) return;
   const uint64_t rb = bch_row_bytes(format, n_cols);
-  const SplitInputs x = split_inputs(s, xf, n_tokens, n_cols, split);
-  if (format == 12)
-    matmul_fmt<12>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
-  else if (format == 1)
-    matmul_fmt<1>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
-  else if (format == 14)
-    matmul_fmt<14>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
-  else if (format == 13)
-    matmul_fmt<13>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
-  else if (format == 8)
-    matmul_fmt<8>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
-  else if (format == 2)
-    matmul_fmt<2>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
-  else
-    matmul_fmt<0>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
+  // The fp16 inputs and their scales (n_tokens·(2·n_cols + 4) bytes, within
+  // matmul_split_bytes), then the split-K partials.
+  _Float16 *hx = static_cast<_Float16 *>(scratch);
+  float *unscale = reinterpret_cast<float *>(hx + (uint64_t)n_tokens * n_cols);
+  k_split_hi<<<n_tokens, 256, 0, s>>>(xf, n_cols, hx, unscale);
+  const HiInputs x{hx, unscale};
+  const uint64_t used = (matmul_split_bytes(n_tokens, n_cols) + 255) / 256 * 256;
+  float *part = reinterpret_cast<float *>(static_cast<uint8_t *>(scratch) + used);
+  const uint64_t part_floats = scratch_bytes > used ? (scratch_bytes - used) / 4 : 0;
+  const uint32_t cus = device_cus();
+  switch (format) {
+    case 12: gemm_fmt<12>(s, W, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
+    case 1: gemm_fmt<1>(s, W, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
+    case 14: gemm_fmt<14>(s, W, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
+    case 13: gemm_fmt<13>(s, W, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
+    case 8: gemm_fmt<8>(s, W, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
+    case 2: gemm_fmt<2>(s, W, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
+    default: gemm_fmt<0>(s, W, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
+  }
 }
 
 static bool matmul_format(uint32_t f) {
@@ -511,7 +998,7 @@ extern "C" int bch_matmul_noalloc(bch_ctx *ctx, uint32_t format, bch_view weight
   if (!ctx->recording && !ctx->capturing) return fail(BCH_ERR_NOT_RECORDING, "no recording is open");
   set_lds_limits();
   // No profiling events here (creating them allocates): the launch only.
-  if (n_tokens) run_matmul(ctx->stream, format, W, n_rows, n_cols, xp, yp, n_tokens, store, split);
+  if (n_tokens) run_matmul(ctx->stream, format, W, n_rows, n_cols, xp, yp, n_tokens, store, split, kNoAllocScratchBytes);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(BCH_ERR_EXECUTION, "matmul_noalloc launch: %s", hipGetErrorString(e));
   return BCH_OK;
@@ -542,8 +1029,9 @@ extern "C" int bch_matmul(bch_ctx *ctx, uint32_t format, bch_view weights, uint3
                      : format == 1  ? "matmul_f16"
                                     : "matmul_f32";
   void *split = nullptr;
-  BCH_TRY(ctx_scratch(ctx, matmul_split_bytes(n_tokens, n_cols), &split));
+  const uint64_t scratch_bytes = matmul_scratch_bytes(n_tokens, n_cols, n_rows);
+  BCH_TRY(ctx_scratch(ctx, scratch_bytes, &split));
   return launch(ctx, {name, n_rows, n_cols, rb * n_rows}, [&](hipStream_t s) {
-    if (n_tokens) run_matmul(s, format, W, n_rows, n_cols, xp, yp, n_tokens, store, split);
+    if (n_tokens) run_matmul(s, format, W, n_rows, n_cols, xp, yp, n_tokens, store, split, scratch_bytes);
   });
 }

@@ -55,7 +55,8 @@ struct bch_qwen35 : bch::Sequence {
   uint32_t prefill_splits = 1;
   // Device memory.
   void *k_cache = nullptr, *v_cache = nullptr;
-  void *split = nullptr;  // prefill GEMM inputs split into fp16 halves (matmul_split_bytes)
+  void *split = nullptr;  // prefill GEMM scratch: split inputs and split-K partials (matmul_scratch_bytes)
+  uint64_t split_bytes = 0;
   float *conv_state = nullptr, *delta_state = nullptr;
   float *hidden = nullptr, *normed = nullptr, *q_gate = nullptr, *q = nullptr, *k = nullptr, *v = nullptr,
         *attn = nullptr, *proj = nullptr, *conv_out = nullptr, *z = nullptr, *beta = nullptr, *alpha = nullptr,
@@ -181,9 +182,9 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
     run_rms_norm(st, hidden, L.attn_norm, normed, n, count, norm_eps);
     if (L.attention) {
       const uint32_t ci = L.cache_index;
-      run_matmul(st, L.wq.format, L.wq.data, 2 * q_dim, n, normed, q_gate, count, 0, split);
-      run_matmul(st, L.wk.format, L.wk.data, kv_dim, n, normed, k, count, 0, split);
-      run_matmul(st, L.wv.format, L.wv.data, kv_dim, n, normed, v, count, 0, split);
+      run_matmul(st, L.wq.format, L.wq.data, 2 * q_dim, n, normed, q_gate, count, 0, split, split_bytes);
+      run_matmul(st, L.wk.format, L.wk.data, kv_dim, n, normed, k, count, 0, split, split_bytes);
+      run_matmul(st, L.wv.format, L.wv.data, kv_dim, n, normed, v, count, 0, split, split_bytes);
       // The queries come out of the interleaved query/gate projection.
       run_norm_rope(st, q_gate, q, false, L.q_norm, n_heads, head_dim, n_rot, 2 * head_dim, pos, nullptr, count,
                     2 * q_dim, q_dim, rope_theta, norm_eps, 0);
@@ -217,13 +218,13 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
         ad.max_splits = attn_decode_max_splits(pos + q0 + nq, head_dim, kv_half);
         run_attn_prefill(st, ad, kv_half, nq);
       }
-      run_matmul(st, L.wo.format, L.wo.data, n, q_dim, attn, hidden, count, 1, split);
+      run_matmul(st, L.wo.format, L.wo.data, n, q_dim, attn, hidden, count, 1, split, split_bytes);
     } else {
       const uint32_t di = L.cache_index;
-      run_matmul(st, L.qkv.format, L.qkv.data, conv_dim, n, normed, proj, count, 0, split);
-      run_matmul(st, L.z.format, L.z.data, value_dim, n, normed, z, count, 0, split);
-      run_matmul(st, L.beta.format, L.beta.data, n_v, n, normed, beta, count, 0, split);
-      run_matmul(st, L.alpha.format, L.alpha.data, n_v, n, normed, alpha, count, 0, split);
+      run_matmul(st, L.qkv.format, L.qkv.data, conv_dim, n, normed, proj, count, 0, split, split_bytes);
+      run_matmul(st, L.z.format, L.z.data, value_dim, n, normed, z, count, 0, split, split_bytes);
+      run_matmul(st, L.beta.format, L.beta.data, n_v, n, normed, beta, count, 0, split, split_bytes);
+      run_matmul(st, L.alpha.format, L.alpha.data, n_v, n, normed, alpha, count, 0, split, split_bytes);
       run_gdn_conv(st, proj, L.taps, conv_layer(di), conv_out, conv_dim, conv_kernel, count);
       GdnArgs g{};
       g.y = conv_out;
@@ -243,12 +244,12 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
       // Batches of more than one token take the chunked (WY) form.
       if (count == 1 || !chunk_scratch || !run_gdn_chunked(st, g, chunk_scratch)) run_gdn_recurrence(st, g);
       run_gdn_gated_norm(st, delta_out, L.ssm_norm, z, v_dim, count * n_v, norm_eps);
-      run_matmul(st, L.out.format, L.out.data, n, value_dim, delta_out, hidden, count, 1, split);
+      run_matmul(st, L.out.format, L.out.data, n, value_dim, delta_out, hidden, count, 1, split, split_bytes);
     }
     run_rms_norm(st, hidden, L.ffn_norm, normed, n, count, norm_eps);
-    run_matmul(st, L.gate.format, L.gate.data, n_ff, n, normed, ffn, count, 0, split);
-    run_matmul(st, L.up.format, L.up.data, n_ff, n, normed, ffn, count, 2, split);
-    run_matmul(st, L.down.format, L.down.data, n, n_ff, ffn, hidden, count, 1, split);
+    run_matmul(st, L.gate.format, L.gate.data, n_ff, n, normed, ffn, count, 0, split, split_bytes);
+    run_matmul(st, L.up.format, L.up.data, n_ff, n, normed, ffn, count, 2, split, split_bytes);
+    run_matmul(st, L.down.format, L.down.data, n, n_ff, ffn, hidden, count, 1, split, split_bytes);
     if (trace) run_copy(st, hidden, this->trace + (1 + il) * tstride, count * n, nullptr, 0);
   }
   if (trace) run_rms_norm(st, hidden, output_norm, this->trace + (1 + n_layers) * tstride, n, count, norm_eps);
@@ -379,7 +380,8 @@ int bch_qwen35_new(bch_ctx *ctx, const bch_qwen35_model *md, uint32_t n_ctx, int
            (rc = m->alloc_t(rows * m->value_dim + 4, &m->z)) || (rc = m->alloc_t(rows * m->n_v + 4, &m->beta)) ||
            (rc = m->alloc_t(rows * m->n_v + 4, &m->alpha)) || (rc = m->alloc_t(rows * m->value_dim + 4, &m->delta_out)) ||
            (rc = m->alloc_t(rows * m->n_ff, &m->ffn)) ||
-           (rc = m->alloc(matmul_split_bytes((uint32_t)rows, std::max({n, m->q_dim, m->value_dim, m->n_ff})),
+           (rc = m->alloc(m->split_bytes = matmul_scratch_bytes((uint32_t)rows,
+                                                                std::max({n, m->q_dim, m->value_dim, m->n_ff}), n),
                           &m->split)) || (rc = m->alloc_t(partial_floats + 4, &m->partials)) ||
            (rc = m->alloc_t((uint64_t)kQwenAttnQueryBatch * std::max(1u, m->n_heads), &m->counters)) ||
            (rc = m->alloc_t(gdn_chunk_scratch_floats(m->n_v, m->k_dim, m->v_dim, (uint32_t)rows), &m->chunk_scratch)) ||

@@ -232,13 +232,25 @@ def test_matmul_random_q4k(hip):
     matmul_check(hip, Format.Q4K, w, n_rows, n_cols, n_tokens, Store.OVERWRITE, 5e-3, inputs=x)
 
 
+def half_inputs(x):
+    """The prefill GEMM's inputs: each token scaled by the power of two that
+    puts its largest magnitude in [2^13, 2^14), rounded to fp16, unscaled."""
+    x = np.asarray(x, np.float32)
+    mx = np.abs(x).max(axis=1, keepdims=True)
+    _, ex = np.frexp(mx)
+    scale = np.ldexp(1.0, np.clip(14 - ex, -100, 100)).astype(np.float32)
+    scale[mx == 0] = 1.0
+    return (x * scale).astype(np.float16).astype(np.float64) / scale
+
+
 @pytest.mark.parametrize("fmt", [Format.Q4K, Format.Q6K, Format.Q8_0, Format.Q4_0, Format.Q5K])
 def test_matmul_other_formats(hip, fmt):
     """The prefill GEMM on every block format of real files: each weight is
     the scalar path's dequantised value rounded to half (as the reference's
-    expanded half tiles, lfm2_metal.rs:936-985), inputs keep ~22 bits; so
-    the result equals X times the half-rounded dense matrix within 1e-5, and
-    the exact product within the 5e-3 half tolerance."""
+    expanded half tiles, lfm2_metal.rs:936-985) and each token's inputs are
+    rounded to half after a power-of-two scaling, so the result equals the
+    product of those two roundings within 1e-5 (fp32 accumulation), and the
+    exact product within 5e-3."""
     from bobcat_amd.synth import block_matrix
 
     rng = np.random.default_rng(int(fmt))
@@ -247,13 +259,38 @@ def test_matmul_other_formats(hip, fmt):
     x = rng.standard_normal((n_tokens, n_cols)).astype(np.float32)
     dense = oracle.dequantize(int(fmt), w, n_rows * n_cols).reshape(n_rows, n_cols)
     exact = x.astype(np.float64) @ dense.astype(np.float64).T
-    halves = x.astype(np.float64) @ dense.astype(np.float16).astype(np.float64).T
+    halves = half_inputs(x) @ dense.astype(np.float16).astype(np.float64).T
     wb, xb, yb = hip.buffer_from(w), hip.buffer_from(x), hip.new_buffer(n_tokens * n_rows * 4)
     run(hip, lambda: hip.matmul(fmt, wb.at(0), n_rows, n_cols, xb.at(0), yb.at(0), n_tokens, Store.OVERWRITE))
     got = hip.read(yb.at(0), np.empty((n_tokens, n_rows), np.float32))
     scale = np.abs(exact).max()
     assert np.abs(got - halves).max() / scale < 1e-5
     assert np.abs(got - exact).max() / scale < 5e-3
+
+
+@pytest.mark.parametrize("n_rows,n_cols,n_tokens", [(2048, 10752, 300), (10752, 2048, 512), (512, 2048, 512),
+                                                    (6144, 2048, 200), (64, 512, 129)])
+@pytest.mark.parametrize("store", [Store.OVERWRITE, Store.ACCUMULATE, Store.SWIGLU])
+def test_matmul_tiles_and_splits(hip, n_rows, n_cols, n_tokens, store):
+    """Config-scale shapes through every tile choice (256- and 128-token
+    tiles, 128- and 64-row tiles) and column split (up to 8 splits, added
+    by the reduction), against the product of the half-rounded operands."""
+    rng = np.random.default_rng(n_rows + n_tokens)
+    w = q4k_matrix(rng, n_rows, n_cols)
+    x = rng.standard_normal((n_tokens, n_cols)).astype(np.float32)
+    dense = oracle.dequantize(int(Format.Q4K), w, n_rows * n_cols).reshape(n_rows, n_cols)
+    prod = half_inputs(x) @ dense.astype(np.float16).astype(np.float64).T
+    prior = rng.standard_normal((n_tokens, n_rows)).astype(np.float32)
+    if store == Store.OVERWRITE:
+        want = prod
+    elif store == Store.ACCUMULATE:
+        want = prior + prod
+    else:
+        want = prior / (1.0 + np.exp(-prior.astype(np.float64))) * prod
+    wb, xb, yb = hip.buffer_from(w), hip.buffer_from(x), hip.buffer_from(prior)
+    run(hip, lambda: hip.matmul(Format.Q4K, wb.at(0), n_rows, n_cols, xb.at(0), yb.at(0), n_tokens, store))
+    got = hip.read(yb.at(0), np.empty((n_tokens, n_rows), np.float32))
+    assert np.abs(got - want).max() / np.abs(want).max() < 1e-5
 
 
 def test_matmul_f16(hip):

@@ -27,6 +27,7 @@ from bobcat_amd.qwen35 import (QWEN35_TINY, QWEN35_TINY_64, QWEN35_TINY_V192, QW
 pytestmark = pytest.mark.gpu
 
 TOLERANCE = 1e-4
+PREFILL_TOLERANCE = 1e-3
 HALF_TOLERANCE = 5e-3
 
 
@@ -68,8 +69,12 @@ def test_steps_match_oracle_layer_by_layer(hip, weights, kv_half):
 
 @pytest.mark.parametrize("kv_half", [False, True])
 def test_prefill_trace_matches_oracle(hip, weights, kv_half):
+    """The batched pass against the oracle's token-by-token steps.  The
+    prefill GEMM rounds weights and inputs to half precision (the weights
+    as the reference's expanded half tiles), so with an f32 KV cache the
+    layers match within 1e-3 relative rather than the decode path's 1e-4."""
     cfg = weights.cfg
-    tol = HALF_TOLERANCE if kv_half else TOLERANCE
+    tol = HALF_TOLERANCE if kv_half else PREFILL_TOLERANCE
     toks = prompt(cfg, 30, seed=2)
     gpu = Qwen35Hip(hip, weights, n_ctx=40, kv_half=kv_half)
     lg, (emb, layers, final) = gpu.prefill(toks, trace=True)
