@@ -230,7 +230,12 @@ uint32_t attn_prefill_splits(uint32_t n_heads, uint32_t n_kv, uint32_t head_dim,
 // all; matmul_split_bytes alone allows none).
 uint64_t matmul_split_bytes(uint32_t n_rows, uint32_t n_cols);
 uint64_t matmul_scratch_bytes(uint32_t n_tokens, uint32_t n_cols, uint32_t n_rows);
+// store 3: y = silu(W·x) ⊙ (W2·x), W and W2 the gate and up matrices of
+// a SwiGLU (same format and shape).  split_ready: the previous run_matmul
+// on this scratch had the same x, n_tokens and n_cols, so its fp16 inputs
+// are reused instead of converted again.
 void run_matmul(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,
-                float *y, uint32_t n_tokens, uint32_t store, void *scratch, uint64_t scratch_bytes);
+                float *y, uint32_t n_tokens, uint32_t store, void *scratch, uint64_t scratch_bytes,
+                bool split_ready = false, const uint8_t *W2 = nullptr);
 
 }  // namespace bch

@@ -239,8 +239,9 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
     } else {
       const uint32_t ci = L.cache_index;
       run_matmul(s, L.wq.format, L.wq.data, m->q_dim, n, m->normed, m->q, count, 0, m->split, m->split_bytes);
-      run_matmul(s, L.wk.format, L.wk.data, m->kv_dim, n, m->normed, m->k, count, 0, m->split, m->split_bytes);
-      run_matmul(s, L.wv.format, L.wv.data, m->kv_dim, n, m->normed, m->v, count, 0, m->split, m->split_bytes);
+      // (k and v reuse the fp16 inputs q's launch converted.)
+      run_matmul(s, L.wk.format, L.wk.data, m->kv_dim, n, m->normed, m->k, count, 0, m->split, m->split_bytes, true);
+      run_matmul(s, L.wv.format, L.wv.data, m->kv_dim, n, m->normed, m->v, count, 0, m->split, m->split_bytes, true);
       check_finite(s, "q", il, m->q, (uint64_t)count * m->q_dim);
       check_finite(s, "k", il, m->k, (uint64_t)count * m->kv_dim);
       check_finite(s, "v", il, m->v, (uint64_t)count * m->kv_dim);
@@ -308,10 +309,16 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
       }
       check_finite(s, "moe", il, m->hidden, (uint64_t)count * n);
     } else {
-      run_matmul(s, L.gate.format, L.gate.data, m->n_ff, n, m->normed, m->ffn, count, 0, m->split, m->split_bytes);
-      check_finite(s, "gate", il, m->ffn, (uint64_t)count * m->n_ff);
-      run_matmul(s, L.up.format, L.up.data, m->n_ff, n, m->normed, m->ffn, count, 2, m->split, m->split_bytes);
-      check_finite(s, "up", il, m->ffn, (uint64_t)count * m->n_ff);
+      if (L.gate.format == L.up.format) {
+        // Gate and up in one paired launch: ffn = silu(gate·x) ⊙ (up·x).
+        run_matmul(s, L.gate.format, L.gate.data, m->n_ff, n, m->normed, m->ffn, count, 3, m->split, m->split_bytes,
+                   false, L.up.data);
+      } else {
+        run_matmul(s, L.gate.format, L.gate.data, m->n_ff, n, m->normed, m->ffn, count, 0, m->split, m->split_bytes);
+        check_finite(s, "gate", il, m->ffn, (uint64_t)count * m->n_ff);
+        run_matmul(s, L.up.format, L.up.data, m->n_ff, n, m->normed, m->ffn, count, 2, m->split, m->split_bytes, true);
+      }
+      check_finite(s, "swiglu", il, m->ffn, (uint64_t)count * m->n_ff);
       run_matmul(s, L.down.format, L.down.data, n, m->n_ff, m->ffn, m->hidden, count, 1, m->split, m->split_bytes);
       check_finite(s, "down", il, m->hidden, (uint64_t)count * n);
     }

@@ -531,11 +531,20 @@ __device__ __forceinline__ void gemm_dequant_all(const uint8_t *__restrict__ row
 }
 
 // Y (store) or partials: D[token][row] of the launch.  Splits > 1 write
-// partial products to P[split] (k_gemm_reduce applies the store).
+// partial products to P[split] (k_gemm_reduce applies the store).  STORE 3
+// is the SwiGLU pair (Metal::matmul_experts's paired tile,
+// matmul.metal:249-395, for dense matrices): the tile's first RB/2 rows
+// are rows of W (gate projections), the other RB/2 the same rows of W2
+// (up projections), and Y receives silu(gate)·up for RB/2 output rows, so
+// the gate products never go through memory and each token's inputs are
+// loaded once for both matrices.
 template <uint32_t FMT, int STORE, int RB, int NW, int NB>
-__global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W, uint64_t row_bytes, HiInputs X,
-                                                  float *__restrict__ Y, float *__restrict__ P, uint32_t n_rows,
-                                                  uint32_t n_cols, uint32_t n_tokens, uint32_t splits) {
+__global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W, const uint8_t *__restrict__ W2,
+                                                  uint64_t row_bytes, HiInputs X, float *__restrict__ Y,
+                                                  float *__restrict__ P, uint32_t n_rows, uint32_t n_cols,
+                                                  uint32_t n_tokens, uint32_t splits) {
+  constexpr bool PAIR = STORE == 3;
+  constexpr int OR = PAIR ? RB / 2 : RB;  // output rows per tile
   constexpr int NT = 64 * NW;          // threads
   constexpr int MB = RB / 32;          // row blocks
   constexpr int BT = 32 * NB * NW;     // tokens per tile
@@ -548,7 +557,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W,
   __shared__ __align__(16) _Float16 A[3][RB * kGA];
   __shared__ float us_s[BT];           // the tile's token scales
   const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64, h = lane / 32;
-  const uint32_t n_rt = (n_rows + RB - 1) / RB, n_tt = (n_tokens + BT - 1) / BT;
+  const uint32_t n_rt = (n_rows + OR - 1) / OR, n_tt = (n_tokens + BT - 1) / BT;
   const uint32_t total = n_rt * n_tt * splits;
   // XCD-aware order: workgroup L runs on XCD L % 8, so logical tile
   // (L % 8)·⌈total/8⌉ + L/8 hands each XCD a contiguous run, split-major
@@ -557,7 +566,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W,
   const uint32_t per = (total + 7) / 8, logical = (blockIdx.x % 8) * per + blockIdx.x / 8;
   if (logical >= total) return;
   const uint32_t rt = logical % n_rt, tt = (logical / n_rt) % n_tt, sp = logical / (n_rt * n_tt);
-  const uint32_t row0 = rt * RB, tok0 = tt * BT;
+  const uint32_t row0 = rt * OR, tok0 = tt * BT;
   const uint32_t n_stages = n_cols / kGk;
   const uint32_t st0 = (uint32_t)((uint64_t)sp * n_stages / splits);
   const uint32_t st1 = (uint32_t)((uint64_t)(sp + 1) * n_stages / splits);
@@ -566,7 +575,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W,
   // Dequantising role: weight row ar, part ac.  (Rows past the end are
   // clamped; their outputs are never stored.)
   const int ar = tid / TPR, ac = tid % TPR;
-  const uint8_t *wrow = W + (uint64_t)min(row0 + ar, n_rows - 1) * row_bytes;
+  const uint8_t *wrow = PAIR && ar >= OR ? W2 + (uint64_t)min(row0 + ar - OR, n_rows - 1) * row_bytes
+                                         : W + (uint64_t)min(row0 + ar, n_rows - 1) * row_bytes;
   // MFMA role: tokens tok0 + 32·NB·wave + 32j + lane%32 (clamped), lane half h.
   const u32x4 *xrow[NB];
 #pragma unroll
@@ -678,7 +688,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W,
   // addresses) are unconditional so that they issue together; only the
   // stores test bounds.
 #pragma unroll
-  for (int i = 0; i < MB; i++) {
+  for (int i = 0; i < OR / 32; i++) {
     const uint32_t row = row0 + 32 * i + lane % 32;
     const uint32_t rowc = min(row, n_rows - 1);
 #pragma unroll
@@ -690,11 +700,14 @@ __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W,
       for (int e = 0; e < 16; e++) {
         const int tl = tw + 8 * (e / 4) + 4 * h + e % 4;
         v[e] = acc[i][j][e] * us_s[tl];
-        if (STORE != 0 && splits == 1) prior[e] = Y[(uint64_t)min(tok0 + tl, n_tokens - 1) * n_rows + rowc];
+        if (PAIR) prior[e] = acc[i + OR / 32][j][e] * us_s[tl];  // the up product
+        else if (STORE != 0 && splits == 1) prior[e] = Y[(uint64_t)min(tok0 + tl, n_tokens - 1) * n_rows + rowc];
       }
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        if (splits > 1)
+        if (PAIR)
+          v[e] = silu_f(v[e]) * prior[e];
+        else if (splits > 1)
           ;
         else if (STORE == 1)
           v[e] += prior[e];
@@ -734,17 +747,22 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ P
 }
 
 template <uint32_t FMT, int RB, int NW, int NB>
-static void gemm_launch(hipStream_t s, const uint8_t *W, uint64_t rb, const HiInputs &x, float *y, float *part,
-                        uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens, uint32_t store, uint32_t splits) {
-  const uint32_t total = div_ceil(n_rows, RB) * div_ceil(n_tokens, 32 * NB * NW) * splits;
+static void gemm_launch(hipStream_t s, const uint8_t *W, const uint8_t *W2, uint64_t rb, const HiInputs &x, float *y,
+                        float *part, uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens, uint32_t store,
+                        uint32_t splits) {
+  const uint32_t out_rows = store == 3 ? RB / 2 : RB;
+  const uint32_t total = div_ceil(n_rows, out_rows) * div_ceil(n_tokens, 32 * NB * NW) * splits;
   const dim3 grid(8 * div_ceil(total, 8));
-  if (splits > 1 || store == 0)
-    k_gemm<FMT, 0, RB, NW, NB><<<grid, 64 * NW, 0, s>>>(W, rb, x, y, part, n_rows, n_cols, n_tokens, splits);
+  const dim3 block(64 * NW);
+  if (store == 3)
+    k_gemm<FMT, 3, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, 1);
+  else if (splits > 1 || store == 0)
+    k_gemm<FMT, 0, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, splits);
   else if (store == 1)
-    k_gemm<FMT, 1, RB, NW, NB><<<grid, 64 * NW, 0, s>>>(W, rb, x, y, part, n_rows, n_cols, n_tokens, splits);
+    k_gemm<FMT, 1, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, splits);
   else
-    k_gemm<FMT, 2, RB, NW, NB><<<grid, 64 * NW, 0, s>>>(W, rb, x, y, part, n_rows, n_cols, n_tokens, splits);
-  if (splits > 1) {
+    k_gemm<FMT, 2, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, splits);
+  if (splits > 1 && store != 3) {
     const uint64_t n = (uint64_t)n_tokens * n_rows;
     const dim3 g((uint32_t)((n + 255) / 256));
     if (store == 0)
@@ -781,16 +799,21 @@ static GemmShape gemm_shape(uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens,
 }
 
 template <uint32_t FMT>
-static void gemm_fmt(hipStream_t s, const uint8_t *W, uint64_t rb, const HiInputs &x, float *y, float *part,
-                     uint64_t part_floats, uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens, uint32_t store,
-                     uint32_t cus) {
-  GemmShape g = gemm_shape(n_rows, n_cols, n_tokens, part_floats, cus);
+static void gemm_fmt(hipStream_t s, const uint8_t *W, const uint8_t *W2, uint64_t rb, const HiInputs &x, float *y,
+                     float *part, uint64_t part_floats, uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens,
+                     uint32_t store, uint32_t cus) {
+  GemmShape g = gemm_shape(store == 3 ? 2 * n_rows : n_rows, n_cols, n_tokens, part_floats, cus);
+  if (store == 3) {
+    // The pair needs 128-row tiles (64 output rows) and no column split.
+    g.splits = 1;
+    if (g.cfg == 2) g.cfg = 1;
+  }
   if (g.cfg == 0)
-    gemm_launch<FMT, 128, 8, 1>(s, W, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits);
+    gemm_launch<FMT, 128, 8, 1>(s, W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits);
   else if (g.cfg == 1)
-    gemm_launch<FMT, 128, 4, 1>(s, W, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits);
+    gemm_launch<FMT, 128, 4, 1>(s, W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits);
   else
-    gemm_launch<FMT, 64, 4, 1>(s, W, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits);
+    gemm_launch<FMT, 64, 4, 1>(s, W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits);
 }
 
 template <uint32_t FMT, int MB>
@@ -855,27 +878,29 @@ static uint32_t device_cus() {
 }
 
 void run_matmul(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *xf,
-                float *y, uint32_t n_tokens, uint32_t store, void *scratch, uint64_t scratch_bytes) {
+                float *y, uint32_t n_tokens, uint32_t store, void *scratch, uint64_t scratch_bytes, bool split_ready,
+                const uint8_t *W2) {
   if (!n_tokens) return;
   const uint64_t rb = bch_row_bytes(format, n_cols);
   // The fp16 inputs and their scales (n_tokens·(2·n_cols + 4) bytes, within
-  // matmul_split_bytes), then the split-K partials.
+  // matmul_split_bytes), then the split-K partials.  With split_ready the
+  // previous launch on this scratch converted the same inputs.
   _Float16 *hx = static_cast<_Float16 *>(scratch);
   float *unscale = reinterpret_cast<float *>(hx + (uint64_t)n_tokens * n_cols);
-  k_split_hi<<<n_tokens, 256, 0, s>>>(xf, n_cols, hx, unscale);
+  if (!split_ready) k_split_hi<<<n_tokens, 256, 0, s>>>(xf, n_cols, hx, unscale);
   const HiInputs x{hx, unscale};
   const uint64_t used = (matmul_split_bytes(n_tokens, n_cols) + 255) / 256 * 256;
   float *part = reinterpret_cast<float *>(static_cast<uint8_t *>(scratch) + used);
   const uint64_t part_floats = scratch_bytes > used ? (scratch_bytes - used) / 4 : 0;
   const uint32_t cus = device_cus();
   switch (format) {
-    case 12: gemm_fmt<12>(s, W, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
-    case 1: gemm_fmt<1>(s, W, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
-    case 14: gemm_fmt<14>(s, W, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
-    case 13: gemm_fmt<13>(s, W, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
-    case 8: gemm_fmt<8>(s, W, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
-    case 2: gemm_fmt<2>(s, W, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
-    default: gemm_fmt<0>(s, W, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
+    case 12: gemm_fmt<12>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
+    case 1: gemm_fmt<1>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
+    case 14: gemm_fmt<14>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
+    case 13: gemm_fmt<13>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
+    case 8: gemm_fmt<8>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
+    case 2: gemm_fmt<2>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
+    default: gemm_fmt<0>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
   }
 }
 

@@ -183,8 +183,9 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
     if (L.attention) {
       const uint32_t ci = L.cache_index;
       run_matmul(st, L.wq.format, L.wq.data, 2 * q_dim, n, normed, q_gate, count, 0, split, split_bytes);
-      run_matmul(st, L.wk.format, L.wk.data, kv_dim, n, normed, k, count, 0, split, split_bytes);
-      run_matmul(st, L.wv.format, L.wv.data, kv_dim, n, normed, v, count, 0, split, split_bytes);
+      // (k and v reuse the fp16 inputs q's launch converted.)
+      run_matmul(st, L.wk.format, L.wk.data, kv_dim, n, normed, k, count, 0, split, split_bytes, true);
+      run_matmul(st, L.wv.format, L.wv.data, kv_dim, n, normed, v, count, 0, split, split_bytes, true);
       // The queries come out of the interleaved query/gate projection.
       run_norm_rope(st, q_gate, q, false, L.q_norm, n_heads, head_dim, n_rot, 2 * head_dim, pos, nullptr, count,
                     2 * q_dim, q_dim, rope_theta, norm_eps, 0);
@@ -222,9 +223,9 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
     } else {
       const uint32_t di = L.cache_index;
       run_matmul(st, L.qkv.format, L.qkv.data, conv_dim, n, normed, proj, count, 0, split, split_bytes);
-      run_matmul(st, L.z.format, L.z.data, value_dim, n, normed, z, count, 0, split, split_bytes);
-      run_matmul(st, L.beta.format, L.beta.data, n_v, n, normed, beta, count, 0, split, split_bytes);
-      run_matmul(st, L.alpha.format, L.alpha.data, n_v, n, normed, alpha, count, 0, split, split_bytes);
+      run_matmul(st, L.z.format, L.z.data, value_dim, n, normed, z, count, 0, split, split_bytes, true);
+      run_matmul(st, L.beta.format, L.beta.data, n_v, n, normed, beta, count, 0, split, split_bytes, true);
+      run_matmul(st, L.alpha.format, L.alpha.data, n_v, n, normed, alpha, count, 0, split, split_bytes, true);
       run_gdn_conv(st, proj, L.taps, conv_layer(di), conv_out, conv_dim, conv_kernel, count);
       GdnArgs g{};
       g.y = conv_out;
@@ -247,8 +248,14 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
       run_matmul(st, L.out.format, L.out.data, n, value_dim, delta_out, hidden, count, 1, split, split_bytes);
     }
     run_rms_norm(st, hidden, L.ffn_norm, normed, n, count, norm_eps);
-    run_matmul(st, L.gate.format, L.gate.data, n_ff, n, normed, ffn, count, 0, split, split_bytes);
-    run_matmul(st, L.up.format, L.up.data, n_ff, n, normed, ffn, count, 2, split, split_bytes);
+    if (L.gate.format == L.up.format) {
+      // Gate and up in one paired launch: ffn = silu(gate·x) ⊙ (up·x).
+      run_matmul(st, L.gate.format, L.gate.data, n_ff, n, normed, ffn, count, 3, split, split_bytes, false,
+                 L.up.data);
+    } else {
+      run_matmul(st, L.gate.format, L.gate.data, n_ff, n, normed, ffn, count, 0, split, split_bytes);
+      run_matmul(st, L.up.format, L.up.data, n_ff, n, normed, ffn, count, 2, split, split_bytes, true);
+    }
     run_matmul(st, L.down.format, L.down.data, n, n_ff, ffn, hidden, count, 1, split, split_bytes);
     if (trace) run_copy(st, hidden, this->trace + (1 + il) * tstride, count * n, nullptr, 0);
   }
