@@ -774,28 +774,34 @@ static void gemm_launch(hipStream_t s, const uint8_t *W, const uint8_t *W2, uint
   }
 }
 
-// Tile and column split of a launch: 256-token tiles for batches of more
-// than 128 tokens (128 otherwise), 128-row tiles (64 for matrices of at
-// most 64 rows), then split K (at least 4 stages per split, partials
-// within `part_floats`) until the tiles cover the CUs.
+// Tile and column split of a launch, from measurements at 512 tokens: the
+// largest tile that still gives most CUs a workgroup, unsplit — 128 x 256
+// for 10752 x 2048 (168 tiles, 52 us), 128 x 128 for 6144 x 2048 (192
+// tiles, 35 us); long rows split K on the large tile — 2048 x 10752 with
+// 8 splits (49 us; 221 unsplit); the rest take 64 x 128 tiles, splitting
+// while the workgroups fit the CUs — 2048 x 2048 with 2 (23 us), 512 x 2048
+// with 4 (14 us).  Partials must fit `part_floats`.
 struct GemmShape {
   uint32_t cfg, splits;  // cfg 0: 128 rows x 256 tokens, 8 waves; 1: 128 x 128, 4 waves; 2: 64 x 128, 4 waves
 };
 
 static GemmShape gemm_shape(uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens, uint64_t part_floats, uint32_t cus) {
-  const uint32_t cfg = n_rows <= 64 ? 2 : n_tokens > 128 ? 0 : 1;
-  const uint32_t bt = cfg == 0 ? 256 : 128, br = cfg == 2 ? 64 : 128;
-  const uint64_t tiles = (uint64_t)div_ceil(n_rows, br) * div_ceil(n_tokens, bt);
-  // Doubling the splits while the workgroups still fit the CUs: at 512
-  // tokens a 10752 x 2048 matrix (168 tiles) runs best unsplit (51 us; 73
-  // with two splits and their reduction), 2048 x 10752 (32 tiles) with 8
-  // (49 us; 220 unsplit), 6144 x 2048 (96 tiles) with 2.
-  uint32_t splits = 1;
+  auto tiles = [&](uint32_t br, uint32_t bt) { return (uint64_t)div_ceil(n_rows, br) * div_ceil(n_tokens, bt); };
+  const uint64_t enough = (uint64_t)cus * 3 / 5;
   const uint32_t n_stages = n_cols / kGk;
-  while (splits < kMaxSplitK && tiles * splits * 2 <= cus && n_stages / (2 * splits) >= 4 &&
-         (uint64_t)2 * splits * n_tokens * n_rows <= part_floats)
-    splits *= 2;
-  return {cfg, splits};
+  auto fits = [&](uint32_t splits) {
+    return splits <= kMaxSplitK && n_stages / splits >= 8 && (uint64_t)splits * n_tokens * n_rows <= part_floats;
+  };
+  if (n_tokens > 128 && n_rows > 64 && tiles(128, 256) >= enough) return {0, 1};
+  if (n_tokens > 128 && n_rows > 64 && n_cols >= 8192) {
+    uint32_t splits = 1;
+    while (tiles(128, 256) * splits < cus && fits(2 * splits)) splits *= 2;
+    return {0, splits};
+  }
+  if (n_rows > 64 && tiles(128, 128) >= enough) return {1, 1};
+  uint32_t splits = 1;
+  while (tiles(64, 128) * splits * 2 <= cus && fits(2 * splits)) splits *= 2;
+  return {2, splits};
 }
 
 template <uint32_t FMT>
