@@ -230,6 +230,11 @@ uint32_t attn_prefill_splits(uint32_t n_heads, uint32_t n_kv, uint32_t head_dim,
 // all; matmul_split_bytes alone allows none).
 uint64_t matmul_split_bytes(uint32_t n_rows, uint32_t n_cols);
 uint64_t matmul_scratch_bytes(uint32_t n_tokens, uint32_t n_cols, uint32_t n_rows);
+// run_rms_norm's output for `rows` rows of n, and in `scratch` the fp16
+// inputs a following run_matmul(..., x = out, n_tokens = rows, n_cols = n,
+// scratch, ..., split_ready = true) reads.
+void run_rms_norm_split(hipStream_t s, const float *x, const float *w, float *out, uint32_t n, uint32_t rows,
+                        float eps, void *scratch);
 // store 3: y = silu(W·x) ⊙ (W2·x), W and W2 the gate and up matrices of
 // a SwiGLU (same format and shape).  split_ready: the previous run_matmul
 // on this scratch had the same x, n_tokens and n_cols, so its fp16 inputs

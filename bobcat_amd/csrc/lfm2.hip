@@ -226,11 +226,13 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
   if (trace) run_copy(s, m->hidden, m->trace, count * n, nullptr, 0);
   for (uint32_t il = 0; il < m->n_layers; il++) {
     const Layer &L = m->layers[il];
-    run_rms_norm(s, m->hidden, L.attn_norm, m->normed, n, count, m->norm_eps);
+    // The norm also writes the fp16 inputs of the projection that follows.
+    run_rms_norm_split(s, m->hidden, L.attn_norm, m->normed, n, count, m->norm_eps, m->split);
     check_finite(s, "attn_norm", il, m->normed, (uint64_t)count * n);
     if (!L.attention) {
       float *hist = m->conv_state + (uint64_t)L.cache_index * (m->conv_kernel - 1) * n;
-      run_matmul(s, L.in_proj.format, L.in_proj.data, 3 * n, n, m->normed, m->bcx, count, 0, m->split, m->split_bytes);
+      run_matmul(s, L.in_proj.format, L.in_proj.data, 3 * n, n, m->normed, m->bcx, count, 0, m->split, m->split_bytes,
+                 true);
       check_finite(s, "in_proj", il, m->bcx, (uint64_t)count * 3 * n);
       run_short_conv_batch(s, m->bcx, L.taps, hist, m->conv_out, n, m->conv_kernel, count);
       check_finite(s, "short_conv", il, m->conv_out, (uint64_t)count * n);
@@ -238,8 +240,8 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
       check_finite(s, "out_proj", il, m->hidden, (uint64_t)count * n);
     } else {
       const uint32_t ci = L.cache_index;
-      run_matmul(s, L.wq.format, L.wq.data, m->q_dim, n, m->normed, m->q, count, 0, m->split, m->split_bytes);
-      // (k and v reuse the fp16 inputs q's launch converted.)
+      run_matmul(s, L.wq.format, L.wq.data, m->q_dim, n, m->normed, m->q, count, 0, m->split, m->split_bytes, true);
+      // (q, k and v read the fp16 inputs the norm wrote.)
       run_matmul(s, L.wk.format, L.wk.data, m->kv_dim, n, m->normed, m->k, count, 0, m->split, m->split_bytes, true);
       run_matmul(s, L.wv.format, L.wv.data, m->kv_dim, n, m->normed, m->v, count, 0, m->split, m->split_bytes, true);
       check_finite(s, "q", il, m->q, (uint64_t)count * m->q_dim);
@@ -283,7 +285,10 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
       run_matmul(s, L.wo.format, L.wo.data, n, m->q_dim, m->attn, m->hidden, count, 1, m->split, m->split_bytes);
       check_finite(s, "attn_output", il, m->hidden, (uint64_t)count * n);
     }
-    run_rms_norm(s, m->hidden, L.ffn_norm, m->normed, n, count, m->norm_eps);
+    if (L.moe)
+      run_rms_norm(s, m->hidden, L.ffn_norm, m->normed, n, count, m->norm_eps);
+    else
+      run_rms_norm_split(s, m->hidden, L.ffn_norm, m->normed, n, count, m->norm_eps, m->split);
     check_finite(s, "ffn_norm", il, m->normed, (uint64_t)count * n);
     if (L.moe) {
       // Route the whole batch in one launch, then each token's experts.
@@ -312,9 +317,10 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
       if (L.gate.format == L.up.format) {
         // Gate and up in one paired launch: ffn = silu(gate·x) ⊙ (up·x).
         run_matmul(s, L.gate.format, L.gate.data, m->n_ff, n, m->normed, m->ffn, count, 3, m->split, m->split_bytes,
-                   false, L.up.data);
+                   true, L.up.data);
       } else {
-        run_matmul(s, L.gate.format, L.gate.data, m->n_ff, n, m->normed, m->ffn, count, 0, m->split, m->split_bytes);
+        run_matmul(s, L.gate.format, L.gate.data, m->n_ff, n, m->normed, m->ffn, count, 0, m->split, m->split_bytes,
+                   true);
         check_finite(s, "gate", il, m->ffn, (uint64_t)count * m->n_ff);
         run_matmul(s, L.up.format, L.up.data, m->n_ff, n, m->normed, m->ffn, count, 2, m->split, m->split_bytes, true);
       }

@@ -411,6 +411,45 @@ __global__ __launch_bounds__(256) void k_split_hi(const float *__restrict__ X, u
   }
 }
 
+// k_rms_norm (ops.hip) and k_split_hi in one pass over each row: `out`
+// receives exactly k_rms_norm's values (same per-thread sums, reduction and
+// scale), and H/unscale the fp16 form of those values that k_split_hi would
+// make, so the GEMM that follows skips its own conversion.
+__global__ __launch_bounds__(256) void k_rms_norm_split(const float *__restrict__ x, const float *__restrict__ w,
+                                                       float *__restrict__ out, uint32_t n, float eps,
+                                                       _Float16 *__restrict__ H, float *__restrict__ unscale) {
+  __shared__ float red[4];
+  const uint32_t t = blockIdx.x, tid = threadIdx.x;
+  const float *xr = x + (uint64_t)t * n;
+  float *orow = out + (uint64_t)t * n;
+  float ss = 0.f;
+  for (uint32_t i = tid; i < n; i += 256) ss = fmaf(xr[i], xr[i], ss);
+  ss = block_sum<256>(ss, red);
+  const float scale = (float)(1.0 / sqrt((double)ss / (double)n + (double)eps));
+  float mx = 0.f;
+  for (uint32_t i = tid; i < n; i += 256) {
+    const float v = w[i] * (xr[i] * scale);
+    orow[i] = v;
+    mx = fmaxf(mx, fabsf(v));
+  }
+  mx = block_max<256>(mx, red);
+  int ex = 0;
+  if (mx > 0.f) frexpf(mx, &ex);  // mx < 2^ex
+  const int k = max(-100, min(100, 14 - ex));
+  const float s2 = ldexpf(1.0f, k);
+  if (tid == 0) unscale[t] = ldexpf(1.0f, -k);
+  _Float16 *hrow = H + (uint64_t)t * n;
+  for (uint32_t i = tid; i < n; i += 256) hrow[i] = (_Float16)(orow[i] * s2);
+}
+
+void run_rms_norm_split(hipStream_t s, const float *x, const float *w, float *out, uint32_t n, uint32_t rows,
+                        float eps, void *scratch) {
+  if (!rows) return;
+  _Float16 *hx = static_cast<_Float16 *>(scratch);
+  float *unscale = reinterpret_cast<float *>(hx + (uint64_t)rows * n);
+  k_rms_norm_split<<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale);
+}
+
 struct HiInputs {
   const _Float16 *h;
   const float *unscale;

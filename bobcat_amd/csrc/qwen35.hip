@@ -179,11 +179,11 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
   if (trace) run_copy(st, hidden, this->trace, count * n, nullptr, 0);
   for (uint32_t il = 0; il < n_layers; il++) {
     const QwenLayer &L = layers[il];
-    run_rms_norm(st, hidden, L.attn_norm, normed, n, count, norm_eps);
+    // The norm also writes the fp16 inputs of the projections that follow.
+    run_rms_norm_split(st, hidden, L.attn_norm, normed, n, count, norm_eps, split);
     if (L.attention) {
       const uint32_t ci = L.cache_index;
-      run_matmul(st, L.wq.format, L.wq.data, 2 * q_dim, n, normed, q_gate, count, 0, split, split_bytes);
-      // (k and v reuse the fp16 inputs q's launch converted.)
+      run_matmul(st, L.wq.format, L.wq.data, 2 * q_dim, n, normed, q_gate, count, 0, split, split_bytes, true);
       run_matmul(st, L.wk.format, L.wk.data, kv_dim, n, normed, k, count, 0, split, split_bytes, true);
       run_matmul(st, L.wv.format, L.wv.data, kv_dim, n, normed, v, count, 0, split, split_bytes, true);
       // The queries come out of the interleaved query/gate projection.
@@ -222,7 +222,7 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
       run_matmul(st, L.wo.format, L.wo.data, n, q_dim, attn, hidden, count, 1, split, split_bytes);
     } else {
       const uint32_t di = L.cache_index;
-      run_matmul(st, L.qkv.format, L.qkv.data, conv_dim, n, normed, proj, count, 0, split, split_bytes);
+      run_matmul(st, L.qkv.format, L.qkv.data, conv_dim, n, normed, proj, count, 0, split, split_bytes, true);
       run_matmul(st, L.z.format, L.z.data, value_dim, n, normed, z, count, 0, split, split_bytes, true);
       run_matmul(st, L.beta.format, L.beta.data, n_v, n, normed, beta, count, 0, split, split_bytes, true);
       run_matmul(st, L.alpha.format, L.alpha.data, n_v, n, normed, alpha, count, 0, split, split_bytes, true);
@@ -247,13 +247,13 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
       run_gdn_gated_norm(st, delta_out, L.ssm_norm, z, v_dim, count * n_v, norm_eps);
       run_matmul(st, L.out.format, L.out.data, n, value_dim, delta_out, hidden, count, 1, split, split_bytes);
     }
-    run_rms_norm(st, hidden, L.ffn_norm, normed, n, count, norm_eps);
+    run_rms_norm_split(st, hidden, L.ffn_norm, normed, n, count, norm_eps, split);
     if (L.gate.format == L.up.format) {
       // Gate and up in one paired launch: ffn = silu(gate·x) ⊙ (up·x).
-      run_matmul(st, L.gate.format, L.gate.data, n_ff, n, normed, ffn, count, 3, split, split_bytes, false,
+      run_matmul(st, L.gate.format, L.gate.data, n_ff, n, normed, ffn, count, 3, split, split_bytes, true,
                  L.up.data);
     } else {
-      run_matmul(st, L.gate.format, L.gate.data, n_ff, n, normed, ffn, count, 0, split, split_bytes);
+      run_matmul(st, L.gate.format, L.gate.data, n_ff, n, normed, ffn, count, 0, split, split_bytes, true);
       run_matmul(st, L.up.format, L.up.data, n_ff, n, normed, ffn, count, 2, split, split_bytes, true);
     }
     run_matmul(st, L.down.format, L.down.data, n, n_ff, ffn, hidden, count, 1, split, split_bytes);
