@@ -295,6 +295,44 @@ def host_cpu():
     return int(cores), model
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+
+
+def gemm_leg(hip, reps: int = 20):
+    """The prefill GEMM at LFM2-2.6B's shapes for a 512-token batch: the FFN
+    gate projection (10752 x 2048) and down projection (2048 x 10752) on
+    Q4_K weights, each launch timed over `reps` repetitions with HIP events
+    (each includes the input conversion to fp16).  TFLOP/s counts the
+    2·rows·cols·tokens of the product; the fraction is of MI355X's dense
+    fp16 MFMA peak."""
+    from bobcat_amd.backend import Format, Store
+    from bobcat_amd.synth import q4k_matrix
+
+    rng = np.random.default_rng(5)
+    out = {}
+    for name, rows, cols, store in (("ffn_gate_10752x2048", 10752, 2048, Store.OVERWRITE),
+                                    ("ffn_down_2048x10752", 2048, 10752, Store.ACCUMULATE)):
+        w = hip.buffer_from(q4k_matrix(rng, rows, cols))
+        x = hip.buffer_from(rng.standard_normal(PROMPT * cols).astype(np.float32))
+        y = hip.new_buffer(PROMPT * rows * 4)
+
+        def run(n):
+            hip.begin()
+            for _ in range(n):
+                hip.matmul(Format.Q4K, w.at(0), rows, cols, x.at(0), y.at(0), PROMPT, store)
+            return hip.end()
+
+        run(3)
+        sec = run(reps) / reps
+        tflops = 2.0 * rows * cols * PROMPT / sec / 1e12
+        out[name] = {"us": round(sec * 1e6, 2), "tflops": round(tflops, 1),
+                     "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+        for b in (w, x, y):
+            b.free()
+    out["peak_tflops"] = MFMA_F16_PEAK_TFLOPS
+    return out
+
+
 def cpu_baseline(weights, gemv_case, budget_s: float):
     """The reference's CPU path (the oracle) on the host, in the same run: the
     model's decode rate single-threaded (the reference's scalar path runs on
@@ -371,6 +409,8 @@ def main() -> int:
         log(f"gemv: {g}")
         if args.gemv_only:
             return 0
+        gm = gemm_leg(hip)
+        log(f"prefill gemm: {gm}")
         t = time.perf_counter()
         weights = weights_of(args.model)
         cfg = weights.cfg
@@ -416,6 +456,7 @@ def main() -> int:
         **{k: v for k, v in summary.items() if k != "decode_tok_s"},
         "long_context": lres,
         "models": side or None,
+        "prefill_gemm": gm,
         "roofline": {"kernel": "matvec_q4k (config 1, 8192x2048)", "bound": "hbm",
                      "achieved": round(g["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
