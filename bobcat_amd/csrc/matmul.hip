@@ -1,19 +1,13 @@
 // Prefill GEMM: Y[t] (store) W·X[t] for a batch of tokens, on MFMA.
 //
-// Counterpart of Metal::matmul and Metal::expand + matmul_f16
-// (crates/bobcat-metal/src/backend.rs:2470-2549, matmul.metal:249-438,
-// quant.metal:276-306).  The reference expands Q4_K matrices to fp16 before
-// a full 512-token batch; here each workgroup dequantises its weight tile
-// straight into LDS instead, so the expanded matrix never touches HBM.
-//
-// Two kernels: k_gemm for dense matrices (described at its definition
-// below) and k_matmul for the expert-grouped launches of the MoE layers.
-// k_matmul's tile is 128 weight rows x 64 tokens in pipeline steps of 128
-// columns; before it, k_split_rows scales each token's inputs by a power of
-// two into fp16 range and splits them into an fp16 high part and an fp16
-// residual, and both are multiplied, so those inputs keep ~22 bits.
-// Weights go to LDS as fp16 (the reference's expanded half tiles);
-// accumulation is fp32.
+// Counterpart of Metal::matmul, Metal::matmul_experts and Metal::expand +
+// matmul_f16 (crates/bobcat-metal/src/backend.rs:2470-2549,
+// matmul.metal:249-504, quant.metal:276-306).  The reference expands Q4_K
+// matrices to fp16 before a full 512-token batch; here each workgroup
+// dequantises its weight tile straight into LDS instead, so the expanded
+// matrix never touches HBM.  One kernel, k_gemm (described at its
+// definition), serves dense and expert-grouped launches; accumulation is
+// fp32.
 #include <mutex>
 #include "formats.h"
 #include "kernels.h"
@@ -21,12 +15,7 @@
 
 namespace bch {
 
-constexpr int kBM = 128;      // weight rows of the larger tile
-constexpr int kBN = 64;       // tokens per tile
 constexpr int kBK = 256;      // columns a row must be a multiple of (one Q4_K super-block)
-constexpr int kStep = 128;    // columns per pipeline step (half a super-block)
-constexpr int kPad = 8;       // halves of padding per LDS row (bank spread, 16-byte rows)
-constexpr int kLds = kStep + kPad;
 
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -34,298 +23,14 @@ typedef float float16_t __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
 
-// The raw bytes of 64 consecutive weights of a row (one Q4_K unit: the
-// super-block header and the pair's 32 quant bytes), for prefetching.
-struct RawUnit {
-  uint4 h, q0, q1;
-};
-
-__device__ __forceinline__ RawUnit fetch_q4k(const uint8_t *__restrict__ row, uint32_t k256, int p) {
-  const uint8_t *blk = row + (k256 / 256) * 144;
-  const uint4 *qp = reinterpret_cast<const uint4 *>(blk + 16 + 32 * p);
-  return RawUnit{*reinterpret_cast<const uint4 *>(blk), qp[0], qp[1]};
-}
-
-// Q4_K unit p of a super-block to 64 halves: (d·sc)·q − dmin·m per element.
-__device__ __forceinline__ void expand_q4k(const RawUnit &u, int p, _Float16 *dst) {
-  const uint32_t qw[8] = {u.q0.x, u.q0.y, u.q0.z, u.q0.w, u.q1.x, u.q1.y, u.q1.z, u.q1.w};
-  const uint32_t sc = q4k_pair_scales(u.h.y, u.h.z, u.h.w, p);
-  const float d = half_bits_to_float(u.h.x & 0xffffu), dmin = half_bits_to_float(u.h.x >> 16);
-  const float a_lo = d * ubyte0(sc), a_hi = d * ubyte1(sc);
-  const float b_lo = dmin * ubyte2(sc), b_hi = dmin * ubyte3(sc);
-#pragma unroll
-  for (int k = 0; k < 8; k++) {
-    const uint32_t lo = qw[k] & 0x0f0f0f0fu, hi = (qw[k] >> 4) & 0x0f0f0f0fu;
-    half4_t l4, h4;
-    l4[0] = (_Float16)(a_lo * ubyte0(lo) - b_lo);
-    l4[1] = (_Float16)(a_lo * ubyte1(lo) - b_lo);
-    l4[2] = (_Float16)(a_lo * ubyte2(lo) - b_lo);
-    l4[3] = (_Float16)(a_lo * ubyte3(lo) - b_lo);
-    h4[0] = (_Float16)(a_hi * ubyte0(hi) - b_hi);
-    h4[1] = (_Float16)(a_hi * ubyte1(hi) - b_hi);
-    h4[2] = (_Float16)(a_hi * ubyte2(hi) - b_hi);
-    h4[3] = (_Float16)(a_hi * ubyte3(hi) - b_hi);
-    *reinterpret_cast<half4_t *>(dst + 4 * k) = l4;
-    *reinterpret_cast<half4_t *>(dst + 32 + 4 * k) = h4;
-  }
-}
-
-// F16/F32 rows: 64 consecutive weights from column k to halves.
-template <uint32_t FMT>
-__device__ __forceinline__ void expand_float(const uint8_t *__restrict__ row, uint32_t k, _Float16 *dst) {
-  if constexpr (FMT == 1) {
-    const uint4 *src = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(row) + k);
-    uint4 *o = reinterpret_cast<uint4 *>(dst);
-#pragma unroll
-    for (int i = 0; i < 8; i++) o[i] = src[i];
-  } else {
-    const float4 *src = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(row) + k);
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const float4 v = src[i];
-      half4_t h;
-      h[0] = (_Float16)v.x;
-      h[1] = (_Float16)v.y;
-      h[2] = (_Float16)v.z;
-      h[3] = (_Float16)v.w;
-      *reinterpret_cast<half4_t *>(dst + 4 * i) = h;
-    }
-  }
-}
-
-// Q8_0 / Q4_0 / Q5_K / Q6_K rows: 64 consecutive weights from column k, each
-// dequantised exactly as the scalar path does (formats.h dequant_elem), then
-// rounded to half.  (These formats appear in a few tensors of real Q4_K_M
-// files; the byte-wise reads are not tuned.)
-template <uint32_t FMT>
-__device__ __forceinline__ void expand_generic(const uint8_t *__restrict__ row, uint32_t k, _Float16 *dst) {
-#pragma unroll 8
-  for (int i = 0; i < 64; i += 4) {
-    half4_t h;
-#pragma unroll
-    for (int j = 0; j < 4; j++) h[j] = (_Float16)dequant_elem(FMT, row, k + i + j);
-    *reinterpret_cast<half4_t *>(dst + i) = h;
-  }
-}
-
-// Row t of X [n_rows x n_cols] f32 to fp16 high and low parts: with s the
-// power of two that puts max|x_t| in [2^13, 2^14) (half precision cannot
-// overflow in the MFMA operands), hi = fp16(x·s), lo = fp16(x·s − hi), and
-// unscale[t] = 1/s.  Each group of 8 columns is stored as its 8 high halves
-// then its 8 low halves (32 bytes), so a GEMM thread's 32 columns of a step
-// are 128 contiguous bytes.  One workgroup per row.
-__global__ __launch_bounds__(256) void k_split_rows(const float *__restrict__ X, uint32_t n_cols,
-                                                   _Float16 *__restrict__ HL, float *__restrict__ unscale) {
-  const uint32_t t = blockIdx.x, tid = threadIdx.x;
-  const float4 *x4 = reinterpret_cast<const float4 *>(X + (uint64_t)t * n_cols);
-  const uint32_t n4 = n_cols / 4;
-  float mx = 0.f;
-  for (uint32_t i = tid; i < n4; i += 256) {
-    const float4 v = x4[i];
-    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-  }
-  __shared__ float red[4];
-  mx = wave_max(mx);
-  if (tid % 64 == 0) red[tid / 64] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  int ex = 0;
-  if (mx > 0.f) frexpf(mx, &ex);  // mx < 2^ex
-  const int k = max(-100, min(100, 14 - ex));
-  const float scale = ldexpf(1.0f, k);
-  if (tid == 0) unscale[t] = ldexpf(1.0f, -k);
-  _Float16 *row = HL + (uint64_t)t * 2 * n_cols;
-  for (uint32_t i = tid; i < n4; i += 256) {
-    const float4 v4 = x4[i];
-    const float v[4] = {v4.x * scale, v4.y * scale, v4.z * scale, v4.w * scale};
-    half4_t h, l;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      h[j] = (_Float16)v[j];
-      l[j] = (_Float16)(v[j] - (float)h[j]);
-    }
-    _Float16 *g = row + (i / 2) * 16 + (i % 2) * 4;
-    *reinterpret_cast<half4_t *>(g) = h;
-    *reinterpret_cast<half4_t *>(g + 8) = l;
-  }
-}
-
-// The split inputs of a launch: rows of 2·n_cols halves (groups of 8 high
-// then 8 low) and the per-row unscale, carved from one scratch region.
-struct SplitInputs {
-  const _Float16 *hl;
-  const float *unscale;
-};
-
-static SplitInputs split_inputs(hipStream_t s, const float *x, uint32_t n_rows, uint32_t n_cols, void *scratch) {
-  _Float16 *hl = static_cast<_Float16 *>(scratch);
-  float *u = reinterpret_cast<float *>(hl + (uint64_t)n_rows * 2 * n_cols);
-  if (n_rows) k_split_rows<<<n_rows, 256, 0, s>>>(x, n_cols, hl, u);
-  return SplitInputs{hl, u};
-}
-
-// Tile 128 weight rows x 64 tokens; 256 threads = 4 waves in a 2x2
-// arrangement, each wave owning 64 rows x 32 tokens as two 32x32 MFMA
-// blocks.  A pipeline step covers 128 columns: thread t expands weight row
-// t/2, unit t%2, and splits 32 inputs of token t/4.  The next step's weight
-// and input loads are issued into registers before this step's MFMAs.
 // Expert groups of a grouped launch (Metal::matmul_experts): the entries of
 // expert e are positions offsets[e] .. offsets[e+1] of `entries`, each entry
 // v = token·n_used + slot; entry v reads input row v / x_div and writes
-// output row v.  The token tiles of all experts are numbered one after the
-// other along blockIdx.y.
+// output row v.
 struct ExpertGroups {
   const uint32_t *offsets, *entries;
   uint32_t n_experts, x_div;
 };
-
-template <uint32_t FMT, int STORE, int MB, bool GROUPED>
-__global__ __launch_bounds__(256) void k_matmul(const uint8_t *__restrict__ W, uint64_t row_bytes, SplitInputs X,
-                                                float *__restrict__ Y, uint32_t n_rows, uint32_t n_cols,
-                                                uint32_t n_tokens, ExpertGroups groups) {
-  constexpr int BM = 64 * MB;           // weight rows of this tile (MB 32-row blocks per wave)
-  extern __shared__ _Float16 lds[];
-  _Float16 *A = lds;                    // [BM][kLds]
-  _Float16 *Bh = A + BM * kLds;         // [kBN][kLds]
-  _Float16 *Bl = Bh + kBN * kLds;       // [kBN][kLds]
-  const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
-  // Dense launches are one-dimensional and XCD-aware: workgroup L runs on
-  // XCD L % 8 (round-robin dispatch), so logical tile (L % 8)·⌈total/8⌉ + L/8
-  // gives each XCD a contiguous run of tiles in token-tile-major order — the
-  // row tiles sharing a token tile's inputs then share that XCD's L2 instead
-  // of every XCD reading every input tile.
-  uint32_t row_tile = blockIdx.x, tok_tile = blockIdx.y;
-  if constexpr (!GROUPED) {
-    const uint32_t n_rt = (n_rows + BM - 1) / BM, total = n_rt * ((n_tokens + kBN - 1) / kBN);
-    const uint32_t per = (total + 7) / 8, logical = (blockIdx.x % 8) * per + blockIdx.x / 8;
-    if (logical >= total) return;
-    row_tile = logical % n_rt;
-    tok_tile = logical / n_rt;
-  }
-  const uint32_t row0 = row_tile * BM;
-  uint32_t tok0 = tok_tile * kBN, tok_end = n_tokens;  // positions [tok0, tok_end) of this tile's group
-  const int wm = wave / 2, wn = wave % 2;
-  if constexpr (GROUPED) {
-    // Find this tile's expert: the offsets go to LDS, one thread walks them.
-    __shared__ uint32_t off_s[kMoeMaxExperts + 1];
-    __shared__ uint32_t pick[3];
-    for (uint32_t e = tid; e <= groups.n_experts; e += 256) off_s[e] = groups.offsets[e];
-    __syncthreads();
-    if (tid == 0) {
-      uint32_t t = blockIdx.y, e = 0;
-      for (; e < groups.n_experts; e++) {
-        const uint32_t tiles = (off_s[e + 1] - off_s[e] + kBN - 1) / kBN;
-        if (t < tiles) break;
-        t -= tiles;
-      }
-      pick[0] = e;
-      pick[1] = e < groups.n_experts ? off_s[e] + t * kBN : 0;
-      pick[2] = e < groups.n_experts ? off_s[e + 1] : 0;
-    }
-    __syncthreads();
-    if (pick[0] >= groups.n_experts) return;  // past the last tile (the grid is an upper bound)
-    W += (uint64_t)pick[0] * n_rows * row_bytes;
-    tok0 = pick[1];
-    tok_end = pick[2];
-  }
-  // Input and output rows of tile position p.
-  auto x_row = [&](uint32_t p) { return GROUPED ? groups.entries[p] / groups.x_div : p; };
-  auto y_row = [&](uint32_t p) { return GROUPED ? groups.entries[p] : p; };
-
-  // This thread's weight row and unit (threads past 2·BM stage no weights),
-  // and token and quarter.
-  const bool a_thread = tid < 2 * BM;
-  const int ar = a_thread ? tid / 2 : 0, aq = tid % 2;
-  const uint8_t *wrow = W + (uint64_t)min(row0 + ar, n_rows - 1) * row_bytes;
-  const int bt = tid / 4, bq = tid % 4;
-  // (Tokens past the tile's end stage a copy of the last row; their output
-  // columns are never stored.)
-  // This thread's 32 columns of a step: 4 groups of (8 high, 8 low) halves.
-  const uint4 *xrow = reinterpret_cast<const uint4 *>(X.hl + (uint64_t)x_row(min(tok0 + bt, tok_end - 1)) * 2 * n_cols +
-                                                      2 * 32 * bq);
-
-  // Loads of a step, issued a step ahead.  (Plain locals rather than an
-  // array captured by a lambda: the compiler kept such an array in scratch
-  // memory, which waited on each load.)
-  RawUnit ra{};
-  uint4 x0, x1, x2, x3, x4, x5, x6, x7;
-#define BCH_PREFETCH(k0)                                                                     \
-  do {                                                                                       \
-    if constexpr (FMT == 12)                                                                 \
-      if (a_thread) ra = fetch_q4k(wrow, (k0) & ~255u, (int)(((k0) & 255u) / 64) + aq);       \
-    const uint4 *src_ = xrow + (k0) / 4;                                                     \
-    x0 = src_[0], x1 = src_[1], x2 = src_[2], x3 = src_[3];                                  \
-    x4 = src_[4], x5 = src_[5], x6 = src_[6], x7 = src_[7];                                  \
-  } while (0)
-
-  float16_t total[MB];
-#pragma unroll
-  for (int b = 0; b < MB; b++)
-#pragma unroll
-    for (int i = 0; i < 16; i++) total[b][i] = 0.f;
-
-  BCH_PREFETCH(0u);
-  for (uint32_t k0 = 0; k0 < n_cols; k0 += kStep) {
-    // Stage this step: weights to halves, inputs scaled and split.
-    if (a_thread) {
-      if constexpr (FMT == 12)
-        expand_q4k(ra, (int)((k0 & 255u) / 64) + aq, A + ar * kLds + 64 * aq);
-      else if constexpr (FMT == 2 || FMT == 8 || FMT == 13 || FMT == 14)
-        expand_generic<FMT>(wrow, k0 + 64 * aq, A + ar * kLds + 64 * aq);
-      else
-        expand_float<FMT>(wrow, k0 + 64 * aq, A + ar * kLds + 64 * aq);
-    }
-    {
-      uint4 *dh = reinterpret_cast<uint4 *>(Bh + bt * kLds + 32 * bq);
-      uint4 *dl = reinterpret_cast<uint4 *>(Bl + bt * kLds + 32 * bq);
-      dh[0] = x0, dl[0] = x1, dh[1] = x2, dl[1] = x3;
-      dh[2] = x4, dl[2] = x5, dh[3] = x6, dl[3] = x7;
-    }
-    __syncthreads();
-    if (k0 + kStep < n_cols) BCH_PREFETCH(k0 + kStep);
-    // 8 k-steps of 16 (gfx950's 32x32x16 f16 MFMA): lane supplies
-    // A[row = lane%32][k + 8*(lane/32) .. +8] and B[k + 8*(lane/32) .. +8][col = lane%32].
-    const _Float16 *arow0 = A + (wm * 32 * MB + lane % 32) * kLds + 8 * (lane / 32);
-    const _Float16 *bhrow = Bh + (wn * 32 + lane % 32) * kLds + 8 * (lane / 32);
-    const _Float16 *blrow = Bl + (wn * 32 + lane % 32) * kLds + 8 * (lane / 32);
-#pragma unroll 4
-    for (int kk = 0; kk < kStep; kk += 16) {
-      const half8_t bh = *reinterpret_cast<const half8_t *>(bhrow + kk);
-      const half8_t bl = *reinterpret_cast<const half8_t *>(blrow + kk);
-      half8_t a[MB];
-#pragma unroll
-      for (int b = 0; b < MB; b++) a[b] = *reinterpret_cast<const half8_t *>(arow0 + 32 * b * kLds + kk);
-#pragma unroll
-      for (int b = 0; b < MB; b++) total[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[b], bh, total[b], 0, 0, 0);
-#pragma unroll
-      for (int b = 0; b < MB; b++) total[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[b], bl, total[b], 0, 0, 0);
-    }
-    __syncthreads();
-  }
-  // total[b][r] holds D[row = 32b + 8*(r/4) + 4*(lane/32) + r%4][token = lane%32].
-  const uint32_t tok = tok0 + wn * 32 + lane % 32;
-  if (tok >= tok_end) return;
-  const uint64_t yr = y_row(tok);
-  const float us = X.unscale[x_row(tok)];  // undoes the token's input scaling
-#pragma unroll
-  for (int b = 0; b < MB; b++)
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const uint32_t row = row0 + wm * 32 * MB + 32 * b + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-      if (row < n_rows) {
-        float *y = Y + yr * n_rows + row;
-        const float v = total[b][r] * us;
-        if (STORE == 0)
-          *y = v;
-        else if (STORE == 1)
-          *y += v;
-        else
-          *y = silu_f(*y) * v;
-      }
-    }
-}
-
-#undef BCH_PREFETCH
 
 // --- the dense prefill GEMM -------------------------------------------------
 //
@@ -577,11 +282,19 @@ __device__ __forceinline__ void gemm_dequant_all(const uint8_t *__restrict__ row
 // (up projections), and Y receives silu(gate)·up for RB/2 output rows, so
 // the gate products never go through memory and each token's inputs are
 // loaded once for both matrices.
-template <uint32_t FMT, int STORE, int RB, int NW, int NB>
+//
+// GROUPED: the expert-grouped launch (Metal::matmul_experts, matmul.metal:
+// 462-504).  W (and W2) stack n_experts matrices; the entries of expert e
+// are positions offsets[e] .. offsets[e+1] of `entries`, entry v =
+// token·n_used + slot reading input row v / x_div and writing output row
+// v.  blockIdx.x is the row tile, blockIdx.y numbers the token tiles of
+// all experts one after the other (the grid is an upper bound).
+template <uint32_t FMT, int STORE, int RB, int NW, int NB, bool GROUPED = false>
 __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W, const uint8_t *__restrict__ W2,
                                                   uint64_t row_bytes, HiInputs X, float *__restrict__ Y,
                                                   float *__restrict__ P, uint32_t n_rows, uint32_t n_cols,
-                                                  uint32_t n_tokens, uint32_t splits) {
+                                                  uint32_t n_tokens, uint32_t splits, ExpertGroups groups) {
+  static_assert(!GROUPED || STORE == 0 || STORE == 3, "grouped launches overwrite");
   constexpr bool PAIR = STORE == 3;
   constexpr int OR = PAIR ? RB / 2 : RB;  // output rows per tile
   constexpr int NT = 64 * NW;          // threads
@@ -596,16 +309,47 @@ __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W,
   __shared__ __align__(16) _Float16 A[3][RB * kGA];
   __shared__ float us_s[BT];           // the tile's token scales
   const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64, h = lane / 32;
-  const uint32_t n_rt = (n_rows + OR - 1) / OR, n_tt = (n_tokens + BT - 1) / BT;
-  const uint32_t total = n_rt * n_tt * splits;
-  // XCD-aware order: workgroup L runs on XCD L % 8, so logical tile
-  // (L % 8)·⌈total/8⌉ + L/8 hands each XCD a contiguous run, split-major
-  // then token-tile-major: the row tiles sharing a token tile's inputs share
-  // that XCD's L2.
-  const uint32_t per = (total + 7) / 8, logical = (blockIdx.x % 8) * per + blockIdx.x / 8;
-  if (logical >= total) return;
-  const uint32_t rt = logical % n_rt, tt = (logical / n_rt) % n_tt, sp = logical / (n_rt * n_tt);
-  const uint32_t row0 = rt * OR, tok0 = tt * BT;
+  __shared__ uint32_t ent_s[GROUPED ? BT : 1];  // grouped: the tile's entries
+  uint32_t rt, sp = 0, tok0, tok_end = n_tokens;  // tokens [tok0, tok_end) of this tile's group
+  if constexpr (GROUPED) {
+    // Find this tile's expert: the offsets go to LDS, one thread walks them.
+    __shared__ uint32_t off_s[kMoeMaxExperts + 1];
+    __shared__ uint32_t pick[3];
+    for (uint32_t e = tid; e <= groups.n_experts; e += NT) off_s[e] = groups.offsets[e];
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t t = blockIdx.y, e = 0;
+      for (; e < groups.n_experts; e++) {
+        const uint32_t tiles = (off_s[e + 1] - off_s[e] + BT - 1) / BT;
+        if (t < tiles) break;
+        t -= tiles;
+      }
+      pick[0] = e;
+      pick[1] = e < groups.n_experts ? off_s[e] + t * BT : 0;
+      pick[2] = e < groups.n_experts ? off_s[e + 1] : 0;
+    }
+    __syncthreads();
+    if (pick[0] >= groups.n_experts) return;  // past the last tile (uniform)
+    W += (uint64_t)pick[0] * n_rows * row_bytes;
+    if (PAIR) W2 += (uint64_t)pick[0] * n_rows * row_bytes;
+    tok0 = pick[1];
+    tok_end = pick[2];
+    rt = blockIdx.x;
+    if (tid < BT) ent_s[tid] = groups.entries[min(tok0 + tid, tok_end - 1)];
+  } else {
+    const uint32_t n_rt = (n_rows + OR - 1) / OR, n_tt = (n_tokens + BT - 1) / BT;
+    const uint32_t total = n_rt * n_tt * splits;
+    // XCD-aware order: workgroup L runs on XCD L % 8, so logical tile
+    // (L % 8)·⌈total/8⌉ + L/8 hands each XCD a contiguous run, split-major
+    // then token-tile-major: the row tiles sharing a token tile's inputs
+    // share that XCD's L2.
+    const uint32_t per = (total + 7) / 8, logical = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    if (logical >= total) return;
+    rt = logical % n_rt;
+    sp = logical / (n_rt * n_tt);
+    tok0 = ((logical / n_rt) % n_tt) * BT;
+  }
+  const uint32_t row0 = rt * OR;
   const uint32_t n_stages = n_cols / kGk;
   const uint32_t st0 = (uint32_t)((uint64_t)sp * n_stages / splits);
   const uint32_t st1 = (uint32_t)((uint64_t)(sp + 1) * n_stages / splits);
@@ -617,13 +361,20 @@ __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W,
   const uint8_t *wrow = PAIR && ar >= OR ? W2 + (uint64_t)min(row0 + ar - OR, n_rows - 1) * row_bytes
                                          : W + (uint64_t)min(row0 + ar, n_rows - 1) * row_bytes;
   // MFMA role: tokens tok0 + 32·NB·wave + 32j + lane%32 (clamped), lane half h.
+  // (Grouped: entry p reads input row entries[p] / x_div.)
+  auto x_index = [&](uint32_t p) -> uint32_t {
+    if constexpr (GROUPED)
+      return groups.entries[min(p, tok_end - 1)] / groups.x_div;
+    else
+      return min(p, n_tokens - 1);
+  };
   const u32x4 *xrow[NB];
 #pragma unroll
   for (int j = 0; j < NB; j++)
-    xrow[j] = reinterpret_cast<const u32x4 *>(
-        X.h + (uint64_t)min(tok0 + 32 * NB * wave + 32 * j + lane % 32, n_tokens - 1) * n_cols + 16 * h);
+    xrow[j] = reinterpret_cast<const u32x4 *>(X.h + (uint64_t)x_index(tok0 + 32 * NB * wave + 32 * j + lane % 32) *
+                                                        n_cols + 16 * h);
   static_assert(BT <= NT, "one thread per token scale");
-  if (tid < BT) us_s[tid] = X.unscale[min(tok0 + tid, n_tokens - 1)];
+  if (tid < BT) us_s[tid] = X.unscale[x_index(tok0 + tid)];
 
   // The lane's inputs of a stage: token block j, k-step s at v[4j + s].
   struct BRegs {
@@ -742,6 +493,13 @@ __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W,
         if (PAIR) prior[e] = acc[i + OR / 32][j][e] * us_s[tl];  // the up product
         else if (STORE != 0 && splits == 1) prior[e] = Y[(uint64_t)min(tok0 + tl, n_tokens - 1) * n_rows + rowc];
       }
+      // Output row of tile token tl: the token itself, or (grouped) its entry.
+      auto y_row = [&](int tl) -> uint64_t {
+        if constexpr (GROUPED)
+          return ent_s[tl];
+        else
+          return tok0 + tl;
+      };
 #pragma unroll
       for (int e = 0; e < 16; e++) {
         if (PAIR)
@@ -755,14 +513,14 @@ __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W,
       }
       float *dst = splits > 1 ? P + (uint64_t)sp * n_tokens * n_rows : Y;
       if (row >= n_rows) continue;
-      if (tb + 32 <= n_tokens) {
+      if (tb + 32 <= tok_end) {
 #pragma unroll
-        for (int e = 0; e < 16; e++) dst[(uint64_t)(tb + 8 * (e / 4) + 4 * h + e % 4) * n_rows + row] = v[e];
+        for (int e = 0; e < 16; e++) dst[y_row(tw + 8 * (e / 4) + 4 * h + e % 4) * n_rows + row] = v[e];
       } else {
 #pragma unroll
         for (int e = 0; e < 16; e++) {
-          const uint32_t tok = tb + 8 * (e / 4) + 4 * h + e % 4;
-          if (tok < n_tokens) dst[(uint64_t)tok * n_rows + row] = v[e];
+          const int tl = tw + 8 * (e / 4) + 4 * h + e % 4;
+          if (tok0 + tl < tok_end) dst[y_row(tl) * n_rows + row] = v[e];
         }
       }
     }
@@ -794,13 +552,13 @@ static void gemm_launch(hipStream_t s, const uint8_t *W, const uint8_t *W2, uint
   const dim3 grid(8 * div_ceil(total, 8));
   const dim3 block(64 * NW);
   if (store == 3)
-    k_gemm<FMT, 3, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, 1);
+    k_gemm<FMT, 3, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, 1, ExpertGroups{});
   else if (splits > 1 || store == 0)
-    k_gemm<FMT, 0, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, splits);
+    k_gemm<FMT, 0, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, splits, ExpertGroups{});
   else if (store == 1)
-    k_gemm<FMT, 1, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, splits);
+    k_gemm<FMT, 1, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, splits, ExpertGroups{});
   else
-    k_gemm<FMT, 2, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, splits);
+    k_gemm<FMT, 2, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, splits, ExpertGroups{});
   if (splits > 1 && store != 3) {
     const uint64_t n = (uint64_t)n_tokens * n_rows;
     const dim3 g((uint32_t)((n + 255) / 256));
@@ -861,48 +619,6 @@ static void gemm_fmt(hipStream_t s, const uint8_t *W, const uint8_t *W2, uint64_
     gemm_launch<FMT, 64, 4, 1>(s, W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits);
 }
 
-template <uint32_t FMT, int MB>
-static void matmul_tile(hipStream_t s, const uint8_t *W, uint64_t rb, const SplitInputs &x, float *y, uint32_t n_rows,
-                        uint32_t n_cols, uint32_t n_tokens, uint32_t store) {
-  const uint32_t total = div_ceil(n_rows, 64 * MB) * div_ceil(n_tokens, kBN);
-  const dim3 grid(8 * div_ceil(total, 8));  // XCD-aware tile order (see k_matmul)
-  const size_t lds = (size_t)(64 * MB + 2 * kBN) * kLds * sizeof(_Float16);
-  const ExpertGroups none{};
-  if (store == 0)
-    k_matmul<FMT, 0, MB, false><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_tokens, none);
-  else if (store == 1)
-    k_matmul<FMT, 1, MB, false><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_tokens, none);
-  else
-    k_matmul<FMT, 2, MB, false><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_tokens, none);
-}
-
-// Grouped launch over n_entries entries (64-row tiles; an expert's tiles
-// are few).  Store 0 overwrites, 2 applies SiLU(y)·product.
-template <uint32_t FMT>
-static void matmul_experts_fmt(hipStream_t s, const uint8_t *W, uint64_t rb, const SplitInputs &x, float *y,
-                               uint32_t n_rows, uint32_t n_cols, uint32_t n_entries, uint32_t store,
-                               const ExpertGroups &g) {
-  dim3 grid(div_ceil(n_rows, 64), div_ceil(n_entries, kBN) + g.n_experts);
-  const size_t lds = (size_t)(64 + 2 * kBN) * kLds * sizeof(_Float16);
-  if (store == 2)
-    k_matmul<FMT, 2, 1, true><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_entries, g);
-  else
-    k_matmul<FMT, 0, 1, true><<<grid, 256, lds, s>>>(W, rb, x, y, n_rows, n_cols, n_entries, g);
-}
-
-// 128-row tiles when they give the chip at least two workgroups per CU,
-// 64-row tiles (twice the workgroups) otherwise.
-template <uint32_t FMT>
-static void matmul_fmt(hipStream_t s, const uint8_t *W, uint64_t rb, const SplitInputs &x, float *y, uint32_t n_rows,
-                       uint32_t n_cols, uint32_t n_tokens, uint32_t store) {
-  const uint64_t big_tiles = (uint64_t)div_ceil(n_rows, 128) * div_ceil(n_tokens, kBN);
-  if (big_tiles >= 512)
-    matmul_tile<FMT, 2>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
-  else
-    matmul_tile<FMT, 1>(s, W, rb, x, y, n_rows, n_cols, n_tokens, store);
-}
-
-static void set_lds_limits();
 
 uint64_t matmul_split_bytes(uint32_t n_rows, uint32_t n_cols) { return (uint64_t)n_rows * (4ull * n_cols + 4); }
 
@@ -957,43 +673,32 @@ void run_matmul_experts(hipStream_t s, uint32_t format, const uint8_t *W, const 
                         uint32_t n_cols, uint32_t n_experts, const float *xf, bool shared_input,
                         const uint32_t *offsets, const uint32_t *entries, uint32_t n_used, float *y,
                         uint32_t n_tokens, void *split) {
-  set_lds_limits();
+  if (!n_tokens) return;
   const uint64_t rb = bch_row_bytes(format, n_cols);
-  const SplitInputs x = split_inputs(s, xf, shared_input ? n_tokens : n_used * n_tokens, n_cols, split);
+  const uint32_t input_rows = shared_input ? n_tokens : n_used * n_tokens;
+  _Float16 *hx = static_cast<_Float16 *>(split);
+  float *unscale = reinterpret_cast<float *>(hx + (uint64_t)input_rows * n_cols);
+  k_split_hi<<<input_rows, 256, 0, s>>>(xf, n_cols, hx, unscale);
+  const HiInputs x{hx, unscale};
   const ExpertGroups g{offsets, entries, n_experts, shared_input ? n_used : 1u};
+  // 128 x 128 tiles (4 waves): an expert's tokens are few.  With `up` the
+  // gate and up matrices run as one paired launch (64 output rows a tile).
   const uint32_t n_entries = n_used * n_tokens;
-  auto one = [&](const uint8_t *w, uint32_t store) {
-    if (format == 12)
-      matmul_experts_fmt<12>(s, w, rb, x, y, n_rows, n_cols, n_entries, store, g);
-    else if (format == 1)
-      matmul_experts_fmt<1>(s, w, rb, x, y, n_rows, n_cols, n_entries, store, g);
+  const uint32_t out_rows = up ? 64 : 128;
+  const dim3 grid(div_ceil(n_rows, out_rows), div_ceil(n_entries, 128) + n_experts);
+  auto go = [&](auto fmt) {
+    constexpr uint32_t F = decltype(fmt)::value;
+    if (up)
+      k_gemm<F, 3, 128, 4, 1, true><<<grid, 256, 0, s>>>(W, up, rb, x, y, nullptr, n_rows, n_cols, n_entries, 1, g);
     else
-      matmul_experts_fmt<0>(s, w, rb, x, y, n_rows, n_cols, n_entries, store, g);
+      k_gemm<F, 0, 128, 4, 1, true><<<grid, 256, 0, s>>>(W, W, rb, x, y, nullptr, n_rows, n_cols, n_entries, 1, g);
   };
-  one(W, 0);
-  if (up) one(up, 2);  // SwiGLU: the up products times SiLU of the gate products
-}
-
-static void set_lds_limits() {
-  static bool done = false;
-  if (done) return;
-  done = true;
-  const int lds = (kBM + 2 * kBN) * kLds * sizeof(_Float16);
-#define BCH_SET(F, S)                                                                                          \
-  hipFuncSetAttribute((const void *)k_matmul<F, S, 2, false>, hipFuncAttributeMaxDynamicSharedMemorySize, lds); \
-  hipFuncSetAttribute((const void *)k_matmul<F, S, 1, false>, hipFuncAttributeMaxDynamicSharedMemorySize, lds)
-  BCH_SET(12, 0); BCH_SET(12, 1); BCH_SET(12, 2);
-  BCH_SET(1, 0); BCH_SET(1, 1); BCH_SET(1, 2);
-  BCH_SET(0, 0); BCH_SET(0, 1); BCH_SET(0, 2);
-  BCH_SET(14, 0); BCH_SET(14, 1); BCH_SET(14, 2);
-  BCH_SET(13, 0); BCH_SET(13, 1); BCH_SET(13, 2);
-  BCH_SET(8, 0); BCH_SET(8, 1); BCH_SET(8, 2);
-  BCH_SET(2, 0); BCH_SET(2, 1); BCH_SET(2, 2);
-#undef BCH_SET
-#define BCH_SET(F, S) \
-  hipFuncSetAttribute((const void *)k_matmul<F, S, 1, true>, hipFuncAttributeMaxDynamicSharedMemorySize, lds)
-  BCH_SET(12, 0); BCH_SET(12, 2); BCH_SET(1, 0); BCH_SET(1, 2); BCH_SET(0, 0); BCH_SET(0, 2);
-#undef BCH_SET
+  if (format == 12)
+    go(std::integral_constant<uint32_t, 12>{});
+  else if (format == 1)
+    go(std::integral_constant<uint32_t, 1>{});
+  else
+    go(std::integral_constant<uint32_t, 0>{});
 }
 
 // --- bch_matmul_noalloc: the split inputs in a static device array ---------
@@ -1066,7 +771,6 @@ extern "C" int bch_matmul_noalloc(bch_ctx *ctx, uint32_t format, bch_view weight
   void *split = noalloc_scratch(ctx->device);
   if (!split) return fail(BCH_ERR_NO_DEVICE, "matmul_noalloc: the scratch of device %d is not set up", ctx->device);
   if (!ctx->recording && !ctx->capturing) return fail(BCH_ERR_NOT_RECORDING, "no recording is open");
-  set_lds_limits();
   // No profiling events here (creating them allocates): the launch only.
   if (n_tokens) run_matmul(ctx->stream, format, W, n_rows, n_cols, xp, yp, n_tokens, store, split, kNoAllocScratchBytes);
   const hipError_t e = hipGetLastError();
@@ -1090,7 +794,6 @@ extern "C" int bch_matmul(bch_ctx *ctx, uint32_t format, bch_view weights, uint3
   BCH_TRY(view_ptr(ctx, "matmul", y, (uint64_t)n_tokens * n_rows * 4, &yp));
   if (reinterpret_cast<uintptr_t>(W) % 16 || reinterpret_cast<uintptr_t>(xp) % 16)
     return fail(BCH_ERR_ARGUMENT, "matmul: weights and inputs must be 16-byte aligned");
-  set_lds_limits();
   const char *name = format == 12 ? "matmul_q4k"
                      : format == 14 ? "matmul_q6k"
                      : format == 13 ? "matmul_q5k"

@@ -24,6 +24,7 @@ import oracle
 from bobcat_amd import BobcatError
 from bobcat_amd.backend import Format, NormSpec
 from bobcat_amd.synth import q4k_matrix
+from tests.test_gpu_ops import half_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -151,9 +152,11 @@ def test_grouped_experts_match_oracle(hip, n_experts, n_used, n_ff, n_embd, n_to
     grouping (expert by expert, token order within), matmul_experts (SwiGLU
     with shared token inputs, then down on the entries' rows) and moe_combine
     (slots summed in route order, then added).  Weights round to half in the
-    MFMA tiles as the reference's expanded half tiles do, so the products are
-    compared with half-rounded dequantised weights in float64, within 1e-5 of
-    each row's term-scale."""
+    MFMA tiles as the reference's expanded half tiles do, and each input row
+    rounds to half after a power-of-two scaling (the reference's expert tiles
+    take half inputs, matmul.metal:509-518), so the products are compared
+    with half-rounded weights and inputs in float64, within 1e-5 of each
+    row's term-scale."""
     rng = np.random.default_rng(n_experts * 7 + n_tokens)
     gate = expert_case(rng, n_experts, n_ff, n_embd)
     up = expert_case(rng, n_experts, n_ff, n_embd)
@@ -186,10 +189,11 @@ def test_grouped_experts_match_oracle(hip, n_experts, n_used, n_ff, n_embd, n_to
             .astype(np.float64)
 
     used = sorted(set(flat.tolist()))
+    xh = half_inputs(x)
     for e in used:
         G, U = half_dense(gate, e, n_ff, n_embd, rb), half_dense(up, e, n_ff, n_embd, rb)
         for v in np.nonzero(flat == e)[0]:
-            xv = x[v // n_used].astype(np.float64)
+            xv = xh[v // n_used]
             g, u = G @ xv, U @ xv
             silu = g / (1 + np.exp(-g))
             sg, su = np.abs(G) @ np.abs(xv), np.abs(U) @ np.abs(xv)
@@ -199,10 +203,11 @@ def test_grouped_experts_match_oracle(hip, n_experts, n_used, n_ff, n_embd, n_to
     run(hip, lambda: hip.matmul_experts(Format.Q4K, db.at(0), None, n_embd, n_ff, n_experts, ffb.at(0), False,
                                         offb.at(0), entb.at(0), n_used, outb.at(0), n_tokens))
     out = hip.read(outb.at(0), np.empty(n_entries * n_embd, np.float32)).reshape(n_entries, n_embd)
+    fh = half_inputs(ffn)
     for e in used:
         D = half_dense(down, e, n_embd, n_ff, rbd)
         for v in np.nonzero(flat == e)[0]:
-            fv = ffn[v].astype(np.float64)
+            fv = fh[v]
             want, scale = D @ fv, np.abs(D) @ np.abs(fv)
             assert np.abs(out[v] - want).max() <= 1e-5 * scale.max() + 1e-30, (e, v)
 
