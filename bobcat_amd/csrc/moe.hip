@@ -364,15 +364,26 @@ bool run_experts_down(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t
 // `entries`, in token order, and offsets[n_experts] the total.  One
 // workgroup of 16 waves; wave w takes experts w, w + 16, ...: its lanes test
 // 64 consecutive entries at a time and a ballot prefix places the matches.
+// The entries' experts are first copied to LDS as bytes (up to
+// kGroupLdsEntries entries; larger batches read them from the route), so
+// the scans cost LDS reads rather than dependent global loads.
 constexpr int kGroupWaves = 16;
+constexpr uint32_t kGroupLdsEntries = 16384;
+static_assert(kMoeMaxExperts <= 256, "expert ids fit a byte");
 
 __global__ __launch_bounds__(kGroupWaves * 64) void k_moe_group(const uint32_t *__restrict__ route,
                                                                 uint32_t *__restrict__ offsets,
                                                                 uint32_t *__restrict__ entries, uint32_t n_experts,
                                                                 uint32_t n_used, uint32_t n_tokens) {
   __shared__ uint32_t counts[kMoeMaxExperts];
+  __shared__ uint8_t ids[kGroupLdsEntries];
   const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64, n_entries = n_used * n_tokens;
-  auto expert_of = [&](uint32_t v) { return route[2ull * n_used * (v / n_used) + v % n_used]; };
+  auto route_expert = [&](uint32_t v) { return route[2ull * n_used * (v / n_used) + v % n_used]; };
+  const bool staged = n_entries <= kGroupLdsEntries;
+  if (staged)
+    for (uint32_t v = threadIdx.x; v < n_entries; v += kGroupWaves * 64) ids[v] = (uint8_t)route_expert(v);
+  __syncthreads();
+  auto expert_of = [&](uint32_t v) -> uint32_t { return staged ? ids[v] : route_expert(v); };
   for (uint32_t e = wave; e < n_experts; e += kGroupWaves) {
     uint32_t c = 0;
     for (uint32_t v = lane; v < n_entries; v += 64) c += expert_of(v) == e;
