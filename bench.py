@@ -381,6 +381,7 @@ def main() -> int:
     ap.add_argument("--skip-side", action="store_true", help="skip the other model configs")
     ap.add_argument("--long-only", action="store_true", help="only the 32K-context leg (for profiling)")
     ap.add_argument("--gemv-only", action="store_true", help="only the config-1 GEMV leg (for profiling)")
+    ap.add_argument("--gemm-only", action="store_true", help="only the prefill GEMM leg (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the decode loop is single-device (as in the reference) "
@@ -404,6 +405,9 @@ def main() -> int:
         if args.long_only:
             lres = long_leg(hip, weights_of(args.model))
             log(f"long context: {lres}")
+            return 0
+        if args.gemm_only:
+            log(f"prefill gemm: {gemm_leg(hip)}")
             return 0
         g = gemv_leg(hip, reps=10)
         log(f"gemv: {g}")
