@@ -300,9 +300,13 @@ __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W,
   constexpr int NT = 64 * NW;          // threads
   constexpr int MB = RB / 32;          // row blocks
   constexpr int BT = 32 * NB * NW;     // tokens per tile
-  constexpr int WPT = RB * kGk / NT;   // weights a thread dequantises per stage (32 or 16)
-  constexpr int TPR = NT / RB;         // threads per weight row
-  static_assert(WPT == 32 || WPT == 16, "a thread dequantises 16 or 32 weights per stage");
+  // Weights a thread dequantises per stage (16 or 32): the first DT threads
+  // dequantise (all of them unless RB x 64 does not divide evenly, as for
+  // 192-row tiles, where the last waves only run MFMAs).
+  constexpr int WPT = RB * kGk / NT > 16 ? 32 : 16;
+  constexpr int TPR = kGk / WPT;       // threads per weight row
+  constexpr int DT = RB * TPR;         // dequantising threads
+  static_assert(DT <= NT && DT % 64 == 0 && RB * kGk / NT <= 32, "dequantisation roles");
   constexpr int PARTS = WPT / 8;       // Q4_K dequantisation parts per stage (4 or 2)
   constexpr int MFMAS = MB * NB * 4;   // MFMAs per wave per stage
   constexpr int GAP = MFMAS / PARTS;   // MFMAs between dequantisation parts
@@ -357,7 +361,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W,
 
   // Dequantising role: weight row ar, part ac.  (Rows past the end are
   // clamped; their outputs are never stored.)
-  const int ar = tid / TPR, ac = tid % TPR;
+  const bool dq = tid < DT;  // (wave-uniform)
+  const int ar = dq ? tid / TPR : 0, ac = tid % TPR;
   const uint8_t *wrow = PAIR && ar >= OR ? W2 + (uint64_t)min(row0 + ar - OR, n_rows - 1) * row_bytes
                                          : W + (uint64_t)min(row0 + ar, n_rows - 1) * row_bytes;
   // MFMA role: tokens tok0 + 32·NB·wave + 32j + lane%32 (clamped), lane half h.
@@ -406,11 +411,13 @@ __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W,
   GemmRaw r0{}, r1{}, r2{};
   BRegs b0{}, b1{}, b2{};
   constexpr int NL = (FMT == 12 ? 2 : 0) + 4 * NB;  // loads a step issues
-  gemm_fetch<FMT, WPT>(wrow, st0 * kGk, ac, r0);
+  if (dq) gemm_fetch<FMT, WPT>(wrow, st0 * kGk, ac, r0);
   load_b(st0, b0);
-  gemm_fetch<FMT, WPT>(wrow, min(st0 + 1, last) * kGk, ac, r1);
-  gemm_dequant_all<FMT, WPT>(wrow, st0 * kGk, ac, r0, &A[0][ar * kGA]);
-  gemm_fetch<FMT, WPT>(wrow, min(st0 + 2, last) * kGk, ac, r2);
+  if (dq) {
+    gemm_fetch<FMT, WPT>(wrow, min(st0 + 1, last) * kGk, ac, r1);
+    gemm_dequant_all<FMT, WPT>(wrow, st0 * kGk, ac, r0, &A[0][ar * kGA]);
+    gemm_fetch<FMT, WPT>(wrow, min(st0 + 2, last) * kGk, ac, r2);
+  }
   load_b(min(st0 + 1, last), b1);
   __syncthreads();
 
@@ -422,14 +429,14 @@ __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W,
     // loads issued just above them.)
     __builtin_amdgcn_s_waitcnt((NL & 15) | ((NL >> 4) << 14) | 0x0f70);  // vmcnt(NL)
     load_b(min(st + 2, last), b2n);
-    gemm_fetch<FMT, WPT>(wrow, min(st + 3, last) * kGk, ac, rq);
+    if (DT == NT || dq) gemm_fetch<FMT, WPT>(wrow, min(st + 3, last) * kGk, ac, rq);
     const bool valid = st + 1 <= last;
     const uint32_t kn = min(st + 1, last) * kGk;
     Q4kScales f{};
     if constexpr (FMT == 12)
       f = q4k_scales(rn, kn, valid);
     else
-      gemm_dequant_direct<FMT, WPT>(wrow, kn, ac, valid, anext);
+      if (DT == NT || dq) gemm_dequant_direct<FMT, WPT>(wrow, kn, ac, valid, anext);
     // MFMAs k-step by k-step, each k-step's weight fragments read from LDS
     // one k-step ahead, a part of the next stage's dequantisation after
     // every GAP MFMAs, fenced so the scheduler keeps that order.
@@ -452,7 +459,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W,
                                                              wf[s & 1][i], acc[i][j], 0, 0, 0);
           if constexpr (FMT == 12) {
             const int m = (s * MB + i) * NB + j;  // MFMA index in the stage
-            if (m % GAP == GAP - 1) {
+            if (m % GAP == GAP - 1 && (DT == NT || dq)) {
               switch (m / GAP) {
                 case 0: q4k_part<WPT, 0>(rn, f, ac, anext); break;
                 case 1: q4k_part<WPT, 1>(rn, f, ac, anext); break;
@@ -607,9 +614,21 @@ static void gemm_fmt(hipStream_t s, const uint8_t *W, const uint8_t *W2, uint64_
                      uint32_t store, uint32_t cus) {
   GemmShape g = gemm_shape(store == 3 ? 2 * n_rows : n_rows, n_cols, n_tokens, part_floats, cus);
   if (store == 3) {
-    // The pair needs 128-row tiles (64 output rows) and no column split.
+    // The pair needs 128- or 192-row tiles (64 or 96 output rows) and no
+    // column split.  With 256-token tiles it takes 192 rows when that needs
+    // fewer rounds of workgroups over the CUs per row of work: at 512
+    // tokens a 10752-row pair is 224 tiles of 96 rows (one round) instead
+    // of 336 of 64 (two rounds, 80 CUs running a second tile).
     g.splits = 1;
     if (g.cfg == 2) g.cfg = 1;
+    const uint64_t tt = div_ceil(n_tokens, 256), c = cus ? cus : 256;
+    auto rounds = [&](uint32_t out_rows) { return (div_ceil(n_rows, out_rows) * tt + c - 1) / c; };
+    if (g.cfg == 0 && rounds(96) * 192 < rounds(64) * 128) {
+      const uint32_t total = div_ceil(n_rows, 96) * (uint32_t)tt;
+      k_gemm<FMT, 3, 192, 8, 1><<<dim3(8 * div_ceil(total, 8)), dim3(512), 0, s>>>(
+          W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, 1, ExpertGroups{});
+      return;
+    }
   }
   if (g.cfg == 0)
     gemm_launch<FMT, 128, 8, 1>(s, W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits);
