@@ -85,41 +85,76 @@ __device__ __forceinline__ int gemm_base(int s) { return (s & 1) * 8 + (s >> 1) 
 
 // Row t of X to fp16 with the power of two that puts max|x_t| in
 // [2^13, 2^14): H[t][c] = fp16(x·s), unscale[t] = 1/s.  One workgroup per
-// row.
+// row.  PER > 0: each thread keeps its PER float4 (i = tid + 256·k) in
+// registers, so the row is read once; PER = 0 loops, re-reading.
+template <int PER>
 __global__ __launch_bounds__(256) void k_split_hi(const float *__restrict__ X, uint32_t n_cols,
                                                  _Float16 *__restrict__ H, float *__restrict__ unscale) {
   const uint32_t t = blockIdx.x, tid = threadIdx.x;
   const float4 *x4 = reinterpret_cast<const float4 *>(X + (uint64_t)t * n_cols);
+  half4_t *row = reinterpret_cast<half4_t *>(H + (uint64_t)t * n_cols);
   const uint32_t n4 = n_cols / 4;
+  float4 xv[PER > 0 ? PER : 1];
   float mx = 0.f;
-  for (uint32_t i = tid; i < n4; i += 256) {
-    const float4 v = x4[i];
-    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  auto amax = [](float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); };
+  if constexpr (PER > 0) {
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+      const uint32_t i = tid + 256 * k;
+      xv[k] = i < n4 ? x4[i] : float4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int k = 0; k < PER; k++) mx = fmaxf(mx, amax(xv[k]));
+  } else {
+    for (uint32_t i = tid; i < n4; i += 256) mx = fmaxf(mx, amax(x4[i]));
   }
   __shared__ float red[4];
-  mx = wave_max(mx);
-  if (tid % 64 == 0) red[tid / 64] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  mx = block_max<256>(mx, red);
   int ex = 0;
   if (mx > 0.f) frexpf(mx, &ex);  // mx < 2^ex
-  const int k = max(-100, min(100, 14 - ex));
-  const float scale = ldexpf(1.0f, k);
-  if (tid == 0) unscale[t] = ldexpf(1.0f, -k);
-  half4_t *row = reinterpret_cast<half4_t *>(H + (uint64_t)t * n_cols);
-  for (uint32_t i = tid; i < n4; i += 256) {
-    const float4 v = x4[i];
+  const int k2 = max(-100, min(100, 14 - ex));
+  const float scale = ldexpf(1.0f, k2);
+  if (tid == 0) unscale[t] = ldexpf(1.0f, -k2);
+  auto put = [&](uint32_t i, float4 v) {
     half4_t o;
     o[0] = (_Float16)(v.x * scale), o[1] = (_Float16)(v.y * scale);
     o[2] = (_Float16)(v.z * scale), o[3] = (_Float16)(v.w * scale);
     row[i] = o;
+  };
+  if constexpr (PER > 0) {
+#pragma unroll
+    for (int k = 0; k < PER; k++)
+      if (tid + 256 * k < n4) put(tid + 256 * k, xv[k]);
+  } else {
+    for (uint32_t i = tid; i < n4; i += 256) put(i, x4[i]);
   }
+}
+
+// Row t of X [rows x n_cols] to fp16 with the power of two that puts
+// max|x_t| in [2^13, 2^14) (k_split_hi), choosing the register form by
+// row length.
+static void split_hi(hipStream_t s, const float *x, uint32_t rows, uint32_t n_cols, _Float16 *h, float *unscale) {
+  if (!rows) return;
+  const uint32_t per = div_ceil(n_cols / 4, 256);
+  if (per <= 2)
+    k_split_hi<2><<<rows, 256, 0, s>>>(x, n_cols, h, unscale);
+  else if (per <= 4)
+    k_split_hi<4><<<rows, 256, 0, s>>>(x, n_cols, h, unscale);
+  else if (per <= 12)
+    k_split_hi<12><<<rows, 256, 0, s>>>(x, n_cols, h, unscale);
+  else
+    k_split_hi<0><<<rows, 256, 0, s>>>(x, n_cols, h, unscale);
 }
 
 // k_rms_norm (ops.hip) and k_split_hi in one pass over each row: `out`
 // receives exactly k_rms_norm's values (same per-thread sums, reduction and
 // scale), and H/unscale the fp16 form of those values that k_split_hi would
 // make, so the GEMM that follows skips its own conversion.
+//
+// PER > 0: each thread keeps its PER elements (i = tid + 256·k, the order
+// of k_rms_norm's sums) in registers, so the row is read once; PER = 0
+// loops over rows of any length, re-reading.
+template <int PER>
 __global__ __launch_bounds__(256) void k_rms_norm_split(const float *__restrict__ x, const float *__restrict__ w,
                                                        float *__restrict__ out, uint32_t n, float eps,
                                                        _Float16 *__restrict__ H, float *__restrict__ unscale) {
@@ -127,24 +162,55 @@ __global__ __launch_bounds__(256) void k_rms_norm_split(const float *__restrict_
   const uint32_t t = blockIdx.x, tid = threadIdx.x;
   const float *xr = x + (uint64_t)t * n;
   float *orow = out + (uint64_t)t * n;
+  _Float16 *hrow = H + (uint64_t)t * n;
+  float xv[PER > 0 ? PER : 1], wv[PER > 0 ? PER : 1];
   float ss = 0.f;
-  for (uint32_t i = tid; i < n; i += 256) ss = fmaf(xr[i], xr[i], ss);
+  if constexpr (PER > 0) {
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+      const uint32_t i = tid + 256 * k;
+      xv[k] = i < n ? xr[i] : 0.f;
+      wv[k] = i < n ? w[i] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < PER; k++)
+      if (tid + 256 * k < n) ss = fmaf(xv[k], xv[k], ss);
+  } else {
+    for (uint32_t i = tid; i < n; i += 256) ss = fmaf(xr[i], xr[i], ss);
+  }
   ss = block_sum<256>(ss, red);
   const float scale = (float)(1.0 / sqrt((double)ss / (double)n + (double)eps));
   float mx = 0.f;
-  for (uint32_t i = tid; i < n; i += 256) {
-    const float v = w[i] * (xr[i] * scale);
-    orow[i] = v;
-    mx = fmaxf(mx, fabsf(v));
+  if constexpr (PER > 0) {
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+      const uint32_t i = tid + 256 * k;
+      xv[k] = wv[k] * (xv[k] * scale);
+      if (i < n) {
+        orow[i] = xv[k];
+        mx = fmaxf(mx, fabsf(xv[k]));
+      }
+    }
+  } else {
+    for (uint32_t i = tid; i < n; i += 256) {
+      const float v = w[i] * (xr[i] * scale);
+      orow[i] = v;
+      mx = fmaxf(mx, fabsf(v));
+    }
   }
   mx = block_max<256>(mx, red);
   int ex = 0;
   if (mx > 0.f) frexpf(mx, &ex);  // mx < 2^ex
-  const int k = max(-100, min(100, 14 - ex));
-  const float s2 = ldexpf(1.0f, k);
-  if (tid == 0) unscale[t] = ldexpf(1.0f, -k);
-  _Float16 *hrow = H + (uint64_t)t * n;
-  for (uint32_t i = tid; i < n; i += 256) hrow[i] = (_Float16)(orow[i] * s2);
+  const int k2 = max(-100, min(100, 14 - ex));
+  const float s2 = ldexpf(1.0f, k2);
+  if (tid == 0) unscale[t] = ldexpf(1.0f, -k2);
+  if constexpr (PER > 0) {
+#pragma unroll
+    for (int k = 0; k < PER; k++)
+      if (tid + 256 * k < n) hrow[tid + 256 * k] = (_Float16)(xv[k] * s2);
+  } else {
+    for (uint32_t i = tid; i < n; i += 256) hrow[i] = (_Float16)(orow[i] * s2);
+  }
 }
 
 void run_rms_norm_split(hipStream_t s, const float *x, const float *w, float *out, uint32_t n, uint32_t rows,
@@ -152,7 +218,14 @@ void run_rms_norm_split(hipStream_t s, const float *x, const float *w, float *ou
   if (!rows) return;
   _Float16 *hx = static_cast<_Float16 *>(scratch);
   float *unscale = reinterpret_cast<float *>(hx + (uint64_t)rows * n);
-  k_rms_norm_split<<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale);
+  if (n <= 1024)
+    k_rms_norm_split<4><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale);
+  else if (n <= 2048)
+    k_rms_norm_split<8><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale);
+  else if (n <= 4096)
+    k_rms_norm_split<16><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale);
+  else
+    k_rms_norm_split<0><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale);
 }
 
 struct HiInputs {
@@ -667,7 +740,7 @@ void run_matmul(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_row
   // previous launch on this scratch converted the same inputs.
   _Float16 *hx = static_cast<_Float16 *>(scratch);
   float *unscale = reinterpret_cast<float *>(hx + (uint64_t)n_tokens * n_cols);
-  if (!split_ready) k_split_hi<<<n_tokens, 256, 0, s>>>(xf, n_cols, hx, unscale);
+  if (!split_ready) split_hi(s, xf, n_tokens, n_cols, hx, unscale);
   const HiInputs x{hx, unscale};
   const uint64_t used = (matmul_split_bytes(n_tokens, n_cols) + 255) / 256 * 256;
   float *part = reinterpret_cast<float *>(static_cast<uint8_t *>(scratch) + used);
@@ -697,7 +770,7 @@ void run_matmul_experts(hipStream_t s, uint32_t format, const uint8_t *W, const 
   const uint32_t input_rows = shared_input ? n_tokens : n_used * n_tokens;
   _Float16 *hx = static_cast<_Float16 *>(split);
   float *unscale = reinterpret_cast<float *>(hx + (uint64_t)input_rows * n_cols);
-  k_split_hi<<<input_rows, 256, 0, s>>>(xf, n_cols, hx, unscale);
+  split_hi(s, xf, input_rows, n_cols, hx, unscale);
   const HiInputs x{hx, unscale};
   const ExpertGroups g{offsets, entries, n_experts, shared_input ? n_used : 1u};
   // 128 x 128 tiles (4 waves): an expert's tokens are few.  With `up` the
