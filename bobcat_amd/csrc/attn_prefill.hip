@@ -31,12 +31,23 @@ constexpr int kPrefQ = 32;        // queries per workgroup
 constexpr int kPrefKeys = 32;     // keys per block
 constexpr int kVtStride = 40;     // halves per V^T row in LDS (32 keys + padding)
 
+// The output gate of gated attention (Qwen3.5, qwen35.rs:422-424): with
+// `gate` set, output element d of (query z, head h) is multiplied by
+// sigmoid(gate[z·query_stride + h·head_stride + d]).
+struct AttnGate {
+  const float *gate;
+  uint32_t head_stride, query_stride;
+  __device__ float at(uint32_t z, uint32_t head, uint32_t d) const {
+    return gate ? 1.0f / (1.0f + expf(-gate[(uint64_t)z * query_stride + (uint64_t)head * head_stride + d])) : 1.f;
+  }
+};
+
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_prefill(const float *__restrict__ q, const _Float16 *__restrict__ kc,
                                                       const _Float16 *__restrict__ vc, float *__restrict__ out,
                                                       uint32_t n_heads, uint32_t n_kv, uint32_t first_pos,
                                                       uint32_t n_queries, uint32_t q_stride, uint32_t out_stride,
-                                                      float scale, float *__restrict__ partials) {
+                                                      float scale, float *__restrict__ partials, AttnGate gate) {
   constexpr int KS = HD / 16;  // k-steps of the score product
   constexpr int OB = HD / 32;  // 32-row blocks of the output
   __shared__ _Float16 vt[HD * kVtStride];  // V^T of the current key block: [d][key]
@@ -178,7 +189,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *__restrict__ 
         for (int i = 0; i < 4; i++) orow[d + i] = o[b][4 * g + i];
       } else {
         *reinterpret_cast<float4 *>(orow + d) =
-            float4{o[b][4 * g] * inv, o[b][4 * g + 1] * inv, o[b][4 * g + 2] * inv, o[b][4 * g + 3] * inv};
+            float4{o[b][4 * g] * inv * gate.at(q0 + col, head, d), o[b][4 * g + 1] * inv * gate.at(q0 + col, head, d + 1),
+                   o[b][4 * g + 2] * inv * gate.at(q0 + col, head, d + 2),
+                   o[b][4 * g + 3] * inv * gate.at(q0 + col, head, d + 3)};
       }
     }
 }
@@ -187,7 +200,8 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *__restrict__ 
 // of HD threads per (query, head).
 template <int HD>
 __global__ __launch_bounds__(HD) void k_attn_prefill_combine(const float *__restrict__ partials, float *__restrict__ out,
-                                                              uint32_t n_heads, uint32_t n_split, uint32_t out_stride) {
+                                                              uint32_t n_heads, uint32_t n_split, uint32_t out_stride,
+                                                              AttnGate gate) {
   const uint32_t slot = blockIdx.x, z = slot / n_heads, head = slot % n_heads, d = threadIdx.x;
   const float *pp = partials + (uint64_t)slot * n_split * (HD + 2);
   float M = -INFINITY;
@@ -198,11 +212,12 @@ __global__ __launch_bounds__(HD) void k_attn_prefill_combine(const float *__rest
     L = fmaf(pp[sp * (HD + 2) + 1], w, L);
     O = fmaf(pp[sp * (HD + 2) + 2 + d], w, O);
   }
-  out[(uint64_t)z * out_stride + (uint64_t)head * HD + d] = O / L;
+  out[(uint64_t)z * out_stride + (uint64_t)head * HD + d] = O / L * gate.at(z, head, d);
 }
 
 bool attn_prefill_mfma_supported(uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, bool kv_half) {
-  return kv_half && n_kv && n_heads % n_kv == 0 && n_heads / n_kv <= 4 && (head_dim == 64 || head_dim == 128);
+  return kv_half && n_kv && n_heads % n_kv == 0 && n_heads / n_kv <= 4 &&
+         (head_dim == 64 || head_dim == 128 || head_dim == 256);
 }
 
 uint32_t attn_prefill_splits(uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t first_pos,
@@ -224,24 +239,28 @@ uint32_t attn_prefill_splits(uint32_t n_heads, uint32_t n_kv, uint32_t head_dim,
 void run_attn_prefill_mfma(hipStream_t s, const float *q, const void *k_cache, const void *v_cache, float *out,
                            uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t first_pos,
                            uint32_t n_queries, uint32_t q_stride, uint32_t out_stride, float scale, float *partials,
-                           uint64_t partial_floats) {
+                           uint64_t partial_floats, const float *gate, uint32_t gate_head_stride,
+                           uint32_t gate_query_stride) {
   if (!n_queries) return;
   const uint32_t n_split =
       partials ? attn_prefill_splits(n_heads, n_kv, head_dim, first_pos, n_queries, partial_floats) : 1;
   const dim3 grid((n_queries + kPrefQ - 1) / kPrefQ, n_kv, n_split);
   const _Float16 *kc = static_cast<const _Float16 *>(k_cache);
   const _Float16 *vc = static_cast<const _Float16 *>(v_cache);
-  if (head_dim == 64) {
-    k_attn_prefill<64><<<grid, 256, 0, s>>>(q, kc, vc, out, n_heads, n_kv, first_pos, n_queries, q_stride,
-                                            out_stride, scale, partials);
+  const AttnGate g{gate, gate_head_stride, gate_query_stride};
+  auto go = [&](auto hd) {
+    constexpr int HD = decltype(hd)::value;
+    k_attn_prefill<HD><<<grid, 256, 0, s>>>(q, kc, vc, out, n_heads, n_kv, first_pos, n_queries, q_stride,
+                                            out_stride, scale, partials, g);
     if (n_split > 1)
-      k_attn_prefill_combine<64><<<n_queries * n_heads, 64, 0, s>>>(partials, out, n_heads, n_split, out_stride);
-  } else {
-    k_attn_prefill<128><<<grid, 256, 0, s>>>(q, kc, vc, out, n_heads, n_kv, first_pos, n_queries, q_stride,
-                                             out_stride, scale, partials);
-    if (n_split > 1)
-      k_attn_prefill_combine<128><<<n_queries * n_heads, 128, 0, s>>>(partials, out, n_heads, n_split, out_stride);
-  }
+      k_attn_prefill_combine<HD><<<n_queries * n_heads, HD, 0, s>>>(partials, out, n_heads, n_split, out_stride, g);
+  };
+  if (head_dim == 64)
+    go(std::integral_constant<int, 64>{});
+  else if (head_dim == 128)
+    go(std::integral_constant<int, 128>{});
+  else
+    go(std::integral_constant<int, 256>{});
 }
 
 }  // namespace bch
@@ -254,7 +273,7 @@ extern "C" int bch_attention_prefill(bch_ctx *ctx, bch_view q, bch_view k_cache,
   const uint64_t last_pos = (uint64_t)first_pos + n_queries;
   if (!attn_prefill_mfma_supported(n_heads, n_kv_heads, head_dim, true) || last_pos > n_ctx)
     return fail(BCH_ERR_ATTENTION_LIMITS,
-                "attention_prefill: f16 caches, heads of 64 or 128, at most 4 query heads per KV head and positions "
+                "attention_prefill: f16 caches, heads of 64, 128 or 256, at most 4 query heads per KV head and positions "
                 "inside the context, got %u and %u heads of %u at positions up to %llu of %u",
                 n_heads, n_kv_heads, head_dim, (unsigned long long)last_pos, n_ctx);
   const uint64_t query_bytes = (uint64_t)n_queries * n_heads * head_dim * 4;
@@ -271,6 +290,7 @@ extern "C" int bch_attention_prefill(bch_ctx *ctx, bch_view q, bch_view k_cache,
     return fail(BCH_ERR_ARGUMENT, "attention_prefill: operands must be 16-byte aligned");
   return launch(ctx, {"attention_prefill", 0, 0, 0}, [&](hipStream_t s) {
     run_attn_prefill_mfma(s, qp, kp, vp, op, n_heads, n_kv_heads, head_dim, first_pos, n_queries,
-                          n_heads * head_dim, n_heads * head_dim, 1.0f / sqrtf((float)head_dim), nullptr, 0);
+                          n_heads * head_dim, n_heads * head_dim, 1.0f / sqrtf((float)head_dim), nullptr, 0,
+                          nullptr, 0, 0);
   });
 }

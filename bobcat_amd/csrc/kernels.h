@@ -209,12 +209,15 @@ void run_attention(hipStream_t s, const float *q, const void *k_cache, const voi
 // attn_prefill.hip: causal GQA attention of n_queries queries at positions
 // first_pos.. over the f16 cache (their keys already stored), on MFMA.  q and
 // out rows are q_stride / out_stride floats apart, head h at h·head_dim.
-// `partials` (nullable) is scratch for key splits.
+// `partials` (nullable) is scratch for key splits.  `gate` (nullable): the
+// output of (query z, head h) is scaled element-wise by sigmoid of the gate
+// at gate + z·gate_query_stride + h·gate_head_stride (gated attention).
 bool attn_prefill_mfma_supported(uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, bool kv_half);
 void run_attn_prefill_mfma(hipStream_t s, const float *q, const void *k_cache, const void *v_cache, float *out,
                            uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t first_pos,
                            uint32_t n_queries, uint32_t q_stride, uint32_t out_stride, float scale,
-                           float *partials, uint64_t partial_floats);
+                           float *partials, uint64_t partial_floats, const float *gate = nullptr,
+                           uint32_t gate_head_stride = 0, uint32_t gate_query_stride = 0);
 // Key splits run_attn_prefill_mfma uses for a batch (1 without scratch):
 // long contexts split the keys so the launch fills the chip, each split's
 // (max, sum, output) partials going to `partials` (partial_floats floats).

@@ -61,6 +61,7 @@ struct bch_qwen35 : bch::Sequence {
   float *hidden = nullptr, *normed = nullptr, *q_gate = nullptr, *q = nullptr, *k = nullptr, *v = nullptr,
         *attn = nullptr, *proj = nullptr, *conv_out = nullptr, *z = nullptr, *beta = nullptr, *alpha = nullptr,
         *delta_out = nullptr, *ffn = nullptr, *partials = nullptr;
+  uint64_t partial_floats = 0;  // floats of `partials`
   float *chunk_scratch = nullptr;  // the chunked DeltaNet form's per-chunk matrices (prefill)
   uint32_t *counters = nullptr;
 
@@ -196,6 +197,11 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
       else
         run_copy(st, v, static_cast<float *>(cache_slot(v_cache, ci, pos)), count * kv_dim, nullptr, 0);
       // Attention with the output gate of each head applied in the same launch.
+      if (attn_prefill_mfma_supported(n_heads, n_kv_heads, head_dim, kv_half))
+        run_attn_prefill_mfma(st, q, cache_layer(k_cache, ci), cache_layer(v_cache, ci), attn, n_heads, n_kv_heads,
+                              head_dim, pos, count, q_dim, q_dim, 1.0f / sqrtf((float)head_dim), partials,
+                              partial_floats, q_gate + head_dim, 2 * head_dim, 2 * q_dim);
+      else
       for (uint32_t q0 = 0; q0 < count; q0 += kQwenAttnQueryBatch) {
         const uint32_t nq = std::min(kQwenAttnQueryBatch, count - q0);
         AttnDecodeArgs ad{};
@@ -375,6 +381,7 @@ int bch_qwen35_new(bch_ctx *ctx, const bch_qwen35_model *md, uint32_t n_ctx, int
     m->prefill_splits = attention_splits(n_ctx, std::max(1u, m->n_kv_heads), ctx->n_cus);
     const uint64_t partial_floats = attention_partial_floats(std::min<uint32_t>(m->batch, kQwenAttnQueryBatch),
                                                             m->n_heads, hd, attn_decode_max_splits(n_ctx, hd, m->kv_half));
+    m->partial_floats = partial_floats;
     int rc = 0;
     (void)((rc = m->alloc(cache, &m->k_cache)) || (rc = m->alloc(cache, &m->v_cache)) ||
            (rc = m->alloc_t((uint64_t)m->n_delta * m->conv_dim * (m->conv_kernel - 1), &m->conv_state)) ||

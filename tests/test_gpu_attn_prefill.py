@@ -5,7 +5,7 @@ reference-shaped bch_attention path.
 Inputs follow crates/bobcat/tests/metal_attention.rs:19-48 (the q/k/v
 formulas (i·19%97−48)/67, (i·29%83−41)/53, (i·31%83−41)/53 over an f16
 cache) on the reference's shapes that this kernel takes (f16 cache, heads of
-64 or 128, ≤ 4 query heads per KV head) plus prefill-sized batches.  The
+64, 128 or 256, ≤ 4 query heads per KV head) plus prefill-sized batches.  The
 queries and probabilities enter the MFMA products as f16 high + low parts
 (~22 bits), so the bound is 1e-5 absolute (outputs are below 1 in
 magnitude) instead of the op-level kernel's 1e-6.
@@ -22,7 +22,7 @@ pytestmark = pytest.mark.gpu
 
 ATTENTION_LIMITS = 9
 CASES = [(63, 7, 4, 2, 64), (64, 73, 4, 1, 128), (63, 70, 4, 2, 64), (0, 512, 32, 8, 64), (100, 200, 16, 4, 128),
-         (37, 1, 4, 1, 64), (0, 33, 8, 8, 64)]
+         (37, 1, 4, 1, 64), (0, 33, 8, 8, 64), (5, 70, 8, 2, 256), (0, 130, 8, 2, 256)]
 
 
 def run(hip, fn):
@@ -84,7 +84,7 @@ def test_attention_prefill_matches_float64(hip, first, queries, heads, kv_heads,
 
 def test_attention_prefill_limits(hip):
     b = hip.new_buffer(1 << 20)
-    for heads, kv_heads, dim in [(4, 1, 256), (10, 2, 64), (8, 1, 64), (4, 1, 32)]:
+    for heads, kv_heads, dim in [(4, 1, 512), (10, 2, 64), (8, 1, 64), (4, 1, 32)]:
         hip.begin()
         with pytest.raises(BobcatError) as e:
             hip.attention_prefill(b.at(0), b.at(0), b.at(0), b.at(0), heads, kv_heads, dim, 0, 1, 16)
