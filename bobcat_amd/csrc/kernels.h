@@ -233,17 +233,32 @@ uint32_t attn_prefill_splits(uint32_t n_heads, uint32_t n_kv, uint32_t head_dim,
 // all; matmul_split_bytes alone allows none).
 uint64_t matmul_split_bytes(uint32_t n_rows, uint32_t n_cols);
 uint64_t matmul_scratch_bytes(uint32_t n_tokens, uint32_t n_cols, uint32_t n_rows);
+// A column-split sum an accumulating run_matmul left for the next kernel:
+// y += Σ_split part[split] (n floats each), in split order.
+struct PendingSum {
+  const float *part = nullptr;
+  uint32_t splits = 0;
+  uint64_t n = 0;
+};
+// Adds a pending sum into y (its run_matmul's y) and clears it.
+void finish_pending_sum(hipStream_t s, PendingSum &p, float *y);
 // run_rms_norm's output for `rows` rows of n, and in `scratch` the fp16
 // inputs a following run_matmul(..., x = out, n_tokens = rows, n_cols = n,
-// scratch, ..., split_ready = true) reads.
-void run_rms_norm_split(hipStream_t s, const float *x, const float *w, float *out, uint32_t n, uint32_t rows,
-                        float eps, void *scratch);
+// scratch, ..., split_ready = true) reads.  With `pending` (left by the
+// run_matmul that accumulated into x, on the same scratch) x first
+// receives that sum, written back to x; the pending sum is then cleared.
+void run_rms_norm_split(hipStream_t s, float *x, const float *w, float *out, uint32_t n, uint32_t rows, float eps,
+                        void *scratch, PendingSum *pending = nullptr);
 // store 3: y = silu(W·x) ⊙ (W2·x), W and W2 the gate and up matrices of
 // a SwiGLU (same format and shape).  split_ready: the previous run_matmul
 // on this scratch had the same x, n_tokens and n_cols, so its fp16 inputs
 // are reused instead of converted again.
+// defer (store 1 only): when the launch splits the columns, the partial sums
+// are left in scratch and described in *defer instead of added to y; the
+// caller passes *defer to the run_rms_norm_split that reads y next, or to
+// finish_pending_sum.  (*defer is cleared when nothing is left pending.)
 void run_matmul(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,
                 float *y, uint32_t n_tokens, uint32_t store, void *scratch, uint64_t scratch_bytes,
-                bool split_ready = false, const uint8_t *W2 = nullptr);
+                bool split_ready = false, const uint8_t *W2 = nullptr, PendingSum *defer = nullptr);
 
 }  // namespace bch

@@ -224,10 +224,16 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
   run_embed(s, m->token_embd.format, m->token_embd.data, bch_row_bytes(m->token_embd.format, n), m->tokens + pos,
             m->hidden, n, count, nullptr);
   if (trace) run_copy(s, m->hidden, m->trace, count * n, nullptr, 0);
+  // A column-split sum into the residual stream (out_proj, wo, down) is left
+  // to the norm that reads the residual next, unless something else reads
+  // it first (the trace copy, the MoE norm, the diagnostics checks).
+  PendingSum pend;
+  PendingSum *const defer = trace || check_mode() ? nullptr : &pend;
   for (uint32_t il = 0; il < m->n_layers; il++) {
     const Layer &L = m->layers[il];
+    PendingSum *const defer_ffn = L.moe ? nullptr : defer;
     // The norm also writes the fp16 inputs of the projection that follows.
-    run_rms_norm_split(s, m->hidden, L.attn_norm, m->normed, n, count, m->norm_eps, m->split);
+    run_rms_norm_split(s, m->hidden, L.attn_norm, m->normed, n, count, m->norm_eps, m->split, &pend);
     check_finite(s, "attn_norm", il, m->normed, (uint64_t)count * n);
     if (!L.attention) {
       float *hist = m->conv_state + (uint64_t)L.cache_index * (m->conv_kernel - 1) * n;
@@ -236,7 +242,8 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
       check_finite(s, "in_proj", il, m->bcx, (uint64_t)count * 3 * n);
       run_short_conv_batch(s, m->bcx, L.taps, hist, m->conv_out, n, m->conv_kernel, count);
       check_finite(s, "short_conv", il, m->conv_out, (uint64_t)count * n);
-      run_matmul(s, L.out_proj.format, L.out_proj.data, n, n, m->conv_out, m->hidden, count, 1, m->split, m->split_bytes);
+      run_matmul(s, L.out_proj.format, L.out_proj.data, n, n, m->conv_out, m->hidden, count, 1, m->split, m->split_bytes,
+                 false, nullptr, defer_ffn);
       check_finite(s, "out_proj", il, m->hidden, (uint64_t)count * n);
     } else {
       const uint32_t ci = L.cache_index;
@@ -282,13 +289,14 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
         run_attn_prefill(s, ad, m->kv_half, nq);
       }
       check_finite(s, "attention", il, m->attn, (uint64_t)count * m->q_dim);
-      run_matmul(s, L.wo.format, L.wo.data, n, m->q_dim, m->attn, m->hidden, count, 1, m->split, m->split_bytes);
+      run_matmul(s, L.wo.format, L.wo.data, n, m->q_dim, m->attn, m->hidden, count, 1, m->split, m->split_bytes, false,
+                 nullptr, defer_ffn);
       check_finite(s, "attn_output", il, m->hidden, (uint64_t)count * n);
     }
     if (L.moe)
       run_rms_norm(s, m->hidden, L.ffn_norm, m->normed, n, count, m->norm_eps);
     else
-      run_rms_norm_split(s, m->hidden, L.ffn_norm, m->normed, n, count, m->norm_eps, m->split);
+      run_rms_norm_split(s, m->hidden, L.ffn_norm, m->normed, n, count, m->norm_eps, m->split, &pend);
     check_finite(s, "ffn_norm", il, m->normed, (uint64_t)count * n);
     if (L.moe) {
       // Route the whole batch in one launch, then each token's experts.
@@ -325,11 +333,13 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
         run_matmul(s, L.up.format, L.up.data, m->n_ff, n, m->normed, m->ffn, count, 2, m->split, m->split_bytes, true);
       }
       check_finite(s, "swiglu", il, m->ffn, (uint64_t)count * m->n_ff);
-      run_matmul(s, L.down.format, L.down.data, n, m->n_ff, m->ffn, m->hidden, count, 1, m->split, m->split_bytes);
+      run_matmul(s, L.down.format, L.down.data, n, m->n_ff, m->ffn, m->hidden, count, 1, m->split, m->split_bytes,
+                 false, nullptr, defer);
       check_finite(s, "down", il, m->hidden, (uint64_t)count * n);
     }
     if (trace) run_copy(s, m->hidden, m->trace + (1 + il) * tstride, count * n, nullptr, 0);
   }
+  finish_pending_sum(s, pend, m->hidden);
   if (trace) run_rms_norm(s, m->hidden, m->output_norm, m->trace + (1 + m->n_layers) * tstride, n, count, m->norm_eps);
   if (want_logits)
     run_matvec(s, m->output.format, m->output.data, m->n_vocab, n, m->hidden + (uint64_t)(count - 1) * n, m->logits,

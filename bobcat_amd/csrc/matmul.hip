@@ -154,15 +154,27 @@ static void split_hi(hipStream_t s, const float *x, uint32_t rows, uint32_t n_co
 // PER > 0: each thread keeps its PER elements (i = tid + 256·k, the order
 // of k_rms_norm's sums) in registers, so the row is read once; PER = 0
 // loops over rows of any length, re-reading.
-template <int PER>
-__global__ __launch_bounds__(256) void k_rms_norm_split(const float *__restrict__ x, const float *__restrict__ w,
+//
+// SUM: x first receives the column-split partial products of the GEMM
+// that accumulated into it (P[split][row][i], added in split order and then
+// to x, exactly as k_gemm_reduce<1> would), and the sums are written back.
+template <int PER, bool SUM>
+__global__ __launch_bounds__(256) void k_rms_norm_split(float *__restrict__ x, const float *__restrict__ w,
                                                        float *__restrict__ out, uint32_t n, float eps,
-                                                       _Float16 *__restrict__ H, float *__restrict__ unscale) {
+                                                       _Float16 *__restrict__ H, float *__restrict__ unscale,
+                                                       const float *__restrict__ P, uint32_t splits) {
   __shared__ float red[4];
   const uint32_t t = blockIdx.x, tid = threadIdx.x;
-  const float *xr = x + (uint64_t)t * n;
+  float *xr = x + (uint64_t)t * n;
   float *orow = out + (uint64_t)t * n;
   _Float16 *hrow = H + (uint64_t)t * n;
+  const uint64_t pstride = (uint64_t)gridDim.x * n;
+  const float *prow = P + (uint64_t)t * n;
+  auto pending = [&](uint32_t i) {
+    float v = prow[i];
+    for (uint32_t sp = 1; sp < splits; sp++) v += prow[sp * pstride + i];
+    return v;
+  };
   float xv[PER > 0 ? PER : 1], wv[PER > 0 ? PER : 1];
   float ss = 0.f;
   if constexpr (PER > 0) {
@@ -172,10 +184,22 @@ __global__ __launch_bounds__(256) void k_rms_norm_split(const float *__restrict_
       xv[k] = i < n ? xr[i] : 0.f;
       wv[k] = i < n ? w[i] : 0.f;
     }
+    if constexpr (SUM) {
+#pragma unroll
+      for (int k = 0; k < PER; k++) {
+        const uint32_t i = tid + 256 * k;
+        if (i < n) {
+          xv[k] += pending(i);
+          xr[i] = xv[k];
+        }
+      }
+    }
 #pragma unroll
     for (int k = 0; k < PER; k++)
       if (tid + 256 * k < n) ss = fmaf(xv[k], xv[k], ss);
   } else {
+    if constexpr (SUM)
+      for (uint32_t i = tid; i < n; i += 256) xr[i] += pending(i);  // each thread re-reads only its own elements
     for (uint32_t i = tid; i < n; i += 256) ss = fmaf(xr[i], xr[i], ss);
   }
   ss = block_sum<256>(ss, red);
@@ -213,19 +237,49 @@ __global__ __launch_bounds__(256) void k_rms_norm_split(const float *__restrict_
   }
 }
 
-void run_rms_norm_split(hipStream_t s, const float *x, const float *w, float *out, uint32_t n, uint32_t rows,
-                        float eps, void *scratch) {
+template <int STORE>
+__global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ P, uint32_t splits, uint64_t n,
+                                                     float *__restrict__ Y);
+
+void finish_pending_sum(hipStream_t s, PendingSum &p, float *y) {
+  if (p.splits > 1) {
+    const dim3 g((uint32_t)((p.n + 255) / 256));
+    k_gemm_reduce<1><<<g, 256, 0, s>>>(p.part, p.splits, p.n, y);
+  }
+  p = PendingSum{};
+}
+
+void run_rms_norm_split(hipStream_t s, float *x, const float *w, float *out, uint32_t n, uint32_t rows, float eps,
+                        void *scratch, PendingSum *pending) {
   if (!rows) return;
   _Float16 *hx = static_cast<_Float16 *>(scratch);
   float *unscale = reinterpret_cast<float *>(hx + (uint64_t)rows * n);
+  bool sum = pending && pending->splits > 1;
+  if (sum && (pending->n != (uint64_t)rows * n ||
+              reinterpret_cast<const uint8_t *>(pending->part) < reinterpret_cast<uint8_t *>(unscale + rows))) {
+    // Not this norm's rows, or the fp16 inputs written here would cover the
+    // partials: add them first.
+    finish_pending_sum(s, *pending, x);
+    sum = false;
+  }
+  const float *P = sum ? pending->part : nullptr;
+  const uint32_t splits = sum ? pending->splits : 0;
+  auto go = [&](auto per) {
+    constexpr int PER = decltype(per)::value;
+    if (sum)
+      k_rms_norm_split<PER, true><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale, P, splits);
+    else
+      k_rms_norm_split<PER, false><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale, P, splits);
+  };
   if (n <= 1024)
-    k_rms_norm_split<4><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale);
+    go(std::integral_constant<int, 4>{});
   else if (n <= 2048)
-    k_rms_norm_split<8><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale);
+    go(std::integral_constant<int, 8>{});
   else if (n <= 4096)
-    k_rms_norm_split<16><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale);
+    go(std::integral_constant<int, 16>{});
   else
-    k_rms_norm_split<0><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale);
+    go(std::integral_constant<int, 0>{});
+  if (pending) *pending = PendingSum{};
 }
 
 struct HiInputs {
@@ -626,7 +680,7 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ P
 template <uint32_t FMT, int RB, int NW, int NB>
 static void gemm_launch(hipStream_t s, const uint8_t *W, const uint8_t *W2, uint64_t rb, const HiInputs &x, float *y,
                         float *part, uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens, uint32_t store,
-                        uint32_t splits) {
+                        uint32_t splits, PendingSum *defer) {
   const uint32_t out_rows = store == 3 ? RB / 2 : RB;
   const uint32_t total = div_ceil(n_rows, out_rows) * div_ceil(n_tokens, 32 * NB * NW) * splits;
   const dim3 grid(8 * div_ceil(total, 8));
@@ -639,6 +693,11 @@ static void gemm_launch(hipStream_t s, const uint8_t *W, const uint8_t *W2, uint
     k_gemm<FMT, 1, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, splits, ExpertGroups{});
   else
     k_gemm<FMT, 2, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, splits, ExpertGroups{});
+  if (splits > 1 && store == 1 && defer) {
+    // The next kernel (k_rms_norm_split) adds the partials.
+    *defer = PendingSum{part, splits, (uint64_t)n_tokens * n_rows};
+    return;
+  }
   if (splits > 1 && store != 3) {
     const uint64_t n = (uint64_t)n_tokens * n_rows;
     const dim3 g((uint32_t)((n + 255) / 256));
@@ -684,7 +743,7 @@ static GemmShape gemm_shape(uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens,
 template <uint32_t FMT>
 static void gemm_fmt(hipStream_t s, const uint8_t *W, const uint8_t *W2, uint64_t rb, const HiInputs &x, float *y,
                      float *part, uint64_t part_floats, uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens,
-                     uint32_t store, uint32_t cus) {
+                     uint32_t store, uint32_t cus, PendingSum *defer) {
   GemmShape g = gemm_shape(store == 3 ? 2 * n_rows : n_rows, n_cols, n_tokens, part_floats, cus);
   if (store == 3) {
     // The pair needs 128- or 192-row tiles (64 or 96 output rows) and no
@@ -704,11 +763,11 @@ static void gemm_fmt(hipStream_t s, const uint8_t *W, const uint8_t *W2, uint64_
     }
   }
   if (g.cfg == 0)
-    gemm_launch<FMT, 128, 8, 1>(s, W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits);
+    gemm_launch<FMT, 128, 8, 1>(s, W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits, defer);
   else if (g.cfg == 1)
-    gemm_launch<FMT, 128, 4, 1>(s, W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits);
+    gemm_launch<FMT, 128, 4, 1>(s, W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits, defer);
   else
-    gemm_launch<FMT, 64, 4, 1>(s, W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits);
+    gemm_launch<FMT, 64, 4, 1>(s, W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits, defer);
 }
 
 
@@ -732,7 +791,8 @@ static uint32_t device_cus() {
 
 void run_matmul(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *xf,
                 float *y, uint32_t n_tokens, uint32_t store, void *scratch, uint64_t scratch_bytes, bool split_ready,
-                const uint8_t *W2) {
+                const uint8_t *W2, PendingSum *defer) {
+  if (defer) *defer = PendingSum{};
   if (!n_tokens) return;
   const uint64_t rb = bch_row_bytes(format, n_cols);
   // The fp16 inputs and their scales (n_tokens·(2·n_cols + 4) bytes, within
@@ -747,13 +807,13 @@ void run_matmul(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_row
   const uint64_t part_floats = scratch_bytes > used ? (scratch_bytes - used) / 4 : 0;
   const uint32_t cus = device_cus();
   switch (format) {
-    case 12: gemm_fmt<12>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
-    case 1: gemm_fmt<1>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
-    case 14: gemm_fmt<14>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
-    case 13: gemm_fmt<13>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
-    case 8: gemm_fmt<8>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
-    case 2: gemm_fmt<2>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
-    default: gemm_fmt<0>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus); break;
+    case 12: gemm_fmt<12>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus, defer); break;
+    case 1: gemm_fmt<1>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus, defer); break;
+    case 14: gemm_fmt<14>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus, defer); break;
+    case 13: gemm_fmt<13>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus, defer); break;
+    case 8: gemm_fmt<8>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus, defer); break;
+    case 2: gemm_fmt<2>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus, defer); break;
+    default: gemm_fmt<0>(s, W, W2, rb, x, y, part, part_floats, n_rows, n_cols, n_tokens, store, cus, defer); break;
   }
 }
 

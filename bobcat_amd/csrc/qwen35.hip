@@ -178,10 +178,14 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
   run_embed(st, token_embd.format, token_embd.data, bch_row_bytes(token_embd.format, n), tokens + pos, hidden, n,
             count, nullptr);
   if (trace) run_copy(st, hidden, this->trace, count * n, nullptr, 0);
+  // A column-split sum into the residual stream (wo, out, down) is left to
+  // the norm that reads the residual next (not when tracing copies it).
+  PendingSum pend;
+  PendingSum *const defer = trace ? nullptr : &pend;
   for (uint32_t il = 0; il < n_layers; il++) {
     const QwenLayer &L = layers[il];
     // The norm also writes the fp16 inputs of the projections that follow.
-    run_rms_norm_split(st, hidden, L.attn_norm, normed, n, count, norm_eps, split);
+    run_rms_norm_split(st, hidden, L.attn_norm, normed, n, count, norm_eps, split, &pend);
     if (L.attention) {
       const uint32_t ci = L.cache_index;
       run_matmul(st, L.wq.format, L.wq.data, 2 * q_dim, n, normed, q_gate, count, 0, split, split_bytes, true);
@@ -225,7 +229,7 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
         ad.max_splits = attn_decode_max_splits(pos + q0 + nq, head_dim, kv_half);
         run_attn_prefill(st, ad, kv_half, nq);
       }
-      run_matmul(st, L.wo.format, L.wo.data, n, q_dim, attn, hidden, count, 1, split, split_bytes);
+      run_matmul(st, L.wo.format, L.wo.data, n, q_dim, attn, hidden, count, 1, split, split_bytes, false, nullptr, defer);
     } else {
       const uint32_t di = L.cache_index;
       run_matmul(st, L.qkv.format, L.qkv.data, conv_dim, n, normed, proj, count, 0, split, split_bytes, true);
@@ -251,9 +255,10 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
       // Batches of more than one token take the chunked (WY) form.
       if (count == 1 || !chunk_scratch || !run_gdn_chunked(st, g, chunk_scratch)) run_gdn_recurrence(st, g);
       run_gdn_gated_norm(st, delta_out, L.ssm_norm, z, v_dim, count * n_v, norm_eps);
-      run_matmul(st, L.out.format, L.out.data, n, value_dim, delta_out, hidden, count, 1, split, split_bytes);
+      run_matmul(st, L.out.format, L.out.data, n, value_dim, delta_out, hidden, count, 1, split, split_bytes, false,
+                 nullptr, defer);
     }
-    run_rms_norm_split(st, hidden, L.ffn_norm, normed, n, count, norm_eps, split);
+    run_rms_norm_split(st, hidden, L.ffn_norm, normed, n, count, norm_eps, split, &pend);
     if (L.gate.format == L.up.format) {
       // Gate and up in one paired launch: ffn = silu(gate·x) ⊙ (up·x).
       run_matmul(st, L.gate.format, L.gate.data, n_ff, n, normed, ffn, count, 3, split, split_bytes, true,
@@ -262,9 +267,10 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
       run_matmul(st, L.gate.format, L.gate.data, n_ff, n, normed, ffn, count, 0, split, split_bytes, true);
       run_matmul(st, L.up.format, L.up.data, n_ff, n, normed, ffn, count, 2, split, split_bytes, true);
     }
-    run_matmul(st, L.down.format, L.down.data, n, n_ff, ffn, hidden, count, 1, split, split_bytes);
+    run_matmul(st, L.down.format, L.down.data, n, n_ff, ffn, hidden, count, 1, split, split_bytes, false, nullptr, defer);
     if (trace) run_copy(st, hidden, this->trace + (1 + il) * tstride, count * n, nullptr, 0);
   }
+  finish_pending_sum(st, pend, hidden);
   if (trace) run_rms_norm(st, hidden, output_norm, this->trace + (1 + n_layers) * tstride, n, count, norm_eps);
   if (want_logits)
     run_matvec(st, output.format, output.data, n_vocab, n, hidden + (uint64_t)(count - 1) * n, logits, output_norm,

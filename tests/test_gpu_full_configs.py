@@ -104,6 +104,12 @@ def test_greedy_128_matches_oracle(hip, model):
     half = cls(hip, weights, n_ctx=n_ctx, kv_half=True)
     lh = half.prefill(prompt)
     assert rel(lh, fix["logits0"]) < HALF_TOLERANCE, rel(lh, fix["logits0"])
+    # A traced prefill adds every column-split sum in a launch of its own
+    # (an untraced one leaves the sums into the residual stream to the norm
+    # that reads it next): the logits must not change by a bit.
+    half.reset()
+    lt, _ = half.prefill(prompt, trace=True)
+    assert np.array_equal(lt, lh)
     got_h = half.generate(N_GEN).tolist()
     same = next((i for i, (a, b) in enumerate(zip(got_h, want)) if a != b), N_GEN)
     print(f"{name}: f16 cache agrees with the oracle on the first {same} tokens")
