@@ -195,6 +195,13 @@ void run_short_conv(hipStream_t s, const float *bcx, const float *taps, float *h
                     uint32_t ksize, uint32_t n_tokens);
 void run_short_conv_batch(hipStream_t s, const float *bcx, const float *taps, float *hist, float *out,
                           uint32_t n_embd, uint32_t ksize, uint32_t n_tokens);
+// run_short_conv_batch plus, in scratch, the fp16 inputs of the output
+// (as run_rms_norm_split leaves them) for a following run_matmul(..., x =
+// out, n_tokens, n_cols = n_embd, scratch, ..., split_ready = true), in one
+// launch.  False (nothing launched) for shapes it does not take: ksize
+// other than 3, or more than 4096 channels.
+bool run_short_conv_split(hipStream_t s, const float *bcx, const float *taps, float *hist, float *out,
+                          uint32_t n_embd, uint32_t ksize, uint32_t n_tokens, void *scratch);
 
 // attention.hip.  Causal GQA attention of n_queries queries at positions
 // first_pos + dpos.. over a cache of [pos][n_kv][head_dim] (f16 when

@@ -240,10 +240,12 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
       run_matmul(s, L.in_proj.format, L.in_proj.data, 3 * n, n, m->normed, m->bcx, count, 0, m->split, m->split_bytes,
                  true);
       check_finite(s, "in_proj", il, m->bcx, (uint64_t)count * 3 * n);
-      run_short_conv_batch(s, m->bcx, L.taps, hist, m->conv_out, n, m->conv_kernel, count);
+      // The convolution also writes the fp16 inputs of the out projection.
+      const bool split = run_short_conv_split(s, m->bcx, L.taps, hist, m->conv_out, n, m->conv_kernel, count, m->split);
+      if (!split) run_short_conv_batch(s, m->bcx, L.taps, hist, m->conv_out, n, m->conv_kernel, count);
       check_finite(s, "short_conv", il, m->conv_out, (uint64_t)count * n);
       run_matmul(s, L.out_proj.format, L.out_proj.data, n, n, m->conv_out, m->hidden, count, 1, m->split, m->split_bytes,
-                 false, nullptr, defer_ffn);
+                 split, nullptr, defer_ffn);
       check_finite(s, "out_proj", il, m->hidden, (uint64_t)count * n);
     } else {
       const uint32_t ci = L.cache_index;

@@ -226,6 +226,101 @@ __global__ void k_short_conv_batch(const float *__restrict__ bcx, const float *_
   out[(uint64_t)tok * n_embd + ch] = bcx[(uint64_t)tok * 3 * n_embd + n_embd + ch] * sum;
 }
 
+// k_short_conv_batch, k_short_conv_history and the fp16 conversion of the
+// output that the out projection's GEMM reads (k_split_hi in matmul.hip) in
+// one launch.  Workgroup b takes tokens kConvTokens·b .. +kConvTokens-1
+// over every channel (thread tid: channels tid + 1024·c), so it also holds
+// each token's largest magnitude.  Only the first workgroup reads the
+// history (the ksize-1 positions before the batch, all of them within its
+// tokens), and it writes the new history after those reads.  The
+// arithmetic is that of the separate kernels, operation for operation.
+constexpr uint32_t kConvTokens = 2;
+constexpr uint32_t kConvThreads = 1024;
+
+template <int CPT, int KS>
+__global__ __launch_bounds__(kConvThreads) void k_short_conv_split(const float *__restrict__ bcx, const float *__restrict__ taps,
+                                                         float *__restrict__ hist, float *__restrict__ out,
+                                                         uint32_t n_embd, uint32_t n_tokens, _Float16 *__restrict__ H,
+                                                         float *__restrict__ unscale) {
+  constexpr int TC = kConvTokens, NH = KS - 1, NW = TC + NH;  // window: tokens t0-NH .. t0+TC-1
+  constexpr uint32_t NT = kConvThreads;
+  __shared__ float red[NT / 64];
+  const uint32_t tid = threadIdx.x, t0 = blockIdx.x * TC;
+  float v[CPT][TC], mx[TC];
+#pragma unroll
+  for (int j = 0; j < TC; j++) mx[j] = 0.f;
+#pragma unroll
+  for (int c = 0; c < CPT; c++) {
+    const uint32_t ch = min(tid + NT * c, n_embd - 1);  // (clamped lanes compute and drop)
+    // Every load of the channel first: B·X over the window (the history
+    // before the batch), C of the tokens, the taps.
+    float bx[NW], cv[TC], tp[KS];
+#pragma unroll
+    for (int i = 0; i < NW; i++) {
+      const int src = (int)t0 - NH + i;
+      if (src >= 0) {
+        const float *r = bcx + (uint64_t)min((uint32_t)src, n_tokens - 1) * 3 * n_embd;
+        bx[i] = r[ch] * r[2 * n_embd + ch];
+      } else {
+        bx[i] = hist[(uint32_t)(src + NH) * n_embd + ch];  // (first workgroup only)
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < TC; j++) cv[j] = bcx[(uint64_t)min(t0 + j, n_tokens - 1) * 3 * n_embd + n_embd + ch];
+#pragma unroll
+    for (int k = 0; k < KS; k++) tp[k] = taps[(uint64_t)ch * KS + k];
+#pragma unroll
+    for (int j = 0; j < TC; j++) {
+      float sum = 0.f;
+#pragma unroll
+      for (int k = 0; k < KS; k++) sum = fmaf(tp[k], bx[j + k], sum);
+      v[c][j] = cv[j] * sum;
+      if (tid + NT * c < n_embd && t0 + j < n_tokens) {
+        out[(uint64_t)(t0 + j) * n_embd + ch] = v[c][j];
+        mx[j] = fmaxf(mx[j], fabsf(v[c][j]));
+      }
+    }
+  }
+  if (blockIdx.x == 0) {
+    // The new history: B·X of the batch's last NH tokens (the old history
+    // where the batch is shorter), written after this workgroup's reads.
+#pragma unroll
+    for (int c = 0; c < CPT; c++) {
+      const uint32_t ch = tid + NT * c;
+      if (ch >= n_embd) continue;
+      float next[NH];
+#pragma unroll
+      for (int k = 0; k < NH; k++) {
+        const int src = (int)n_tokens - (NH - k);
+        if (src >= 0) {
+          const float *row = bcx + (uint64_t)src * 3 * n_embd;
+          next[k] = row[ch] * row[2 * n_embd + ch];
+        } else {
+          next[k] = hist[(uint32_t)(src + NH) * n_embd + ch];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < NH; k++) hist[k * n_embd + ch] = next[k];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < TC; j++) {
+    const uint32_t tok = t0 + j;
+    const float m = block_max<NT>(mx[j], red);
+    if (tok >= n_tokens) continue;  // (uniform)
+    int ex = 0;
+    if (m > 0.f) frexpf(m, &ex);  // m < 2^ex
+    const int k2 = max(-100, min(100, 14 - ex));
+    const float scale = ldexpf(1.0f, k2);
+    if (tid == 0) unscale[tok] = ldexpf(1.0f, -k2);
+#pragma unroll
+    for (int c = 0; c < CPT; c++) {
+      const uint32_t ch = tid + NT * c;
+      if (ch < n_embd) H[(uint64_t)tok * n_embd + ch] = (_Float16)(v[c][j] * scale);
+    }
+  }
+}
+
 // short_conv_history (conv.metal:80-108).
 __global__ void k_short_conv_history(const float *__restrict__ bcx, float *__restrict__ hist, uint32_t n_embd,
                                      uint32_t ksize, uint32_t n_tokens) {
@@ -401,6 +496,23 @@ void run_embed_next(hipStream_t s, uint32_t format, const uint8_t *W, uint64_t r
 void run_short_conv(hipStream_t s, const float *bcx, const float *taps, float *hist, float *out, uint32_t n_embd,
                     uint32_t ksize, uint32_t n_tokens) {
   k_short_conv<<<div_ceil(n_embd, 256), 256, 0, s>>>(bcx, taps, hist, out, n_embd, ksize, n_tokens);
+}
+
+bool run_short_conv_split(hipStream_t s, const float *bcx, const float *taps, float *hist, float *out,
+                          uint32_t n_embd, uint32_t ksize, uint32_t n_tokens, void *scratch) {
+  // LFM2's convolutions have 3 taps; other sizes take the separate kernels.
+  if (!n_tokens || ksize != 3 || n_embd == 0 || n_embd > 4 * kConvThreads) return false;
+  _Float16 *hx = static_cast<_Float16 *>(scratch);
+  float *unscale = reinterpret_cast<float *>(hx + (uint64_t)n_tokens * n_embd);
+  const uint32_t grid = div_ceil(n_tokens, kConvTokens);
+  const uint32_t cpt = div_ceil(n_embd, kConvThreads);
+  if (cpt <= 1)
+    k_short_conv_split<1, 3><<<grid, kConvThreads, 0, s>>>(bcx, taps, hist, out, n_embd, n_tokens, hx, unscale);
+  else if (cpt <= 2)
+    k_short_conv_split<2, 3><<<grid, kConvThreads, 0, s>>>(bcx, taps, hist, out, n_embd, n_tokens, hx, unscale);
+  else
+    k_short_conv_split<4, 3><<<grid, kConvThreads, 0, s>>>(bcx, taps, hist, out, n_embd, n_tokens, hx, unscale);
+  return true;
 }
 
 void run_short_conv_batch(hipStream_t s, const float *bcx, const float *taps, float *hist, float *out,
