@@ -158,11 +158,12 @@ static void split_hi(hipStream_t s, const float *x, uint32_t rows, uint32_t n_co
 // SUM: x first receives the column-split partial products of the GEMM
 // that accumulated into it (P[split][row][i], added in split order and then
 // to x, exactly as k_gemm_reduce<1> would), and the sums are written back.
-template <int PER, bool SUM>
+template <int PER, int SPLITS>
 __global__ __launch_bounds__(256) void k_rms_norm_split(float *__restrict__ x, const float *__restrict__ w,
                                                        float *__restrict__ out, uint32_t n, float eps,
                                                        _Float16 *__restrict__ H, float *__restrict__ unscale,
                                                        const float *__restrict__ P, uint32_t splits) {
+  constexpr bool SUM = SPLITS > 0;
   __shared__ float red[4];
   const uint32_t t = blockIdx.x, tid = threadIdx.x;
   float *xr = x + (uint64_t)t * n;
@@ -175,6 +176,11 @@ __global__ __launch_bounds__(256) void k_rms_norm_split(float *__restrict__ x, c
     for (uint32_t sp = 1; sp < splits; sp++) v += prow[sp * pstride + i];
     return v;
   };
+  // The partials of element i, all loaded before any is added (SPLITS > 0).
+  auto partials = [&](uint32_t i, float *pv) __attribute__((always_inline)) {
+#pragma unroll
+    for (int sp = 0; sp < (SUM ? SPLITS : 1); sp++) pv[sp] = prow[sp * pstride + i];
+  };
   float xv[PER > 0 ? PER : 1], wv[PER > 0 ? PER : 1];
   float ss = 0.f;
   if constexpr (PER > 0) {
@@ -185,11 +191,17 @@ __global__ __launch_bounds__(256) void k_rms_norm_split(float *__restrict__ x, c
       wv[k] = i < n ? w[i] : 0.f;
     }
     if constexpr (SUM) {
+      float pv[PER][SUM ? SPLITS : 1];
+#pragma unroll
+      for (int k = 0; k < PER; k++) partials(min(tid + 256 * k, n - 1), pv[k]);
 #pragma unroll
       for (int k = 0; k < PER; k++) {
         const uint32_t i = tid + 256 * k;
+        float v = pv[k][0];
+#pragma unroll
+        for (int sp = 1; sp < SPLITS; sp++) v += pv[k][sp];
         if (i < n) {
-          xv[k] += pending(i);
+          xv[k] += v;
           xr[i] = xv[k];
         }
       }
@@ -255,7 +267,8 @@ void run_rms_norm_split(hipStream_t s, float *x, const float *w, float *out, uin
   _Float16 *hx = static_cast<_Float16 *>(scratch);
   float *unscale = reinterpret_cast<float *>(hx + (uint64_t)rows * n);
   bool sum = pending && pending->splits > 1;
-  if (sum && (pending->n != (uint64_t)rows * n ||
+  const uint32_t ps = sum ? pending->splits : 0;
+  if (sum && (pending->n != (uint64_t)rows * n || (ps != 2 && ps != 4 && ps != 8) ||
               reinterpret_cast<const uint8_t *>(pending->part) < reinterpret_cast<uint8_t *>(unscale + rows))) {
     // Not this norm's rows, or the fp16 inputs written here would cover the
     // partials: add them first.
@@ -266,10 +279,14 @@ void run_rms_norm_split(hipStream_t s, float *x, const float *w, float *out, uin
   const uint32_t splits = sum ? pending->splits : 0;
   auto go = [&](auto per) {
     constexpr int PER = decltype(per)::value;
-    if (sum)
-      k_rms_norm_split<PER, true><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale, P, splits);
+    if (!sum)
+      k_rms_norm_split<PER, 0><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale, P, splits);
+    else if (splits == 2)
+      k_rms_norm_split<PER, 2><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale, P, splits);
+    else if (splits == 4)
+      k_rms_norm_split<PER, 4><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale, P, splits);
     else
-      k_rms_norm_split<PER, false><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale, P, splits);
+      k_rms_norm_split<PER, 8><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale, P, splits);
   };
   if (n <= 1024)
     go(std::integral_constant<int, 4>{});
