@@ -188,6 +188,10 @@ void run_norm_rope(hipStream_t s, const float *src, void *dst, bool half, const 
 void run_convert_half(hipStream_t s, const float *src, void *dst, uint32_t n, const uint32_t *dpos,
                       uint64_t dst_pos_stride);
 void run_copy(hipStream_t s, const float *src, float *dst, uint32_t n, const uint32_t *dpos, uint64_t dst_pos_stride);
+// rows x cols floats, rows src_stride apart, to rows dst_stride apart (f16
+// when half).
+void run_copy_rows(hipStream_t s, const float *src, uint32_t src_stride, void *dst, uint32_t dst_stride, bool half,
+                   uint32_t cols, uint32_t rows);
 void run_embed(hipStream_t s, uint32_t format, const uint8_t *W, uint64_t row_bytes, const uint32_t *tokens,
                float *out, uint32_t n_embd, uint32_t n_tokens, const uint32_t *dpos);
 void run_argmax(hipStream_t s, const float *x, uint32_t *out, uint32_t n, uint32_t *dpos, bool advance);

@@ -35,6 +35,9 @@ struct Layer {
   const float *taps = nullptr;
   DevMatrix in_proj, out_proj, wq, wk, wv, wo, gate, up, down;
   const float *q_norm = nullptr, *k_norm = nullptr;
+  // Rows of wq, wk and wv together when the three lie back to back in
+  // device memory in one format (one prefill GEMM), else 0.
+  uint32_t qkv_rows = 0;
   // Mixture of experts (lfm2.rs:128-142): the F32 router, the routing bias
   // and the stacked expert matrices.
   bool moe = false;
@@ -60,6 +63,7 @@ struct bch_lfm2 : bch::Sequence {
   void *k_cache = nullptr, *v_cache = nullptr;
   float *conv_state = nullptr, *hidden = nullptr, *normed = nullptr, *bcx = nullptr, *conv_out = nullptr;
   float *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *ffn = nullptr;
+  float *qkv = nullptr;  // prefill: q | k | v of each token from one GEMM (Layer::qkv_rows)
   float *partials = nullptr;
   uint64_t partial_floats = 0;  // floats of `partials`
   uint32_t *counters = nullptr;
@@ -249,22 +253,28 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
       check_finite(s, "out_proj", il, m->hidden, (uint64_t)count * n);
     } else {
       const uint32_t ci = L.cache_index;
-      run_matmul(s, L.wq.format, L.wq.data, m->q_dim, n, m->normed, m->q, count, 0, m->split, m->split_bytes, true);
-      // (q, k and v read the fp16 inputs the norm wrote.)
-      run_matmul(s, L.wk.format, L.wk.data, m->kv_dim, n, m->normed, m->k, count, 0, m->split, m->split_bytes, true);
-      run_matmul(s, L.wv.format, L.wv.data, m->kv_dim, n, m->normed, m->v, count, 0, m->split, m->split_bytes, true);
-      check_finite(s, "q", il, m->q, (uint64_t)count * m->q_dim);
-      check_finite(s, "k", il, m->k, (uint64_t)count * m->kv_dim);
-      check_finite(s, "v", il, m->v, (uint64_t)count * m->kv_dim);
-      run_norm_rope(s, m->q, m->q, false, L.q_norm, m->n_heads, m->head_dim, m->head_dim, m->head_dim, pos, nullptr,
-                    count, m->q_dim, m->q_dim, m->rope_theta, m->norm_eps, 0);
-      run_norm_rope(s, m->k, m->cache_slot(m->k_cache, ci, pos), m->kv_half, L.k_norm, m->n_kv_heads, m->head_dim,
-                    m->head_dim, m->head_dim, pos, nullptr, count, m->kv_dim, m->kv_dim, m->rope_theta, m->norm_eps,
+      // q, k and v (which read the fp16 inputs the norm wrote): one GEMM
+      // when the three matrices lie back to back, each token's row then
+      // q | k | v.
+      const float *qs = m->q, *ks = m->k, *vs = m->v;
+      uint32_t qkv_stride = m->q_dim, kv_stride = m->kv_dim;
+      if (L.qkv_rows) {
+        run_matmul(s, L.wq.format, L.wq.data, L.qkv_rows, n, m->normed, m->qkv, count, 0, m->split, m->split_bytes,
+                   true);
+        qs = m->qkv, ks = m->qkv + m->q_dim, vs = m->qkv + m->q_dim + m->kv_dim;
+        qkv_stride = kv_stride = L.qkv_rows;
+      } else {
+        run_matmul(s, L.wq.format, L.wq.data, m->q_dim, n, m->normed, m->q, count, 0, m->split, m->split_bytes, true);
+        run_matmul(s, L.wk.format, L.wk.data, m->kv_dim, n, m->normed, m->k, count, 0, m->split, m->split_bytes, true);
+        run_matmul(s, L.wv.format, L.wv.data, m->kv_dim, n, m->normed, m->v, count, 0, m->split, m->split_bytes, true);
+      }
+      check_finite(s, "q", il, qs, (uint64_t)count * qkv_stride);
+      run_norm_rope(s, qs, m->q, false, L.q_norm, m->n_heads, m->head_dim, m->head_dim, m->head_dim, pos, nullptr,
+                    count, qkv_stride, m->q_dim, m->rope_theta, m->norm_eps, 0);
+      run_norm_rope(s, ks, m->cache_slot(m->k_cache, ci, pos), m->kv_half, L.k_norm, m->n_kv_heads, m->head_dim,
+                    m->head_dim, m->head_dim, pos, nullptr, count, kv_stride, m->kv_dim, m->rope_theta, m->norm_eps,
                     0);
-      if (m->kv_half)
-        run_convert_half(s, m->v, m->cache_slot(m->v_cache, ci, pos), count * m->kv_dim, nullptr, 0);
-      else
-        run_copy(s, m->v, static_cast<float *>(m->cache_slot(m->v_cache, ci, pos)), count * m->kv_dim, nullptr, 0);
+      run_copy_rows(s, vs, kv_stride, m->cache_slot(m->v_cache, ci, pos), m->kv_dim, m->kv_half, m->kv_dim, count);
       if (attn_prefill_mfma_supported(m->n_heads, m->n_kv_heads, m->head_dim, m->kv_half))
         run_attn_prefill_mfma(s, m->q, m->cache_layer(m->k_cache, ci), m->cache_layer(m->v_cache, ci), m->attn,
                               m->n_heads, m->n_kv_heads, m->head_dim, pos, count, m->q_dim, m->q_dim,
@@ -481,6 +491,15 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
       return cleanup(rc);
   }
   if (int rc = m->upload(up)) return cleanup(rc);
+  bool any_qkv = false;
+  for (Layer &L : m->layers) {
+    if (!L.attention || L.wq.format != L.wk.format || L.wq.format != L.wv.format) continue;
+    const uint64_t rb = bch_row_bytes(L.wq.format, n);
+    if (L.wk.data == L.wq.data + rb * m->q_dim && L.wv.data == L.wk.data + rb * m->kv_dim) {
+      L.qkv_rows = m->q_dim + 2 * m->kv_dim;
+      any_qkv = true;
+    }
+  }
   // Buffers (Lfm2Metal::new, lfm2_metal.rs:153-203).
   {
     const uint64_t rows = m->batch;
@@ -499,6 +518,7 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
            (rc = m->alloc_t(rows * 3 * n, &m->bcx)) || (rc = m->alloc_t(rows * n, &m->conv_out)) ||
            (rc = m->alloc_t(rows * m->q_dim + 4, &m->q)) || (rc = m->alloc_t(rows * m->kv_dim + 4, &m->k)) ||
            (rc = m->alloc_t(rows * m->kv_dim + 4, &m->v)) || (rc = m->alloc_t(rows * m->q_dim + 4, &m->attn)) ||
+           (any_qkv && (rc = m->alloc_t(rows * (m->q_dim + 2 * m->kv_dim), &m->qkv))) ||
            (rc = m->alloc_t(std::max<uint64_t>(rows * m->n_ff, (uint64_t)m->n_used * m->n_ff_expert), &m->ffn)) ||
            (rc = m->alloc_t(partial_floats + 4, &m->partials)) ||
            (rc = m->alloc_t((uint64_t)kAttnQueryBatch * std::max(1u, m->n_heads), &m->counters)) ||

@@ -114,6 +114,20 @@ __global__ void k_convert_half(const float *__restrict__ src, __half *__restrict
   dst[off + i] = __float2half(src[i]);
 }
 
+// rows x cols floats from rows src_stride apart to rows dst_stride apart,
+// as f16 (half) or f32.
+template <bool HALF>
+__global__ void k_copy_rows(const float *__restrict__ src, uint32_t src_stride, void *__restrict__ dst,
+                            uint32_t dst_stride, uint32_t cols) {
+  const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x, r = blockIdx.y;
+  if (c >= cols) return;
+  const float v = src[(uint64_t)r * src_stride + c];
+  if (HALF)
+    static_cast<__half *>(dst)[(uint64_t)r * dst_stride + c] = __float2half(v);
+  else
+    static_cast<float *>(dst)[(uint64_t)r * dst_stride + c] = v;
+}
+
 __global__ void k_copy(const float *__restrict__ src, float *__restrict__ dst, uint32_t n, const uint32_t *dpos,
                        uint64_t dst_pos_stride) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -464,6 +478,16 @@ void run_norm_rope(hipStream_t s, const float *src, void *dst, bool half, const 
 void run_convert_half(hipStream_t s, const float *src, void *dst, uint32_t n, const uint32_t *dpos,
                       uint64_t dst_pos_stride) {
   if (n) k_convert_half<<<div_ceil(n, 256), 256, 0, s>>>(src, static_cast<__half *>(dst), n, dpos, dst_pos_stride);
+}
+
+void run_copy_rows(hipStream_t s, const float *src, uint32_t src_stride, void *dst, uint32_t dst_stride, bool half,
+                   uint32_t cols, uint32_t rows) {
+  if (!cols || !rows) return;
+  const dim3 grid(div_ceil(cols, 256), rows);
+  if (half)
+    k_copy_rows<true><<<grid, 256, 0, s>>>(src, src_stride, dst, dst_stride, cols);
+  else
+    k_copy_rows<false><<<grid, 256, 0, s>>>(src, src_stride, dst, dst_stride, cols);
 }
 
 void run_copy(hipStream_t s, const float *src, float *dst, uint32_t n, const uint32_t *dpos, uint64_t dst_pos_stride) {
