@@ -62,9 +62,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *__restrict__ 
   const uint32_t kend = first_pos + min(q0 + kPrefQ, n_queries);  // keys of the block's last query, exclusive
   const uint64_t row_elems = (uint64_t)n_kv * HD;                 // cache elements per position
   // Key split blockIdx.z of gridDim.z: a contiguous run of whole 32-key
-  // blocks.  The host gives every split at least two blocks, so each split
-  // starts at or before the tile's first query and every query sees a key
-  // of every split.
+  // blocks of the tile's keys (possibly none, or none visible to a query:
+  // that split's partial then has max -inf and sum 0, and weighs nothing in
+  // the combine).
   const uint32_t n_blocks = (kend + kPrefKeys - 1) / kPrefKeys, n_split = gridDim.z, split = blockIdx.z;
   const uint32_t kb_lo = split * n_blocks / n_split * kPrefKeys, kb_hi = (split + 1) * n_blocks / n_split * kPrefKeys;
 
@@ -133,14 +133,17 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *__restrict__ 
       mx = fmaxf(mx, sc[r]);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);  // finite: key 0 is visible to every query
-    const float corr = expf(m_run - m_new);
+    // -inf while no key of this split has been visible to the query (a
+    // causal split can start after it): the block then adds exact zeros.
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float corr = expf(m_run - m_use);
     m_run = m_new;
     float psum = 0.f;
     ph4_t ph[4], pl[4];
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const float p = expf(sc[r] - m_new);
+      const float p = expf(sc[r] - m_use);
       psum += p;
       const _Float16 h = (_Float16)p;
       ph[r / 4][r % 4] = h;
@@ -220,16 +223,21 @@ bool attn_prefill_mfma_supported(uint32_t n_heads, uint32_t n_kv, uint32_t head_
          (head_dim == 64 || head_dim == 128 || head_dim == 256);
 }
 
+uint64_t attn_prefill_partial_floats(uint32_t n_queries, uint32_t n_heads, uint32_t head_dim, uint32_t splits) {
+  return (uint64_t)n_queries * n_heads * splits * (head_dim + 2);
+}
+
 uint32_t attn_prefill_splits(uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t first_pos,
                              uint32_t n_queries, uint64_t partial_floats) {
   if (!n_queries) return 1;
-  // Enough workgroups for two per CU, each split at least kMinSplitKeys keys
-  // of the batch's first tile (so at least two 32-key blocks of every tile),
-  // and no more partials than the scratch holds.
-  constexpr uint32_t kTargetGroups = 512, kMinSplitKeys = 1024, kMaxSplits = 16;
+  // Enough workgroups for two per CU, at least kMinSplitBlocks 32-key blocks
+  // per split of the batch's middle tile, and no more partials than the
+  // scratch holds.
+  constexpr uint32_t kTargetGroups = 512, kMinSplitBlocks = 2, kMaxSplits = 16;
   const uint32_t tiles = (n_queries + kPrefQ - 1) / kPrefQ;
   uint32_t want = (kTargetGroups + tiles * n_kv - 1) / (tiles * n_kv);
-  want = std::min(want, (first_pos + std::min<uint32_t>(kPrefQ, n_queries)) / kMinSplitKeys);
+  const uint32_t mid_blocks = (first_pos + (n_queries + 1) / 2 + kPrefKeys - 1) / kPrefKeys;
+  want = std::min(want, mid_blocks / kMinSplitBlocks);
   want = std::min<uint32_t>(want, kMaxSplits);
   const uint64_t per_split = (uint64_t)n_queries * n_heads * (head_dim + 2);
   want = (uint32_t)std::min<uint64_t>(want, partial_floats / per_split);

@@ -230,10 +230,12 @@ void run_attn_prefill_mfma(hipStream_t s, const float *q, const void *k_cache, c
                            float *partials, uint64_t partial_floats, const float *gate = nullptr,
                            uint32_t gate_head_stride = 0, uint32_t gate_query_stride = 0);
 // Key splits run_attn_prefill_mfma uses for a batch (1 without scratch):
-// long contexts split the keys so the launch fills the chip, each split's
+// the keys are split so the launch fills the chip, each split's
 // (max, sum, output) partials going to `partials` (partial_floats floats).
 uint32_t attn_prefill_splits(uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t first_pos,
                              uint32_t n_queries, uint64_t partial_floats);
+// Floats of the partials of n_queries queries in `splits` key splits.
+uint64_t attn_prefill_partial_floats(uint32_t n_queries, uint32_t n_heads, uint32_t head_dim, uint32_t splits);
 
 // matmul.hip.  Y[t] (store) W·X[t] for n_tokens rows; store 0 overwrite,
 // 1 accumulate, 2 swiglu (y = silu(y) * product).

@@ -504,8 +504,11 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
   {
     const uint64_t rows = m->batch;
     const uint64_t cache = (uint64_t)m->n_attn * n_ctx * m->kv_dim * (m->kv_half ? 2 : 4);
-    const uint64_t partial_floats = attention_partial_floats(std::min<uint32_t>(m->batch, kAttnQueryBatch), m->n_heads,
+    uint64_t partial_floats = attention_partial_floats(std::min<uint32_t>(m->batch, kAttnQueryBatch), m->n_heads,
                                                             hd, attn_decode_max_splits(n_ctx, hd, m->kv_half));
+    // The MFMA prefill attention splits the keys of a batch up to 4 ways.
+    if (attn_prefill_mfma_supported(m->n_heads, m->n_kv_heads, hd, m->kv_half))
+      partial_floats = std::max(partial_floats, attn_prefill_partial_floats(m->batch, m->n_heads, hd, 4));
     m->partial_floats = partial_floats;
     const uint32_t widest = std::max({n, m->q_dim, m->n_ff});
     const uint64_t split_bytes = m->split_bytes =

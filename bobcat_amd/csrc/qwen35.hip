@@ -385,8 +385,11 @@ int bch_qwen35_new(bch_ctx *ctx, const bch_qwen35_model *md, uint32_t n_ctx, int
     const uint64_t rows = m->batch;
     const uint64_t cache = (uint64_t)m->n_attn * n_ctx * m->kv_dim * (m->kv_half ? 2 : 4);
     m->prefill_splits = attention_splits(n_ctx, std::max(1u, m->n_kv_heads), ctx->n_cus);
-    const uint64_t partial_floats = attention_partial_floats(std::min<uint32_t>(m->batch, kQwenAttnQueryBatch),
+    uint64_t partial_floats = attention_partial_floats(std::min<uint32_t>(m->batch, kQwenAttnQueryBatch),
                                                             m->n_heads, hd, attn_decode_max_splits(n_ctx, hd, m->kv_half));
+    // The MFMA prefill attention splits the keys of a batch up to 4 ways.
+    if (attn_prefill_mfma_supported(m->n_heads, m->n_kv_heads, hd, m->kv_half))
+      partial_floats = std::max(partial_floats, attn_prefill_partial_floats(m->batch, m->n_heads, hd, 4));
     m->partial_floats = partial_floats;
     int rc = 0;
     (void)((rc = m->alloc(cache, &m->k_cache)) || (rc = m->alloc(cache, &m->v_cache)) ||
