@@ -71,8 +71,9 @@ __global__ __launch_bounds__(kGdnCols * 64) void k_gdn_recurrence(GdnArgs a) {
       }
       if (lane < kGdnCols) vs[j][lane] = tok[2 * key_dim + head * a.v_dim + col0 + lane];
       if (lane == 0) {
-        const float b = a.beta[(uint64_t)(t0 + j) * a.n_v + head];
-        const float d = a.alpha[(uint64_t)(t0 + j) * a.n_v + head];
+        const uint64_t gs = a.gate_stride ? a.gate_stride : a.n_v;
+        const float b = a.beta[(uint64_t)(t0 + j) * gs + head];
+        const float d = a.alpha[(uint64_t)(t0 + j) * gs + head];
         bs[j] = a.raw_gates ? sigmoid_f(b) : b;
         ds[j] = a.raw_gates ? expf(a.a[head] * softplus_f(d + a.dt_bias[head])) : d;
       }
@@ -289,8 +290,9 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_prep(GdnArgs a, float *__rest
   if (wave == 0) {
     float b = 0.f, l = 0.f;
     if (lane < L) {
-      const float rb = a.beta[(uint64_t)(t0 + lane) * a.n_v + head];
-      const float rd = a.alpha[(uint64_t)(t0 + lane) * a.n_v + head];
+      const uint64_t gs = a.gate_stride ? a.gate_stride : a.n_v;
+      const float rb = a.beta[(uint64_t)(t0 + lane) * gs + head];
+      const float rd = a.alpha[(uint64_t)(t0 + lane) * gs + head];
       b = a.raw_gates ? sigmoid_f(rb) : rb;
       l = a.raw_gates ? a.a[head] * softplus_f(rd + a.dt_bias[head]) : logf(rd);
     }
@@ -502,39 +504,41 @@ bool run_gdn_chunked(hipStream_t s, const GdnArgs &a, float *scratch) {
 // launch then leaves the latest k-1 inputs in `hist` (after every read of
 // the old history).
 __global__ void k_gdn_conv(const float *__restrict__ x, const float *__restrict__ taps, const float *__restrict__ hist,
-                           float *__restrict__ y, uint32_t channels, uint32_t ksize, uint32_t n_tokens) {
+                           float *__restrict__ y, uint32_t channels, uint32_t ksize, uint32_t n_tokens,
+                           uint32_t x_stride) {
   const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (uint64_t)n_tokens * channels) return;
   const uint32_t t = (uint32_t)(i / channels), c = (uint32_t)(i % channels), past = ksize - 1;
   const float *tp = taps + (uint64_t)c * ksize;
-  float sum = tp[past] * x[i];
+  float sum = tp[past] * x[(uint64_t)t * x_stride + c];
   for (uint32_t j = 0; j < past; j++) {
     const int src = (int)t - (int)past + (int)j;  // token of window slot j
-    const float w = src >= 0 ? x[(uint64_t)src * channels + c] : hist[(uint64_t)c * past + (past + src)];
+    const float w = src >= 0 ? x[(uint64_t)src * x_stride + c] : hist[(uint64_t)c * past + (past + src)];
     sum += tp[j] * w;
   }
   y[i] = sum / (1.0f + expf(-sum));
 }
 
 __global__ void k_gdn_conv_history(const float *__restrict__ x, float *__restrict__ hist, uint32_t channels,
-                                   uint32_t ksize, uint32_t n_tokens) {
+                                   uint32_t ksize, uint32_t n_tokens, uint32_t x_stride) {
   const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= channels) return;
   const uint32_t past = ksize - 1;
   float window[kGdnMaxKernel - 1];
   for (uint32_t j = 0; j < past; j++) {
     const int src = (int)n_tokens - (int)past + (int)j;
-    window[j] = src >= 0 ? x[(uint64_t)src * channels + c] : hist[(uint64_t)c * past + (past + src)];
+    window[j] = src >= 0 ? x[(uint64_t)src * x_stride + c] : hist[(uint64_t)c * past + (past + src)];
   }
   for (uint32_t j = 0; j < past; j++) hist[(uint64_t)c * past + j] = window[j];
 }
 
 void run_gdn_conv(hipStream_t s, const float *x, const float *taps, float *hist, float *y, uint32_t channels,
-                  uint32_t ksize, uint32_t n_tokens) {
+                  uint32_t ksize, uint32_t n_tokens, uint32_t x_stride) {
   const uint64_t n = (uint64_t)n_tokens * channels;
   if (!n) return;
-  k_gdn_conv<<<(uint32_t)((n + 255) / 256), 256, 0, s>>>(x, taps, hist, y, channels, ksize, n_tokens);
-  k_gdn_conv_history<<<(channels + 255) / 256, 256, 0, s>>>(x, hist, channels, ksize, n_tokens);
+  const uint32_t xs = x_stride ? x_stride : channels;
+  k_gdn_conv<<<(uint32_t)((n + 255) / 256), 256, 0, s>>>(x, taps, hist, y, channels, ksize, n_tokens, xs);
+  k_gdn_conv_history<<<(channels + 255) / 256, 256, 0, s>>>(x, hist, channels, ksize, n_tokens, xs);
 }
 
 // gdn_gates (gdn.metal:125-149): beta <- sigmoid(beta), alpha <- the decay
@@ -555,9 +559,11 @@ void run_gdn_gates(hipStream_t s, float *beta, float *alpha, const float *a, con
 
 // The gated output norm (qwen35.rs:505-511): one wave per row of v_dim.
 __global__ __launch_bounds__(64) void k_gdn_gated_norm(float *x, const float *__restrict__ w,
-                                                       const float *__restrict__ z, uint32_t v_dim, float eps) {
+                                                       const float *__restrict__ z, uint32_t v_dim, float eps,
+                                                       uint32_t n_v, uint32_t z_stride) {
   float *row = x + (uint64_t)blockIdx.x * v_dim;
-  const float *g = z + (uint64_t)blockIdx.x * v_dim;
+  const float *g = z_stride ? z + (uint64_t)(blockIdx.x / n_v) * z_stride + (uint64_t)(blockIdx.x % n_v) * v_dim
+                            : z + (uint64_t)blockIdx.x * v_dim;
   float ss = 0.f;
   for (uint32_t i = threadIdx.x; i < v_dim; i += 64) ss = fmaf(row[i], row[i], ss);
   ss = wave_sum(ss);
@@ -569,8 +575,8 @@ __global__ __launch_bounds__(64) void k_gdn_gated_norm(float *x, const float *__
 }
 
 void run_gdn_gated_norm(hipStream_t s, float *x, const float *w, const float *z, uint32_t v_dim, uint32_t n_rows,
-                        float eps) {
-  k_gdn_gated_norm<<<n_rows, 64, 0, s>>>(x, w, z, v_dim, eps);
+                        float eps, uint32_t n_v, uint32_t z_stride) {
+  k_gdn_gated_norm<<<n_rows, 64, 0, s>>>(x, w, z, v_dim, eps, std::max(1u, n_v), z_stride);
 }
 
 // attention_gate (gdn.metal:306-322): each query head's output times the

@@ -122,7 +122,7 @@ bool fast_matvec_gdn_in(hipStream_t s, uint32_t format, const uint8_t *Wqkv, con
                         float *conv_out, float *z, float *beta, float *alpha, uint32_t n_cus);
 struct GdnArgs {
   const float *y;                 // [n_tokens][conv_dim], after the convolution
-  const float *beta, *alpha;      // [n_tokens][n_v]: raw projections (raw_gates) or gated
+  const float *beta, *alpha;      // [n_tokens][n_v] (rows gate_stride apart): raw projections (raw_gates) or gated
   const float *a, *dt_bias;       // [n_v], for raw gates
   float *state;                   // [n_v][k_dim][v_dim]
   float *out;                     // [n_tokens][n_v·v_dim]
@@ -133,6 +133,7 @@ struct GdnArgs {
   // becomes norm_w ⊙ rmsnorm(out) ⊙ silu(gate_z[head]) in the same launch.
   const float *norm_w, *gate_z;
   float norm_eps;
+  uint32_t gate_stride;  // floats between the tokens' beta (and alpha) rows; 0: n_v
 };
 // Whether a one-token recurrence runs k_gdn_step (which fuses the gated norm).
 bool gdn_step_supported(const GdnArgs &a);
@@ -143,13 +144,16 @@ bool run_gdn_recurrence(hipStream_t s, const GdnArgs &a);
 bool gdn_chunked_supported(const GdnArgs &a);
 uint64_t gdn_chunk_scratch_floats(uint32_t n_v, uint32_t k_dim, uint32_t v_dim, uint32_t n_tokens);
 bool run_gdn_chunked(hipStream_t s, const GdnArgs &a, float *scratch);
+// x_stride: floats between the tokens' input rows (0: channels).
 void run_gdn_conv(hipStream_t s, const float *x, const float *taps, float *hist, float *y, uint32_t channels,
-                  uint32_t ksize, uint32_t n_tokens);
+                  uint32_t ksize, uint32_t n_tokens, uint32_t x_stride = 0);
 void run_gdn_gates(hipStream_t s, float *beta, float *alpha, const float *a, const float *dt_bias, uint32_t n_v,
                    uint32_t n);
 // x[r] (v_dim floats per row) = w ⊙ rmsnorm(x[r]) ⊙ silu(z[r]), in place.
+// z_stride: floats between the tokens' gate rows, each n_v heads of v_dim
+// (0: the rows are contiguous).
 void run_gdn_gated_norm(hipStream_t s, float *x, const float *w, const float *z, uint32_t v_dim, uint32_t n_rows,
-                        float eps);
+                        float eps, uint32_t n_v = 1, uint32_t z_stride = 0);
 // attn[t][h·hd + d] *= sigmoid(q_gate[t][(2h + 1)·hd + d]).
 void run_attention_gate(hipStream_t s, float *attn, const float *q_gate, uint32_t head_dim, uint32_t q_dim,
                         uint32_t n_tokens);

@@ -36,6 +36,10 @@ struct QwenLayer {
   DevMatrix qkv, z, beta, alpha, out;
   const float *taps = nullptr, *dt_bias = nullptr, *a = nullptr, *ssm_norm = nullptr;
   DevMatrix gate, up, down;
+  // Prefill: rows of wq | wk | wv (attention) or qkv | z | beta | alpha
+  // (DeltaNet) when they lie back to back in device memory in one format
+  // (one GEMM), else 0.
+  uint32_t fused_rows = 0;
 };
 
 }  // namespace bch
@@ -61,6 +65,7 @@ struct bch_qwen35 : bch::Sequence {
   float *hidden = nullptr, *normed = nullptr, *q_gate = nullptr, *q = nullptr, *k = nullptr, *v = nullptr,
         *attn = nullptr, *proj = nullptr, *conv_out = nullptr, *z = nullptr, *beta = nullptr, *alpha = nullptr,
         *delta_out = nullptr, *ffn = nullptr, *partials = nullptr;
+  float *fused = nullptr;  // prefill: the output rows of a QwenLayer::fused_rows GEMM
   uint64_t partial_floats = 0;  // floats of `partials`
   float *chunk_scratch = nullptr;  // the chunked DeltaNet form's per-chunk matrices (prefill)
   uint32_t *counters = nullptr;
@@ -188,23 +193,30 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
     run_rms_norm_split(st, hidden, L.attn_norm, normed, n, count, norm_eps, split, &pend);
     if (L.attention) {
       const uint32_t ci = L.cache_index;
-      run_matmul(st, L.wq.format, L.wq.data, 2 * q_dim, n, normed, q_gate, count, 0, split, split_bytes, true);
-      run_matmul(st, L.wk.format, L.wk.data, kv_dim, n, normed, k, count, 0, split, split_bytes, true);
-      run_matmul(st, L.wv.format, L.wv.data, kv_dim, n, normed, v, count, 0, split, split_bytes, true);
+      // The interleaved query/gate projection, k and v: one GEMM when the
+      // matrices lie back to back (each token's row then q/gate | k | v).
+      const float *qg = q_gate, *ks = k, *vs = v;
+      uint32_t qg_stride = 2 * q_dim, kv_stride = kv_dim;
+      if (L.fused_rows) {
+        run_matmul(st, L.wq.format, L.wq.data, L.fused_rows, n, normed, fused, count, 0, split, split_bytes, true);
+        qg = fused, ks = fused + 2 * q_dim, vs = fused + 2 * q_dim + kv_dim;
+        qg_stride = kv_stride = L.fused_rows;
+      } else {
+        run_matmul(st, L.wq.format, L.wq.data, 2 * q_dim, n, normed, q_gate, count, 0, split, split_bytes, true);
+        run_matmul(st, L.wk.format, L.wk.data, kv_dim, n, normed, k, count, 0, split, split_bytes, true);
+        run_matmul(st, L.wv.format, L.wv.data, kv_dim, n, normed, v, count, 0, split, split_bytes, true);
+      }
       // The queries come out of the interleaved query/gate projection.
-      run_norm_rope(st, q_gate, q, false, L.q_norm, n_heads, head_dim, n_rot, 2 * head_dim, pos, nullptr, count,
-                    2 * q_dim, q_dim, rope_theta, norm_eps, 0);
-      run_norm_rope(st, k, cache_slot(k_cache, ci, pos), kv_half, L.k_norm, n_kv_heads, head_dim, n_rot, head_dim, pos,
-                    nullptr, count, kv_dim, kv_dim, rope_theta, norm_eps, 0);
-      if (kv_half)
-        run_convert_half(st, v, cache_slot(v_cache, ci, pos), count * kv_dim, nullptr, 0);
-      else
-        run_copy(st, v, static_cast<float *>(cache_slot(v_cache, ci, pos)), count * kv_dim, nullptr, 0);
+      run_norm_rope(st, qg, q, false, L.q_norm, n_heads, head_dim, n_rot, 2 * head_dim, pos, nullptr, count,
+                    qg_stride, q_dim, rope_theta, norm_eps, 0);
+      run_norm_rope(st, ks, cache_slot(k_cache, ci, pos), kv_half, L.k_norm, n_kv_heads, head_dim, n_rot, head_dim,
+                    pos, nullptr, count, kv_stride, kv_dim, rope_theta, norm_eps, 0);
+      run_copy_rows(st, vs, kv_stride, cache_slot(v_cache, ci, pos), kv_dim, kv_half, kv_dim, count);
       // Attention with the output gate of each head applied in the same launch.
       if (attn_prefill_mfma_supported(n_heads, n_kv_heads, head_dim, kv_half))
         run_attn_prefill_mfma(st, q, cache_layer(k_cache, ci), cache_layer(v_cache, ci), attn, n_heads, n_kv_heads,
                               head_dim, pos, count, q_dim, q_dim, 1.0f / sqrtf((float)head_dim), partials,
-                              partial_floats, q_gate + head_dim, 2 * head_dim, 2 * q_dim);
+                              partial_floats, qg + head_dim, 2 * head_dim, qg_stride);
       else
       for (uint32_t q0 = 0; q0 < count; q0 += kQwenAttnQueryBatch) {
         const uint32_t nq = std::min(kQwenAttnQueryBatch, count - q0);
@@ -219,9 +231,9 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
         ad.counters = counters;
         ad.out = attn + (uint64_t)q0 * q_dim;
         ad.out_stride = q_dim;
-        ad.gate = q_gate + (uint64_t)q0 * 2 * q_dim + head_dim;
+        ad.gate = qg + (uint64_t)q0 * qg_stride + head_dim;
         ad.gate_head_stride = 2 * head_dim;
-        ad.gate_query_stride = 2 * q_dim;
+        ad.gate_query_stride = qg_stride;
         ad.n_heads = n_heads;
         ad.n_kv = n_kv_heads;
         ad.head_dim = head_dim;
@@ -232,15 +244,26 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
       run_matmul(st, L.wo.format, L.wo.data, n, q_dim, attn, hidden, count, 1, split, split_bytes, false, nullptr, defer);
     } else {
       const uint32_t di = L.cache_index;
-      run_matmul(st, L.qkv.format, L.qkv.data, conv_dim, n, normed, proj, count, 0, split, split_bytes, true);
-      run_matmul(st, L.z.format, L.z.data, value_dim, n, normed, z, count, 0, split, split_bytes, true);
-      run_matmul(st, L.beta.format, L.beta.data, n_v, n, normed, beta, count, 0, split, split_bytes, true);
-      run_matmul(st, L.alpha.format, L.alpha.data, n_v, n, normed, alpha, count, 0, split, split_bytes, true);
-      run_gdn_conv(st, proj, L.taps, conv_layer(di), conv_out, conv_dim, conv_kernel, count);
+      // qkv, z, beta and alpha: one GEMM when the matrices lie back to back
+      // (each token's row then qkv | z | beta | alpha).
+      const float *ps = proj, *zs = z, *bs = beta, *as = alpha;
+      uint32_t stride = 0;
+      if (L.fused_rows) {
+        run_matmul(st, L.qkv.format, L.qkv.data, L.fused_rows, n, normed, fused, count, 0, split, split_bytes, true);
+        ps = fused, zs = fused + conv_dim, bs = zs + value_dim, as = bs + n_v;
+        stride = L.fused_rows;
+      } else {
+        run_matmul(st, L.qkv.format, L.qkv.data, conv_dim, n, normed, proj, count, 0, split, split_bytes, true);
+        run_matmul(st, L.z.format, L.z.data, value_dim, n, normed, z, count, 0, split, split_bytes, true);
+        run_matmul(st, L.beta.format, L.beta.data, n_v, n, normed, beta, count, 0, split, split_bytes, true);
+        run_matmul(st, L.alpha.format, L.alpha.data, n_v, n, normed, alpha, count, 0, split, split_bytes, true);
+      }
+      run_gdn_conv(st, ps, L.taps, conv_layer(di), conv_out, conv_dim, conv_kernel, count, stride);
       GdnArgs g{};
       g.y = conv_out;
-      g.beta = beta;
-      g.alpha = alpha;
+      g.beta = bs;
+      g.alpha = as;
+      g.gate_stride = stride;
       g.a = L.a;
       g.dt_bias = L.dt_bias;
       g.state = state_layer(di);
@@ -254,7 +277,7 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
       g.raw_gates = true;
       // Batches of more than one token take the chunked (WY) form.
       if (count == 1 || !chunk_scratch || !run_gdn_chunked(st, g, chunk_scratch)) run_gdn_recurrence(st, g);
-      run_gdn_gated_norm(st, delta_out, L.ssm_norm, z, v_dim, count * n_v, norm_eps);
+      run_gdn_gated_norm(st, delta_out, L.ssm_norm, zs, v_dim, count * n_v, norm_eps, n_v, stride);
       run_matmul(st, L.out.format, L.out.data, n, value_dim, delta_out, hidden, count, 1, split, split_bytes, false,
                  nullptr, defer);
     }
@@ -381,6 +404,18 @@ int bch_qwen35_new(bch_ctx *ctx, const bch_qwen35_model *md, uint32_t n_ctx, int
       return cleanup(rc);
   }
   if (int rc = m->upload(up)) return cleanup(rc);
+  uint32_t fused_widest = 0;
+  for (QwenLayer &L : m->layers) {
+    // Matrices the uploader placed back to back (in the order they were added).
+    auto follows = [&](const DevMatrix &a, const DevMatrix &b) {
+      return a.format == b.format && b.data == a.data + bch_row_bytes(a.format, n) * a.n_rows;
+    };
+    if (L.attention ? follows(L.wq, L.wk) && follows(L.wk, L.wv)
+                    : follows(L.qkv, L.z) && follows(L.z, L.beta) && follows(L.beta, L.alpha))
+      L.fused_rows = L.attention ? L.wq.n_rows + L.wk.n_rows + L.wv.n_rows
+                                 : L.qkv.n_rows + L.z.n_rows + L.beta.n_rows + L.alpha.n_rows;
+    fused_widest = std::max(fused_widest, L.fused_rows);
+  }
   {
     const uint64_t rows = m->batch;
     const uint64_t cache = (uint64_t)m->n_attn * n_ctx * m->kv_dim * (m->kv_half ? 2 : 4);
@@ -396,7 +431,8 @@ int bch_qwen35_new(bch_ctx *ctx, const bch_qwen35_model *md, uint32_t n_ctx, int
            (rc = m->alloc_t((uint64_t)m->n_delta * m->conv_dim * (m->conv_kernel - 1), &m->conv_state)) ||
            (rc = m->alloc_t((uint64_t)m->n_delta * m->n_v * m->k_dim * m->v_dim, &m->delta_state)) ||
            (rc = m->alloc_t(rows * n, &m->hidden)) || (rc = m->alloc_t(rows * n, &m->normed)) ||
-           (rc = m->alloc_t(rows * 2 * m->q_dim + 4, &m->q_gate)) || (rc = m->alloc_t(rows * m->q_dim + 4, &m->q)) ||
+           (rc = m->alloc_t(rows * 2 * m->q_dim + 4, &m->q_gate)) ||
+           (fused_widest && (rc = m->alloc_t(rows * fused_widest, &m->fused))) || (rc = m->alloc_t(rows * m->q_dim + 4, &m->q)) ||
            (rc = m->alloc_t(rows * m->kv_dim + 4, &m->k)) || (rc = m->alloc_t(rows * m->kv_dim + 4, &m->v)) ||
            (rc = m->alloc_t(rows * m->q_dim + 4, &m->attn)) || (rc = m->alloc_t(rows * m->conv_dim + 4, &m->proj)) ||
            (rc = m->alloc_t(rows * m->conv_dim + 4, &m->conv_out)) ||
