@@ -523,6 +523,10 @@ __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W,
     xrow[j] = reinterpret_cast<const u32x4 *>(X.h + (uint64_t)x_index(tok0 + 32 * NB * wave + 32 * j + lane % 32) *
                                                         n_cols + 16 * h);
   static_assert(BT <= NT, "one thread per token scale");
+  // Grouped: a wave whose tokens all lie past its expert's entries (an
+  // expert's last tile is often partly empty) skips its MFMAs; it still
+  // takes its share of the dequantisation.
+  const bool live = __builtin_amdgcn_readfirstlane(tok0 + 32 * NB * wave < tok_end ? 1 : 0) != 0;
   if (tid < BT) us_s[tid] = X.unscale[x_index(tok0 + tid)];
 
   // The lane's inputs of a stage: token block j, k-step s at v[4j + s].
@@ -599,8 +603,9 @@ __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W,
       for (int i = 0; i < MB; i++)
 #pragma unroll
         for (int j = 0; j < NB; j++) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, bq.v[4 * j + s]),
-                                                             wf[s & 1][i], acc[i][j], 0, 0, 0);
+          if (!GROUPED || live)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, bq.v[4 * j + s]),
+                                                               wf[s & 1][i], acc[i][j], 0, 0, 0);
           if constexpr (FMT == 12) {
             const int m = (s * MB + i) * NB + j;  // MFMA index in the stage
             if (m % GAP == GAP - 1 && (DT == NT || dq)) {

@@ -362,11 +362,13 @@ bool run_experts_down(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t
 // Entries v = token·n_used + slot grouped by expert (moe.metal:122-175 is
 // the reference's kernel): offsets[e] is where expert e's entries start in
 // `entries`, in token order, and offsets[n_experts] the total.  One
-// workgroup of 16 waves; wave w takes experts w, w + 16, ...: its lanes test
-// 64 consecutive entries at a time and a ballot prefix places the matches.
-// The entries' experts are first copied to LDS as bytes (up to
-// kGroupLdsEntries entries; larger batches read them from the route), so
-// the scans cost LDS reads rather than dependent global loads.
+// workgroup of 16 waves; wave w takes a contiguous run of the entries.  The
+// entries' experts are first copied to LDS as bytes (up to
+// kGroupLdsEntries entries; larger batches read them from the route).  Each
+// wave counts its run's entries per expert 64 at a time, one ballot per
+// distinct expert among the 64; a prefix over (expert, wave) gives every
+// wave its first slot for each expert; a second pass over the run places
+// the entries, so each expert's entries keep their order.
 constexpr int kGroupWaves = 16;
 constexpr uint32_t kGroupLdsEntries = 16384;
 static_assert(kMoeMaxExperts <= 256, "expert ids fit a byte");
@@ -375,36 +377,80 @@ __global__ __launch_bounds__(kGroupWaves * 64) void k_moe_group(const uint32_t *
                                                                 uint32_t *__restrict__ offsets,
                                                                 uint32_t *__restrict__ entries, uint32_t n_experts,
                                                                 uint32_t n_used, uint32_t n_tokens) {
-  __shared__ uint32_t counts[kMoeMaxExperts];
+  __shared__ uint32_t slot[kGroupWaves][kMoeMaxExperts];  // per (wave, expert): count, then next slot
+  __shared__ uint32_t total[kMoeMaxExperts];
   __shared__ uint8_t ids[kGroupLdsEntries];
   const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64, n_entries = n_used * n_tokens;
   auto route_expert = [&](uint32_t v) { return route[2ull * n_used * (v / n_used) + v % n_used]; };
   const bool staged = n_entries <= kGroupLdsEntries;
   if (staged)
     for (uint32_t v = threadIdx.x; v < n_entries; v += kGroupWaves * 64) ids[v] = (uint8_t)route_expert(v);
+  for (uint32_t e = lane; e < n_experts; e += 64) slot[wave][e] = 0;
   __syncthreads();
   auto expert_of = [&](uint32_t v) -> uint32_t { return staged ? ids[v] : route_expert(v); };
-  for (uint32_t e = wave; e < n_experts; e += kGroupWaves) {
-    uint32_t c = 0;
-    for (uint32_t v = lane; v < n_entries; v += 64) c += expert_of(v) == e;
-    for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
-    if (lane == 0) counts[e] = c;
+  const uint32_t per = (n_entries + kGroupWaves * 64 - 1) / (kGroupWaves * 64) * 64;  // entries per wave
+  const uint32_t v0 = min(wave * per, n_entries), v1 = min(v0 + per, n_entries);
+  const uint64_t below = (1ull << lane) - 1;
+  // For each distinct expert le among this slice's lanes (those with v < v1),
+  // in order of the lowest lane holding it: fn(le, ballot of its lanes).
+  auto distinct = [&](uint32_t e, bool valid, auto fn) {
+    uint64_t todo = __ballot(valid);
+    while (todo) {
+      const uint32_t leader = (uint32_t)__ffsll((unsigned long long)todo) - 1;
+      const uint32_t le = __shfl(e, leader, 64);
+      const uint64_t mask = __ballot(valid && e == le);
+      fn(le, mask);
+      todo &= ~mask;
+    }
+  };
+  for (uint32_t first = v0; first < v1; first += 64) {
+    const uint32_t v = first + lane;
+    const bool valid = v < v1;
+    const uint32_t e = valid ? expert_of(v) : 0;
+    distinct(e, valid, [&](uint32_t le, uint64_t mask) {
+      if (lane == 0) slot[wave][le] += (uint32_t)__popcll(mask);
+    });
   }
   __syncthreads();
-  for (uint32_t e = wave; e < n_experts; e += kGroupWaves) {
+  // Expert totals, their exclusive prefix (offsets), then each wave's first
+  // slot per expert.
+  for (uint32_t e = threadIdx.x; e < n_experts; e += kGroupWaves * 64) {
+    uint32_t t = 0;
+    for (int w = 0; w < kGroupWaves; w++) t += slot[w][e];
+    total[e] = t;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
     uint32_t start = 0;
-    for (uint32_t b = 0; b < e; b++) start += counts[b];
-    if (lane == 0) {
+    for (uint32_t e = 0; e < n_experts; e++) {
+      const uint32_t t = total[e];
+      total[e] = start;
       offsets[e] = start;
-      if (e == n_experts - 1) offsets[n_experts] = start + counts[e];
+      start += t;
     }
-    for (uint32_t first = 0; first < n_entries; first += 64) {
-      const uint32_t v = first + lane;
-      const bool match = v < n_entries && expert_of(v) == e;
-      const uint64_t mask = __ballot(match);
-      if (match) entries[start + __popcll(mask & ((1ull << lane) - 1))] = v;
-      start += __popcll(mask);
+    offsets[n_experts] = start;
+  }
+  __syncthreads();
+  for (uint32_t e = threadIdx.x; e < n_experts; e += kGroupWaves * 64) {
+    uint32_t start = total[e];
+    for (int w = 0; w < kGroupWaves; w++) {
+      const uint32_t c = slot[w][e];
+      slot[w][e] = start;
+      start += c;
     }
+  }
+  __syncthreads();
+  for (uint32_t first = v0; first < v1; first += 64) {
+    const uint32_t v = first + lane;
+    const bool valid = v < v1;
+    const uint32_t e = valid ? expert_of(v) : 0;
+    distinct(e, valid, [&](uint32_t le, uint64_t mask) {
+      const uint32_t base = slot[wave][le];
+      if (valid && e == le) entries[base + (uint32_t)__popcll(mask & below)] = v;
+      __builtin_amdgcn_wave_barrier();
+      if (lane == 0) slot[wave][le] = base + (uint32_t)__popcll(mask);
+      __builtin_amdgcn_wave_barrier();
+    });
   }
 }
 
