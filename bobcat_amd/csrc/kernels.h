@@ -89,10 +89,12 @@ constexpr uint32_t kMoeMaxUsed = 8;       // MOE_MAX_USED
 // Batched experts (prefill): grouping, grouped GEMM, weighted combine.
 void run_moe_group(hipStream_t s, const uint32_t *route, uint32_t *offsets, uint32_t *entries, uint32_t n_experts,
                    uint32_t n_used, uint32_t n_tokens);
+// split_ready (shared_input only): `split` already holds x's fp16 inputs
+// (run_rms_norm_split wrote them), so they are not converted again.
 void run_matmul_experts(hipStream_t s, uint32_t format, const uint8_t *W, const uint8_t *up, uint32_t n_rows,
                         uint32_t n_cols, uint32_t n_experts, const float *x, bool shared_input,
                         const uint32_t *offsets, const uint32_t *entries, uint32_t n_used, float *y,
-                        uint32_t n_tokens, void *split);
+                        uint32_t n_tokens, void *split, bool split_ready = false);
 void run_moe_combine(hipStream_t s, const float *x, const uint32_t *route, float *y, uint32_t n_embd,
                      uint32_t n_used, uint32_t n_tokens);
 // With `scores` (n_tokens · n_experts floats of scratch) and `counters`

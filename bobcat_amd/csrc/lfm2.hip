@@ -230,12 +230,11 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
   if (trace) run_copy(s, m->hidden, m->trace, count * n, nullptr, 0);
   // A column-split sum into the residual stream (out_proj, wo, down) is left
   // to the norm that reads the residual next, unless something else reads
-  // it first (the trace copy, the MoE norm, the diagnostics checks).
+  // it first (the trace copy, the diagnostics checks).
   PendingSum pend;
   PendingSum *const defer = trace || check_mode() ? nullptr : &pend;
   for (uint32_t il = 0; il < m->n_layers; il++) {
     const Layer &L = m->layers[il];
-    PendingSum *const defer_ffn = L.moe ? nullptr : defer;
     // The norm also writes the fp16 inputs of the projection that follows.
     run_rms_norm_split(s, m->hidden, L.attn_norm, m->normed, n, count, m->norm_eps, m->split, &pend);
     check_finite(s, "attn_norm", il, m->normed, (uint64_t)count * n);
@@ -249,7 +248,7 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
       if (!split) run_short_conv_batch(s, m->bcx, L.taps, hist, m->conv_out, n, m->conv_kernel, count);
       check_finite(s, "short_conv", il, m->conv_out, (uint64_t)count * n);
       run_matmul(s, L.out_proj.format, L.out_proj.data, n, n, m->conv_out, m->hidden, count, 1, m->split, m->split_bytes,
-                 split, nullptr, defer_ffn);
+                 split, nullptr, defer);
       check_finite(s, "out_proj", il, m->hidden, (uint64_t)count * n);
     } else {
       const uint32_t ci = L.cache_index;
@@ -302,13 +301,11 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
       }
       check_finite(s, "attention", il, m->attn, (uint64_t)count * m->q_dim);
       run_matmul(s, L.wo.format, L.wo.data, n, m->q_dim, m->attn, m->hidden, count, 1, m->split, m->split_bytes, false,
-                 nullptr, defer_ffn);
+                 nullptr, defer);
       check_finite(s, "attn_output", il, m->hidden, (uint64_t)count * n);
     }
-    if (L.moe)
-      run_rms_norm(s, m->hidden, L.ffn_norm, m->normed, n, count, m->norm_eps);
-    else
-      run_rms_norm_split(s, m->hidden, L.ffn_norm, m->normed, n, count, m->norm_eps, m->split, &pend);
+    // (The MoE experts' shared input is this norm's output too.)
+    run_rms_norm_split(s, m->hidden, L.ffn_norm, m->normed, n, count, m->norm_eps, m->split, &pend);
     check_finite(s, "ffn_norm", il, m->normed, (uint64_t)count * n);
     if (L.moe) {
       // Route the whole batch in one launch, then each token's experts.
@@ -322,7 +319,7 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
         run_moe_group(s, m->route, m->moe_offsets, m->moe_entries, m->n_experts, m->n_used, count);
         run_matmul_experts(s, L.gate_exps.format, L.gate_exps.data, L.up_exps.data, m->n_ff_expert, n,
                            m->n_experts, m->normed, true, m->moe_offsets, m->moe_entries, m->n_used, m->expert_ffn,
-                           count, m->split);
+                           count, m->split, true);
         run_matmul_experts(s, L.down_exps.format, L.down_exps.data, nullptr, n, m->n_ff_expert, m->n_experts,
                            m->expert_ffn, false, m->moe_offsets, m->moe_entries, m->n_used, m->expert_out, count,
                            m->split);

@@ -846,13 +846,13 @@ static bool matmul_format(uint32_t f) {
 void run_matmul_experts(hipStream_t s, uint32_t format, const uint8_t *W, const uint8_t *up, uint32_t n_rows,
                         uint32_t n_cols, uint32_t n_experts, const float *xf, bool shared_input,
                         const uint32_t *offsets, const uint32_t *entries, uint32_t n_used, float *y,
-                        uint32_t n_tokens, void *split) {
+                        uint32_t n_tokens, void *split, bool split_ready) {
   if (!n_tokens) return;
   const uint64_t rb = bch_row_bytes(format, n_cols);
   const uint32_t input_rows = shared_input ? n_tokens : n_used * n_tokens;
   _Float16 *hx = static_cast<_Float16 *>(split);
   float *unscale = reinterpret_cast<float *>(hx + (uint64_t)input_rows * n_cols);
-  split_hi(s, xf, input_rows, n_cols, hx, unscale);
+  if (!(split_ready && shared_input)) split_hi(s, xf, input_rows, n_cols, hx, unscale);
   const HiInputs x{hx, unscale};
   const ExpertGroups g{offsets, entries, n_experts, shared_input ? n_used : 1u};
   // 128 x 128 tiles (4 waves): an expert's tokens are few.  With `up` the
