@@ -707,9 +707,12 @@ static void gemm_launch(hipStream_t s, const uint8_t *W, const uint8_t *W2, uint
   const uint32_t total = div_ceil(n_rows, out_rows) * div_ceil(n_tokens, 32 * NB * NW) * splits;
   const dim3 grid(8 * div_ceil(total, 8));
   const dim3 block(64 * NW);
-  if (store == 3)
-    k_gemm<FMT, 3, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, 1, ExpertGroups{});
-  else if (splits > 1 || store == 0)
+  if (store == 3) {
+    // (Paired tiles hold whole 32-row blocks of both matrices.)
+    if constexpr (RB % 64 == 0)
+      k_gemm<FMT, 3, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, 1,
+                                                        ExpertGroups{});
+  } else if (splits > 1 || store == 0)
     k_gemm<FMT, 0, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, splits, ExpertGroups{});
   else if (store == 1)
     k_gemm<FMT, 1, RB, NW, NB><<<grid, block, 0, s>>>(W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, splits, ExpertGroups{});
@@ -740,7 +743,8 @@ static void gemm_launch(hipStream_t s, const uint8_t *W, const uint8_t *W2, uint
 // while the workgroups fit the CUs — 2048 x 2048 with 2 (23 us), 512 x 2048
 // with 4 (14 us).  Partials must fit `part_floats`.
 struct GemmShape {
-  uint32_t cfg, splits;  // cfg 0: 128 rows x 256 tokens, 8 waves; 1: 128 x 128, 4 waves; 2: 64 x 128, 4 waves
+  // cfg 0: 128 rows x 256 tokens, 8 waves; 1: 128 x 128, 4 waves; 2: 64 x 128, 4 waves; 3: 96 x 128, 4 waves
+  uint32_t cfg, splits;
 };
 
 static GemmShape gemm_shape(uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens, uint64_t part_floats, uint32_t cus) {
@@ -756,7 +760,13 @@ static GemmShape gemm_shape(uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens,
     while (tiles(128, 256) * splits < cus && fits(2 * splits)) splits *= 2;
     return {0, splits};
   }
-  if (n_rows > 64 && tiles(128, 128) >= enough) return {1, 1};
+  if (n_rows > 64 && tiles(128, 128) >= enough) {
+    // 96-row tiles when they cover the CUs in fewer rounds of less work
+    // (6144 x 2048 at 512 tokens: 256 workgroups instead of 192).
+    auto rounds = [&](uint32_t br) { return (tiles(br, 128) + cus - 1) / cus; };
+    if (rounds(96) * 96 < rounds(128) * 128) return {3, 1};
+    return {1, 1};
+  }
   uint32_t splits = 1;
   while (tiles(64, 128) * splits * 2 <= cus && fits(2 * splits)) splits *= 2;
   return {2, splits};
@@ -774,7 +784,7 @@ static void gemm_fmt(hipStream_t s, const uint8_t *W, const uint8_t *W2, uint64_
     // tokens a 10752-row pair is 224 tiles of 96 rows (one round) instead
     // of 336 of 64 (two rounds, 80 CUs running a second tile).
     g.splits = 1;
-    if (g.cfg == 2) g.cfg = 1;
+    if (g.cfg == 2 || g.cfg == 3) g.cfg = 1;
     const uint64_t tt = div_ceil(n_tokens, 256), c = cus ? cus : 256;
     auto rounds = [&](uint32_t out_rows) { return (div_ceil(n_rows, out_rows) * tt + c - 1) / c; };
     if (g.cfg == 0 && rounds(96) * 192 < rounds(64) * 128) {
@@ -784,7 +794,9 @@ static void gemm_fmt(hipStream_t s, const uint8_t *W, const uint8_t *W2, uint64_
       return;
     }
   }
-  if (g.cfg == 0)
+  if (g.cfg == 3 && store != 3)
+    gemm_launch<FMT, 96, 4, 1>(s, W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits, defer);
+  else if (g.cfg == 0)
     gemm_launch<FMT, 128, 8, 1>(s, W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits, defer);
   else if (g.cfg == 1)
     gemm_launch<FMT, 128, 4, 1>(s, W, W2, rb, x, y, part, n_rows, n_cols, n_tokens, store, g.splits, defer);

@@ -269,12 +269,13 @@ def test_matmul_other_formats(hip, fmt):
 
 
 @pytest.mark.parametrize("n_rows,n_cols,n_tokens", [(2048, 10752, 300), (10752, 2048, 512), (512, 2048, 512),
-                                                    (6144, 2048, 200), (64, 512, 129)])
+                                                    (6144, 2048, 200), (6144, 2048, 512), (64, 512, 129)])
 @pytest.mark.parametrize("store", [Store.OVERWRITE, Store.ACCUMULATE, Store.SWIGLU])
 def test_matmul_tiles_and_splits(hip, n_rows, n_cols, n_tokens, store):
     """Config-scale shapes through every tile choice (256- and 128-token
-    tiles, 128- and 64-row tiles) and column split (up to 8 splits, added
-    by the reduction), against the product of the half-rounded operands."""
+    tiles, 128-, 96- and 64-row tiles) and column split (up to 8 splits,
+    added by the reduction), against the product of the half-rounded
+    operands."""
     rng = np.random.default_rng(n_rows + n_tokens)
     w = q4k_matrix(rng, n_rows, n_cols)
     x = rng.standard_normal((n_tokens, n_cols)).astype(np.float32)
