@@ -258,32 +258,38 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_prep(GdnArgs a, float *__rest
   float *Wg = base, *Ug = Wg + C * KD, *Qg = Ug + (uint64_t)C * vd, *Kt = Qg + C * KD, *Pg = Kt + C * KD;
   float *gC = Pg + C * C;
   // The l2-normalised query (times q_scale) and key of each token
-  // (qwen35.rs:464-470); rows past the chunk's end are zero.
-  for (uint32_t j = wave; j < (uint32_t)C; j += 4) {
-    float q[R], k[R], sq = 0.f, sk = 0.f;
-    if (j < L) {
-      const float *tok = a.y + (uint64_t)(t0 + j) * conv_dim;
+  // (qwen35.rs:464-470); rows past the chunk's end are zero.  Wave w takes
+  // tokens w, w+4, ..., all of their loads issued before any is used.
+  {
+    constexpr int TW = C / 4;  // tokens per wave
+    float q[TW][R], k[TW][R];
+#pragma unroll
+    for (int jj = 0; jj < TW; jj++) {
+      const uint32_t j = wave + 4 * jj;
+      const float *tok = a.y + (uint64_t)(t0 + min(j, L - 1)) * conv_dim;
 #pragma unroll
       for (int i = 0; i < R; i++) {
-        q[i] = tok[key_head * KD + lane * R + i];
-        k[i] = tok[key_dim + key_head * KD + lane * R + i];
+        q[jj][i] = j < L ? tok[key_head * KD + lane * R + i] : 0.f;
+        k[jj][i] = j < L ? tok[key_dim + key_head * KD + lane * R + i] : 0.f;
       }
-#pragma unroll
-      for (int i = 0; i < R; i++) {
-        sq = fmaf(q[i], q[i], sq);
-        sk = fmaf(k[i], k[i], sk);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < R; i++) q[i] = k[i] = 0.f;
     }
-    sq = wave_sum(sq);
-    sk = wave_sum(sk);
-    const float fq = a.q_scale / sqrtf(sq + 1e-6f), fk = 1.0f / sqrtf(sk + 1e-6f);
 #pragma unroll
-    for (int i = 0; i < R; i++) {
-      qs[j][lane * R + i] = q[i] * fq;
-      ks[j][lane * R + i] = k[i] * fk;
+    for (int jj = 0; jj < TW; jj++) {
+      const uint32_t j = wave + 4 * jj;
+      float sq = 0.f, sk = 0.f;
+#pragma unroll
+      for (int i = 0; i < R; i++) {
+        sq = fmaf(q[jj][i], q[jj][i], sq);
+        sk = fmaf(k[jj][i], k[jj][i], sk);
+      }
+      sq = wave_sum(sq);
+      sk = wave_sum(sk);
+      const float fq = a.q_scale / sqrtf(sq + 1e-6f), fk = 1.0f / sqrtf(sk + 1e-6f);
+#pragma unroll
+      for (int i = 0; i < R; i++) {
+        qs[j][lane * R + i] = q[jj][i] * fq;
+        ks[j][lane * R + i] = k[jj][i] * fk;
+      }
     }
   }
   // Gates: beta, and the running sum of the log-decays in float64.
