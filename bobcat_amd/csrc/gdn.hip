@@ -246,7 +246,8 @@ __host__ __device__ constexpr uint64_t gdn_chunk_floats(uint32_t kd, uint32_t vd
 template <int KD>
 __global__ __launch_bounds__(256) void k_gdn_chunk_prep(GdnArgs a, float *__restrict__ scratch, uint32_t n_chunks) {
   constexpr int C = kGdnC, KP = KD + 1, R = KD / 64;
-  __shared__ float qs[C][KP], ks[C][KP], am[C][C + 1];
+  __shared__ float qs[C][KP], ks[C][KP];
+  __shared__ __align__(16) float amT[C][C + 4];  // A transposed: amT[u][t] = A[t][u]
   __shared__ float bs[C], wgam[C];
   __shared__ double lg[C];
   const uint32_t tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
@@ -340,7 +341,7 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_prep(GdnArgs a, float *__rest
       for (int j = 0; j < 4; j++) {
         const uint32_t t = 4 * ti + i, u = 4 * si + j;
         const float dec = (u <= t && t < L) ? expf((float)(lg[t] - lg[u])) : 0.f;
-        am[t][u] = u < t ? bs[t] * dec * kk[i][j] : 0.f;
+        amT[u][t] = u < t ? bs[t] * dec * kk[i][j] : 0.f;
         Pg[t * C + u] = dec * qk[i][j];
       }
   }
@@ -366,12 +367,21 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_prep(GdnArgs a, float *__rest
 #pragma unroll
       for (int t = 0; t < C; t++) x[t] = (uint32_t)t < L ? bs[t] * v[(uint64_t)t * conv_dim] : 0.f;
     }
+    // Column by column: once x_u is final it enters every later row, so
+    // each step has up to 63 independent FMAs (a row-by-row loop waits on
+    // one dependent chain of 2016).  Every row still adds its terms in
+    // order u = 0, 1, ..., as the row-by-row form does.
 #pragma unroll
-    for (int t = 1; t < C; t++) {
-      float acc = x[t];
+    for (int u = 0; u < C - 1; u++) {
+      // Rows u+1 .. C-1 of column u, four per 16-byte LDS read.
 #pragma unroll
-      for (int u = 0; u < t; u++) acc = fmaf(-am[t][u], x[u], acc);
-      x[t] = acc;
+      for (int t4 = (u + 1) / 4; t4 < C / 4; t4++) {
+        const float4 a4 = *reinterpret_cast<const float4 *>(&amT[u][4 * t4]);
+        const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (4 * t4 + i > u) x[4 * t4 + i] = fmaf(-av[i], x[u], x[4 * t4 + i]);
+      }
     }
     if (col < KD) {
 #pragma unroll
