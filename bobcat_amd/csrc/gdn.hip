@@ -258,6 +258,16 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_prep(GdnArgs a, float *__rest
   float *base = scratch + ((uint64_t)head * n_chunks + chunk) * gdn_chunk_floats(KD, vd);
   float *Wg = base, *Ug = Wg + C * KD, *Qg = Ug + (uint64_t)C * vd, *Kt = Qg + C * KD, *Pg = Kt + C * KD;
   float *gC = Pg + C * C;
+  // The value column this thread solves first (column tid of [W | U] when it
+  // is a U column), loaded before anything else: nothing before the forward
+  // substitution depends on it.
+  const bool pre_u = tid >= (uint32_t)KD && tid < KD + vd;
+  float vpre[C];
+  {
+    const float *v = a.y + (uint64_t)t0 * conv_dim + 2 * key_dim + head * vd + (pre_u ? tid - KD : 0);
+#pragma unroll
+    for (int t = 0; t < C; t++) vpre[t] = pre_u && (uint32_t)t < L ? v[(uint64_t)t * conv_dim] : 0.f;
+  }
   // The l2-normalised query (times q_scale) and key of each token
   // (qwen35.rs:464-470); rows past the chunk's end are zero.  Wave w takes
   // tokens w, w+4, ..., all of their loads issued before any is used.
@@ -362,6 +372,9 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_prep(GdnArgs a, float *__rest
     if (col < KD) {
 #pragma unroll
       for (int t = 0; t < C; t++) x[t] = wgam[t] * ks[t][col];
+    } else if (col == tid) {
+#pragma unroll
+      for (int t = 0; t < C; t++) x[t] = (uint32_t)t < L ? bs[t] * vpre[t] : 0.f;
     } else {
       const float *v = a.y + (uint64_t)t0 * conv_dim + 2 * key_dim + head * vd + (col - KD);
 #pragma unroll
