@@ -412,7 +412,8 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_scan(GdnArgs a, const float *
   constexpr int C = kGdnC, KP = KD + 4;
   static_assert(NC == 8, "the thread layout below assumes 8 columns");
   __shared__ __align__(16) float w_s[C][KP], q_s[C][KP], k_s[C][KP];
-  __shared__ float p_s[C][C + 1], s_s[KD][NC], d_s[C][NC];
+  __shared__ float p_s[C][C + 1];
+  __shared__ __align__(16) float s_s[KD][NC], d_s[C][NC];
   const uint32_t tid = threadIdx.x, vd = a.v_dim;
   // Blocks are numbered so that the column blocks of one head run on one
   // XCD (workgroup i goes to XCD i % 8) and share its L2.
@@ -448,27 +449,38 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_scan(GdnArgs a, const float *
     for (uint32_t e = tid; e < (uint32_t)(C * C); e += 256) p_s[e / C][e % C] = Pg[e];
     const float u0 = Ug[(uint64_t)dt * vd + col0 + dc], u1 = Ug[(uint64_t)dt * vd + col0 + dc + 1];
     __syncthreads();
-    // D = U - W S0.
+    // D = U - W S0 (16- and 8-byte LDS reads; r ascending as before).
     float d0 = u0, d1 = u1;
-    for (int r = 0; r < KD; r++) {
-      const float w = w_s[dt][r];
-      d0 = fmaf(-w, s_s[r][dc], d0);
-      d1 = fmaf(-w, s_s[r][dc + 1], d1);
+    for (int r = 0; r < KD; r += 4) {
+      const float4 w4 = *reinterpret_cast<const float4 *>(&w_s[dt][r]);
+      const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float2 s2 = *reinterpret_cast<const float2 *>(&s_s[r + i][dc]);
+        d0 = fmaf(-wv[i], s2.x, d0);
+        d1 = fmaf(-wv[i], s2.y, d1);
+      }
     }
     d_s[dt][dc] = d0;
     d_s[dt][dc + 1] = d1;
     __syncthreads();
     // O = diag(gamma) Q S0 + P D.
     float o0 = 0.f, o1 = 0.f;
-    for (int r = 0; r < KD; r++) {
-      const float q = q_s[dt][r];
-      o0 = fmaf(q, s_s[r][dc], o0);
-      o1 = fmaf(q, s_s[r][dc + 1], o1);
+    for (int r = 0; r < KD; r += 4) {
+      const float4 q4 = *reinterpret_cast<const float4 *>(&q_s[dt][r]);
+      const float qv[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float2 s2 = *reinterpret_cast<const float2 *>(&s_s[r + i][dc]);
+        o0 = fmaf(qv[i], s2.x, o0);
+        o1 = fmaf(qv[i], s2.y, o1);
+      }
     }
     for (uint32_t u = 0; u <= dt; u++) {
       const float pv = p_s[dt][u];
-      o0 = fmaf(pv, d_s[u][dc], o0);
-      o1 = fmaf(pv, d_s[u][dc + 1], o1);
+      const float2 d2 = *reinterpret_cast<const float2 *>(&d_s[u][dc]);
+      o0 = fmaf(pv, d2.x, o0);
+      o1 = fmaf(pv, d2.y, o1);
     }
     if (dt < L) {
       float *orow = a.out + (uint64_t)(t0 + dt) * a.n_v * vd + head * vd + col0;
@@ -482,8 +494,11 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_scan(GdnArgs a, const float *
       for (int j = 0; j < 4; j++) acc[j] = gC * srow[j];
       for (int u = 0; u < C; u++) {
         const float kv = k_s[u][sr];
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[j] = fmaf(kv, d_s[u][sc + j], acc[j]);
+        const float4 d4 = *reinterpret_cast<const float4 *>(&d_s[u][sc]);
+        acc[0] = fmaf(kv, d4.x, acc[0]);
+        acc[1] = fmaf(kv, d4.y, acc[1]);
+        acc[2] = fmaf(kv, d4.z, acc[2]);
+        acc[3] = fmaf(kv, d4.w, acc[3]);
       }
 #pragma unroll
       for (int j = 0; j < 4; j++) srow[j] = acc[j];
