@@ -208,7 +208,7 @@ int bch_attention(bch_ctx *ctx, bch_view q, bch_view k_cache, bch_view v_cache, 
                   uint32_t head_dim, uint32_t first_pos, uint32_t n_queries, uint32_t n_ctx);
 /* MI355X addition (no counterpart in the reference): the prefill form of
  * Metal::attention (backend.rs:2150-2320, attention_flash attention.metal:
- * 289-480) on MFMA, for an f16 cache, head_dim 64 or 128 and at most 4 query
+ * 289-480) on MFMA, for an f16 cache, head_dim 64, 128 or 256 and at most 4 query
  * heads per KV head (else BCH_ERR_ATTENTION_LIMITS).  Queries and
  * probabilities enter the products as f16 high + low parts (~22 bits), so
  * results agree with bch_attention to ~1e-6 of the outputs' scale, not
