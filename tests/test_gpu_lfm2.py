@@ -204,9 +204,9 @@ def test_long_context_decode(hip, kv_half):
 
 def test_long_context_prefill_key_splits(hip):
     """A 40-token prefill after 2,900 cached positions (f16 cache, n_ctx 8192)
-    splits the keys of the MFMA prefill attention in two, each split's
-    partials combined afterwards; its logits and the next steps against the
-    oracle."""
+    splits the keys of the MFMA prefill attention over several workgroups,
+    each split's partials combined afterwards; its logits and the next steps
+    against the oracle."""
     w = Lfm2Weights(LFM2_TINY_F16, seed=14)
     toks = prompt(LFM2_TINY_F16, 2944, seed=15)
     gpu = Lfm2Hip(hip, w, n_ctx=8192, kv_half=True)
