@@ -119,7 +119,8 @@ struct ExpertSwigluItems {
 // [channel][k-1], the oldest first), rows [r0, r0+r1) the output gate z,
 // then r2 rows of beta and r2 of alpha (raw; the recurrence gates them).
 struct GdnInItems {
-  static constexpr bool kPre = false;
+  // A q/k/v channel's taps and history are read with the batch's weights.
+  static constexpr bool kPre = true;
   static constexpr int kRows = 1;
   static constexpr bool kArgmax = false;
   const uint8_t *Wqkv, *Wz, *Wb, *Wa;
@@ -134,6 +135,48 @@ struct GdnInItems {
     if (item < r0 + r1) return Wz + (uint64_t)(item - r0) * rb;
     if (item < r0 + r1 + r2) return Wb + (uint64_t)(item - r0 - r1) * rb;
     return Wa + (uint64_t)(item - r0 - r1 - r2) * rb;
+  }
+  struct Pre {
+    float t[kGdnMaxKernel], h[kGdnMaxKernel - 1];
+  };
+  __device__ Pre preload(uint32_t item) const {
+    Pre pre{};
+    if (item < r0) {
+      const uint32_t past = ksize - 1;
+#pragma unroll
+      for (int k = 0; k < (int)kGdnMaxKernel; k++) pre.t[k] = (uint32_t)k < ksize ? taps[(uint64_t)item * ksize + k] : 0.f;
+#pragma unroll
+      for (int k = 0; k < (int)kGdnMaxKernel - 1; k++) pre.h[k] = (uint32_t)k < past ? hist[(uint64_t)item * past + k] : 0.f;
+    }
+    return pre;
+  }
+  // store() with the preloaded taps and history: the same operations in the
+  // same order.
+  __device__ void store_pre(uint32_t item, const float *v, float scale, const Pre &pre) const {
+    const float y = v[0] * scale;
+    if (item < r0) {
+      const uint32_t past = ksize - 1;
+      float *h = hist + (uint64_t)item * past;
+      float last = 0.f;
+#pragma unroll
+      for (int k = 0; k < (int)kGdnMaxKernel; k++)
+        if ((uint32_t)k == past) last = pre.t[k];
+      float sum = last * y;
+#pragma unroll
+      for (int j = 0; j < (int)kGdnMaxKernel - 1; j++)
+        if ((uint32_t)j < past) sum += pre.t[j] * pre.h[j];
+      conv_out[item] = silu_g(sum);
+#pragma unroll
+      for (int j = 0; j < (int)kGdnMaxKernel - 2; j++)
+        if ((uint32_t)j + 1 < past) h[j] = pre.h[j + 1];
+      h[past - 1] = y;
+    } else if (item < r0 + r1) {
+      z[item - r0] = y;
+    } else if (item < r0 + r1 + r2) {
+      beta[item - r0 - r1] = y;
+    } else {
+      alpha[item - r0 - r1 - r2] = y;
+    }
   }
   __device__ void store(uint32_t item, const float *v, float scale) const {
     const float y = v[0] * scale;
