@@ -134,6 +134,16 @@ __device__ __forceinline__ uint32_t q4k_pair_scales(uint32_t h1, uint32_t h2, ui
   return p < 2 ? low : high;
 }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also waits for
+// every outstanding global load of the wave (s_waitcnt vmcnt(0)), which
+// would hold a kernel that has its weight loads in flight until all of them
+// have arrived; this barrier lets those loads keep streaming.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Device-scope relaxed accesses for data one workgroup hands to another on
 // any XCD (they go past the non-coherent L2 of the writer's XCD).
 template <class T>

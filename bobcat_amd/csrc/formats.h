@@ -518,16 +518,21 @@ struct Q5K {
 
 // --- Q4_K with integer activations --------------------------------------
 //
-// The decode GEMV's Q4_K path.  The staged input is turned, once per
-// workgroup, into exact integers per 32-element block: with E the exponent
-// of the block's largest |x| (|x| < 2^E), x_int = rint(x · 2^(21−E)) (22
-// bits, error ≤ 2^(E−22), below the rounding of the block's largest
-// element), split into three signed bytes x_int = d0 + 2^8·d1 + 2^16·d2
-// (d0, d1 in [−128, 127], d2 in [−32, 32]).  Then Σ q·x_int over a block is
-// three v_dot4_i32_i8 per four nibbles on the raw nibble bytes, exact in
-// int32 (|Σ| ≤ 32·15·2^21 < 2^31), instead of a conversion and an FMA per
-// weight; the block's scale 2^(E−21) is folded into the (d·sc) multiply.
-// The minimum term uses the block sums of the unquantised inputs.
+// The decode GEMV's Q4_K path.  The staged input is quantised, once per
+// workgroup, to 22-bit fixed point per 32-element block: with E the exponent
+// of the block's largest |x| (|x| < 2^E), x_int = rint(x · 2^(21−E)), so
+// every input carries an absolute error of at most 2^(E−22) — eight times
+// the half-ulp 2^(E−25) of the block's largest element, and an element 2^-k
+// times that largest one keeps about 22−k significant bits (the reference
+// multiplies the f32 inputs themselves, quant.metal:364-386).  The error of a
+// row is thus at most Σ_blocks Σ|w|·2^(E_b−22), far inside the reference's
+// bound of 1e-5 of the row's Σ|w·x| (metal_matvec.rs:16-19).  x_int splits
+// into three signed bytes x_int = d0 + 2^8·d1 + 2^16·d2 (d0, d1 in
+// [−128, 127], d2 in [−32, 32]).  Then Σ q·x_int over a block is three
+// v_dot4_i32_i8 per four nibbles on the raw nibble bytes, exact in int32
+// (|Σ| ≤ 32·15·2^21 < 2^31), instead of a conversion and an FMA per weight;
+// the block's scale 2^(E−21) is folded into the (d·sc) multiply.  The
+// minimum term uses the block sums of the unquantised inputs.
 constexpr uint32_t kDigitUnitBytes = 208;  // 3 planes × 2 blocks × 32 bytes, then xs[2], sum[2]
 
 struct Q4K8 {
@@ -641,7 +646,7 @@ __device__ __forceinline__ void digitize_units(float *xs, uint32_t n_units) {
 #pragma unroll
     for (int dg = 0; dg < 3; dg++) planes[i][dg][0] = pk[dg][0], planes[i][dg][1] = pk[dg][1];
   }
-  __syncthreads();
+  lds_barrier();
 #pragma unroll
   for (int i = 0; i < kMaxChunks; i++) {
     const uint32_t c = tid + (uint32_t)i * T;

@@ -540,28 +540,44 @@ static void launch_gemv(hipStream_t s, const P &p, const float *x, const float *
 template <class F>
 constexpr bool kFewBatches = F::kFormat == 8 || F::kFormat == 2 || F::kFormat == 14 || F::kFormat == 13;
 
+// The largest items per group rpg_for picks for a policy.
+template <class P>
+constexpr int kMaxRpg = P::kRows == 1 ? (P::kArgmax ? 2 : 4) : P::kRows == 2 ? 2 : 1;
+
 template <class F, int LPR, bool NORM, class P>
 static void gemv_rpg(hipStream_t s, int rpg, const P &p, const float *x, const float *nw, float eps,
                      uint32_t n_items, uint32_t n_units, uint32_t n_cols) {
-  if constexpr (kFewBatches<F>) {
-    if (rpg >= 2)
-      launch_gemv<F, LPR, 2, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols);
-    else
-      launch_gemv<F, LPR, 1, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols);
-    return;
-  } else {
-    switch (rpg) {
-      case 8: launch_gemv<F, LPR, 8, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols); break;
-      case 4: launch_gemv<F, LPR, 4, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols); break;
-      case 2: launch_gemv<F, LPR, 2, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols); break;
-      default: launch_gemv<F, LPR, 1, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols); break;
-    }
+  constexpr int kMax = kFewBatches<F> ? std::min(2, kMaxRpg<P>) : kMaxRpg<P>;
+  if constexpr (kMax >= 4) {
+    if (rpg >= 4) return launch_gemv<F, LPR, 4, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols);
   }
+  if constexpr (kMax >= 2) {
+    if (rpg >= 2) return launch_gemv<F, LPR, 2, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols);
+  }
+  launch_gemv<F, LPR, 1, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols);
 }
+
+// Which norm modes a policy is built for: the drivers always fuse the RMS
+// norm into SwiGLU, the conv and DeltaNet input projections, q/k/v and the
+// logits, and never into the experts' rows; other calls take the per-unit
+// kernel of matvec.hip.
+template <class P>
+inline constexpr bool kNormBuilt = true;
+template <class P>
+inline constexpr bool kPlainBuilt = true;
+template <> inline constexpr bool kPlainBuilt<SwigluItems> = false;
+template <> inline constexpr bool kPlainBuilt<ConvItems> = false;
+template <> inline constexpr bool kPlainBuilt<GdnInItems> = false;
+template <> inline constexpr bool kPlainBuilt<ThreeItems> = false;
+template <> inline constexpr bool kPlainBuilt<ArgmaxItems> = false;
+template <> inline constexpr bool kNormBuilt<ExpertSwigluItems> = false;
 
 template <class F, bool NORM, class P>
 static bool gemv_dispatch(hipStream_t s, const P &p, const float *x, const float *nw, float eps, uint32_t n_items,
                           uint32_t n_cols, uint32_t n_cus) {
+  if constexpr (NORM ? !kNormBuilt<P> : !kPlainBuilt<P>) {
+    return false;
+  } else {
   if (n_cols % F::kUnit) return false;  // a row must be whole units
   const uint32_t n_units = n_cols / F::kUnit;
   const int lpr = lanes_for(n_units);
@@ -579,12 +595,14 @@ static bool gemv_dispatch(hipStream_t s, const P &p, const float *x, const float
     default: return false;
   }
   return true;
+  }
 }
 
 template <class P>
 static bool gemv_any(hipStream_t s, uint32_t format, const P &p, const float *x, const float *nw, float eps,
                      uint32_t n_items, uint32_t n_cols, uint32_t n_cus) {
   const bool norm = nw != nullptr;
+  if (norm ? !kNormBuilt<P> : !kPlainBuilt<P>) return false;
   // Integer activations where a workgroup serves many rows (rows of at most
   // 64 units); for wide rows (the down projection: a few rows per
   // workgroup) converting the staged input costs more than it saves.

@@ -73,6 +73,28 @@ bool fast_matvec_conv(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t
                       const float *norm_w, float eps, const float *taps, float *history, float *out, uint32_t n_embd,
                       uint32_t ksize, uint32_t n_cus);
 
+// gemv_slab.hip: the slab GEMV (every weight load of a workgroup issued
+// before its input is staged) for Q4_K rows; the fast_* functions above try
+// these first.  Each returns false, launching nothing, for shapes it does not
+// serve.
+bool slab_matvec(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols, const float *x,
+                 float *y, const float *nw, float eps, bool accumulate, uint32_t n_cus);
+bool slab_matvec3(hipStream_t s, uint32_t format, const uint8_t *W0, const uint8_t *W1, const uint8_t *W2, uint32_t r0,
+                  uint32_t r1, uint32_t r2, uint32_t n_cols, const float *x, float *y0, float *y1, float *y2,
+                  const float *nw, float eps, uint32_t n_cus);
+bool slab_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const uint8_t *Wu, uint32_t n_rows,
+                 uint32_t n_cols, const float *x, float *y, const float *nw, float eps, uint32_t n_cus);
+bool slab_experts_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, const uint8_t *Wu, uint32_t n_ff,
+                         uint32_t n_cols, const uint32_t *ids, uint32_t n_used, const float *x, float *y,
+                         uint32_t n_cus);
+bool slab_conv(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_cols, const float *x, const float *nw,
+               float eps, const float *taps, float *history, float *out, uint32_t n_embd, uint32_t ksize,
+               uint32_t n_cus);
+bool slab_gdn_in(hipStream_t s, uint32_t format, const uint8_t *Wqkv, const uint8_t *Wz, const uint8_t *Wb,
+                 const uint8_t *Wa, uint32_t conv_dim, uint32_t value_dim, uint32_t n_v, uint32_t n_cols,
+                 const float *x, const float *nw, float eps, const float *taps, float *hist, uint32_t ksize,
+                 float *conv_out, float *z, float *beta, float *alpha, uint32_t n_cus);
+
 // The logits GEMV with a per-workgroup argmax partial (at most
 // kArgmaxPartials); false when the shape has no fast path.
 constexpr uint32_t kArgmaxPartials = 1024;
@@ -171,7 +193,8 @@ struct SampleArgs {
   uint32_t n_recent;
   uint32_t *dpos;
   uint32_t *out;
-  uint64_t *rng;  // wyrand state
+  uint64_t *rng;  // wyrand state; null: the draw is `draw`
+  float draw;
   float temperature, top_p, min_p, penalty;
   uint32_t top_k;
 };

@@ -153,6 +153,42 @@ def test_q4k_gemv_config1_tolerance(hip):
     assert rel[big].max() < 1e-3
 
 
+@pytest.mark.parametrize("cols", [2048, 4096])
+def test_q4k_gemv_block_dynamic_range(hip, cols):
+    """Inputs whose 32-element blocks mix magnitudes 1e6 apart (one value of
+    ~1e3 among values of ~1e-3).  The Q4_K decode GEMV quantises each block's
+    inputs to 22-bit fixed point relative to the block's largest |x| < 2^E,
+    an absolute error of at most 2^(E-22) per input.  Checked against the
+    oracle at the reference's term-scale bound (metal_matvec.rs:16-19), and
+    every row against that quantisation bound itself: |err_r| <=
+    sum over blocks b of sum_l |w_rl| * 2^(E_b - 22), plus the reference's
+    1e-5 of the row's own term scale for the f32 arithmetic."""
+    rows = 2048
+    rng = np.random.default_rng(31)
+    w = q4k_matrix(rng, rows, cols)
+    x = (rng.standard_normal(cols) * 1e-3).astype(np.float32)
+    blocks = x.reshape(-1, 32)
+    big_at = rng.integers(0, 32, blocks.shape[0])
+    blocks[np.arange(blocks.shape[0]), big_at] = (rng.choice([-1.0, 1.0], blocks.shape[0]) *
+                                                  rng.uniform(500, 1500, blocks.shape[0])).astype(np.float32)
+    x = blocks.reshape(-1)
+    oracle.set_threads(8)
+    want = oracle.matvec(12, w, rows, cols, x).astype(np.float64)
+    wb, xb, yb = hip.buffer_from(w), hip.buffer_from(x), hip.new_buffer(rows * 4)
+    hip.begin()
+    hip.matvec(Format.Q4K, wb.at(0), rows, cols, xb.at(0), yb.at(0))
+    hip.end()
+    got = hip.read(yb.at(0), np.empty(rows, np.float32)).astype(np.float64)
+    err = np.abs(got - want)
+    assert err.max() / term_scale(Format.Q4K, w, rows, cols, x) < TOLERANCE
+    wd = np.abs(dense(Format.Q4K, w, rows, cols).astype(np.float64))
+    exp = np.frexp(np.abs(blocks.astype(np.float64)).max(axis=1))[1]  # max|x| < 2^E
+    quant = wd.reshape(rows, -1, 32).sum(axis=2) @ np.ldexp(1.0, exp - 22)
+    accum = TOLERANCE * (wd @ np.abs(x.astype(np.float64)))  # f32 arithmetic, per row
+    assert (err <= quant + accum).all(), float((err / (quant + accum)).max())
+    print(f"dynamic range {cols} cols: worst error {float((err / (quant + accum)).max()):.3g} of the bound")
+
+
 @pytest.mark.parametrize("fmt,nbytes,ne,scales", [
     (Format.Q4K, 144, 256, [0, 2]), (Format.Q5K, 176, 256, [0, 2]), (Format.Q6K, 210, 256, [208]),
     (Format.Q8_0, 34, 32, [0]), (Format.Q4_0, 18, 32, [0]), (Format.F16, 2, 1, []),
