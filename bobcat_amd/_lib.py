@@ -182,6 +182,7 @@ PROTOTYPES = {
     "bch_qwen35_restore": (_int, [_vp, _vp, _u64]),
     "bch_qwen35_last_gpu_seconds": (C.c_double, [_vp]),
     "bch_sample": (_int, [_vp, View, _u32, View, _u32, C.POINTER(Sampling), View, View]),
+    "bch_sample_draw": (_int, [_vp, View, _u32, View, _u32, C.POINTER(Sampling), C.c_float, View]),
     "bch_lfm2_generate_sampled": (_int, [_vp, C.POINTER(C.c_uint32), _u32, C.POINTER(Sampling), _u64]),
     "bch_moe_route": (_int, [_vp, View, C.POINTER(Norm), View, View, View, View, _u32, _u32, _u32, _u32]),
     "bch_matvec_experts_swiglu": (_int, [_vp, _u32, View, View, _u32, _u32, _u32, View, View, _u32, View, _u32]),

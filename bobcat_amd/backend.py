@@ -283,6 +283,10 @@ class Hip:
         check(lib().bch_sample(self.handle, _view(logits), n_vocab, _view(recent), n_recent, C.byref(settings),
                                _view(rng_state), _view(out)))
 
+    def sample_draw(self, logits, n_vocab, recent, n_recent, settings, u, out):
+        check(lib().bch_sample_draw(self.handle, _view(logits), n_vocab, _view(recent), n_recent, C.byref(settings),
+                                    u, _view(out)))
+
     def argmax(self, x, out, n):
         check(lib().bch_argmax(self.handle, _view(x), _view(out), n))
 

@@ -805,7 +805,8 @@ static void gemm_fmt(hipStream_t s, const uint8_t *W, const uint8_t *W2, uint64_
 }
 
 
-uint64_t matmul_split_bytes(uint32_t n_rows, uint32_t n_cols) { return (uint64_t)n_rows * (4ull * n_cols + 4); }
+// The fp16 inputs (2 bytes a column) and one f32 unscale per row of inputs.
+uint64_t matmul_split_bytes(uint32_t n_rows, uint32_t n_cols) { return (uint64_t)n_rows * (2ull * n_cols + 4); }
 
 uint64_t matmul_scratch_bytes(uint32_t n_tokens, uint32_t n_cols, uint32_t n_rows) {
   return (matmul_split_bytes(n_tokens, n_cols) + 255) / 256 * 256 + 4ull * kMaxSplitK * n_tokens * n_rows;
@@ -939,12 +940,18 @@ extern "C" int bch_matmul_noalloc(bch_ctx *ctx, uint32_t format, bch_view weight
   if (store > 2) return fail(BCH_ERR_ARGUMENT, "matmul_noalloc: unknown store mode %u", store);
   if (n_rows == 0 || n_cols == 0 || n_cols % kBK)
     return fail(BCH_ERR_ARGUMENT, "matmul_noalloc: %u x %u needs columns in multiples of %d", n_rows, n_cols, kBK);
-  const uint64_t need = matmul_split_bytes(n_tokens, n_cols);
+  // The inputs plus the partials of the column split bch_matmul picks for
+  // this shape: when they fit, the launch below picks the same split (its
+  // smaller budget still holds it), so the results equal bch_matmul's bit
+  // for bit.
+  const GemmShape g = gemm_shape(n_rows, n_cols, n_tokens, (uint64_t)kMaxSplitK * n_tokens * n_rows, device_cus());
+  const uint64_t need = (matmul_split_bytes(n_tokens, n_cols) + 255) / 256 * 256 +
+                        (g.splits > 1 ? 4ull * g.splits * n_tokens * n_rows : 0);
   if (need > kNoAllocScratchBytes)
     return fail(BCH_ERR_ARGUMENT,
-                "matmul_noalloc: %u tokens of %u columns need %llu bytes of scratch, more than its %llu "
+                "matmul_noalloc: %u tokens of %u x %u need %llu bytes of scratch, more than its %llu "
                 "(use bch_matmul)",
-                n_tokens, n_cols, (unsigned long long)need, (unsigned long long)kNoAllocScratchBytes);
+                n_tokens, n_rows, n_cols, (unsigned long long)need, (unsigned long long)kNoAllocScratchBytes);
   const uint64_t rb = bch_row_bytes(format, n_cols);
   const uint8_t *W;
   const float *xp;

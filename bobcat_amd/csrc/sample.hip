@@ -54,6 +54,16 @@ __device__ __forceinline__ float wyrand_f32(uint64_t *state) {
   return __uint_as_float(0x3f800000u | (u >> 9)) - 1.0f;
 }
 
+// The draw of a sampling launch: the generator's next f32, advancing its
+// state, or the caller's draw when the launch has no generator.
+__device__ __forceinline__ float next_draw(const SampleArgs &a) {
+  if (!a.rng) return a.draw;
+  uint64_t st = *a.rng;
+  const float u = wyrand_f32(&st);
+  *a.rng = st;
+  return u;
+}
+
 // Exclusive prefix sum of one value per thread over the workgroup; `total`
 // receives the sum.  Uses shuffles within a wave and LDS across waves.
 template <class T>
@@ -126,36 +136,48 @@ __device__ __forceinline__ float ord_value(uint32_t key) {
   return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
 }
 
+// Weights are summed in 64-bit fixed point (2^-40 units): integer sums do
+// not depend on the order the histogram's atomic adds land in, so a launch
+// (and every replay of a captured graph) cuts at the same rank for the same
+// inputs.  Weights lie in [0, 1] (probabilities) or are 1 (counts), so a
+// sum over up to 2^23 candidates stays below 2^63.
+constexpr double kMassOne = 1099511627776.0;  // 2^40
+constexpr uint32_t kSampleMaxVocab = 1u << 23;
+__device__ __forceinline__ uint64_t mass_fixed(float w) { return __double2ull_rn((double)w * kMassOne); }
+
 // The first rank whose cumulative weight reaches `target` (>= when
-// `inclusive`, > otherwise), among the elements passing `pred`, as a cut.
-// When the total weight never gets there (rounding), the cut is the last
-// such element and `found` is false.  A radix descent over the 32-bit keys,
-// 8 bits a pass, with weight histograms; the elements tied at the final key
-// weigh the same, so the id of the crossing one follows by division.
+// `inclusive`, > otherwise; target in 2^-40 units), among the elements
+// passing `pred`, as a cut.  When the total weight never gets there
+// (rounding), the cut is the last such element and `found` is false.  A
+// radix descent over the 32-bit keys, 8 bits a pass, with weight
+// histograms; the elements tied at the final key weigh the same, so the id
+// of the crossing one follows by division.
 template <class Pred, class Weight>
-__device__ Cut mass_cut(const float *logits, uint32_t n, float target, bool inclusive, Pred pred, Weight weight,
-                        float *bins, uint32_t *u16, uint32_t *sel_s, float *above_s, bool *found) {
+__device__ Cut mass_cut(const float *logits, uint32_t n, uint64_t target, bool inclusive, Pred pred, Weight weight,
+                        uint64_t *bins, uint32_t *u16, uint32_t *sel_s, uint64_t *above_s, bool *found) {
   constexpr uint32_t kNone = 0xffffffffu;
   const uint32_t tid = threadIdx.x;
   uint32_t prefix = 0;
-  float above = 0.f;  // weight of the keys above the current prefix
+  uint64_t above = 0;  // weight of the keys above the current prefix
   bool reached = true;
   for (int shift = 24; shift >= 0; shift -= 8) {
-    for (uint32_t i = tid; i < 256; i += kSampleThreads) bins[i] = 0.f;
+    for (uint32_t i = tid; i < 256; i += kSampleThreads) bins[i] = 0;
     __syncthreads();
     const uint32_t hi_mask = shift == 24 ? 0u : ~0u << (shift + 8);
     for (uint32_t i = tid; i < n; i += kSampleThreads) {
       const float v = logits[i];
       const uint32_t key = ord_key(v);
-      if ((key & hi_mask) == (prefix & hi_mask) && pred(i)) atomicAdd(&bins[(key >> shift) & 255u], weight(v));
+      if ((key & hi_mask) == (prefix & hi_mask) && pred(i))
+        atomicAdd(reinterpret_cast<unsigned long long *>(&bins[(key >> shift) & 255u]),
+                  (unsigned long long)mass_fixed(weight(v)));
     }
     __syncthreads();
     if (tid == 0) {
-      float acc = above;
+      uint64_t acc = above;
       uint32_t bin = kNone, last = kNone;
       for (int b = 255; b >= 0; b--) {
-        if (bins[b] <= 0.f) continue;
-        const float next = acc + bins[b];
+        if (bins[b] == 0) continue;
+        const uint64_t next = acc + bins[b];
         if (inclusive ? next >= target : next > target) {
           bin = (uint32_t)b;
           break;
@@ -191,19 +213,21 @@ __device__ Cut mass_cut(const float *logits, uint32_t n, float target, bool incl
   block_scan<uint32_t>(c, u16, &n_tied);
   uint32_t j = n_tied - 1;
   if (reached) {
-    const float wk = weight(ord_value(prefix));
-    const float need = wk > 0.f ? (target - above) / wk : 0.f;  // ties before the crossing, as a real
-    float f = inclusive ? ceilf(need) - 1.f : floorf(need);
-    if (!(f >= 0.f)) f = 0.f;
-    if (f < (float)j) j = (uint32_t)f;
+    // Ties before the crossing one: each weighs wk, and `above` + f·wk is
+    // still short of the target for the f that precede it.
+    const uint64_t wk = mass_fixed(weight(ord_value(prefix)));
+    const uint64_t rem = target > above ? target - above : 0;
+    uint64_t f = 0;
+    if (wk > 0) f = inclusive ? (rem > 0 ? (rem - 1) / wk : 0) : rem / wk;
+    if (f < (uint64_t)j) j = (uint32_t)f;
   }
   *found = reached;
   const uint32_t id = nth_tied_id(logits, n, prefix, j, pred, u16, sel_s);
   return Cut{prefix, id};
 }
 
-__device__ void sample_large(const SampleArgs &a, uint32_t k, float *bins, uint32_t *u16, float *f16s, uint32_t *sel_s,
-                             float *above_s, uint32_t *token_s) {
+__device__ void sample_large(const SampleArgs &a, uint32_t k, uint64_t *bins, uint32_t *u16, float *f16s,
+                             uint32_t *sel_s, uint64_t *above_s, uint32_t *token_s) {
   const uint32_t tid = threadIdx.x, n = a.n;
   const float *logits = a.logits;
   // 1. The top-k set as a cut (top_k = 0 or >= n keeps everything).
@@ -211,8 +235,8 @@ __device__ void sample_large(const SampleArgs &a, uint32_t k, float *bins, uint3
   if (k < n) {
     bool f;
     topk = mass_cut(
-        logits, n, (float)k, true, [](uint32_t) { return true; }, [](float) { return 1.0f; }, bins, u16, sel_s,
-        above_s, &f);
+        logits, n, (uint64_t)k << 40, true, [](uint32_t) { return true; }, [](float) { return 1.0f; }, bins, u16,
+        sel_s, above_s, &f);
   }
   auto in_topk = [&](uint32_t i) { return before_cut(ord_key(logits[i]), i, topk); };
   // 2. Softmax at temperature 1 over the candidates.
@@ -227,7 +251,7 @@ __device__ void sample_large(const SampleArgs &a, uint32_t k, float *bins, uint3
   auto prob = [=](float v) { return expf(v - mx) / S; };
   // 3. Top-p: the shortest prefix reaching top_p (all candidates when none does).
   bool reached = false;
-  Cut topp = mass_cut(logits, n, a.top_p, true, in_topk, prob, bins, u16, sel_s, above_s, &reached);
+  Cut topp = mass_cut(logits, n, mass_fixed(a.top_p), true, in_topk, prob, bins, u16, sel_s, above_s, &reached);
   if (!reached) topp = topk;
   // 4. Min-p: drop candidates below the first one's probability times min_p.
   const float floor_p = (1.0f / S) * a.min_p;
@@ -244,15 +268,11 @@ __device__ void sample_large(const SampleArgs &a, uint32_t k, float *bins, uint3
     if (kept(i)) qp += tq(logits[i]);
   const float Sq = block_sum<kSampleThreads>(qp, f16s);
   __shared__ float draw_s;
-  if (tid == 0) {
-    uint64_t st = *a.rng;
-    draw_s = wyrand_f32(&st);
-    *a.rng = st;
-  }
+  if (tid == 0) draw_s = next_draw(a);
   __syncthreads();
   const float u = draw_s;
   bool got = false;
-  const Cut c = mass_cut(logits, n, u, false, kept, [=](float v) { return tq(v) / Sq; }, bins, u16, sel_s,
+  const Cut c = mass_cut(logits, n, mass_fixed(u), false, kept, [=](float v) { return tq(v) / Sq; }, bins, u16, sel_s,
                          above_s, &got);
   if (tid == 0) *token_s = c.id;
   __syncthreads();
@@ -266,9 +286,9 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   __shared__ float f16s[16];
   __shared__ uint64_t k16[16];
   __shared__ uint32_t prefix_s, remain_s, keep_s, token_s;
-  __shared__ float large_bins[256];
+  __shared__ uint64_t large_bins[256];
   __shared__ uint32_t large_sel[2];
-  __shared__ float large_above;
+  __shared__ uint64_t large_above;
   const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
   const uint32_t n = a.n;
   float *logits = a.logits;
@@ -451,9 +471,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     float qcum = block_scan<float>(qrun, f16s, &qtotal);
     __shared__ float draw_s;
     if (tid == 0) {
-      uint64_t st = *a.rng;
-      draw_s = wyrand_f32(&st);
-      *a.rng = st;
+      draw_s = next_draw(a);
       token_s = cidx[keep - 1];  // the last kept candidate when rounding leaves the draw uncovered
       keep_s = keep;             // reused below as the first index whose cumulative mass passes the draw
     }
@@ -493,6 +511,7 @@ extern "C" int bch_sample(bch_ctx *ctx, bch_view logits, uint32_t n_vocab, bch_v
                           const bch_sampling *settings, bch_view rng_state, bch_view out) {
   if (!settings) return fail(BCH_ERR_ARGUMENT, "sample: no settings");
   if (n_vocab == 0) return fail(BCH_ERR_ARGUMENT, "sample: an empty vocabulary");
+  if (n_vocab > kSampleMaxVocab) return fail(BCH_ERR_ARGUMENT, "sample: more than 2^23 logits");
   SampleArgs a{};
   BCH_TRY(view_ptr(ctx, "sample", logits, (uint64_t)n_vocab * 4, &a.logits));
   if (n_recent) BCH_TRY(view_ptr(ctx, "sample", recent, (uint64_t)n_recent * 4, &a.recent));
@@ -507,4 +526,26 @@ extern "C" int bch_sample(bch_ctx *ctx, bch_view logits, uint32_t n_vocab, bch_v
   a.min_p = settings->min_p;
   a.penalty = settings->repeat_penalty;
   return launch(ctx, {"sample", 1, n_vocab, 0}, [&](hipStream_t s) { run_sample(s, a); });
+}
+
+extern "C" int bch_sample_draw(bch_ctx *ctx, bch_view logits, uint32_t n_vocab, bch_view recent, uint32_t n_recent,
+                               const bch_sampling *settings, float u, bch_view out) {
+  if (!settings) return fail(BCH_ERR_ARGUMENT, "sample_draw: no settings");
+  if (n_vocab == 0) return fail(BCH_ERR_ARGUMENT, "sample_draw: an empty vocabulary");
+  if (n_vocab > kSampleMaxVocab) return fail(BCH_ERR_ARGUMENT, "sample_draw: more than 2^23 logits");
+  if (!(u >= 0.0f && u < 1.0f)) return fail(BCH_ERR_ARGUMENT, "sample_draw: the draw is outside [0, 1)");
+  SampleArgs a{};
+  BCH_TRY(view_ptr(ctx, "sample_draw", logits, (uint64_t)n_vocab * 4, &a.logits));
+  if (n_recent) BCH_TRY(view_ptr(ctx, "sample_draw", recent, (uint64_t)n_recent * 4, &a.recent));
+  BCH_TRY(view_ptr(ctx, "sample_draw", out, 4, &a.out));
+  a.rng = nullptr;
+  a.draw = u;
+  a.n = n_vocab;
+  a.n_recent = n_recent;
+  a.temperature = settings->temperature;
+  a.top_k = settings->top_k;
+  a.top_p = settings->top_p;
+  a.min_p = settings->min_p;
+  a.penalty = settings->repeat_penalty;
+  return launch(ctx, {"sample_draw", 1, n_vocab, 0}, [&](hipStream_t s) { run_sample(s, a); });
 }

@@ -220,15 +220,17 @@ int bch_attention_prefill(bch_ctx *ctx, bch_view q, bch_view k_cache, bch_view v
 uint64_t bch_attention_scratch_floats(uint32_t n_heads, uint32_t head_dim, uint32_t n_ctx,
                                       uint32_t n_queries);
 
-/* bch_matmul without any allocation: the same kernels and results as
- * bch_matmul, with the per-launch input split (n_tokens·(4·n_cols + 4)
- * bytes) in a static device array of bch_matmul_noalloc_max_bytes() (16 MiB)
- * that each GPU holds for the life of the process, instead of context
- * scratch that may grow with hipMalloc.  No counterpart in the reference: it
- * is for callers that cannot allocate (code under HIP graph capture, serving
- * loops that forbid allocation).  Larger launches fail with
- * BCH_ERR_ARGUMENT.  All calls on one GPU share the array, so calls that
- * overlap on one GPU (other streams or threads) race. */
+/* bch_matmul without any allocation: the same kernels, column split and
+ * results (bit for bit) as bch_matmul, with the launch's scratch — its fp16
+ * inputs, n_tokens·(2·n_cols + 4) bytes, and the partial sums of the column
+ * split bch_matmul picks for the shape, 4·splits·n_tokens·n_rows bytes when
+ * it splits — in a static device array of bch_matmul_noalloc_max_bytes()
+ * (16 MiB) that each GPU holds for the life of the process, instead of
+ * context scratch that may grow with hipMalloc.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, serving loops that forbid allocation).  Launches needing more
+ * fail with BCH_ERR_ARGUMENT.  All calls on one GPU share the array, so
+ * calls that overlap on one GPU (other streams or threads) race. */
 int bch_matmul_noalloc(bch_ctx *ctx, uint32_t format, bch_view weights, uint32_t n_rows, uint32_t n_cols,
                        bch_view x, bch_view y, uint32_t n_tokens, uint32_t store);
 uint64_t bch_matmul_noalloc_max_bytes(void);
@@ -313,10 +315,19 @@ typedef int (*bch_emit_fn)(uint32_t token, void *user);
  * penalty over the distinct tokens of the last 64 of `recent` (applied to
  * `logits` in place), top-k, top-p, min-p, temperature, then a draw from the
  * wyrand generator whose 8-byte state is at `rng_state` (advanced by one
- * draw).  The token goes to `out` (4 bytes).  At most 4096 candidates
- * survive top-k (top_k = 0 or > 4096 keeps the 4096 largest logits). */
+ * draw).  The token goes to `out` (4 bytes).  Every candidate of the
+ * vocabulary takes part: top_k = 0 (or top_k >= n_vocab) keeps them all, and
+ * any top_k up to n_vocab is honoured exactly. */
 int bch_sample(bch_ctx *ctx, bch_view logits, uint32_t n_vocab, bch_view recent, uint32_t n_recent,
                const bch_sampling *settings, bch_view rng_state, bch_view out);
+
+/* bch_sample with the draw given: `u` in [0, 1) takes the place of the
+ * generator's f32 (sampler.rs:102-109 walks the kept candidates with it).
+ * No counterpart in the reference, whose Sampler owns its generator; for
+ * callers that keep their own random stream.  Fails with BCH_ERR_ARGUMENT
+ * for u outside [0, 1). */
+int bch_sample_draw(bch_ctx *ctx, bch_view logits, uint32_t n_vocab, bch_view recent, uint32_t n_recent,
+                    const bch_sampling *settings, float u, bch_view out);
 
 /* ------------------------------------------------------------------ */
 /* Gated DeltaNet and gated attention (Qwen3.5)                        */

@@ -62,6 +62,8 @@ def lib() -> C.CDLL:
             "orc_qwen35_step": (C.c_int, [vp, vp, u32, fp, fp, fp, fp]),
             "orc_sample": (u32, [fp, u32, C.POINTER(u32), u32, vp, C.POINTER(C.c_uint64)]),
             "orc_wyrand": (C.c_uint64, [C.POINTER(C.c_uint64)]),
+            "orc_sample_u": (u32, [fp, u32, C.POINTER(u32), u32, vp, C.c_float]),
+            "orc_u32_to_f32": (C.c_float, [u32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(h, name)
@@ -162,6 +164,19 @@ def sample(logits, recent, settings: Sampling, state: int):
     tok = lib().orc_sample(_fp(lg), lg.size, rc.ctypes.data_as(C.POINTER(C.c_uint32)), rc.size,
                            C.cast(C.byref(settings), C.c_void_p), C.byref(st))
     return int(tok), int(st.value)
+
+
+def sample_u(logits, recent, settings: Sampling, u: float) -> int:
+    """Sampler::sample with the draw `u` (0 <= u < 1) given instead of generated."""
+    lg = np.array(logits, np.float32)
+    rc = np.ascontiguousarray(recent, np.uint32)
+    return int(lib().orc_sample_u(_fp(lg), lg.size, rc.ctypes.data_as(C.POINTER(C.c_uint32)), rc.size,
+                                  C.cast(C.byref(settings), C.c_void_p), u))
+
+
+def u32_to_f32(x: int) -> float:
+    """fastrand's Rng::f32 of a 32-bit draw."""
+    return float(lib().orc_u32_to_f32(x))
 
 
 def short_conv(bcx: np.ndarray, taps: np.ndarray, hist: np.ndarray, n_embd: int, k: int, n_tokens: int):

@@ -643,8 +643,12 @@ static void cand_softmax(orc_cand *c, uint32_t n, float temperature) {
   for (uint32_t i = 0; i < n; i++) c[i].v /= sum;
 }
 
-EXPORT uint32_t orc_sample(float *logits, uint32_t n, const uint32_t *recent, uint32_t n_recent,
-                           const bch_sampling *st, uint64_t *rng) {
+/* Sampler::sample (sampler.rs:45-112).  The draw comes from `rng` (fastrand's
+ * f32, advancing the state) or, when `rng` is NULL, is `u` itself: the
+ * reference's loop over the candidates with `draw` given, so tests can place
+ * it on either side of a candidate boundary. */
+static uint32_t sample_core(float *logits, uint32_t n, const uint32_t *recent, uint32_t n_recent,
+                            const bch_sampling *st, uint64_t *rng, float u) {
   if (fabsf(st->repeat_penalty - 1.0f) > 1.1920929e-7f) {
     uint32_t start = n_recent > 64 ? n_recent - 64 : 0;
     for (uint32_t i = start; i < n_recent; i++) {
@@ -681,7 +685,7 @@ EXPORT uint32_t orc_sample(float *logits, uint32_t n, const uint32_t *recent, ui
     if (c[i].v >= floor_p) c[kept++] = c[i];
   for (uint32_t i = 0; i < kept; i++) c[i].v = logf(c[i].v);
   cand_softmax(c, kept, st->temperature);
-  float draw = orc_wyrand_f32(rng);
+  float draw = rng ? orc_wyrand_f32(rng) : u;
   uint32_t token = kept ? c[kept - 1].id : 0;
   for (uint32_t i = 0; i < kept; i++) {
     if (draw < c[i].v) {
@@ -692,6 +696,26 @@ EXPORT uint32_t orc_sample(float *logits, uint32_t n, const uint32_t *recent, ui
   }
   free(c);
   return token;
+}
+
+EXPORT uint32_t orc_sample(float *logits, uint32_t n, const uint32_t *recent, uint32_t n_recent,
+                           const bch_sampling *st, uint64_t *rng) {
+  return sample_core(logits, n, recent, n_recent, st, rng, 0.0f);
+}
+
+/* orc_sample with the draw given (0 <= u < 1) instead of taken from a generator. */
+EXPORT uint32_t orc_sample_u(float *logits, uint32_t n, const uint32_t *recent, uint32_t n_recent,
+                             const bch_sampling *st, float u) {
+  return sample_core(logits, n, recent, n_recent, st, NULL, u);
+}
+
+/* fastrand's f32 of a 32-bit draw: its 23 high bits as the mantissa of a
+ * float in [1, 2), minus one (Rng::f32). */
+EXPORT float orc_u32_to_f32(uint32_t x) {
+  uint32_t bits = 0x3f800000u | (x >> 9);
+  float f;
+  memcpy(&f, &bits, 4);
+  return f - 1.0f;
 }
 
 /* ---------------------------------------------------------------- */

@@ -46,6 +46,12 @@ MODELS = {
     "lfm2-2.6b": (LFM2_2_6B, Lfm2Weights, oracle.Lfm2State),
     "lfm2-8b-a1b": (LFM2_8B_A1B, Lfm2Weights, oracle.Lfm2State),
 }
+# Long-context fixtures: (model, prompt length, greedy steps).  The 2.6B at a
+# 4,096-token prompt reaches the long-context attention shape (8 KV heads of
+# 64 over thousands of keys, several key splits in prefill and decode).
+LONG = {
+    "lfm2-2.6b-ctx4k": ("lfm2-2.6b", 4096, 32),
+}
 
 
 def digest(weights) -> str:
@@ -58,8 +64,8 @@ def digest(weights) -> str:
     return h.hexdigest()
 
 
-def prompt_ids(n_vocab: int) -> np.ndarray:
-    return np.random.default_rng(PROMPT_SEED).integers(0, n_vocab, N_PROMPT).astype(np.uint32)
+def prompt_ids(n_vocab: int, n: int = N_PROMPT) -> np.ndarray:
+    return np.random.default_rng(PROMPT_SEED).integers(0, n_vocab, n).astype(np.uint32)
 
 
 def fixture_path(name: str) -> Path:
@@ -67,16 +73,17 @@ def fixture_path(name: str) -> Path:
 
 
 def make(name: str) -> None:
-    cfg, wcls, scls = MODELS[name]
+    base, n_prompt, n_gen = LONG.get(name, (name, N_PROMPT, N_GEN))
+    cfg, wcls, scls = MODELS[base]
     t0 = time.time()
     weights = wcls(cfg, seed=WEIGHT_SEED)
-    prompt = prompt_ids(cfg.n_vocab)
-    cpu = scls(weights, n_ctx=N_PROMPT + N_GEN + 8)
+    prompt = prompt_ids(cfg.n_vocab, n_prompt)
+    cpu = scls(weights, n_ctx=n_prompt + n_gen + 8)
     for t in prompt:
         lg = cpu.step(int(t))
     logits0 = lg.copy()
     toks, gaps = [], []
-    for _ in range(N_GEN):
+    for _ in range(n_gen):
         top = np.argsort(lg, kind="stable")[-2:]
         gaps.append(float(lg[top[1]] - lg[top[0]]))
         nxt = int(np.argmax(lg))

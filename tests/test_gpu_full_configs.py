@@ -1,10 +1,10 @@
 """GPU parity at the BASELINE configs' real sizes.
 
 * configs[0], prefill variant: the Q4_K matrix W [8192 x 2048] of config 1
-  against X [512 x 2048] through bch_matmul, checked against the oracle's
-  scalar matvec of every token (f64 accumulation, scalar.rs:213-220) within
-  the 5e-3 half-precision bound of lfm2_reference.rs:21-25 (the prefill GEMM
-  rounds each dequantised weight to f16, as the reference's expanded tiles
+  against X [512 x 2048] through bch_matmul, every token checked against the
+  scalar path's dequantised weights in float64 (scalar.rs:59-152, 213-220)
+  within the north star's 1e-3 relative bound (the prefill GEMM rounds each
+  dequantised weight and input to f16, as the reference's expanded tiles
   do).
 * configs[1]-[4] (LFM2 350M, Qwen3.5 0.8B, LFM2 2.6B, LFM2 8B-A1B) at full
   size with their seeded random-init weights: a 512-token prompt, then 128
@@ -15,7 +15,8 @@
   1e-3 (the north-star rule), after which the sequences may legitimately
   part.  As lfm2_reference.rs:117-350 does on real files.  The strict run
   uses an f32 KV cache (the oracle's); the f16 cache of the benchmark is run
-  too and must agree on the first-step logits within 5e-3.
+  too: its first-step logits agree within 5e-3 and its 128 tokens follow the
+  same near-tie rule.
 """
 from __future__ import annotations
 
@@ -49,12 +50,25 @@ def test_config1_prefill_variant(hip):
     hip.matmul(Format.Q4K, wb.at(0), n_rows, n_cols, xb.at(0), yb.at(0), n_tokens, Store.OVERWRITE)
     hip.end()
     got = hip.read(yb.at(0), np.empty(n_tokens * n_rows, np.float32)).reshape(n_tokens, n_rows)
+    # Every token against the scalar path's exact dequantised weights in
+    # float64 (oracle.dequantize is scalar::dequantize; the product in f64 is
+    # the oracle's matvec for all 512 tokens at once).  The bound is the
+    # north star's 1e-3 relative to each token's largest output, and the
+    # per-element error is also held to 1e-3 of that token's term scale.
+    wd = oracle.dequantize(int(Format.Q4K), w, n_rows * n_cols).astype(np.float64).reshape(n_rows, n_cols)
+    xd = x.astype(np.float64).reshape(n_tokens, n_cols)
+    want = xd @ wd.T
+    scale = np.abs(xd) @ np.abs(wd).T  # Σ|x·w| per element: the size of the terms summed
+    err = np.abs(got.astype(np.float64) - want)
+    per_token = err.max(axis=1) / np.abs(want).max(axis=1)
+    print(f"config-1 prefill variant: worst token {per_token.max():.3g} of its largest output, "
+          f"worst element {(err / scale).max():.3g} of its term scale")
+    assert per_token.max() < 1e-3, per_token.max()
+    assert (err / scale).max() < 1e-3
+    # The oracle's own scalar matvec on a few tokens agrees with the f64 product.
     oracle.set_threads(16)
-    worst = 0.0
-    for t in range(0, n_tokens, 7):  # every 7th token: the oracle stays within seconds
-        want = oracle.matvec(int(Format.Q4K), w, n_rows, n_cols, x[t * n_cols:(t + 1) * n_cols])
-        worst = max(worst, rel(got[t], want))
-    assert worst < HALF_TOLERANCE, worst
+    for t in (0, 255, 511):
+        assert rel(oracle.matvec(int(Format.Q4K), w, n_rows, n_cols, x[t * n_cols:(t + 1) * n_cols]), want[t]) < 1e-6
     # The first token through the decode GEMV path agrees with its GEMM row.
     yv = hip.new_buffer(n_rows * 4)
     hip.begin()
@@ -111,9 +125,10 @@ def test_greedy_128_matches_oracle(hip, model):
     lt, _ = half.prefill(prompt, trace=True)
     assert np.array_equal(lt, lh)
     got_h = half.generate(N_GEN).tolist()
-    same = next((i for i, (a, b) in enumerate(zip(got_h, want)) if a != b), N_GEN)
-    print(f"{name}: f16 cache agrees with the oracle on the first {same} tokens")
     half.close()
+    # The f16 cache's 128 tokens under the same near-tie rule.
+    at_h = first_divergence(got_h, want, fix["gaps"])
+    print(f"{name}: f16 cache, 128 greedy tokens, {'identical' if at_h is None else f'near-tie flip at {at_h}'}")
 
 
 @pytest.mark.timeout(600)

@@ -12,6 +12,12 @@ restatement of Sampler::sample (crates/bobcat-cli/src/sampler.rs:45-129).
   float64; at most 1% of draws may miss both.
 * The generator stream itself (fastrand's wyrand, not vendored in the
   reference) is restated, not pinned by any vector of the reference.
+* With the draw given (bch_sample_draw), the closed-form cases of
+  tests/test_oracle.py (top-p prefix and renormalisation, the temperature on
+  log-probabilities, the min-p floor, top-p equal to a cumulative sum) land
+  on the tokens the mathematics fixes, on both sides of each boundary.
+* The generator state advances by wyrand's increment per draw (none at
+  temperature 0).
 * The sampled decode of the LFM2 driver at temperature 0 equals greedy
   generation, and at temperature > 0 equals the oracle model sampled with
   the same stream.
@@ -63,6 +69,79 @@ def test_reference_unit_vectors(hip):
     s = GpuSampler(hip, 7)
     for _ in range(200):
         assert s.sample([5.0, 0.0, 0.0], [], settings(1.0, min_p=0.5)) == 0
+
+
+def sample_u(hip, logits, recent, st, u):
+    lb = hip.buffer_from(np.asarray(logits, np.float32))
+    rc = np.asarray(recent if len(recent) else [0], np.uint32)
+    rb, out = hip.buffer_from(rc), hip.new_buffer(4)
+    hip.begin()
+    hip.sample_draw(lb.at(0), len(logits), rb.at(0), len(recent), st, u, out.at(0))
+    hip.end()
+    return int(hip.read(out.at(0), np.empty(1, np.uint32))[0])
+
+
+P3 = np.log(np.array([0.5, 0.3, 0.2], np.float32))
+Q0, Q01 = 0.25 / 0.38, 0.34 / 0.38  # T = 0.5: q ∝ p²
+CLOSED_FORM = [
+    (P3, settings(1.0, top_p=0.75), [(0.0, 0), (0.62, 0), (0.63, 1), (0.999, 1)]),
+    (P3, settings(0.5), [(Q0 - 1e-3, 0), (Q0 + 1e-3, 1), (Q01 - 1e-3, 1), (Q01 + 1e-3, 2)]),
+    (P3, settings(1.0, min_p=0.5), [(0.62, 0), (0.63, 1), (0.999, 1)]),
+    (np.zeros(4, np.float32), settings(1.0, top_p=0.5), [(0.45, 0), (0.70, 1), (0.999, 1)]),
+]
+
+
+@pytest.mark.parametrize("case", range(len(CLOSED_FORM)))
+def test_closed_form_draws(hip, case):
+    logits, st, draws = CLOSED_FORM[case]
+    for u, want in draws:
+        assert oracle.sample_u(logits, [], st, u) == want
+        assert sample_u(hip, logits, [], st, u) == want, (u, want)
+
+
+def test_explicit_draws_match_oracle(hip):
+    """Random logits with draws at least 2e-4 from every candidate boundary
+    of the exact (float64) walk: the GPU's draw lands on the exact answer
+    over small and full-vocabulary candidate sets.  The oracle (the
+    reference's sequential float32 sums) lands there too while the candidate
+    set is small; over 65K-152K candidates its running sums drift by up to
+    ~1e-4, so there the exact walk is the reference point."""
+    rng = np.random.default_rng(11)
+    checked = 0
+    for n, st in [(3000, settings(0.8, 40, 0.9, 0.02, 1.1)), (65536, settings(1.0, 0, 0.95, 0.0, 1.0)),
+                  (151936, settings(0.7, 0, 0.9, 0.05, 1.0)), (65536, settings(1.3, 5000, 1.0, 0.0, 1.2))]:
+        for _ in range(6):
+            logits = (rng.standard_normal(n) * 3).astype(np.float32)
+            recent = rng.integers(0, n, 70).astype(np.uint32)
+            u = float(rng.uniform(0.02, 0.98))
+            want = exact_sample(logits, recent, st, u)
+            if exact_sample(logits, recent, st, u - 2e-4) != want or exact_sample(logits, recent, st, u + 2e-4) != want:
+                continue
+            if n <= 4096:
+                assert oracle.sample_u(logits, recent, st, u) == want, (n, u)
+            assert sample_u(hip, logits, recent, st, u) == want, (n, u)
+            checked += 1
+    assert checked >= 12, checked
+
+
+def test_draw_outside_unit_interval_is_rejected(hip):
+    from bobcat_amd.backend import BobcatError
+    lb, rb, out = hip.buffer_from(P3), hip.buffer_from(np.zeros(1, np.uint32)), hip.new_buffer(4)
+    for u in (1.0, -0.25, float("nan")):
+        hip.begin()
+        with pytest.raises(BobcatError):
+            hip.sample_draw(lb.at(0), 3, rb.at(0), 0, settings(1.0), u, out.at(0))
+        hip.end()
+
+
+def test_generator_state_advances_per_draw(hip):
+    c0, seed = 0x2D358DCCAA6C78A5, 987654321
+    s = GpuSampler(hip, seed)
+    for _ in range(5):
+        s.sample([1.0, 0.5, 0.2], [], settings(1.0))
+    s.sample([1.0, 0.5, 0.2], [], settings(0.0))  # greedy: no draw
+    state = int(hip.read(s.rng.at(0), np.empty(1, np.uint64))[0])
+    assert state == (seed + 5 * c0) % (1 << 64)
 
 
 GRID = [settings(0.7, 20, 0.9, 0.05, 1.0), settings(1.0, 50, 1.0, 0.0, 1.3), settings(1.5, 0, 0.95, 0.02, 1.1),

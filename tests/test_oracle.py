@@ -309,3 +309,77 @@ def test_route_brute_force():
         assert experts[:4] == order[:4]
         norm = sig[order[:4]].sum() + 1e-6
         np.testing.assert_allclose(w[order[:4]], sig[order[:4]] / norm, rtol=1e-5)
+
+
+# --- Sampler::sample (crates/bobcat-cli/src/sampler.rs:75-111) with the draw given ---
+#
+# Cases whose answers the mathematics fixes, each chosen so that a plausible
+# slip fails: the top-p cut (`position(cumulative >= top_p) + 1`), the min-p
+# floor relative to the first candidate, the temperature applied to the log
+# probabilities, and the draw walking the kept candidates.
+
+SAMPLE_P = np.log(np.array([0.5, 0.3, 0.2], np.float32))
+
+
+def st(temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, penalty=1.0):
+    return oracle.Sampling(temperature, top_k, top_p, min_p, penalty)
+
+
+def test_sample_top_p_keeps_the_prefix_and_renormalises():
+    # p = [0.5, 0.3, 0.2]; top_p 0.75 keeps two, renormalised to [0.625, 0.375].
+    s = st(top_p=0.75)
+    assert [oracle.sample_u(SAMPLE_P, [], s, u) for u in (0.0, 0.62, 0.63, 0.999)] == [0, 0, 1, 1]
+
+
+def test_sample_temperature_squares_at_one_half():
+    # T = 0.5 on log-probabilities: q ∝ p² = [0.25, 0.09, 0.04] / 0.38.
+    s = st(temperature=0.5)
+    q0, q01 = 0.25 / 0.38, 0.34 / 0.38  # 0.65789..., 0.89473...
+    cases = [(q0 - 1e-3, 0), (q0 + 1e-3, 1), (q01 - 1e-3, 1), (q01 + 1e-3, 2)]
+    assert [oracle.sample_u(SAMPLE_P, [], s, u) for u, _ in cases] == [t for _, t in cases]
+
+
+def test_sample_min_p_drops_below_the_floor():
+    # min_p 0.5: floor 0.25 drops p = 0.2 and keeps 0.3; kept mass renormalised to [0.625, 0.375].
+    s = st(min_p=0.5)
+    assert [oracle.sample_u(SAMPLE_P, [], s, u) for u in (0.62, 0.63, 0.999)] == [0, 1, 1]
+
+
+def test_sample_top_p_equal_to_a_cumulative_sum():
+    # Four equal logits: p = 0.25 each, exact in float32, cumulative 0.5 after two.
+    # `>=` with `+ 1` keeps two ([0.5, 0.5]); `>` would keep three and `+ 0` one.
+    # (Equal logits keep the lowest ids first here; sort_unstable in the
+    # reference leaves their order open, but not how many are kept.)
+    lg = np.zeros(4, np.float32)
+    s = st(top_p=0.5)
+    assert oracle.sample_u(lg, [], s, 0.45) == 0
+    assert oracle.sample_u(lg, [], s, 0.70) == 1  # three kept would give id 2, one kept id 0
+    assert oracle.sample_u(lg, [], s, 0.999) == 1
+
+
+def test_sample_top_k_then_penalty_order():
+    # Penalty first (3.0 -> 1.5 for a positive logit), then top-k 1 keeps the new largest.
+    lg = np.array([0.1, 3.0, 2.0], np.float32)
+    assert oracle.sample_u(lg, [1], st(top_k=1, penalty=2.0), 0.9) == 2
+    # A negative logit is multiplied: -1 -> -2 falls below -1.5.
+    lg = np.array([-1.5, -1.0], np.float32)
+    assert oracle.sample_u(lg, [1, 1, 1], st(top_k=1, penalty=2.0), 0.5) == 0
+
+
+def test_generator_invariants():
+    # The state advances by the wyrand increment on every draw (mod 2^64);
+    # temperature 0 draws nothing.
+    c0 = 0x2D358DCCAA6C78A5
+    seed = 12345
+    state = seed
+    lg = np.array([1.0, 0.5, 0.2], np.float32)
+    for n in range(1, 6):
+        _, state = oracle.sample(lg, [], st(), state)
+        assert state == (seed + n * c0) % (1 << 64)
+    _, after = oracle.sample(lg, [], st(temperature=0.0), state)
+    assert after == state
+    # Rng::f32 maps a 32-bit draw's 23 high bits into [0, 1).
+    assert oracle.u32_to_f32(0) == 0.0
+    assert oracle.u32_to_f32(0x80000000) == 0.5
+    assert oracle.u32_to_f32(0xFFFFFFFF) == 1.0 - 2.0 ** -23
+    assert oracle.u32_to_f32(0x1FF) == 0.0  # the low 9 bits do not reach the mantissa
