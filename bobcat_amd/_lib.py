@@ -172,6 +172,7 @@ PROTOTYPES = {
     "bch_qwen35_reset": (_int, [_vp]),
     "bch_qwen35_step": (_int, [_vp, _u32, _FP, _FP, _FP, _FP]),
     "bch_qwen35_prefill": (_int, [_vp, C.POINTER(C.c_uint32), _u32, _FP, _FP, _FP, _FP]),
+    "bch_qwen35_hidden": (_int, [_vp, C.POINTER(C.c_uint32), _u32, _FP]),
     "bch_qwen35_greedy_token": (_int, [_vp, C.POINTER(C.c_uint32)]),
     "bch_qwen35_generate": (_int, [_vp, C.POINTER(C.c_uint32), _u32]),
     "bch_qwen35_generate_next": (_int, [_vp, C.POINTER(C.c_uint32), _u32]),

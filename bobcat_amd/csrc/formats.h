@@ -621,10 +621,11 @@ __device__ __forceinline__ void digitize_units(float *xs, uint32_t n_units) {
     }
     // The block's four chunks: consecutive lanes (T and the chunk numbering
     // keep c % 4 == lane % 4).
-    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-    sm += __shfl_xor(sm, 1, 64);
-    sm += __shfl_xor(sm, 2, 64);
+    // (DPP quad permutes: no LDS round trip; every lane runs this code.)
+    mx = fmaxf(mx, dpp<kDppXor1>(mx));
+    mx = fmaxf(mx, dpp<kDppXor2>(mx));
+    sm += dpp<kDppXor1>(sm);
+    sm += dpp<kDppXor2>(sm);
     int e = 0;
     if (mx > 0.f) frexpf(mx, &e);  // mx < 2^e
     const float scale = ldexpf(1.0f, 21 - e);

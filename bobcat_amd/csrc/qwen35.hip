@@ -466,6 +466,14 @@ int bch_qwen35_prefill(bch_qwen35 *m, const uint32_t *tokens, uint32_t n_tokens,
   return m->prefill(tokens, n_tokens, logits, trace_embedding, trace_layers, trace_final);
 }
 
+// Gpu::hidden (crates/bobcat-cli/src/backend.rs:150-160): reset, then
+// Qwen35Metal::prefill with only its final-norm output.
+int bch_qwen35_hidden(bch_qwen35 *m, const uint32_t *tokens, uint32_t n_tokens, float *hidden) {
+  if (!hidden) return fail(BCH_ERR_ARGUMENT, "hidden: no output rows");
+  BCH_TRY(m->reset());
+  return m->prefill(tokens, n_tokens, nullptr, nullptr, nullptr, hidden);
+}
+
 int bch_qwen35_greedy_token(bch_qwen35 *m, uint32_t *token) { return m->greedy_token(token); }
 int bch_qwen35_generate(bch_qwen35 *m, uint32_t *out, uint32_t n) { return m->generate(out, n); }
 int bch_qwen35_generate_next(bch_qwen35 *m, uint32_t *out, uint32_t n) { return m->generate_next(out, n); }

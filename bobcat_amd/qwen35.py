@@ -166,3 +166,11 @@ class Qwen35Weights:
 class Qwen35Hip(SequenceHip):
     """bch_qwen35: one Qwen3.5 sequence on the GPU (Qwen35Metal's API)."""
     _prefix = "bch_qwen35_"
+
+    def hidden(self, tokens) -> np.ndarray:
+        """Gpu::hidden: a new sequence of `tokens`; each token's final-norm row [n_tokens, n_embd]."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        out = np.empty((t.size, self.cfg.n_embd), np.float32)
+        check(self._fn("hidden")(self.handle, t.ctypes.data_as(C.POINTER(C.c_uint32)), t.size,
+                                    out.ctypes.data_as(C.POINTER(C.c_float))))
+        return out

@@ -569,6 +569,13 @@ int bch_qwen35_step(bch_qwen35 *qwen, uint32_t token, float *logits, float *trac
                     float *trace_final);
 int bch_qwen35_prefill(bch_qwen35 *qwen, const uint32_t *tokens, uint32_t n_tokens, float *logits,
                        float *trace_embedding, float *trace_layers, float *trace_final);
+/* Gpu::hidden (crates/bobcat-cli/src/backend.rs:150-160): start a new
+ * sequence (reset) and prefill `tokens`, writing each token's normalised
+ * last hidden state — the final RMSNorm's output, the input of the output
+ * projection — to `hidden`, n_tokens rows of n_embd floats; no logits.  As
+ * Qwen35Metal::prefill(tokens, None, Some(final_norm), None)
+ * (qwen35_metal.rs:557-600), for the decision head. */
+int bch_qwen35_hidden(bch_qwen35 *qwen, const uint32_t *tokens, uint32_t n_tokens, float *hidden);
 int bch_qwen35_greedy_token(bch_qwen35 *qwen, uint32_t *token);
 int bch_qwen35_generate(bch_qwen35 *qwen, uint32_t *out, uint32_t n);
 /* Qwen35Metal's generate_next (same protocol as bch_lfm2_generate_next). */

@@ -88,6 +88,30 @@ def test_prefill_trace_matches_oracle(hip, weights, kv_half):
     gpu.close()
 
 
+@pytest.mark.parametrize("kv_half", [False, True])
+def test_hidden_matches_oracle_final_norm(hip, weights, kv_half):
+    """Gpu::hidden (crates/bobcat-cli/src/backend.rs:150-160) through
+    bch_qwen35_hidden: a new sequence, each token's final-norm row, against
+    the oracle's final norm after each step (qwen35.rs, the input of the
+    output projection), within the prefill bound; it also starts over (the
+    rows do not depend on what ran before) and leaves the sequence at the
+    prompt's length."""
+    cfg = weights.cfg
+    tol = HALF_TOLERANCE if kv_half else PREFILL_TOLERANCE
+    toks = prompt(cfg, 25, seed=8)
+    gpu = Qwen35Hip(hip, weights, n_ctx=40, kv_half=kv_half)
+    gpu.prefill(prompt(cfg, 7, seed=9))  # something to start over from
+    got = gpu.hidden(toks)
+    assert gpu.n_past == len(toks)
+    again = gpu.hidden(toks)
+    gpu.close()
+    assert np.array_equal(got, again)
+    cpu = oracle.Qwen35State(weights, n_ctx=40)
+    for t, tok in enumerate(toks):
+        _, (_, _, wfinal) = cpu.step(tok, trace=True)
+        assert rel(got[t], wfinal) < tol, (t, rel(got[t], wfinal))
+
+
 def test_greedy_generation_matches_oracle(hip, weights):
     cfg = weights.cfg
     toks = prompt(cfg, 9, seed=3)
