@@ -66,8 +66,16 @@ def log(msg: str) -> None:
 
 
 def host_threads() -> int:
-    # The GPU box gives one GPU a 16-core share, whatever os.cpu_count() says.
-    return max(1, min(16, os.cpu_count() or 1))
+    """Threads of the host share this process may use: OMP_NUM_THREADS when
+    the environment sets the share (the GPU box does), else the CPUs this
+    process may run on."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    try:
+        return max(1, len(os.sched_getaffinity(0)))
+    except AttributeError:
+        return max(1, os.cpu_count() or 1)
 
 
 def gemv_leg(hip, reps: int, copies: int = 64):
@@ -266,6 +274,25 @@ def cpu_model_rate(weights, budget_s: float, threads: int):
     return dict(tok_s=n / dt, steps=n, seconds=dt)
 
 
+def cpu_gdn_layer_us(weights, threads: int, budget_s: float = 2.0):
+    """One Gated DeltaNet layer step of Qwen3.5-0.8B by the oracle
+    (qwen35.rs:430-516: the input projections, convolution, recurrence over
+    16 heads' 128 x 128 states, gated norm and output projection)."""
+    import oracle
+
+    oracle.set_threads(threads)
+    st = oracle.Qwen35State(weights, n_ctx=8)
+    st.step(1, logits=False)
+    layer = next(i for i in range(weights.cfg.n_layers) if not weights.cfg.is_attention(i))
+    n, t0 = 0, time.perf_counter()
+    while True:
+        st.delta_step(layer)
+        n += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    return (time.perf_counter() - t0) / n * 1e6
+
+
 def cpu_gemv_us(w, x, threads: int, budget_s: float = 2.0):
     """The oracle's config-1 Q4_K matvec (scalar.rs:213-220) on `threads` threads."""
     import oracle
@@ -336,14 +363,28 @@ def gemm_leg(hip, reps: int = 20):
 def cpu_baseline(weights, gemv_case, budget_s: float):
     """The reference's CPU path (the oracle) on the host, in the same run: the
     model's decode rate single-threaded (the reference's scalar path runs on
-    one core) and over the GPU's host share, and the config-1 GEMV time."""
+    one core) and over the GPU's host share; one decode token of LFM2-350M
+    and one Gated DeltaNet layer step of Qwen3.5-0.8B
+    on both; and the config-1 GEMV time."""
+    from bobcat_amd.lfm2 import LFM2_350M, Lfm2Weights
+    from bobcat_amd.qwen35 import QWEN35_0_8B, Qwen35Weights
+
     online, model = host_cpu()
     threads = host_threads()
     one = cpu_model_rate(weights, budget_s / 2, 1)
     many = cpu_model_rate(weights, budget_s / 2, threads)
+    small = Lfm2Weights(LFM2_350M, seed=WEIGHT_SEED)
+    small_one = cpu_model_rate(small, 2.0, 1)
+    small_many = cpu_model_rate(small, 2.0, threads)
+    del small
+    qwen = Qwen35Weights(QWEN35_0_8B, seed=WEIGHT_SEED)
+    gdn_one, gdn_many = cpu_gdn_layer_us(qwen, 1), cpu_gdn_layer_us(qwen, threads)
+    del qwen
     w, x = gemv_case
     return dict(one_core=one, all_cores=many, threads=threads, online_cores=online, cpu_model=model,
-                gemv_us_1=cpu_gemv_us(w, x, 1), gemv_us_all=cpu_gemv_us(w, x, threads))
+                gemv_us_1=cpu_gemv_us(w, x, 1), gemv_us_all=cpu_gemv_us(w, x, threads),
+                lfm2_350m=dict(one_core=small_one, all_cores=small_many),
+                gdn_layer_us=dict(one_core=gdn_one, all_cores=gdn_many))
 
 
 def model_summary(cfg, mres, name: str):
@@ -473,7 +514,11 @@ def main() -> int:
                           "sample": f"{cpu['all_cores']['steps']} decode steps, rows over {cpu['threads']} threads"},
             "host": {"online_cores": cpu["online_cores"], "cpu_model": cpu["cpu_model"]},
             "gemv_config1_us": {"1_core": round(cpu["gemv_us_1"], 1),
-                                f"{cpu['threads']}_cores": round(cpu["gemv_us_all"], 1)}},
+                                f"{cpu['threads']}_cores": round(cpu["gemv_us_all"], 1)},
+            "lfm2_350m_decode_tok_s": {"1_core": round(cpu["lfm2_350m"]["one_core"]["tok_s"], 3),
+                                       f"{cpu['threads']}_cores": round(cpu["lfm2_350m"]["all_cores"]["tok_s"], 3)},
+            "qwen35_gdn_layer_step_us": {"1_core": round(cpu["gdn_layer_us"]["one_core"], 1),
+                                         f"{cpu['threads']}_cores": round(cpu["gdn_layer_us"]["all_cores"], 1)}},
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -60,6 +60,7 @@ def lib() -> C.CDLL:
             "orc_qwen35_state_free": (None, [vp]),
             "orc_qwen35_n_past": (u32, [vp]),
             "orc_qwen35_step": (C.c_int, [vp, vp, u32, fp, fp, fp, fp]),
+            "orc_qwen35_delta_step": (C.c_int, [vp, vp, u32]),
             "orc_sample": (u32, [fp, u32, C.POINTER(u32), u32, vp, C.POINTER(C.c_uint64)]),
             "orc_wyrand": (C.c_uint64, [C.POINTER(C.c_uint64)]),
             "orc_sample_u": (u32, [fp, u32, C.POINTER(u32), u32, vp, C.c_float]),
@@ -253,6 +254,11 @@ class Qwen35State:
         if rc != 0:
             raise ValueError({-1: "context full", -2: "token outside the vocabulary"}[rc])
         return (lg, (te, tl, tf)) if trace else lg
+
+    def delta_step(self, layer: int) -> None:
+        """One Gated DeltaNet layer (Model::delta_net) on the current input; timing only."""
+        if lib().orc_qwen35_delta_step(C.addressof(self.model.c_model), self.handle, layer) != 0:
+            raise ValueError(f"layer {layer} is not a DeltaNet layer")
 
     def __del__(self):
         try:

@@ -888,6 +888,17 @@ static void q35_delta(const bch_qwen35_model *m, const bch_qwen35_layer *L, uint
   matvec_m(&L->out, s->delta_out, s->mixer_out);
 }
 
+/* One Gated DeltaNet layer of a step (Model::delta_net, qwen35.rs:430-516)
+ * on the state's current normalised input: the CPU baseline's "GDN layer
+ * step".  Returns -1 when layer il is an attention layer. */
+EXPORT int orc_qwen35_delta_step(const bch_qwen35_model *m, orc_qwen35_state *s, uint32_t il) {
+  if (il >= m->n_layers || m->layers[il].is_attention) return -1;
+  uint32_t di = 0;
+  for (uint32_t i = 0; i < il; i++) di += !m->layers[i].is_attention;
+  q35_delta(m, &m->layers[il], di, s);
+  return 0;
+}
+
 /* Model::step (qwen35.rs:280-365); traces as orc_lfm2_step. */
 EXPORT int orc_qwen35_step(const bch_qwen35_model *m, orc_qwen35_state *s, uint32_t token, float *logits,
                            float *trace_embedding, float *trace_layers, float *trace_final) {
