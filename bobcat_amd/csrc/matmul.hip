@@ -369,9 +369,12 @@ __device__ __forceinline__ void gemm_dequant_direct(const uint8_t *__restrict__ 
 }
 
 // Q4_K dequantisation of a thread's stage in parts, so that the parts can
-// be interleaved with MFMAs: q4k_scales once, then part J (one quant dword:
-// 4 low-nibble and 4 high-nibble weights, (d·sc)·q − dmin·m each, rounded
-// to fp16) per call.
+// be interleaved with MFMAs: q4k_scales once, then part J per call — eight
+// weights of one nibble half from two quant dwords, (d·sc)·q − dmin·m each
+// rounded to fp16, stored as one 16-byte LDS write.  (Parts of four low and
+// four high weights stored as two 8-byte writes put four lanes of a wave on
+// each pair of banks, a 2-way conflict on every write; 16-byte writes of
+// eight consecutive weights spread a wave's rows over all banks.)
 struct Q4kScales {
   float a_lo, b_lo, a_hi, b_hi;
 };
@@ -386,20 +389,24 @@ __device__ __forceinline__ Q4kScales q4k_scales(const GemmRaw &r, uint32_t k0, b
 
 template <int WPT, int J>
 __device__ __forceinline__ void q4k_part(const GemmRaw &r, const Q4kScales &f, int c, _Float16 *__restrict__ dst) {
-  constexpr int H = WPT / 2;
-  const uint32_t v = J == 0 ? r.q.x : J == 1 ? r.q.y : J == 2 ? r.q.z : r.q.w;
-  const uint32_t ql = v & 0x0f0f0f0fu, qh = (v >> 4) & 0x0f0f0f0fu;
-  half4_t l4, h4;
-  l4[0] = (_Float16)(f.a_lo * ubyte0(ql) - f.b_lo);
-  l4[1] = (_Float16)(f.a_lo * ubyte1(ql) - f.b_lo);
-  l4[2] = (_Float16)(f.a_lo * ubyte2(ql) - f.b_lo);
-  l4[3] = (_Float16)(f.a_lo * ubyte3(ql) - f.b_lo);
-  h4[0] = (_Float16)(f.a_hi * ubyte0(qh) - f.b_hi);
-  h4[1] = (_Float16)(f.a_hi * ubyte1(qh) - f.b_hi);
-  h4[2] = (_Float16)(f.a_hi * ubyte2(qh) - f.b_hi);
-  h4[3] = (_Float16)(f.a_hi * ubyte3(qh) - f.b_hi);
-  *reinterpret_cast<half4_t *>(dst + H * c + 4 * J) = l4;
-  *reinterpret_cast<half4_t *>(dst + 32 + H * c + 4 * J) = h4;
+  constexpr int H = WPT / 2;                      // weights of each nibble half per thread
+  constexpr int HALVES = H / 8;                   // parts per nibble half (1 or 2)
+  constexpr bool HI = J >= HALVES;                // which nibble half
+  constexpr int P = HI ? J - HALVES : J;          // eight weights P of that half
+  const uint32_t v0 = P == 0 ? r.q.x : r.q.z, v1 = P == 0 ? r.q.y : r.q.w;
+  const uint32_t q0 = HI ? (v0 >> 4) & 0x0f0f0f0fu : v0 & 0x0f0f0f0fu;
+  const uint32_t q1 = HI ? (v1 >> 4) & 0x0f0f0f0fu : v1 & 0x0f0f0f0fu;
+  const float a = HI ? f.a_hi : f.a_lo, b = HI ? f.b_hi : f.b_lo;
+  half8_t w;
+  w[0] = (_Float16)(a * ubyte0(q0) - b);
+  w[1] = (_Float16)(a * ubyte1(q0) - b);
+  w[2] = (_Float16)(a * ubyte2(q0) - b);
+  w[3] = (_Float16)(a * ubyte3(q0) - b);
+  w[4] = (_Float16)(a * ubyte0(q1) - b);
+  w[5] = (_Float16)(a * ubyte1(q1) - b);
+  w[6] = (_Float16)(a * ubyte2(q1) - b);
+  w[7] = (_Float16)(a * ubyte3(q1) - b);
+  *reinterpret_cast<half8_t *>(dst + (HI ? 32 : 0) + H * c + 8 * P) = w;
 }
 
 template <uint32_t FMT, int WPT>
