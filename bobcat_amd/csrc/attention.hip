@@ -222,7 +222,7 @@ uint32_t attention_splits(uint32_t n_keys_max, uint32_t n_kv_heads, uint32_t n_c
 }
 
 uint64_t attention_partial_floats(uint32_t n_queries, uint32_t n_heads, uint32_t head_dim, uint32_t splits) {
-  return (uint64_t)n_queries * n_heads * splits * (head_dim + 2);
+  return (uint64_t)n_queries * n_heads * splits * (head_dim + 4);  // decode partials: 4 + head_dim floats
 }
 
 void run_attention(hipStream_t s, const float *q, const void *k_cache, const void *v_cache, bool kv_half,

@@ -27,6 +27,14 @@ TOLERANCE = 1e-4
 HALF_TOLERANCE = 5e-3
 
 
+def set_grouped(monkeypatch, grouped):
+    """Decode attention with every query head of a KV group in one workgroup
+    (the long-context layout) from the first split on, instead of only when
+    the one-head grid would exceed a round of workgroups."""
+    if grouped:
+        monkeypatch.setenv("BCH_ATTN_GROUPED_ABOVE", "0")
+
+
 def rel(got, want):
     got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
     d = np.abs(got - want)
@@ -44,8 +52,10 @@ def prompt(cfg, n, seed=1):
     return np.random.default_rng(seed).integers(0, cfg.n_vocab, n).tolist()
 
 
+@pytest.mark.parametrize("grouped", [False, True], ids=["head_per_wg", "grouped"])
 @pytest.mark.parametrize("kv_half", [False, True])
-def test_steps_match_oracle_layer_by_layer(hip, weights, kv_half):
+def test_steps_match_oracle_layer_by_layer(hip, weights, kv_half, grouped, monkeypatch):
+    set_grouped(monkeypatch, grouped)
     cfg = weights.cfg
     tol = HALF_TOLERANCE if kv_half else TOLERANCE
     gpu = Lfm2Hip(hip, weights, n_ctx=48, kv_half=kv_half)
@@ -157,12 +167,14 @@ def test_prefill_in_batches_matches_one_batch(hip):
     b.close()
 
 
+@pytest.mark.parametrize("grouped", [False, True], ids=["head_per_wg", "grouped"])
 @pytest.mark.parametrize("kv_half", [False, True])
-def test_decode_across_attention_splits(hip, kv_half):
+def test_decode_across_attention_splits(hip, kv_half, grouped, monkeypatch):
     """Decode steps at positions 1020-1027 cross the split boundary at 1024
     (a split holds 128 f32 or 256 f16 positions of a 64-wide head), so the
     number of splits, and with it the cross-workgroup combine, changes
     between steps (8 to 9 f32 splits, 4 to 5 f16)."""
+    set_grouped(monkeypatch, grouped)
     w = Lfm2Weights(LFM2_TINY, seed=11)
     toks = prompt(LFM2_TINY, 1028, seed=6)
     gpu = Lfm2Hip(hip, w, n_ctx=1100, kv_half=kv_half)
@@ -177,13 +189,15 @@ def test_decode_across_attention_splits(hip, kv_half):
     gpu.close()
 
 
+@pytest.mark.parametrize("grouped", [False, True], ids=["head_per_wg", "grouped"])
 @pytest.mark.parametrize("kv_half", [False, True])
-def test_long_context_decode(hip, kv_half):
+def test_long_context_decode(hip, kv_half, grouped, monkeypatch):
     """A driver sized for a long context (n_ctx 8192: 64 splits of 128 f32 or
     32 of 256 f16 positions, four query heads per KV head) launches a grid of
-    that many splits, dealt to the XCDs by KV group; steps at positions
+    that many splits; steps at positions
     1020-1027 run with 4 to 9 live splits and the parallel split combine,
     against the oracle, and against a driver sized for 1100."""
+    set_grouped(monkeypatch, grouped)
     w = Lfm2Weights(LFM2_TINY_F16, seed=12)
     toks = prompt(LFM2_TINY_F16, 1028, seed=9)
     big = Lfm2Hip(hip, w, n_ctx=8192, kv_half=kv_half)

@@ -31,6 +31,14 @@ PREFILL_TOLERANCE = 1e-3
 HALF_TOLERANCE = 5e-3
 
 
+def set_grouped(monkeypatch, grouped):
+    """Decode attention with every query head of a KV group in one workgroup
+    (the long-context layout) from the first split on, instead of only when
+    the one-head grid would exceed a round of workgroups."""
+    if grouped:
+        monkeypatch.setenv("BCH_ATTN_GROUPED_ABOVE", "0")
+
+
 def rel(got, want):
     got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
     d = np.abs(got - want)
@@ -49,8 +57,10 @@ def prompt(cfg, n, seed=1):
     return np.random.default_rng(seed).integers(0, cfg.n_vocab, n).tolist()
 
 
+@pytest.mark.parametrize("grouped", [False, True], ids=["head_per_wg", "grouped"])
 @pytest.mark.parametrize("kv_half", [False, True])
-def test_steps_match_oracle_layer_by_layer(hip, weights, kv_half):
+def test_steps_match_oracle_layer_by_layer(hip, weights, kv_half, grouped, monkeypatch):
+    set_grouped(monkeypatch, grouped)
     cfg = weights.cfg
     tol = HALF_TOLERANCE if kv_half else TOLERANCE
     gpu = Qwen35Hip(hip, weights, n_ctx=40, kv_half=kv_half)
@@ -326,14 +336,17 @@ def test_attention_gate_matches_float64(hip):
     assert rel(got, attn * (1 / (1 + np.exp(-gate)))) < 1e-6
 
 
+@pytest.mark.parametrize("head_dim", [64, 256])
+@pytest.mark.parametrize("grouped", [False, True], ids=["head_per_wg", "grouped"])
 @pytest.mark.parametrize("kv_half", [False, True])
-def test_long_context_gated_decode(hip, kv_half):
+def test_long_context_gated_decode(hip, kv_half, grouped, head_dim, monkeypatch):
     """Four query heads per KV head in a driver sized for 8192 positions: the
     gated decode kernel over a grid of many splits; steps at positions
-    1020-1027 (4 to 9 live splits, combined in parallel) against the
+    1020-1027 (4 to 33 live splits, combined in parallel) against the
     oracle."""
+    set_grouped(monkeypatch, grouped)
     cfg = Qwen35Config("qwen3.5-group4", n_embd=256, n_ff=512, n_vocab=500, n_layers=4, n_heads=4,
-                       n_kv_heads=1, head_dim=64, n_rot=32, n_k_heads=2, n_v_heads=4, k_head_dim=64,
+                       n_kv_heads=1, head_dim=head_dim, n_rot=32, n_k_heads=2, n_v_heads=4, k_head_dim=64,
                        v_head_dim=64)
     w = Qwen35Weights(cfg, seed=13)
     toks = prompt(cfg, 1028, seed=10)
