@@ -21,40 +21,33 @@ __device__ __forceinline__ uint64_t route_key(float v, uint32_t index) {
   return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - index);
 }
 
-__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const uint64_t o = ((uint64_t)__shfl_xor((uint32_t)(k >> 32), off, 64) << 32) |
-                       (uint64_t)__shfl_xor((uint32_t)k, off, 64);
-    k = k > o ? k : o;
-  }
-  return k;
-}
-
 // Wave 0 of a workgroup: the n_used experts of largest score + bias, ties to
 // the lower expert, and their normalised weights, into out (ids, then
-// weights as float bits).
+// weights as float bits).  Each expert's rank is the number of experts whose
+// (score + bias, index) key is larger, counted by its lane over the keys in
+// LDS (no cross-lane reductions on the critical path); ranks below n_used
+// are the picks, in order.
 __device__ void pick_route(const float *score, const float *__restrict__ bias, uint32_t *__restrict__ out,
                            uint32_t n_experts, uint32_t n_used) {
+  __shared__ uint64_t key_s[kMoeMaxExperts];
+  __shared__ uint32_t pick_s[kMoeMaxUsed];
   const uint32_t lane = threadIdx.x % 64;
-  // Lane l holds experts l and l + 64.
-  uint64_t k0 = lane < n_experts ? route_key(score[lane] + bias[lane], lane) : 0;
-  uint64_t k1 = lane + 64 < n_experts ? route_key(score[lane + 64] + bias[lane + 64], lane + 64) : 0;
-  float sum = 0.f;
-  uint32_t picked[kMoeMaxUsed];
-  for (uint32_t k = 0; k < n_used; k++) {
-    const uint64_t best = wave_max_key(k0 > k1 ? k0 : k1);
-    const uint32_t e = 0xffffffffu - (uint32_t)best;
-    if (e == lane) k0 = 0;
-    if (e == lane + 64) k1 = 0;
-    picked[k] = e;
-    sum += score[e];  // in pick order, as the reference sums the sorted picks
+  for (uint32_t e = lane; e < n_experts; e += 64) key_s[e] = route_key(score[e] + bias[e], e);
+  __builtin_amdgcn_wave_barrier();
+  for (uint32_t e = lane; e < n_experts; e += 64) {
+    const uint64_t ke = key_s[e];
+    uint32_t rank = 0;
+    for (uint32_t j = 0; j < n_experts; j++) rank += key_s[j] > ke ? 1u : 0u;
+    if (rank < n_used) pick_s[rank] = e;
   }
-  const float norm = sum + 1e-6f;  // transformers adds 1e-6 (lfm2.rs:703-705)
+  __builtin_amdgcn_wave_barrier();
   if (lane == 0) {
+    float sum = 0.f;
+    for (uint32_t k = 0; k < n_used; k++) sum += score[pick_s[k]];  // in pick order, as the reference sums the sorted picks
+    const float norm = sum + 1e-6f;  // transformers adds 1e-6 (lfm2.rs:703-705)
     for (uint32_t k = 0; k < n_used; k++) {
-      out[k] = picked[k];
-      out[n_used + k] = __float_as_uint(score[picked[k]] / norm);
+      out[k] = pick_s[k];
+      out[n_used + k] = __float_as_uint(score[pick_s[k]] / norm);
     }
   }
 }
@@ -239,27 +232,26 @@ __global__ __launch_bounds__(256) void k_moe_scores(const float *__restrict__ x,
   if (lane == 0) coherent_store(&counters[t], 0u);
 }
 
-// y[r] += Σ_slot w_slot · (W_{e_slot} row r) · x_slot for one token.  The
-// workgroup stages the USED inputs in LDS (a padded slot per unit, as the
-// GEMV does); a group of LPR lanes takes a row, lane i unit i, loads the
-// row of every picked expert at once, and adds the experts in route order.
+// y[r] += Σ_slot w_slot · (W_{e_slot} row r) · x_slot for one token.  A
+// group of LPR lanes takes a row, lane i unit i, for every picked expert.
+// Load order sets the latency: the route (scalar loads) and the USED inputs
+// are requested first, every weight load of the workgroup's rows as soon as
+// the route has arrived, and the inputs are staged in LDS (a padded slot
+// per unit, as the GEMV does) while the weights are on their way.  The
+// experts are added in route order.
 template <class F, int LPR, int USED>
 __global__ __launch_bounds__(256) void k_experts_down(const uint8_t *__restrict__ W, uint64_t rb, uint32_t n_rows,
                                                       uint32_t n_cols, const float *__restrict__ x,
                                                       const uint32_t *__restrict__ route, float *__restrict__ y) {
   constexpr int T = 256, G = T / LPR;
   constexpr uint32_t kSlot = F::kUnit + (F::kUnit >= 64 ? 4 : 0);
+  // float4 of the inputs per thread held in registers (the rest, if any,
+  // staged after the weights are requested).
+  constexpr int kPer = std::min(8, (USED * LPR * (int)F::kUnit / 4 + T - 1) / T);
   extern __shared__ float4 xs4[];
   float *xs = reinterpret_cast<float *>(xs4);
   const uint32_t tid = threadIdx.x, n_units = n_cols / F::kUnit, per_input = n_units * kSlot;
-  for (int k = 0; k < USED; k++) {
-    const float4 *x4 = reinterpret_cast<const float4 *>(x + (uint64_t)k * n_cols);
-    for (uint32_t i = tid; i < n_cols / 4; i += T) {
-      const uint32_t e = 4 * i;
-      *reinterpret_cast<float4 *>(xs + k * per_input + (e / F::kUnit) * kSlot + e % F::kUnit) = x4[i];
-    }
-  }
-  __syncthreads();
+  const uint32_t n4 = n_cols / 4, all4 = USED * n4;
   uint32_t ids[USED];
   float wts[USED];
 #pragma unroll
@@ -267,26 +259,45 @@ __global__ __launch_bounds__(256) void k_experts_down(const uint8_t *__restrict_
     ids[k] = route[k];
     wts[k] = __uint_as_float(route[USED + k]);
   }
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  float4 xv[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; j++) xv[j] = x4[min(tid + j * T, all4 - 1)];
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
   const uint32_t g = tid / LPR, li = tid % LPR;
   const bool active = li < n_units;
   const uint32_t unit = active ? li : 0u;
-  for (uint32_t r = blockIdx.x * G + g; r < n_rows; r += gridDim.x * G) {
-    typename F::Raw raw[USED];
+  const uint32_t r = blockIdx.x * G + g, rc = min(r, n_rows - 1);
+  typename F::Raw raw[USED];
 #pragma unroll
-    for (int k = 0; k < USED; k++) raw[k] = F::fetch(W + ((uint64_t)ids[k] * n_rows + r) * rb, unit);
-    float dots[USED];
+  for (int k = 0; k < USED; k++) raw[k] = F::fetch(W + ((uint64_t)ids[k] * n_rows + rc) * rb, unit);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  // Staging: input k's element e goes to slot k·per_input + (e / kUnit)·kSlot
+  // + e % kUnit.  Clamped duplicates rewrite the same value.
 #pragma unroll
-    for (int k = 0; k < USED; k++) {
-      typename F::Frag f;
-      F::from_lds(xs + k * per_input + unit * kSlot, f);
-      dots[k] = group_sum<LPR>(active ? F::compute(raw[k], unit, f) : 0.f);
-    }
-    if (li == 0) {
-      float acc = 0.f;
+  for (int j = 0; j < kPer; j++) {
+    const uint32_t i = min(tid + j * T, all4 - 1), k = i / n4, e = 4 * (i % n4);
+    *reinterpret_cast<float4 *>(xs + k * per_input + (e / F::kUnit) * kSlot + e % F::kUnit) = xv[j];
+  }
+  for (uint32_t i = tid + kPer * T; i < all4; i += T) {
+    const uint32_t k = i / n4, e = 4 * (i % n4);
+    *reinterpret_cast<float4 *>(xs + k * per_input + (e / F::kUnit) * kSlot + e % F::kUnit) = x4[i];
+  }
+  lds_barrier();
+  float dots[USED];
 #pragma unroll
-      for (int k = 0; k < USED; k++) acc += wts[k] * dots[k];
-      y[r] += acc;
-    }
+  for (int k = 0; k < USED; k++) {
+    typename F::Frag f;
+    F::from_lds(xs + k * per_input + unit * kSlot, f);
+    dots[k] = group_sum<LPR>(active ? F::compute(raw[k], unit, f) : 0.f);
+  }
+  if (li == 0 && r < n_rows) {
+    float acc = 0.f;
+#pragma unroll
+    for (int k = 0; k < USED; k++) acc += wts[k] * dots[k];
+    y[r] += acc;
   }
 }
 
@@ -316,7 +327,7 @@ static void launch_down(hipStream_t s, const uint8_t *W, uint32_t n_rows, uint32
   const uint64_t rb = bch_row_bytes(F::kFormat, n_cols);
   const size_t lds = (size_t)n_used * (n_cols / F::kUnit) * kSlot * 4;
   const uint32_t groups = 256 / LPR;
-  const uint32_t grid = std::max(1u, std::min((n_rows + groups - 1) / groups, 2 * n_cus));
+  const uint32_t grid = (n_rows + groups - 1) / groups;  // one row per group
   switch (n_used) {
 #define BCH_DOWN(U)                                                                                              \
   case U: {                                                                                                      \
