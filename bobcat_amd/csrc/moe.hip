@@ -26,29 +26,41 @@ __device__ __forceinline__ uint64_t route_key(float v, uint32_t index) {
 // weights as float bits).  Each expert's rank is the number of experts whose
 // (score + bias, index) key is larger, counted by its lane over the keys in
 // LDS (no cross-lane reductions on the critical path); ranks below n_used
-// are the picks, in order.
-__device__ void pick_route(const float *score, const float *__restrict__ bias, uint32_t *__restrict__ out,
-                           uint32_t n_experts, uint32_t n_used) {
+// are the picks, in order.  score and bias are in LDS.
+__device__ void pick_route(const float *score, const float *bias, uint32_t *__restrict__ out, uint32_t n_experts,
+                           uint32_t n_used) {
   __shared__ uint64_t key_s[kMoeMaxExperts];
   __shared__ uint32_t pick_s[kMoeMaxUsed];
+  __shared__ float pscore_s[kMoeMaxUsed];
   const uint32_t lane = threadIdx.x % 64;
   for (uint32_t e = lane; e < n_experts; e += 64) key_s[e] = route_key(score[e] + bias[e], e);
   __builtin_amdgcn_wave_barrier();
   for (uint32_t e = lane; e < n_experts; e += 64) {
     const uint64_t ke = key_s[e];
     uint32_t rank = 0;
-    for (uint32_t j = 0; j < n_experts; j++) rank += key_s[j] > ke ? 1u : 0u;
-    if (rank < n_used) pick_s[rank] = e;
+    // Eight keys' reads in flight at a time (the count is independent of
+    // the order; the clamped duplicates of the last block are not counted).
+    for (uint32_t j0 = 0; j0 < n_experts; j0 += 8) {
+      uint64_t kj[8];
+#pragma unroll
+      for (uint32_t u = 0; u < 8; u++) kj[u] = key_s[min(j0 + u, n_experts - 1)];
+#pragma unroll
+      for (uint32_t u = 0; u < 8; u++) rank += (j0 + u < n_experts && kj[u] > ke) ? 1u : 0u;
+    }
+    if (rank < n_used) {
+      pick_s[rank] = e;
+      pscore_s[rank] = score[e];
+    }
   }
   __builtin_amdgcn_wave_barrier();
-  if (lane == 0) {
-    float sum = 0.f;
-    for (uint32_t k = 0; k < n_used; k++) sum += score[pick_s[k]];  // in pick order, as the reference sums the sorted picks
-    const float norm = sum + 1e-6f;  // transformers adds 1e-6 (lfm2.rs:703-705)
-    for (uint32_t k = 0; k < n_used; k++) {
-      out[k] = pick_s[k];
-      out[n_used + k] = __float_as_uint(score[pick_s[k]] / norm);
-    }
+  // Every lane sums the picked scores in pick order (as the reference sums
+  // the sorted picks); lane k < n_used writes pick k.
+  float sum = 0.f;
+  for (uint32_t k = 0; k < n_used; k++) sum += pscore_s[k];
+  const float norm = sum + 1e-6f;  // transformers adds 1e-6 (lfm2.rs:703-705)
+  if (lane < n_used) {
+    out[lane] = pick_s[lane];
+    out[n_used + lane] = __float_as_uint(pscore_s[lane] / norm);
   }
 }
 
@@ -63,7 +75,7 @@ __global__ __launch_bounds__(1024) void k_moe_route(const float *__restrict__ x,
                                                     uint32_t n_used) {
   extern __shared__ float xs[];
   __shared__ float red[16];
-  __shared__ float score[kMoeMaxExperts];
+  __shared__ float score[kMoeMaxExperts], bias_s[kMoeMaxExperts];
   const uint32_t t = blockIdx.x, tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
   const float *row = x + (uint64_t)t * n_cols;
   // Router rows of this wave's experts (e0 + 16k), kU float4 per lane per
@@ -82,22 +94,49 @@ __global__ __launch_bounds__(1024) void k_moe_route(const float *__restrict__ x,
       w[k][u] = (e_ < n_experts && i_ < n4) ? r4_[i_] : make_float4(0.f, 0.f, 0.f, 0.f);             \
     }                                                                                                \
   }
-  BCH_ROUTER_LOAD(wave, 0u)
-  float ss = 0.f;
-  for (uint32_t i = tid; i < n_cols; i += 1024) {
-    const float v = row[i];
-    xs[i] = v;
-    ss = fmaf(v, v, ss);
+  // The token's inputs and norm weights (two per thread for rows of up to
+  // 2,048 columns) are requested before the router rows: memory returns in
+  // issue order, so the norm waits for them alone.
+  constexpr int kX = 2;
+  float xv[kX], nv[kX];
+#pragma unroll
+  for (int j = 0; j < kX; j++) {
+    const uint32_t i = min(tid + 1024 * j, n_cols - 1);
+    xv[j] = row[i];
+    nv[j] = norm_w ? norm_w[i] : 1.f;
   }
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  BCH_ROUTER_LOAD(wave, 0u)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kX; j++) {
+    const uint32_t i = tid + 1024 * j;
+    ss = i < n_cols ? fmaf(xv[j], xv[j], ss) : ss;
+  }
+  for (uint32_t i = tid + 1024 * kX; i < n_cols; i += 1024) ss = fmaf(row[i], row[i], ss);
+  float scale = 1.f;
   if (norm_w) {
     ss = block_sum<1024>(ss, red);
-    const float scale = (float)(1.0 / sqrt((double)ss / (double)n_cols + (double)eps));
-    for (uint32_t i = tid; i < n_cols; i += 1024) {
-      const float v = norm_w[i] * (xs[i] * scale);
+    scale = (float)(1.0 / sqrt((double)ss / (double)n_cols + (double)eps));
+  }
+#pragma unroll
+  for (int j = 0; j < kX; j++) {
+    const uint32_t i = tid + 1024 * j;
+    if (i < n_cols) {
+      const float v = norm_w ? nv[j] * (xv[j] * scale) : xv[j];
       xs[i] = v;
-      normed[(uint64_t)t * n_cols + i] = v;
+      if (norm_w) normed[(uint64_t)t * n_cols + i] = v;
     }
   }
+  for (uint32_t i = tid + 1024 * kX; i < n_cols; i += 1024) {
+    const float v = norm_w ? norm_w[i] * (row[i] * scale) : row[i];
+    xs[i] = v;
+    if (norm_w) normed[(uint64_t)t * n_cols + i] = v;
+  }
+  for (uint32_t i = tid; i < n_experts; i += 1024) bias_s[i] = bias[i];
   __syncthreads();
   // Each lane sums its columns in increasing order, then the wave sums.
   for (uint32_t e0 = wave; e0 < n_experts; e0 += 16 * kE) {
@@ -128,7 +167,7 @@ __global__ __launch_bounds__(1024) void k_moe_route(const float *__restrict__ x,
 #undef BCH_ROUTER_LOAD
   __syncthreads();
   if (wave != 0) return;
-  pick_route(score, bias, route + (uint64_t)t * 2 * n_used, n_experts, n_used);
+  pick_route(score, bias_s, route + (uint64_t)t * 2 * n_used, n_experts, n_used);
 }
 
 // Routes of decode and prefill tokens with the router spread over the chip:
@@ -147,33 +186,41 @@ __global__ __launch_bounds__(256) void k_moe_scores(const float *__restrict__ x,
                                                     uint32_t n_used) {
   extern __shared__ float xs[];
   __shared__ float red[4];
-  __shared__ float score_s[kMoeMaxExperts];
+  __shared__ float score_s[kMoeMaxExperts], bias_s[kMoeMaxExperts];
   __shared__ uint32_t last_s;
   const uint32_t t = blockIdx.x, tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
   const uint32_t e = 4 * blockIdx.y + wave, n4 = n_cols / 4;
   constexpr int kU = 8, kX = 8;  // router float4 per lane per pass; input elements per thread held
-  const float4 *r4 = reinterpret_cast<const float4 *>(router + (uint64_t)min(e, n_experts - 1) * n_cols);
-  float4 w[kU];
-#pragma unroll
-  for (int u = 0; u < kU; u++) {
-    const uint32_t i = lane + 64 * u;
-    w[u] = (e < n_experts && i < n4) ? r4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+  // The token's inputs and norm weights first, then the router row: memory
+  // returns in issue order, so the norm waits for the inputs alone.  Loads
+  // are unconditional (clamped indices), so the waits count exactly.
   const float *row = x + (uint64_t)t * n_cols;
   float xv[kX], nv[kX];
 #pragma unroll
   for (int j = 0; j < kX; j++) {
-    const uint32_t i = tid + 256 * j;
-    xv[j] = i < n_cols ? row[i] : 0.f;
-    nv[j] = (norm_w && i < n_cols) ? norm_w[i] : 0.f;
+    const uint32_t i = min(tid + 256 * j, n_cols - 1);
+    xv[j] = row[i];
+    nv[j] = norm_w ? norm_w[i] : 1.f;
   }
+  const float bv = bias[min(tid, n_experts - 1)];  // for the route pick (n_experts <= 256 threads)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  const float4 *r4 = reinterpret_cast<const float4 *>(router + (uint64_t)min(e, n_experts - 1) * n_cols);
+  float4 w[kU];
+#pragma unroll
+  for (int u = 0; u < kU; u++) w[u] = r4[min(lane + 64 * u, n4 - 1)];
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
   float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < kX; j++) ss = fmaf(xv[j], xv[j], ss);
+  for (int j = 0; j < kX; j++) ss = tid + 256 * j < n_cols ? fmaf(xv[j], xv[j], ss) : ss;
   for (uint32_t i = tid + 256 * kX; i < n_cols; i += 256) ss = fmaf(row[i], row[i], ss);
   float scale = 1.f;
   if (norm_w) {
-    ss = block_sum<256>(ss, red);
+    ss = wave_sum(ss);
+    if (lane == 0) red[wave] = ss;
+    lds_barrier();
+    ss = red[0] + red[1] + red[2] + red[3];
     scale = (float)(1.0 / sqrt((double)ss / (double)n_cols + (double)eps));
   }
   // Staged as rms_norm computes it: w·(x·scale).
@@ -183,9 +230,8 @@ __global__ __launch_bounds__(256) void k_moe_scores(const float *__restrict__ x,
     if (i < n_cols) xs[i] = norm_w ? nv[j] * (xv[j] * scale) : xv[j];
   }
   for (uint32_t i = tid + 256 * kX; i < n_cols; i += 256) xs[i] = norm_w ? norm_w[i] * (row[i] * scale) : row[i];
-  if (norm_w && blockIdx.y == 0)
-    for (uint32_t i = tid; i < n_cols; i += 256) normed[(uint64_t)t * n_cols + i] = xs[i];  // own elements only
-  __syncthreads();
+  if (tid < n_experts) bias_s[tid] = bv;
+  lds_barrier();
   // Each lane sums its columns in increasing order, then the wave sums (the
   // order k_moe_route uses).
   if (e < n_experts) {
@@ -210,6 +256,8 @@ __global__ __launch_bounds__(256) void k_moe_scores(const float *__restrict__ x,
     acc = wave_sum(acc);
     if (lane == 0) coherent_store(scores + (uint64_t)t * n_experts + e, 1.0f / (1.0f + expf(-acc)));
   }
+  if (norm_w && blockIdx.y == 0)
+    for (uint32_t i = tid; i < n_cols; i += 256) normed[(uint64_t)t * n_cols + i] = xs[i];
   // Hand-off to the token's last workgroup, by the hardware's ordering (as
   // in attn_decode.hip; an agent-scope release would write back the whole
   // L2): the scores are agent-scope atomic stores written through to the
@@ -228,7 +276,7 @@ __global__ __launch_bounds__(256) void k_moe_scores(const float *__restrict__ x,
   if (!last_s || wave != 0) return;
   for (uint32_t i = lane; i < n_experts; i += 64) score_s[i] = coherent_load(scores + (uint64_t)t * n_experts + i);
   __builtin_amdgcn_wave_barrier();
-  pick_route(score_s, bias, route + (uint64_t)t * 2 * n_used, n_experts, n_used);
+  pick_route(score_s, bias_s, route + (uint64_t)t * 2 * n_used, n_experts, n_used);
   if (lane == 0) coherent_store(&counters[t], 0u);
 }
 
