@@ -283,7 +283,7 @@ constexpr uint32_t kGroupedAbove = 1024;
 // CPR: 16-byte chunks per cache row (head_dim * element size / 16); HPW:
 // query heads per workgroup (a divisor of the group) for long contexts.
 template <bool HALF, int CPR, int HPW>
-__global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
+__device__ __forceinline__ void attn_decode_body(const AttnDecodeArgs &a) {
   constexpr uint32_t kElem = HALF ? 2 : 4;
   constexpr uint32_t kEpc = 16 / kElem;  // elements per chunk
   constexpr uint32_t hd = CPR * kEpc;    // head size
@@ -494,52 +494,92 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
   }
   lds_barrier();
 
-  // 4. Each head's softmax over the split's keys, by the whole workgroup.
-  constexpr uint32_t kPer = (kps + kDecThreads - 1) / kDecThreads;
-  float e[HPW][kPer];
-#pragma unroll
-  for (uint32_t j = 0; j < kPer; j++) {
-    const uint32_t r = min(tid + kDecThreads * j, kps - 1);
-    const float4 v4 = p_s[r];
-    const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
-#pragma unroll
-    for (int h = 0; h < HPW; h++) e[h][j] = tid + kDecThreads * j < len ? vv[h] : -INFINITY;
-  }
-#pragma unroll
-  for (int h = 0; h < HPW; h++) {
-    float mx = -INFINITY;
-#pragma unroll
-    for (uint32_t j = 0; j < kPer; j++) mx = fmaxf(mx, e[h][j]);
-    mx = wave_max(mx);
-    if (lane == 0) mw_s[wave][h] = mx;
-  }
-  lds_barrier();
-  float sums[HPW];
-#pragma unroll
-  for (int h = 0; h < HPW; h++) {
-    float mx = mw_s[0][h];
-#pragma unroll
-    for (int w = 1; w < kWaves; w++) mx = fmaxf(mx, mw_s[w][h]);
-    sums[h] = 0.f;
+  // 4-5 for NH heads (the run-time head count, HPW or one): each head's
+  // softmax over the split's keys by the whole workgroup, then P·V.
+  auto softmax_pv = [&]<int NH>() {
+    // 4. Each head's softmax over the split's keys, by the whole workgroup.
+    constexpr uint32_t kPer = (kps + kDecThreads - 1) / kDecThreads;
+    float e[NH][kPer];
 #pragma unroll
     for (uint32_t j = 0; j < kPer; j++) {
-      e[h][j] = expf(e[h][j] - mx);
-      sums[h] += e[h][j];
+      const uint32_t r = min(tid + kDecThreads * j, kps - 1);
+      const float4 v4 = p_s[r];
+      const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+      for (int h = 0; h < NH; h++) e[h][j] = tid + kDecThreads * j < len ? vv[h] : -INFINITY;
     }
-  }
 #pragma unroll
-  for (uint32_t j = 0; j < kPer; j++) {
-    const uint32_t r = tid + kDecThreads * j;
-    if (r < kps)
-      p_s[r] = make_float4(e[0][j], HPW > 1 ? e[HPW > 1 ? 1 : 0][j] : 0.f, HPW > 2 ? e[HPW > 2 ? 2 : 0][j] : 0.f,
-                           HPW > 3 ? e[HPW > 3 ? 3 : 0][j] : 0.f);
-  }
+    for (int h = 0; h < NH; h++) {
+      float mx = -INFINITY;
 #pragma unroll
-  for (int h = 0; h < HPW; h++) {
-    const float sum = wave_sum(sums[h]);
-    if (lane == 0) lw_s[wave][h] = sum;
+      for (uint32_t j = 0; j < kPer; j++) mx = fmaxf(mx, e[h][j]);
+      mx = wave_max(mx);
+      if (lane == 0) mw_s[wave][h] = mx;
+    }
+    lds_barrier();
+    float sums[NH];
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+      float mx = mw_s[0][h];
+#pragma unroll
+      for (int w = 1; w < kWaves; w++) mx = fmaxf(mx, mw_s[w][h]);
+      sums[h] = 0.f;
+#pragma unroll
+      for (uint32_t j = 0; j < kPer; j++) {
+        e[h][j] = expf(e[h][j] - mx);
+        sums[h] += e[h][j];
+      }
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kPer; j++) {
+      const uint32_t r = tid + kDecThreads * j;
+      if (r < kps)
+        p_s[r] = make_float4(e[0][j], NH > 1 ? e[NH > 1 ? 1 : 0][j] : 0.f, NH > 2 ? e[NH > 2 ? 2 : 0][j] : 0.f,
+                             NH > 3 ? e[NH > 3 ? 3 : 0][j] : 0.f);
+    }
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+      const float sum = wave_sum(sums[h]);
+      if (lane == 0) lw_s[wave][h] = sum;
+    }
+    lds_barrier();
+    // 5. P·V from the value chunks in registers: each lane accumulates its
+    // column over its rows (weights of keys past the split's end are zero),
+    // the row slots of a wave are summed by lane moves, and the waves through
+    // LDS.
+    constexpr int kN = NH * (int)kEpc;
+    float acc[kN];
+#pragma unroll
+    for (int k = 0; k < kN; k++) acc[k] = 0.f;
+#pragma unroll
+    for (int i = 0; i < kChunks; i++) {
+      if (wave_row0 + i * kRowsPerPass >= len) break;
+      const float4 pw = p_s[row0 + i * kRowsPerPass];
+      const float pv[4] = {pw.x, pw.y, pw.z, pw.w};
+#pragma unroll
+      for (int h = 0; h < NH; h++) fma_chunk<HALF>(pv[h], vreg[i], acc + h * kEpc);
+    }
+    using Rs = RowSlotSum<CPR, kN>;
+    float red[Rs::kOut];
+    Rs::run(acc, red);
+    if (lane % 16 < (uint32_t)CPR) {
+      const uint32_t sel = Rs::sel(lane);
+#pragma unroll
+      for (int k = 0; k < Rs::kOut; k++) {
+        const uint32_t idx = k * Rs::kStep + sel, h = idx / kEpc, j = idx % kEpc;
+        red_s[wave][h * hd + c * kEpc + j] = red[k];
+      }
+    }
+    lds_barrier();
+  };
+  if constexpr (HPW == 1) {
+    softmax_pv.template operator()<1>();
+  } else {
+    if (hpw == HPW)
+      softmax_pv.template operator()<HPW>();
+    else
+      softmax_pv.template operator()<1>();
   }
-  lds_barrier();
   // Head h's maximum and sum, from the per-wave values in LDS (a register
   // array indexed by a run-time head would go to scratch memory).
   auto head_max = [&](uint32_t h) {
@@ -554,35 +594,6 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
     for (int w = 0; w < kWaves; w++) l += lw_s[w][h];
     return l;
   };
-
-  // 5. P·V from the value chunks in registers: each lane accumulates its
-  // column over its rows (weights of keys past the split's end are zero),
-  // the row slots of a wave are summed by lane moves, and the waves through
-  // LDS.
-  constexpr int kN = HPW * (int)kEpc;
-  float acc[kN];
-#pragma unroll
-  for (int k = 0; k < kN; k++) acc[k] = 0.f;
-#pragma unroll
-  for (int i = 0; i < kChunks; i++) {
-    if (wave_row0 + i * kRowsPerPass >= len) break;
-    const float4 pw = p_s[row0 + i * kRowsPerPass];
-    const float pv[4] = {pw.x, pw.y, pw.z, pw.w};
-#pragma unroll
-    for (int h = 0; h < HPW; h++) fma_chunk<HALF>(pv[h], vreg[i], acc + h * kEpc);
-  }
-  using Rs = RowSlotSum<CPR, kN>;
-  float red[Rs::kOut];
-  Rs::run(acc, red);
-  if (lane % 16 < (uint32_t)CPR) {
-    const uint32_t sel = Rs::sel(lane);
-#pragma unroll
-    for (int k = 0; k < Rs::kOut; k++) {
-      const uint32_t idx = k * Rs::kStep + sel, h = idx / kEpc, j = idx % kEpc;
-      red_s[wave][h * hd + c * kEpc + j] = red[k];
-    }
-  }
-  lds_barrier();
 
   // 6. Output, directly or through the split partials (max, sum, pad,
   // pad, output[hd]: 16-byte aligned outputs).  The output gate of gated
@@ -702,6 +713,19 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
     a.out[(uint64_t)(head0 + h) * hd + f % hd] = O / cl_s[h] * gate[j];
   }
   if (tid == 0) coherent_store(&a.counters[head0], 0u);
+}
+
+// The kernel, in two forms: shapes whose body fits 128 registers without
+// spilling are held to that (four waves per SIMD: a 32K-context grid of
+// 1,024 workgroups resident at once); the others take what they need.
+template <bool HALF, int CPR, int HPW>
+__global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_attn_decode_w4(
+    AttnDecodeArgs a) {
+  attn_decode_body<HALF, CPR, HPW>(a);
+}
+template <bool HALF, int CPR, int HPW>
+__global__ __launch_bounds__(kDecThreads) void k_attn_decode(AttnDecodeArgs a) {
+  attn_decode_body<HALF, CPR, HPW>(a);
 }
 
 // CPR: 16-byte chunks per cache row (head_dim * element size / 16).  Query
@@ -899,15 +923,23 @@ RopeTable rope_table(float theta, uint32_t n_rot) {
   return f;
 }
 
+template <bool HALF, int CPR, int HPW>
+static void launch_decode_cpr(hipStream_t s, const AttnDecodeArgs &a, uint32_t grid) {
+  if constexpr ((HALF && CPR == 8) || (!HALF && CPR <= 16))
+    k_attn_decode_w4<HALF, CPR, HPW><<<grid, kDecThreads, 0, s>>>(a);
+  else
+    k_attn_decode<HALF, CPR, HPW><<<grid, kDecThreads, 0, s>>>(a);
+}
+
 template <bool HALF, int HPW>
 static void launch_decode(hipStream_t s, const AttnDecodeArgs &a, uint32_t grid) {
   switch (a.head_dim * (HALF ? 2 : 4) / 16) {
-    case 4: k_attn_decode<HALF, 4, HPW><<<grid, kDecThreads, 0, s>>>(a); break;
-    case 8: k_attn_decode<HALF, 8, HPW><<<grid, kDecThreads, 0, s>>>(a); break;
-    case 16: k_attn_decode<HALF, 16, HPW><<<grid, kDecThreads, 0, s>>>(a); break;
-    case 32: k_attn_decode<HALF, 32, HPW><<<grid, kDecThreads, 0, s>>>(a); break;
+    case 4: launch_decode_cpr<HALF, 4, HPW>(s, a, grid); break;
+    case 8: launch_decode_cpr<HALF, 8, HPW>(s, a, grid); break;
+    case 16: launch_decode_cpr<HALF, 16, HPW>(s, a, grid); break;
+    case 32: launch_decode_cpr<HALF, 32, HPW>(s, a, grid); break;
     case 64:
-      if constexpr (!HALF) k_attn_decode<HALF, 64, HPW><<<grid, kDecThreads, 0, s>>>(a);
+      if constexpr (!HALF) launch_decode_cpr<HALF, 64, HPW>(s, a, grid);
       break;
     default: break;  // rejected when the driver was created
   }
