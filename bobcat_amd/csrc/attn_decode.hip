@@ -194,16 +194,20 @@ __device__ __forceinline__ float dot_chunk(const float *q, const uint4 &c4) {
   return part;
 }
 
-// Four consecutive floats through the device coherence point (sc1), like
-// coherent_load; p is 16-byte aligned.  The caller waits for it with
-// wait_loads() before use.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ f32x4 coherent_load4(const float *p) {
-  f32x4 v;
-  asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
-  return v;
+// Buffer view of the split partials for loads through the device coherence
+// point (sc1), like coherent_load but 16 bytes at a time.  Buffer loads are
+// instructions the compiler knows and waits for (an inline-asm load is not:
+// the compiler may reuse its destination registers before the data lands).
+// Word 3 is the gfx9 raw-buffer format (32-bit data); loads past `bytes`
+// return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t partials_rsrc(const float *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), 0, bytes, 0x00020000);
 }
-__device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+constexpr int kCachePolicySc1 = 16;  // the sc1 bit of a buffer instruction's cache policy
+__device__ __forceinline__ f32x4 coherent_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, kCachePolicySc1);
+}
 
 // Chunk of 16 bytes (kEpc elements) of a cache row, as floats.
 template <bool HALF>
@@ -642,75 +646,106 @@ __device__ __forceinline__ void attn_decode_body(const AttnDecodeArgs &a) {
   __syncthreads();
   if (!last_s) return;
 
-  // Combine.  (a) Each head's overall maximum M and sum L by one wave, 256
-  // splits' (max, sum) loads in flight at a time, merged block by block.
-  __shared__ float cm_s[HPW], cl_s[HPW];
-  for (uint32_t h = wave; h < hpw; h += kWaves) {
-    const float *pp = a.partials + (uint64_t)(head0 + h) * a.max_splits * stride;
-    float M = -INFINITY, L = 0.f;
-    for (uint32_t b0 = 0; b0 < n_splits; b0 += 256) {
-      float mv[4], lv[4];
-#pragma unroll
-      for (int u = 0; u < 4; u++) {
-        const uint64_t at = (uint64_t)min(b0 + lane + 64 * u, n_splits - 1) * stride;
-        mv[u] = coherent_load(pp + at);
-        lv[u] = coherent_load(pp + at + 1);
-      }
-      float mb = -INFINITY;
-#pragma unroll
-      for (int u = 0; u < 4; u++) mb = fmaxf(mb, mv[u]);  // clamped duplicates change no maximum
-      const float Mn = fmaxf(M, wave_max(mb));
-      float lb = 0.f;
-#pragma unroll
-      for (int u = 0; u < 4; u++)
-        if (b0 + lane + 64 * u < n_splits) lb = fmaf(lv[u], expf(mv[u] - Mn), lb);
-      L = L * expf(M - Mn) + wave_sum(lb);
-      M = Mn;
-    }
-    if (lane == 0) cm_s[h] = M, cl_s[h] = L;
-  }
-  __syncthreads();
-  // (b) Output quads: `groups` threads per quad of 4 consecutive outputs,
-  // each summing every groups-th split with kBatch splits' loads in
-  // flight, then added over the groups through LDS.
+  // Combine.  `groups` threads per quad of 4 consecutive outputs, each
+  // taking every groups-th split; the groups merge through LDS.  When each
+  // thread's splits fit one batch of loads (short contexts), the (max, sum)
+  // headers and the output quads are loaded together and merged with a
+  // running maximum: one round of loads.  Otherwise each head's maximum
+  // comes first (one wave per head, 256 splits' headers at a time), then
+  // the quads in batches of kBatchB splits: fewer rounds than a running
+  // maximum over many small batches.
   const uint32_t quads = n_out / 4, groups = quads >= (uint32_t)kDecThreads ? 1u : kDecThreads / quads;
-  constexpr uint32_t kBatch = 12;
-  __shared__ f32x4 comb_s[kDecThreads];  // [group][quad]
+  constexpr uint32_t kBatchA = 8, kBatchB = 12;
+  __shared__ f32x4 comb_s[kDecThreads];  // [group][quad]: output quads
+  __shared__ float2 cml_s[kDecThreads];  // [group][quad]: (max, sum)
+  __shared__ float cm_s[HPW];
+  const bool one_round = n_splits <= groups * kBatchA;
+  if (!one_round) {
+    for (uint32_t h = wave; h < hpw; h += kWaves) {
+      const float *pp = a.partials + (uint64_t)(head0 + h) * a.max_splits * stride;
+      float M = -INFINITY;
+      for (uint32_t b0 = 0; b0 < n_splits; b0 += 256) {
+        float mv[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) mv[u] = coherent_load(pp + (uint64_t)min(b0 + lane + 64 * u, n_splits - 1) * stride);
+#pragma unroll
+        for (int u = 0; u < 4; u++) M = fmaxf(M, mv[u]);  // clamped duplicates change no maximum
+      }
+      M = wave_max(M);
+      if (lane == 0) cm_s[h] = M;
+    }
+    __syncthreads();
+  }
   if (tid < groups * quads) {
     const uint32_t qd = tid % quads, g = tid / quads, h = 4 * qd / hd, el = 4 * qd % hd;
-    const float *pp = a.partials + (uint64_t)(head0 + h) * a.max_splits * stride + 4 + el;
-    const float M = cm_s[h];
+    // One descriptor for the workgroup's heads (uniform: a per-lane
+    // descriptor would make the compiler loop over its distinct values).
+    const __amdgpu_buffer_rsrc_t rs =
+        partials_rsrc(a.partials + (uint64_t)head0 * a.max_splits * stride, hpw * a.max_splits * stride * 4);
+    const uint32_t hbase = h * a.max_splits;  // head h's first split
+    float M = -INFINITY, L = 0.f;
     f32x4 O = {0.f, 0.f, 0.f, 0.f};
-    for (uint32_t sp0 = g; sp0 < n_splits; sp0 += kBatch * groups) {
-      float mv[kBatch];
-      f32x4 ov[kBatch];
+    if (one_round) {
+      f32x4 hv[kBatchA], ov[kBatchA];
 #pragma unroll
-      for (uint32_t u = 0; u < kBatch; u++) {
-        const uint64_t at = (uint64_t)min(sp0 + u * groups, n_splits - 1) * stride;
-        ov[u] = coherent_load4(pp + at);
-        mv[u] = coherent_load(pp - 4 - el + at);
+      for (uint32_t u = 0; u < kBatchA; u++) {
+        const uint32_t at = (hbase + min(g + u * groups, n_splits - 1)) * stride * 4;
+        hv[u] = coherent_load4(rs, at);
+        ov[u] = coherent_load4(rs, at + 16 + 4 * el);
       }
-      wait_loads();
 #pragma unroll
-      for (uint32_t u = 0; u < kBatch; u++) {
-        const float w = sp0 + u * groups < n_splits ? expf(mv[u] - M) : 0.f;
+      for (uint32_t u = 0; u < kBatchA; u++) M = fmaxf(M, hv[u].x);  // clamped duplicates change no maximum
+#pragma unroll
+      for (uint32_t u = 0; u < kBatchA; u++) {
+        const float w = g + u * groups < n_splits ? expf(hv[u].x - M) : 0.f;
+        L = fmaf(hv[u].y, w, L);
         O.x = fmaf(ov[u].x, w, O.x);
         O.y = fmaf(ov[u].y, w, O.y);
         O.z = fmaf(ov[u].z, w, O.z);
         O.w = fmaf(ov[u].w, w, O.w);
       }
+    } else {
+      M = cm_s[h];
+      for (uint32_t sp0 = g; sp0 < n_splits; sp0 += kBatchB * groups) {
+        float2 mlv[kBatchB];
+        f32x4 ov[kBatchB];
+#pragma unroll
+        for (uint32_t u = 0; u < kBatchB; u++) {
+          const uint32_t at = (hbase + min(sp0 + u * groups, n_splits - 1)) * stride * 4;
+          const f32x4 hv = coherent_load4(rs, at);
+          mlv[u] = make_float2(hv.x, hv.y);
+          ov[u] = coherent_load4(rs, at + 16 + 4 * el);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kBatchB; u++) {
+          const float w = sp0 + u * groups < n_splits ? expf(mlv[u].x - M) : 0.f;
+          L = fmaf(mlv[u].y, w, L);
+          O.x = fmaf(ov[u].x, w, O.x);
+          O.y = fmaf(ov[u].y, w, O.y);
+          O.z = fmaf(ov[u].z, w, O.z);
+          O.w = fmaf(ov[u].w, w, O.w);
+        }
+      }
     }
     comb_s[g * quads + qd] = O;
+    cml_s[g * quads + qd] = make_float2(M, L);
   }
   __syncthreads();
   const float *comb = reinterpret_cast<const float *>(comb_s);
 #pragma unroll
   for (int j = 0; j < kOutPer; j++) {
-    const uint32_t f = tid + j * kDecThreads, h = f / hd;
+    const uint32_t f = tid + j * kDecThreads, h = f / hd, qd = f / 4;
     if (f >= n_out) break;
-    float O = 0.f;
-    for (uint32_t g = 0; g < groups; g++) O += comb[g * n_out + f];
-    a.out[(uint64_t)(head0 + h) * hd + f % hd] = O / cl_s[h] * gate[j];
+    float M = -INFINITY;
+    for (uint32_t g = 0; g < groups; g++) M = fmaxf(M, cml_s[g * quads + qd].x);
+    float O = 0.f, L = 0.f;
+    for (uint32_t g = 0; g < groups; g++) {
+      const float2 ml = cml_s[g * quads + qd];
+      const float w = expf(ml.x - M);  // 0 for a group without splits (max -inf)
+      L = fmaf(ml.y, w, L);
+      O = fmaf(comb[g * n_out + f], w, O);
+    }
+    a.out[(uint64_t)(head0 + h) * hd + f % hd] = O / L * gate[j];
   }
   if (tid == 0) coherent_store(&a.counters[head0], 0u);
 }
@@ -925,7 +960,7 @@ RopeTable rope_table(float theta, uint32_t n_rot) {
 
 template <bool HALF, int CPR, int HPW>
 static void launch_decode_cpr(hipStream_t s, const AttnDecodeArgs &a, uint32_t grid) {
-  if constexpr ((HALF && CPR == 8) || (!HALF && CPR <= 16))
+  if constexpr ((HALF && CPR == 8) || (!HALF && (CPR == 8 || CPR == 16)))
     k_attn_decode_w4<HALF, CPR, HPW><<<grid, kDecThreads, 0, s>>>(a);
   else
     k_attn_decode<HALF, CPR, HPW><<<grid, kDecThreads, 0, s>>>(a);
