@@ -149,18 +149,14 @@ __device__ float combine_partials(const float *pp, uint32_t n_splits, uint32_t s
   return out;
 }
 
-// fmaf(a, h, c) with h one half of a packed f16 pair, converted inside the
-// FMA (v_fma_mix_f32): the f16 value is exact in f32, so the result is that
-// of converting first and then fmaf, in one instruction instead of two.
+// fmaf(a, h, c) with h one half of a packed f16 pair.  The f16 value is
+// exact in f32; the compiler folds the conversion into the FMA
+// (v_fma_mix_f32), one instruction instead of two.
 __device__ __forceinline__ float fma_lo(float a, uint32_t pair, float c) {
-  float r;
-  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(pair), "v"(c));
-  return r;
+  return fmaf(a, (float)__builtin_bit_cast(_Float16, (unsigned short)(pair & 0xffffu)), c);
 }
 __device__ __forceinline__ float fma_hi(float a, uint32_t pair, float c) {
-  float r;
-  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(pair), "v"(c));
-  return r;
+  return fmaf(a, (float)__builtin_bit_cast(_Float16, (unsigned short)(pair >> 16)), c);
 }
 
 // acc[j] += w · (element j of a 16-byte cache chunk), j < 16 / element size.
