@@ -122,30 +122,40 @@ __global__ __launch_bounds__(256 * CB) void k_gdn_step(GdnArgs a) {
   const uint32_t key_head = head % a.n_k, key_dim = a.n_k * a.k_dim;
   const float *tok = a.y;
   float *S = a.state + (uint64_t)head * KD * a.v_dim + col;
-  // The state rows first: their loads overlap the norms below.
-  float rows[RW];
+  // The token's small inputs first, then the state rows: memory returns in
+  // issue order, so the norms below wait for the small loads alone and run
+  // while the state streams in.  The loads are unconditional (every wave
+  // reads a query or key row; waves past 1 discard theirs), so the waits
+  // count exactly.
+  const float *src = tok + (wave == 1 ? key_dim : 0u) + key_head * KD;
+  float e[KD / 64];
 #pragma unroll
-  for (int i = 0; i < RW; i++) rows[i] = S[(uint64_t)(wq * RW + i) * a.v_dim];
+  for (int i = 0; i < KD / 64; i++) e[i] = src[lane * (KD / 64) + i];
   const float v = tok[2 * key_dim + head * a.v_dim + col];
   const float gz = a.norm_w ? a.gate_z[(uint64_t)head * a.v_dim + col] : 0.f;
   const float nw = a.norm_w ? a.norm_w[col] : 0.f;
+  // The head's gate inputs (uniform: scalar loads).
+  const float gb = a.beta[head], gd = a.alpha[head];
+  const float ga = a.raw_gates ? a.a[head] : 0.f, gdt = a.raw_gates ? a.dt_bias[head] : 0.f;
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  float rows[RW];
+#pragma unroll
+  for (int i = 0; i < RW; i++) rows[i] = S[(uint64_t)(wq * RW + i) * a.v_dim];
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
   // Waves 0 and 1 normalise the query and the key (qwen35.rs:464-470).
   if (wave < 2) {
-    const float *src = tok + (wave == 0 ? 0u : key_dim) + key_head * KD;
-    float e[KD / 64], ss = 0.f;
+    float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < KD / 64; i++) {
-      e[i] = src[lane * (KD / 64) + i];
-      ss = fmaf(e[i], e[i], ss);
-    }
+    for (int i = 0; i < KD / 64; i++) ss = fmaf(e[i], e[i], ss);
     ss = wave_sum(ss);
     const float f = wave == 0 ? a.q_scale / sqrtf(ss + 1e-6f) : 1.0f / sqrtf(ss + 1e-6f);
 #pragma unroll
     for (int i = 0; i < KD / 64; i++) (wave == 0 ? qn : kn)[lane * (KD / 64) + i] = e[i] * f;
   } else if (wave == 2 && lane == 0) {
-    const float b = a.beta[head], d = a.alpha[head];
-    gate_s[0] = a.raw_gates ? sigmoid_f(b) : b;
-    gate_s[1] = a.raw_gates ? expf(a.a[head] * softplus_f(d + a.dt_bias[head])) : d;
+    gate_s[0] = a.raw_gates ? sigmoid_f(gb) : gb;
+    gate_s[1] = a.raw_gates ? expf(ga * softplus_f(gd + gdt)) : gd;
   }
   __syncthreads();
   const float beta = gate_s[0], decay = gate_s[1];
