@@ -121,6 +121,60 @@ def gemv_leg(hip, reps: int, copies: int = 64):
                 hot_us=hot * 1e6, hot_gbs=GEMV_BYTES / hot / 1e9)
 
 
+def decode_gemv_leg(hip, reps: int = 8, budget: int = 640 << 20):
+    """The slab GEMVs of one LFM2-2.6B decode token, each at its model shape,
+    for per-kernel counters: the SwiGLU pair (10752 x 2048, RMS-normalised
+    input), the down projection (2048 x 10752, accumulating), the conv layer's
+    in_proj with its gated short convolution (6144 x 2048) and out_proj/wo
+    (2048 x 2048, accumulating).  Each shape rotates over enough copies of
+    its weights (together ~640 MB, beyond the 256 MB MALL) that every launch
+    reads from HBM, as in the model.  Returns microseconds per launch."""
+    from bobcat_amd.backend import Format, NormSpec
+    from bobcat_amd.synth import q4k_matrix
+
+    rng = np.random.default_rng(11)
+    n = 2048
+    x = hip.buffer_from(rng.standard_normal(10752).astype(np.float32))
+    nw = hip.buffer_from((1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32))
+    y = hip.new_buffer(10752 * 4)
+    taps = hip.buffer_from((0.1 * rng.standard_normal(3 * n)).astype(np.float32))
+    hist = hip.new_buffer(2 * n * 4)
+    conv_out = hip.new_buffer(n * 4)
+    norm = NormSpec(nw.at(0), 1e-5)
+    out = {}
+    shapes = [("swiglu_10752x2048", 10752, 2048, 2), ("down_2048x10752", 2048, 10752, 1),
+              ("conv_in_6144x2048", 6144, 2048, 1), ("out_proj_2048x2048", 2048, 2048, 1)]
+    for name, rows, cols, mats in shapes:
+        w = q4k_matrix(rng, rows, cols)
+        copies = max(2, min(64, budget // (mats * w.nbytes)))
+        big = hip.new_buffer(copies * mats * w.nbytes)
+        for c in range(copies * mats):
+            hip.write(big.at(c * w.nbytes), w)
+
+        def launch(i):
+            at = (i % copies) * mats * w.nbytes
+            if name.startswith("swiglu"):
+                hip.matvec_swiglu(Format.Q4K, big.at(at), big.at(at + w.nbytes), rows, cols, x.at(0), norm, y.at(0))
+            elif name.startswith("conv"):
+                hip.matvec_conv(Format.Q4K, big.at(at), cols, x.at(0), norm, taps.at(0), hist.at(0), conv_out.at(0),
+                                n, 3)
+            else:
+                hip.matvec(Format.Q4K, big.at(at), rows, cols, x.at(0), y.at(0), accumulate=True)
+
+        def run(k):
+            hip.begin()
+            for i in range(k):
+                launch(i)
+            return hip.end()
+
+        run(copies)
+        out[name] = round(run(reps * copies) / (reps * copies) * 1e6, 3)
+        big.free()
+    for b in (x, nw, y, taps, hist, conv_out):
+        b.free()
+    return out
+
+
 def oracle_tokens(name: str):
     """The oracle's 128 greedy tokens (and top-2 gaps) for the same seeded model
     and prompt, from the committed fixture tests/golden/greedy_<name>.npz
@@ -423,6 +477,8 @@ def main() -> int:
     ap.add_argument("--long-only", action="store_true", help="only the 32K-context leg (for profiling)")
     ap.add_argument("--gemv-only", action="store_true", help="only the config-1 GEMV leg (for profiling)")
     ap.add_argument("--gemm-only", action="store_true", help="only the prefill GEMM leg (for profiling)")
+    ap.add_argument("--decode-gemv-only", action="store_true",
+                    help="only the 2.6B decode GEMV shapes (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the decode loop is single-device (as in the reference) "
@@ -449,6 +505,9 @@ def main() -> int:
             return 0
         if args.gemm_only:
             log(f"prefill gemm: {gemm_leg(hip)}")
+            return 0
+        if args.decode_gemv_only:
+            log(f"decode gemv: {decode_gemv_leg(hip)}")
             return 0
         g = gemv_leg(hip, reps=10)
         log(f"gemv: {g}")
