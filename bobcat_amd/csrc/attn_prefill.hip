@@ -92,30 +92,54 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *__restrict__ 
     for (int i = 0; i < 16; i++) o[b][i] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  for (uint32_t kb = kb_lo; kb < kb_hi && kb < kend; kb += kPrefKeys) {
-    // Stage V^T of keys kb .. kb+31 (zeros past kend).
-    __syncthreads();
-    for (uint32_t c = tid; c < (uint32_t)(kPrefKeys * HD / 8); c += 256) {
-      const uint32_t key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
-      ph8_t v8;
-      if (kb + key < kend) {
-        v8 = *reinterpret_cast<const ph8_t *>(vc + (uint64_t)(kb + key) * row_elems + (uint64_t)kv * HD + d0);
-      } else {
+  // Key block kb's loads: this thread's VP pieces of V (8 halves each,
+  // staged transposed in LDS) and this lane's K fragments, both with
+  // clamped rows (the staging zeroes V past kend; scores past it are
+  // masked).  Each block's loads are issued one block ahead, before the
+  // current block's MFMAs, so that the memory latency overlaps them
+  // (loading in the block itself put a full round trip on every block).
+  constexpr int VP = kPrefKeys * HD / 8 / 256;
+  static_assert(VP >= 1 && kPrefKeys * HD / 8 == 256 * VP, "V pieces per thread");
+  auto load_v = [&](uint32_t kb, ph8_t *v8) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) v8[j] = (_Float16)0.f;
-      }
-#pragma unroll
-      for (int j = 0; j < 8; j++) vt[(d0 + j) * kVtStride + key] = v8[j];
+    for (int p = 0; p < VP; p++) {
+      const uint32_t c = tid + 256 * p, key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+      const uint32_t row = min(kb + key, kend - 1);
+      v8[p] = *reinterpret_cast<const ph8_t *>(vc + (uint64_t)row * row_elems + (uint64_t)kv * HD + d0);
     }
-    __syncthreads();
-    if (!active) continue;
-
-    // S^T = K·Q^T: lane supplies K[kb + col][16·s + 8·half .. +8].
+  };
+  auto load_k = [&](uint32_t kb, ph8_t *ka) __attribute__((always_inline)) {
     const uint32_t krow = min(kb + col, kend - 1);
     const _Float16 *kr = kc + (uint64_t)krow * row_elems + (uint64_t)kv * HD + 8 * half_id;
-    ph8_t ka[KS];
 #pragma unroll
     for (int s = 0; s < KS; s++) ka[s] = *reinterpret_cast<const ph8_t *>(kr + 16 * s);
+  };
+
+  // (Heads of 256 hold a 32 x 256 f32 output tile per wave in registers:
+  // they load each block in the block itself, as a second register set
+  // would not fit.)
+  constexpr bool kAhead = HD <= 128;
+  auto block = [&](uint32_t kb, const ph8_t *ka, const ph8_t *vcur, ph8_t *kn, ph8_t *vn)
+                   __attribute__((always_inline)) {
+    // Stage V^T of keys kb .. kb+31 (zeros past kend).
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < VP; p++) {
+      const uint32_t c = tid + 256 * p, key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+      const bool in = kb + key < kend;
+#pragma unroll
+      for (int j = 0; j < 8; j++) vt[(d0 + j) * kVtStride + key] = in ? vcur[p][j] : (_Float16)0.f;
+    }
+    __syncthreads();
+    // The next block's loads (a clamped re-read past the split's end).
+    if constexpr (kAhead) {
+      const uint32_t nb = min(kb + kPrefKeys, kb_hi - kPrefKeys);
+      load_v(nb, vn);
+      load_k(nb, kn);
+    }
+    if (!active) return;
+
+    // S^T = K·Q^T: lane supplies K[kb + col][16·s + 8·half .. +8].
     pf16_t sc;
 #pragma unroll
     for (int i = 0; i < 16; i++) sc[i] = 0.f;
@@ -164,6 +188,26 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *__restrict__ 
         o[b] = __builtin_amdgcn_mfma_f32_32x32x8f16(a, ph[j], o[b], 0, 0, 0);
         o[b] = __builtin_amdgcn_mfma_f32_32x32x8f16(a, pl[j], o[b], 0, 0, 0);
       }
+    }
+  };
+  // Two register sets, alternating block by block.
+  const uint32_t kb_end = min(kb_hi, (kend + kPrefKeys - 1) / kPrefKeys * kPrefKeys);
+  if constexpr (kAhead) {
+    if (kb_lo < kb_end) {
+      ph8_t kA[KS], kB[KS], vA[VP], vB[VP];
+      load_v(kb_lo, vA);
+      load_k(kb_lo, kA);
+      for (uint32_t kb = kb_lo; kb < kb_end; kb += 2 * kPrefKeys) {
+        block(kb, kA, vA, kB, vB);
+        if (kb + kPrefKeys < kb_end) block(kb + kPrefKeys, kB, vB, kA, vA);
+      }
+    }
+  } else {
+    for (uint32_t kb = kb_lo; kb < kb_end; kb += kPrefKeys) {
+      ph8_t kA[KS], vA[VP];
+      load_v(kb, vA);
+      if (active) load_k(kb, kA);
+      block(kb, kA, vA, nullptr, nullptr);
     }
   }
   if (!active) return;
