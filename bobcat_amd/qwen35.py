@@ -97,7 +97,13 @@ QWEN35_TINY_V256 = Qwen35Config("qwen3.5-tiny-v256", n_embd=256, n_ff=512, n_voc
 QWEN35_TINY_V192 = Qwen35Config("qwen3.5-tiny-v192", n_embd=256, n_ff=512, n_vocab=500, n_layers=4, n_heads=2,
                                 n_kv_heads=1, head_dim=128, n_rot=32, n_k_heads=2, n_v_heads=4, k_head_dim=128,
                                 v_head_dim=192)
-CONFIGS = {c.name: c for c in (QWEN35_0_8B, QWEN35_TINY, QWEN35_TINY_64, QWEN35_TINY_V256, QWEN35_TINY_V192)}
+# Eight value heads of 128 (1,024 values, as the 0.8B's 2,048): the decode
+# step's gated norm staged by the out projection's slab launch.
+QWEN35_TINY_V1024 = Qwen35Config("qwen3.5-tiny-v1024", n_embd=256, n_ff=512, n_vocab=500, n_layers=4, n_heads=2,
+                                 n_kv_heads=1, head_dim=128, n_rot=64, n_k_heads=4, n_v_heads=8, k_head_dim=128,
+                                 v_head_dim=128)
+CONFIGS = {c.name: c for c in (QWEN35_0_8B, QWEN35_TINY, QWEN35_TINY_64, QWEN35_TINY_V256, QWEN35_TINY_V192,
+                               QWEN35_TINY_V1024)}
 
 
 @dataclass

@@ -21,8 +21,8 @@ import pytest
 
 import oracle
 from bobcat_amd._lib import DeltaShape
-from bobcat_amd.qwen35 import (QWEN35_TINY, QWEN35_TINY_64, QWEN35_TINY_V192, QWEN35_TINY_V256, Qwen35Config,
-                               Qwen35Hip, Qwen35Weights)
+from bobcat_amd.qwen35 import (QWEN35_TINY, QWEN35_TINY_64, QWEN35_TINY_V192, QWEN35_TINY_V256, QWEN35_TINY_V1024,
+                               Qwen35Config, Qwen35Hip, Qwen35Weights)
 
 pytestmark = pytest.mark.gpu
 
@@ -47,7 +47,8 @@ def rel(got, want):
     return float(d.max() / max(np.abs(want).max(), 1e-30))
 
 
-@pytest.fixture(scope="module", params=[QWEN35_TINY, QWEN35_TINY_64, QWEN35_TINY_V256, QWEN35_TINY_V192],
+@pytest.fixture(scope="module", params=[QWEN35_TINY, QWEN35_TINY_64, QWEN35_TINY_V256, QWEN35_TINY_V192,
+                                        QWEN35_TINY_V1024],
                 ids=lambda c: c.name)
 def weights(request):
     return Qwen35Weights(request.param, seed=7)
