@@ -274,11 +274,16 @@ struct RowSlotSum {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-// Query heads per decode workgroup at run time: HPW when the one-head grid
-// would need more than kGroupedAbove workgroups (one round of four per CU),
-// else one (more workgroups, each with a shorter chain of dependent work).
-// BCH_ATTN_GROUPED_ABOVE overrides the bound (0: always grouped; for tests).
-constexpr uint32_t kGroupedAbove = 1024;
+// Query heads per decode workgroup at run time: HPW once the context holds
+// more than a.grouped_above keys, else one (more workgroups, each with a
+// shorter chain of dependent work).  The bound is where the two layouts
+// measured level on one MI355X (32 x 8 heads): ~1,300 keys for 64- and
+// 128-wide f16 heads and f32 caches; 256-wide f16 heads, whose splits hold
+// only 64 keys, gain nothing measurable in a model's decode step below ~8K.  BCH_ATTN_GROUPED_ABOVE overrides it (0: always
+// grouped; for tests).
+static uint32_t grouped_above_keys(uint32_t head_dim, bool kv_half) {
+  return kv_half && head_dim == 256 ? 8192u : 1280u;
+}
 
 // CPR: 16-byte chunks per cache row (head_dim * element size / 16); HPW:
 // query heads per workgroup (a divisor of the group) for long contexts.
@@ -307,7 +312,7 @@ __device__ __forceinline__ void attn_decode_body(const AttnDecodeArgs &a) {
   const uint32_t pos = *a.dpos;
   const uint32_t n_keys = pos + 1;
   const uint32_t n_splits = (n_keys + kps - 1) / kps;
-  const uint32_t hpw = HPW > 1 && a.n_heads * n_splits > a.grouped_above ? (uint32_t)HPW : 1u;
+  const uint32_t hpw = HPW > 1 && n_keys > a.grouped_above ? (uint32_t)HPW : 1u;
   const uint32_t units = a.n_heads / hpw;
   const uint32_t split = blockIdx.x / units, head0 = blockIdx.x % units * hpw;
   if (split >= n_splits) return;
@@ -996,7 +1001,7 @@ static uint32_t heads_per_workgroup(uint32_t group) { return group % 4 == 0 ? 4 
 void run_attn_decode(hipStream_t s, const AttnDecodeArgs &args, bool kv_half) {
   AttnDecodeArgs a = args;
   const char *env = std::getenv("BCH_ATTN_GROUPED_ABOVE");
-  a.grouped_above = env ? (uint32_t)std::strtoul(env, nullptr, 10) : kGroupedAbove;
+  a.grouped_above = env ? (uint32_t)std::strtoul(env, nullptr, 10) : grouped_above_keys(a.head_dim, kv_half);
   // One workgroup per (head, split) covers both layouts: with HPW heads per
   // workgroup the first 1/HPW of the grid works and the rest exits at once.
   const uint32_t hpw = heads_per_workgroup(a.n_heads / a.n_kv);

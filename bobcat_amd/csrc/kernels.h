@@ -37,8 +37,9 @@ struct AttnDecodeArgs {
   // q + z·q_stride, its output at out + z·out_stride, its gate at
   // gate + z·gate_query_stride; partials and counters hold n_queries·n_heads slots.
   uint32_t first_pos, q_stride, out_stride, gate_query_stride;
-  // Decode: one query head per workgroup while n_heads · splits is at most
-  // this, else a group's heads share each workgroup (set by run_attn_decode).
+  // Decode: one query head per workgroup while the context holds at most this
+  // many keys, else a group's heads share each workgroup (set by
+  // run_attn_decode).
   uint32_t grouped_above;
 };
 uint32_t attn_decode_keys_per_split(uint32_t head_dim, bool kv_half);
