@@ -175,6 +175,50 @@ def decode_gemv_leg(hip, reps: int = 8, budget: int = 640 << 20):
     return out
 
 
+def attn_decode_leg(hip, pos: int = LONG_PROMPT + 2, layers: int = 8, reps: int = 8):
+    """The decode attention of one LFM2-2.6B attention layer at a 32K context
+    (32 query heads over 8 KV heads of 64, f16 cache), through
+    bch_attention_decode, for per-kernel counters: the q/k norm, RoPE and
+    cache store of the new position, then attention over pos + 1 keys.
+    `layers` distinct caches (67 MB each, together beyond the 256 MB MALL)
+    are used in turn, as the model's layers are.  Returns microseconds per
+    launch and the algorithmic rate (the K and V rows read once)."""
+    from bobcat_amd.backend import attention_decode_scratch_floats
+
+    heads, kv, hd, n_ctx = 32, 8, 64, LONG_PROMPT + GEN
+    rng = np.random.default_rng(13)
+    layer = n_ctx * kv * hd * 2
+    cache = rng.standard_normal(n_ctx * kv * hd).astype(np.float16)
+    kc = hip.new_buffer(layers * layer)
+    vc = hip.new_buffer(layers * layer)
+    for i in range(layers):
+        hip.write(kc.at(i * layer), cache)
+        hip.write(vc.at(i * layer), cache)
+    q = hip.buffer_from(rng.standard_normal(heads * hd).astype(np.float32))
+    k = hip.buffer_from(rng.standard_normal(kv * hd).astype(np.float32))
+    v = hip.buffer_from(rng.standard_normal(kv * hd).astype(np.float32))
+    qn = hip.buffer_from((1.0 + 0.1 * rng.standard_normal(hd)).astype(np.float32))
+    kn = hip.buffer_from((1.0 + 0.1 * rng.standard_normal(hd)).astype(np.float32))
+    sc = hip.new_buffer(attention_decode_scratch_floats(heads, hd, n_ctx, True) * 4)
+    out = hip.new_buffer(heads * hd * 4)
+
+    def run(n):
+        hip.begin()
+        for i in range(n):
+            at = (i % layers) * layer
+            hip.attention_decode(q.at(0), k.at(0), v.at(0), qn.at(0), kn.at(0), 1e-5, 1e6, hd, kc.at(at), vc.at(at),
+                                 True, sc.at(0), out.at(0), heads, kv, hd, pos, n_ctx)
+        return hip.end()
+
+    run(layers)
+    per = run(reps * layers) / (reps * layers)
+    for b in (kc, vc, q, k, v, qn, kn, sc, out):
+        b.free()
+    kv_bytes = 2 * (pos + 1) * kv * hd * 2
+    return dict(keys=pos + 1, us=round(per * 1e6, 3), kv_mb=round(kv_bytes / 1e6, 2),
+                gbs=round(kv_bytes / per / 1e9, 1))
+
+
 def oracle_tokens(name: str):
     """The oracle's 128 greedy tokens (and top-2 gaps) for the same seeded model
     and prompt, from the committed fixture tests/golden/greedy_<name>.npz
@@ -479,6 +523,8 @@ def main() -> int:
     ap.add_argument("--gemm-only", action="store_true", help="only the prefill GEMM leg (for profiling)")
     ap.add_argument("--decode-gemv-only", action="store_true",
                     help="only the 2.6B decode GEMV shapes (for profiling)")
+    ap.add_argument("--attn-decode-only", action="store_true",
+                    help="only the 2.6B decode attention at a 32K context (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the decode loop is single-device (as in the reference) "
@@ -508,6 +554,9 @@ def main() -> int:
             return 0
         if args.decode_gemv_only:
             log(f"decode gemv: {decode_gemv_leg(hip)}")
+            return 0
+        if args.attn_decode_only:
+            log(f"decode attention: {attn_decode_leg(hip)}")
             return 0
         g = gemv_leg(hip, reps=10)
         log(f"gemv: {g}")

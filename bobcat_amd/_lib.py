@@ -152,6 +152,9 @@ PROTOTYPES = {
     "bch_attention": (_int, [_vp, View, View, View, _int, View, View, _u32, _u32, _u32, _u32, _u32, _u32]),
     "bch_attention_prefill": (_int, [_vp, View, View, View, View, _u32, _u32, _u32, _u32, _u32, _u32]),
     "bch_attention_scratch_floats": (_u64, [_u32, _u32, _u32, _u32]),
+    "bch_attention_decode": (_int, [_vp, View, View, View, View, View, C.c_float, C.c_float, _u32, View, View, _int,
+                                    View, View, _u32, _u32, _u32, _u32, _u32]),
+    "bch_attention_decode_scratch_floats": (_u64, [_u32, _u32, _u32, _int]),
     "bch_matmul": (_int, [_vp, _u32, View, _u32, _u32, View, View, _u32, _u32]),
     "bch_matmul_noalloc": (_int, [_vp, _u32, View, _u32, _u32, View, View, _u32, _u32]),
     "bch_matmul_noalloc_max_bytes": (_u64, []),

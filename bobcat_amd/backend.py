@@ -244,6 +244,12 @@ class Hip:
         check(lib().bch_attention_prefill(self.handle, _view(q), _view(k_cache), _view(v_cache), _view(out),
                                           n_heads, n_kv_heads, head_dim, first_pos, n_queries, n_ctx))
 
+    def attention_decode(self, q, k, v, q_norm, k_norm, eps, rope_theta, n_rot, k_cache, v_cache, kv_half, scratch,
+                         out, n_heads, n_kv_heads, head_dim, pos, n_ctx):
+        check(lib().bch_attention_decode(self.handle, _view(q), _view(k), _view(v), _view(q_norm), _view(k_norm),
+                                         eps, rope_theta, n_rot, _view(k_cache), _view(v_cache), int(kv_half),
+                                         _view(scratch), _view(out), n_heads, n_kv_heads, head_dim, pos, n_ctx))
+
     def matmul(self, fmt, weights, n_rows, n_cols, x, y, n_tokens, store: Store):
         check(lib().bch_matmul(self.handle, int(fmt), _view(weights), n_rows, n_cols, _view(x),
                                _view(y), n_tokens, int(store)))
@@ -295,9 +301,13 @@ def attention_scratch_floats(n_heads: int, head_dim: int, n_ctx: int, n_queries:
     return lib().bch_attention_scratch_floats(n_heads, head_dim, n_ctx, n_queries)
 
 
+def attention_decode_scratch_floats(n_heads: int, head_dim: int, n_ctx: int, kv_half: bool) -> int:
+    return lib().bch_attention_decode_scratch_floats(n_heads, head_dim, n_ctx, int(kv_half))
+
+
 def row_bytes(fmt: int, n_cols: int) -> int:
     return lib().bch_row_bytes(int(fmt), n_cols)
 
 
 __all__ = ["Hip", "Buffer", "ViewRef", "NormSpec", "Format", "Store", "BobcatError",
-           "attention_scratch_floats", "row_bytes"]
+           "attention_scratch_floats", "attention_decode_scratch_floats", "row_bytes"]

@@ -1016,6 +1016,15 @@ void run_attn_decode(hipStream_t s, const AttnDecodeArgs &args, bool kv_half) {
   }
 }
 
+// The standalone decode entry point's scratch: the position word, the
+// n_heads split counters, then (16-byte aligned) the split partials.
+constexpr uint64_t kDecodeScratchHeader = 512;  // floats
+constexpr uint32_t kDecodeMaxHeads = 256;
+
+__global__ void k_attn_decode_setup(uint32_t *scratch, uint32_t pos, uint32_t n_heads) {
+  for (uint32_t i = threadIdx.x; i <= n_heads; i += blockDim.x) scratch[i == 0 ? 0 : 63 + i] = i == 0 ? pos : 0u;
+}
+
 void run_attn_prefill(hipStream_t s, const AttnDecodeArgs &a, bool kv_half, uint32_t n_queries) {
   dim3 grid(a.n_heads, a.max_splits, n_queries);
   if (kv_half)
@@ -1025,3 +1034,68 @@ void run_attn_prefill(hipStream_t s, const AttnDecodeArgs &a, bool kv_half, uint
 }
 
 }  // namespace bch
+
+using namespace bch;
+
+extern "C" uint64_t bch_attention_decode_scratch_floats(uint32_t n_heads, uint32_t head_dim, uint32_t n_ctx,
+                                                        int kv_half) {
+  return kDecodeScratchHeader +
+         (uint64_t)n_heads * attn_decode_max_splits(n_ctx, head_dim, kv_half != 0) * (head_dim + 4);
+}
+
+extern "C" int bch_attention_decode(bch_ctx *ctx, bch_view q, bch_view k, bch_view v, bch_view q_norm,
+                                    bch_view k_norm, float eps, float rope_theta, uint32_t n_rot, bch_view k_cache,
+                                    bch_view v_cache, int kv_half, bch_view scratch, bch_view out, uint32_t n_heads,
+                                    uint32_t n_kv_heads, uint32_t head_dim, uint32_t pos, uint32_t n_ctx) {
+  const bool half = kv_half != 0;
+  if (n_kv_heads == 0 || n_heads % n_kv_heads || n_heads > kDecodeMaxHeads ||
+      attn_decode_keys_per_split(head_dim, half) == 0 || n_rot % 2 || n_rot > head_dim || pos >= n_ctx)
+    return fail(BCH_ERR_ATTENTION_LIMITS,
+                "attention_decode: heads of 16-byte cache rows of 64 to 1024 bytes (a power of two, at most 256 "
+                "elements), KV heads dividing at most %u query heads, an even n_rot up to the head size and a "
+                "position inside the context, got %u and %u heads of %u, n_rot %u, position %u of %u",
+                kDecodeMaxHeads, n_heads, n_kv_heads, head_dim, n_rot, pos, n_ctx);
+  const uint64_t elem = half ? 2 : 4;
+  const uint64_t cache_bytes = ((uint64_t)pos + 1) * n_kv_heads * head_dim * elem;
+  const float *qp, *kp, *vp, *qnp, *knp;
+  void *kcp, *vcp;
+  float *sp, *op;
+  BCH_TRY(view_ptr(ctx, "attention_decode", q, (uint64_t)n_heads * head_dim * 4, &qp));
+  BCH_TRY(view_ptr(ctx, "attention_decode", k, (uint64_t)n_kv_heads * head_dim * 4, &kp));
+  BCH_TRY(view_ptr(ctx, "attention_decode", v, (uint64_t)n_kv_heads * head_dim * 4, &vp));
+  BCH_TRY(view_ptr(ctx, "attention_decode", q_norm, (uint64_t)head_dim * 4, &qnp));
+  BCH_TRY(view_ptr(ctx, "attention_decode", k_norm, (uint64_t)head_dim * 4, &knp));
+  BCH_TRY(view_ptr(ctx, "attention_decode", k_cache, cache_bytes, &kcp));
+  BCH_TRY(view_ptr(ctx, "attention_decode", v_cache, cache_bytes, &vcp));
+  BCH_TRY(view_ptr(ctx, "attention_decode", scratch,
+                   bch_attention_decode_scratch_floats(n_heads, head_dim, n_ctx, kv_half) * 4, &sp));
+  BCH_TRY(view_ptr(ctx, "attention_decode", out, (uint64_t)n_heads * head_dim * 4, &op));
+  if (reinterpret_cast<uintptr_t>(kcp) % 16 || reinterpret_cast<uintptr_t>(vcp) % 16 ||
+      reinterpret_cast<uintptr_t>(sp) % 16)
+    return fail(BCH_ERR_ARGUMENT, "attention_decode: the caches and the scratch must be 16-byte aligned");
+  AttnDecodeArgs a{};
+  a.q = qp;
+  a.k = kp;
+  a.v = vp;
+  a.q_norm = qnp;
+  a.k_norm = knp;
+  a.freqs = rope_table(rope_theta, n_rot);
+  a.eps = eps;
+  a.scale = 1.0f / sqrtf((float)head_dim);
+  a.k_cache = kcp;
+  a.v_cache = vcp;
+  a.partials = sp + kDecodeScratchHeader;
+  a.counters = reinterpret_cast<uint32_t *>(sp) + 64;
+  a.out = op;
+  a.n_heads = n_heads;
+  a.n_kv = n_kv_heads;
+  a.head_dim = head_dim;
+  a.max_splits = attn_decode_max_splits(n_ctx, head_dim, half);
+  a.dpos = reinterpret_cast<const uint32_t *>(sp);
+  a.q_head_stride = head_dim;
+  a.n_rot = n_rot;
+  return launch(ctx, {"attention_decode", 0, 0, 0}, [&](hipStream_t s) {
+    k_attn_decode_setup<<<1, 256, 0, s>>>(reinterpret_cast<uint32_t *>(sp), pos, n_heads);
+    run_attn_decode(s, a, half);
+  });
+}

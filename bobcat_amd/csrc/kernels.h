@@ -24,7 +24,7 @@ struct AttnDecodeArgs {
   RopeTable freqs;
   float eps, scale;
   void *k_cache, *v_cache;         // this layer's caches, [pos][n_kv][head_dim]
-  float *partials;                 // n_heads * max_splits * (head_dim + 2)
+  float *partials;                 // n_heads * max_splits * (head_dim + 4), 16-byte aligned
   uint32_t *counters;              // n_heads zeroed (left zeroed on exit)
   float *out;                      // [n_heads * head_dim]
   uint32_t n_heads, n_kv, head_dim, max_splits;

@@ -219,6 +219,24 @@ int bch_attention_prefill(bch_ctx *ctx, bch_view q, bch_view k_cache, bch_view v
 /* attention_scratch_floats (backend.rs:2739-2748). */
 uint64_t bch_attention_scratch_floats(uint32_t n_heads, uint32_t head_dim, uint32_t n_ctx,
                                       uint32_t n_queries);
+/* MI355X addition (no counterpart in the reference as one call): the
+ * decode step of an LFM2 attention layer after its projections
+ * (lfm2.rs:515-555) as the model drivers run it: each query head and key
+ * head RMS-normalised with q_norm / k_norm [head_dim] (eps), its first
+ * n_rot elements rotated NeoX-style for position `pos` (rope_theta), the
+ * key and value stored in the caches at `pos` (rounded to f16 when
+ * kv_half), then softmax(q·k/√head_dim)·v over positions 0..pos into `out`.
+ * q: [n_heads][head_dim], k and v: [n_kv_heads][head_dim], f32; caches
+ * [pos][kv_head][head_dim].  Head sizes whose cache rows are 64 to 1024
+ * bytes in powers of two, up to 256 elements; at most 256 query heads.
+ * `scratch` holds bch_attention_decode_scratch_floats(...) floats,
+ * 16-byte aligned (the MFMA-scored f16 path agrees with bch_attention to
+ * ~1e-6 of the outputs' scale). */
+int bch_attention_decode(bch_ctx *ctx, bch_view q, bch_view k, bch_view v, bch_view q_norm, bch_view k_norm,
+                         float eps, float rope_theta, uint32_t n_rot, bch_view k_cache, bch_view v_cache,
+                         int kv_half, bch_view scratch, bch_view out, uint32_t n_heads, uint32_t n_kv_heads,
+                         uint32_t head_dim, uint32_t pos, uint32_t n_ctx);
+uint64_t bch_attention_decode_scratch_floats(uint32_t n_heads, uint32_t head_dim, uint32_t n_ctx, int kv_half);
 
 /* bch_matmul without any allocation: the same kernels, column split and
  * results (bit for bit) as bch_matmul, with the launch's scratch — its fp16
