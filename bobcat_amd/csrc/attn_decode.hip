@@ -648,35 +648,16 @@ __device__ __forceinline__ void attn_decode_body(const AttnDecodeArgs &a) {
   if (!last_s) return;
 
   // Combine.  `groups` threads per quad of 4 consecutive outputs, each
-  // taking every groups-th split; the groups merge through LDS.  When each
-  // thread's splits fit one batch of loads (short contexts), the (max, sum)
-  // headers and the output quads are loaded together and merged with a
-  // running maximum: one round of loads.  Otherwise each head's maximum
-  // comes first (one wave per head, 256 splits' headers at a time), then
-  // the quads in batches of kBatchB splits: fewer rounds than a running
-  // maximum over many small batches.
+  // taking every groups-th split; the groups merge through LDS.  The (max,
+  // sum) headers and the output quads of a batch of splits are loaded
+  // together and merged with a running maximum (the sums so far rescaled
+  // when a batch raises it): one round of loads when each thread's splits
+  // fit one batch of kBatchA (short contexts), else batches of kBatchB.
   const uint32_t quads = n_out / 4, groups = quads >= (uint32_t)kDecThreads ? 1u : kDecThreads / quads;
   constexpr uint32_t kBatchA = 8, kBatchB = 12;
   __shared__ f32x4 comb_s[kDecThreads];  // [group][quad]: output quads
   __shared__ float2 cml_s[kDecThreads];  // [group][quad]: (max, sum)
-  __shared__ float cm_s[HPW];
   const bool one_round = n_splits <= groups * kBatchA;
-  if (!one_round) {
-    for (uint32_t h = wave; h < hpw; h += kWaves) {
-      const float *pp = a.partials + (uint64_t)(head0 + h) * a.max_splits * stride;
-      float M = -INFINITY;
-      for (uint32_t b0 = 0; b0 < n_splits; b0 += 256) {
-        float mv[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) mv[u] = coherent_load(pp + (uint64_t)min(b0 + lane + 64 * u, n_splits - 1) * stride);
-#pragma unroll
-        for (int u = 0; u < 4; u++) M = fmaxf(M, mv[u]);  // clamped duplicates change no maximum
-      }
-      M = wave_max(M);
-      if (lane == 0) cm_s[h] = M;
-    }
-    __syncthreads();
-  }
   if (tid < groups * quads) {
     const uint32_t qd = tid % quads, g = tid / quads, h = 4 * qd / hd, el = 4 * qd % hd;
     // One descriptor for the workgroup's heads (uniform: a per-lane
@@ -706,7 +687,6 @@ __device__ __forceinline__ void attn_decode_body(const AttnDecodeArgs &a) {
         O.w = fmaf(ov[u].w, w, O.w);
       }
     } else {
-      M = cm_s[h];
       for (uint32_t sp0 = g; sp0 < n_splits; sp0 += kBatchB * groups) {
         float2 mlv[kBatchB];
         f32x4 ov[kBatchB];
@@ -717,6 +697,13 @@ __device__ __forceinline__ void attn_decode_body(const AttnDecodeArgs &a) {
           mlv[u] = make_float2(hv.x, hv.y);
           ov[u] = coherent_load4(rs, at + 16 + 4 * el);
         }
+        float Mn = M;
+#pragma unroll
+        for (uint32_t u = 0; u < kBatchB; u++) Mn = fmaxf(Mn, mlv[u].x);  // clamped duplicates change no maximum
+        const float c = expf(M - Mn);  // 0 on the first batch (M = -inf)
+        M = Mn;
+        L *= c;
+        O.x *= c, O.y *= c, O.z *= c, O.w *= c;
 #pragma unroll
         for (uint32_t u = 0; u < kBatchB; u++) {
           const float w = sp0 + u * groups < n_splits ? expf(mlv[u].x - M) : 0.f;
