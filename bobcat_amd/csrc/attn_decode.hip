@@ -602,8 +602,11 @@ __device__ __forceinline__ void attn_decode_body(const AttnDecodeArgs &a) {
 
   // 6. Output, directly or through the split partials (max, sum, pad,
   // pad, output[hd]: 16-byte aligned outputs).  The output gate of gated
-  // attention (qwen35.rs:422-424) applies to the combined output.
+  // attention (qwen35.rs:422-424) applies to the combined output.  With
+  // few enough splits (deferred) every split, a single one included, only
+  // stores its partial: the next launch's staging combines them.
   constexpr uint32_t stride = hd + 4;
+  const bool deferred = n_splits <= a.defer_splits;
   float gate[kOutPer];
 #pragma unroll
   for (int j = 0; j < kOutPer; j++) {
@@ -614,7 +617,7 @@ __device__ __forceinline__ void attn_decode_body(const AttnDecodeArgs &a) {
 #pragma unroll
       for (int w = 0; w < kWaves; w++) o += red_s[w][f];
       if (a.gate) gate[j] = 1.0f / (1.0f + expf(-a.gate[(uint64_t)(head0 + h) * a.gate_head_stride + el]));
-      if (n_splits == 1) {
+      if (n_splits == 1 && !deferred) {
         a.out[(uint64_t)(head0 + h) * hd + el] = o / head_sum(h) * gate[j];
       } else {
         float *pp = a.partials + ((uint64_t)(head0 + h) * a.max_splits + split) * stride;
@@ -626,7 +629,7 @@ __device__ __forceinline__ void attn_decode_body(const AttnDecodeArgs &a) {
       }
     }
   }
-  if (n_splits == 1) return;
+  if (n_splits == 1 || deferred) return;
   // Hand-off to the last workgroup of the heads, by the hardware's ordering
   // rather than release/acquire fences (an agent-scope release writes back
   // the XCD's whole L2: 32K-context decode fell from 805 to 434 tok/s with

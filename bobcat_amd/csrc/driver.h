@@ -46,6 +46,10 @@ int check_hip(hipError_t e, const char *what);
 // issues the same launches on the stream one by one (for tools that do not
 // follow graph launches, such as per-kernel tracing).
 bool use_graphs();
+// Positions below which decode attention leaves its splits' combine to the
+// out projection (kDeferSplits splits of the head size's split length);
+// BCH_NO_DEFER=1 makes it 0 (never), for measuring the two forms.
+uint32_t deferred_combine_below(uint32_t head_dim, bool kv_half);
 
 struct Sequence {
   virtual ~Sequence();
@@ -65,8 +69,11 @@ struct Sequence {
   uint64_t *argmax_partials = nullptr;  // kArgmaxPartials argmax keys of the logits
   uint64_t *rng = nullptr;              // sampler state
   // Graphs and timing.
-  hipGraphExec_t step_graph = nullptr, gen_graph = nullptr, sample_graph = nullptr;
-  bch_sampling sample_settings{};  // the settings sample_graph was captured with
+  // Each in two forms: [1] for steps at positions below short_below (the
+  // model's short-context form), [0] for the others.
+  hipGraphExec_t step_graph[2] = {}, gen_graph[2] = {}, sample_graph[2] = {};
+  bch_sampling sample_settings[2] = {};  // the settings sample_graph[i] was captured with
+  uint32_t short_below = 0;  // set by the model: steps below it take its short-context form
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   double last_gpu_seconds = 0.0;
   // Host staging of the small asynchronous uploads (they must outlive the call).
@@ -82,8 +89,9 @@ struct Sequence {
   // One decode step at position *dpos.  With greedy_input the step first
   // takes the argmax of the previous logits (from argmax_partials) as its
   // token; it leaves logits and their argmax partials for the next one.
-  // With trace, it copies the activations into `trace`.
-  virtual void record_step(hipStream_t st, bool greedy_input, bool trace) = 0;
+  // With trace, it copies the activations into `trace`.  short_ctx: the
+  // step runs at a position below short_below.
+  virtual void record_step(hipStream_t st, bool greedy_input, bool trace, bool short_ctx) = 0;
   // A prefill batch of `count` tokens at positions pos.. (tokens already in
   // the ring); the logits of its last token when want_logits.
   virtual void record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool want_logits, bool trace) = 0;
@@ -123,7 +131,10 @@ struct Sequence {
   int set_dpos(uint32_t value);
   int finish();
   int ensure_trace_rows(uint32_t rows);
-  int capture(bool greedy_input, const SampleArgs *sampler, hipGraphExec_t *out);
+  int capture(bool greedy_input, const SampleArgs *sampler, bool short_ctx, hipGraphExec_t *out);
+  // Whether the step at position pos takes the short-context form.
+  bool short_at(uint32_t pos) const { return pos < short_below; }
+  int launch_gen_step(uint32_t pos);
 };
 
 }  // namespace bch

@@ -65,12 +65,19 @@ bool use_graphs() {
   return on;
 }
 
+uint32_t deferred_combine_below(uint32_t head_dim, bool kv_half) {
+  static const bool off = getenv("BCH_NO_DEFER") && atoi(getenv("BCH_NO_DEFER")) != 0;
+  return off ? 0u : kDeferSplits * attn_decode_keys_per_split(head_dim, kv_half);
+}
+
 Sequence::~Sequence() {
   // The context (and its stream) must still be open: free drivers first.
   if (s) hipStreamSynchronize(s);
-  if (step_graph) hipGraphExecDestroy(step_graph);
-  if (gen_graph) hipGraphExecDestroy(gen_graph);
-  if (sample_graph) hipGraphExecDestroy(sample_graph);
+  for (int i = 0; i < 2; i++) {
+    if (step_graph[i]) hipGraphExecDestroy(step_graph[i]);
+    if (gen_graph[i]) hipGraphExecDestroy(gen_graph[i]);
+    if (sample_graph[i]) hipGraphExecDestroy(sample_graph[i]);
+  }
   if (ev0) hipEventDestroy(ev0);
   if (ev1) hipEventDestroy(ev1);
   for (auto &e : stream_ev)
@@ -148,15 +155,27 @@ int Sequence::ensure_trace_rows(uint32_t rows) {
 }
 
 // Capture one decode step (preceded by the sampler when given) as a graph.
-int Sequence::capture(bool greedy_input, const SampleArgs *sampler, hipGraphExec_t *out) {
+int Sequence::capture(bool greedy_input, const SampleArgs *sampler, bool short_ctx, hipGraphExec_t *out) {
   BCH_TRY(check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture"));
   if (sampler) run_sample(s, *sampler);
-  record_step(s, greedy_input, false);
+  record_step(s, greedy_input, false, short_ctx);
   hipGraph_t g;
   BCH_TRY(check_hip(hipStreamEndCapture(s, &g), "end capture"));
   hipError_t e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
   hipGraphDestroy(g);
   return check_hip(e, "instantiate graph");
+}
+
+// One greedy decode step (the argmax of the previous step's logits as its
+// token) at position pos, as a graph replay unless graphs are off.
+int Sequence::launch_gen_step(uint32_t pos) {
+  const bool sh = short_at(pos);
+  if (!use_graphs()) {
+    record_step(s, true, false, sh);
+    return BCH_OK;
+  }
+  if (!gen_graph[sh]) BCH_TRY(capture(true, nullptr, sh, &gen_graph[sh]));
+  return check_hip(hipGraphLaunch(gen_graph[sh], s), "launch decode graph");
 }
 
 int Sequence::reset() {
@@ -183,13 +202,14 @@ int Sequence::step(uint32_t token, float *out_logits, float *trace_embedding, fl
   BCH_TRY(check_hip(hipMemcpyAsync(tokens + n_past, &token_host, 4, hipMemcpyHostToDevice, s), "write token"));
   BCH_TRY(set_dpos(n_past));
   hipEventRecord(ev0, s);
+  const bool sh = short_at(n_past);
   if (traced) {
-    record_step(s, false, true);
+    record_step(s, false, true, sh);
   } else if (use_graphs()) {
-    if (!step_graph) BCH_TRY(capture(false, nullptr, &step_graph));
-    BCH_TRY(check_hip(hipGraphLaunch(step_graph, s), "launch step graph"));
+    if (!step_graph[sh]) BCH_TRY(capture(false, nullptr, sh, &step_graph[sh]));
+    BCH_TRY(check_hip(hipGraphLaunch(step_graph[sh], s), "launch step graph"));
   } else {
-    record_step(s, false, false);
+    record_step(s, false, false, sh);
   }
   BCH_TRY(finish());
   const uint32_t n = n_embd;
@@ -283,12 +303,8 @@ int Sequence::generate(uint32_t *out, uint32_t n) {
   BCH_TRY(set_dpos(n_past - 1));
   hipEventRecord(ev0, s);
   run_argmax_partials(s, logits, n_vocab, argmax_partials, kArgmaxPartials);
-  if (use_graphs()) {
-    if (!gen_graph) BCH_TRY(capture(true, nullptr, &gen_graph));
-    for (uint32_t i = 0; i < n; i++) BCH_TRY(check_hip(hipGraphLaunch(gen_graph, s), "launch decode graph"));
-  } else {
-    for (uint32_t i = 0; i < n; i++) record_step(s, true, false);
-  }
+  // Replay i runs the step at position n_past + i.
+  for (uint32_t i = 0; i < n; i++) BCH_TRY(launch_gen_step(n_past + i));
   BCH_TRY(finish());
   BCH_TRY(check_hip(hipMemcpy(out, tokens + n_past, (uint64_t)n * 4, hipMemcpyDeviceToHost), "read tokens"));
   n_past += n;
@@ -306,12 +322,8 @@ int Sequence::generate_next(uint32_t *out, uint32_t n) {
   BCH_TRY(set_dpos(n_past - 1));
   hipEventRecord(ev0, s);
   run_argmax_partials(s, logits, n_vocab, argmax_partials, kArgmaxPartials);
-  if (use_graphs()) {
-    if (!gen_graph) BCH_TRY(capture(true, nullptr, &gen_graph));
-    for (uint32_t i = 0; i < n; i++) BCH_TRY(check_hip(hipGraphLaunch(gen_graph, s), "launch decode graph"));
-  } else {
-    for (uint32_t i = 0; i < n; i++) record_step(s, true, false);
-  }
+  // Replay i runs the step at position n_past + i.
+  for (uint32_t i = 0; i < n; i++) BCH_TRY(launch_gen_step(n_past + i));
   // The selection after the last step goes one past the consumed tokens
   // (the ring holds n_ctx + 2 entries).
   run_argmax_pick(s, argmax_partials, kArgmaxPartials, tokens + n_past + n);
@@ -346,19 +358,23 @@ int Sequence::generate_sampled(uint32_t *out, uint32_t n, const bch_sampling *se
   sa.top_k = settings->top_k;
   hipEventRecord(ev0, s);
   if (use_graphs()) {
-    if (sample_graph && memcmp(&sample_settings, settings, sizeof(bch_sampling)) != 0) {
-      hipGraphExecDestroy(sample_graph);
-      sample_graph = nullptr;
+    // Replay i runs the step at position n_past + i.
+    for (uint32_t i = 0; i < n; i++) {
+      const bool sh = short_at(n_past + i);
+      if (sample_graph[sh] && memcmp(&sample_settings[sh], settings, sizeof(bch_sampling)) != 0) {
+        hipGraphExecDestroy(sample_graph[sh]);
+        sample_graph[sh] = nullptr;
+      }
+      if (!sample_graph[sh]) {
+        BCH_TRY(capture(false, &sa, sh, &sample_graph[sh]));
+        sample_settings[sh] = *settings;
+      }
+      BCH_TRY(check_hip(hipGraphLaunch(sample_graph[sh], s), "launch sampling graph"));
     }
-    if (!sample_graph) {
-      BCH_TRY(capture(false, &sa, &sample_graph));
-      sample_settings = *settings;
-    }
-    for (uint32_t i = 0; i < n; i++) BCH_TRY(check_hip(hipGraphLaunch(sample_graph, s), "launch sampling graph"));
   } else {
     for (uint32_t i = 0; i < n; i++) {
       run_sample(s, sa);
-      record_step(s, false, false);
+      record_step(s, false, false, short_at(n_past + i));
     }
   }
   BCH_TRY(finish());
@@ -399,7 +415,6 @@ int Sequence::generate_stream(uint32_t max_tokens, bch_emit_fn emit, void *user,
   BCH_TRY(set_dpos(n_past - 1));
   hipEventRecord(ev0, s);
   run_argmax_partials(s, logits, n_vocab, argmax_partials, kArgmaxPartials);
-  if (use_graphs() && !gen_graph) BCH_TRY(capture(true, nullptr, &gen_graph));
   bool pending[kStreamInFlight] = {};
   bool emitting = true;
   uint32_t committed = 0;
@@ -414,11 +429,7 @@ int Sequence::generate_stream(uint32_t max_tokens, bch_emit_fn emit, void *user,
     const int slot = (int)(step % kStreamInFlight);
     if (pending[slot] && (rc = drain(slot)) != BCH_OK) break;
     if (!emitting) break;
-    if (use_graphs()) {
-      if ((rc = check_hip(hipGraphLaunch(gen_graph, s), "launch decode graph")) != BCH_OK) break;
-    } else {
-      record_step(s, true, false);
-    }
+    if ((rc = launch_gen_step(start + step)) != BCH_OK) break;
     run_argmax_pick(s, argmax_partials, kArgmaxPartials, stream_dev + slot);
     if ((rc = check_hip(hipMemcpyAsync(stream_host + slot, stream_dev + slot, 4, hipMemcpyDeviceToHost, s),
                         "read a selected token")) != BCH_OK)

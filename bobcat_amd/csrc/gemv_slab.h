@@ -17,13 +17,79 @@
 // gemv.h).  Workgroup w owns items [w·n/grid, (w+1)·n/grid); group g of
 // the workgroup takes items g, g+G, g+2G, ... of the slab, at most MAXI.
 #pragma once
+#include <type_traits>
+
 #include "gemv.h"
 
 namespace bch {
 
-template <class F, int LPR, int MAXI, bool NORM, class P>
-__global__ __launch_bounds__(256) void k_slab(P p, const float *__restrict__ x, const float *__restrict__ nw,
-                                              float eps, uint32_t n_items, uint32_t n_units, uint32_t n_cols) {
+// Where the input comes from: the vector x itself (PlainIn), or the decode
+// attention's deferred split partials combined on the way in (SplitIn).
+// load() issues a float4's loads (unconditional: the staging waits for them
+// alone), finish() turns them into the float4.
+struct PlainIn {
+  using Raw = float4;
+  __device__ Raw load(const float4 *x4, uint32_t i) const { return x4[i]; }
+  __device__ float4 finish(const Raw &r, uint32_t) const { return r; }
+};
+
+// The combine of the decode attention's last workgroup (attn_decode.hip),
+// for at most kDeferSplits splits: every slot's (max, sum) header and
+// output quad are loaded whatever the split count (slots past it hold
+// stale values and are selected away), so no address waits for *dpos.
+template <bool GATE>
+struct SplitIn {
+  SplitOut a;
+  struct Raw {
+    float4 out, o[kDeferSplits], g;
+    float2 ml[kDeferSplits];
+  };
+  __device__ Raw load(const float4 *x4, uint32_t i) const {
+    Raw r;
+    r.out = x4[i];
+    const uint32_t e = 4 * i, h = e / a.head_dim, el = e % a.head_dim, stride = a.head_dim + 4;
+#pragma unroll
+    for (uint32_t sp = 0; sp < kDeferSplits; sp++) {
+      const float *pp = a.partials + ((uint64_t)h * a.max_splits + min(sp, a.max_splits - 1)) * stride;
+      r.ml[sp] = *reinterpret_cast<const float2 *>(pp);
+      r.o[sp] = *reinterpret_cast<const float4 *>(pp + 4 + el);
+    }
+    if constexpr (GATE) r.g = *reinterpret_cast<const float4 *>(a.gate + (uint64_t)h * a.gate_head_stride + el);
+    return r;
+  }
+  __device__ float4 finish(const Raw &r, uint32_t n_splits) const {
+    if (n_splits > a.defer) return r.out;
+    float M = -INFINITY;
+#pragma unroll
+    for (uint32_t sp = 0; sp < kDeferSplits; sp++) M = sp < n_splits ? fmaxf(M, r.ml[sp].x) : M;
+    float L = 0.f;
+    float4 O = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (uint32_t sp = 0; sp < kDeferSplits; sp++) {
+      if (sp < n_splits) {
+        const float w = expf(r.ml[sp].x - M);
+        L = fmaf(r.ml[sp].y, w, L);
+        O.x = fmaf(r.o[sp].x, w, O.x);
+        O.y = fmaf(r.o[sp].y, w, O.y);
+        O.z = fmaf(r.o[sp].z, w, O.z);
+        O.w = fmaf(r.o[sp].w, w, O.w);
+      }
+    }
+    float4 v = {O.x / L, O.y / L, O.z / L, O.w / L};
+    if constexpr (GATE) {
+      v.x *= 1.0f / (1.0f + expf(-r.g.x));
+      v.y *= 1.0f / (1.0f + expf(-r.g.y));
+      v.z *= 1.0f / (1.0f + expf(-r.g.z));
+      v.w *= 1.0f / (1.0f + expf(-r.g.w));
+    }
+    return v;
+  }
+};
+
+template <class F, int LPR, int MAXI, bool NORM, class P, class In>
+__device__ __forceinline__ void slab_body(const P &p, const float *__restrict__ x, const float *__restrict__ nw,
+                                          float eps, uint32_t n_items, uint32_t n_units, uint32_t n_cols,
+                                          const In &in) {
   constexpr int T = LPR <= 64 ? 256 : LPR;  // threads per workgroup
   constexpr int G = T / LPR;                // groups per workgroup
   constexpr int R = P::kRows;
@@ -45,13 +111,17 @@ __global__ __launch_bounds__(256) void k_slab(P p, const float *__restrict__ x, 
   // Every load below is unconditional (indices clamped into range): a load
   // under a branch makes the compiler's wait counting fall back to waiting
   // for everything, which would hold the staging until the weights arrive.
-  float4 xv[kPer], wv[kPer];
+  typename In::Raw xv[kPer];
+  float4 wv[kPer];
 #pragma unroll
   for (int k = 0; k < kPer; k++) {
     const uint32_t i = min(tid + k * T, n4 - 1);
-    xv[k] = x4[i];
+    xv[k] = in.load(x4, i);
     if (NORM) wv[k] = w4[i];
   }
+  // The deferred attention splits' count (only SplitIn reads it).
+  uint32_t in_splits = 0;
+  if constexpr (!std::is_same_v<In, PlainIn>) in_splits = *in.a.dpos / in.a.kps + 1;
   // Keep the compiler from moving these loads behind the weights.
   asm volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
@@ -88,7 +158,7 @@ __global__ __launch_bounds__(256) void k_slab(P p, const float *__restrict__ x, 
 #pragma unroll
   for (int k = 0; k < kPer; k++) {
     const uint32_t i = tid + k * T, ic = min(i, n4 - 1);
-    float4 v = xv[k];
+    float4 v = in.finish(xv[k], in_splits);
     if (NORM) {
       const float q = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, v.w * v.w)));
       ss += i < n4 ? q : 0.f;
@@ -188,19 +258,40 @@ __global__ __launch_bounds__(256) void k_slab(P p, const float *__restrict__ x, 
   }
 }
 
+template <class F, int LPR, int MAXI, bool NORM, class P>
+__global__ __launch_bounds__(256) void k_slab(P p, const float *__restrict__ x, const float *__restrict__ nw,
+                                              float eps, uint32_t n_items, uint32_t n_units, uint32_t n_cols) {
+  slab_body<F, LPR, MAXI, NORM>(p, x, nw, eps, n_items, n_units, n_cols, PlainIn{});
+}
+// The same with the input from an input policy (SplitIn).
+template <class F, int LPR, int MAXI, bool NORM, class P, class In>
+__global__ __launch_bounds__(256) void k_slab_in(P p, const float *__restrict__ x, const float *__restrict__ nw,
+                                                 float eps, uint32_t n_items, uint32_t n_units, uint32_t n_cols,
+                                                 In in) {
+  slab_body<F, LPR, MAXI, NORM>(p, x, nw, eps, n_items, n_units, n_cols, in);
+}
+
 // Launch with `grid` workgroups; the caller has checked that every group's
 // share of its slab is at most MAXI items.
-template <class F, int LPR, int MAXI, bool NORM, class P>
+template <class F, int LPR, int MAXI, bool NORM, class P, class In = PlainIn>
 static void launch_slab(hipStream_t s, uint32_t grid, const P &p, const float *x, const float *nw, float eps,
-                        uint32_t n_items, uint32_t n_units, uint32_t n_cols) {
+                        uint32_t n_items, uint32_t n_units, uint32_t n_cols, const In &in = In{}) {
   constexpr int threads = LPR <= 64 ? 256 : LPR;
   constexpr uint32_t kSlot = F::kUnit + (F::kUnit >= 64 ? 4 : 0);
   const uint32_t lds = n_units * kSlot * 4;
-  static const bool lds_limit_set =
-      hipFuncSetAttribute(reinterpret_cast<const void *>(k_slab<F, LPR, MAXI, NORM, P>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, 256 * kSlot * 4) == hipSuccess;
-  (void)lds_limit_set;
-  k_slab<F, LPR, MAXI, NORM, P><<<grid, threads, lds, s>>>(p, x, nw, eps, n_items, n_units, n_cols);
+  if constexpr (std::is_same_v<In, PlainIn>) {
+    static const bool lds_limit_set =
+        hipFuncSetAttribute(reinterpret_cast<const void *>(k_slab<F, LPR, MAXI, NORM, P>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 256 * kSlot * 4) == hipSuccess;
+    (void)lds_limit_set;
+    k_slab<F, LPR, MAXI, NORM, P><<<grid, threads, lds, s>>>(p, x, nw, eps, n_items, n_units, n_cols);
+  } else {
+    static const bool lds_limit_set =
+        hipFuncSetAttribute(reinterpret_cast<const void *>(k_slab_in<F, LPR, MAXI, NORM, P, In>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 256 * kSlot * 4) == hipSuccess;
+    (void)lds_limit_set;
+    k_slab_in<F, LPR, MAXI, NORM, P, In><<<grid, threads, lds, s>>>(p, x, nw, eps, n_items, n_units, n_cols, in);
+  }
 }
 
 // Workgroups of a slab launch: two per CU (the measured best; one per CU

@@ -21,36 +21,36 @@ bool slab_enabled() {
   return on;
 }
 
-template <class F, int LPR, bool NORM, class P>
+template <class F, int LPR, bool NORM, class P, class In>
 bool slab_maxi_switch(hipStream_t s, uint32_t maxi, uint32_t grid, const P &p, const float *x, const float *nw,
-                      float eps, uint32_t n_items, uint32_t n_units, uint32_t n_cols) {
+                      float eps, uint32_t n_items, uint32_t n_units, uint32_t n_cols, const In &in) {
   switch (maxi) {
-    case 1: launch_slab<F, LPR, 1, NORM>(s, grid, p, x, nw, eps, n_items, n_units, n_cols); return true;
-    case 2: launch_slab<F, LPR, 2, NORM>(s, grid, p, x, nw, eps, n_items, n_units, n_cols); return true;
-    case 3: launch_slab<F, LPR, 3, NORM>(s, grid, p, x, nw, eps, n_items, n_units, n_cols); return true;
-    case 4: launch_slab<F, LPR, 4, NORM>(s, grid, p, x, nw, eps, n_items, n_units, n_cols); return true;
+    case 1: launch_slab<F, LPR, 1, NORM>(s, grid, p, x, nw, eps, n_items, n_units, n_cols, in); return true;
+    case 2: launch_slab<F, LPR, 2, NORM>(s, grid, p, x, nw, eps, n_items, n_units, n_cols, in); return true;
+    case 3: launch_slab<F, LPR, 3, NORM>(s, grid, p, x, nw, eps, n_items, n_units, n_cols, in); return true;
+    case 4: launch_slab<F, LPR, 4, NORM>(s, grid, p, x, nw, eps, n_items, n_units, n_cols, in); return true;
     default: return false;
   }
 }
 
-template <class F, int LPR, bool NORM, class P>
+template <class F, int LPR, bool NORM, class P, class In = PlainIn>
 bool slab_lpr(hipStream_t s, const P &p, const float *x, const float *nw, float eps, uint32_t n_items,
-              uint32_t n_units, uint32_t n_cols, uint32_t n_cus) {
+              uint32_t n_units, uint32_t n_cols, uint32_t n_cus, const In &in = In{}) {
   constexpr uint32_t G = LPR <= 64 ? 256 / LPR : 1;
   const uint32_t grid = slab_grid(n_items, G, n_cus);
   const uint32_t maxi = slab_maxi(n_items, G, grid);
-  return slab_maxi_switch<F, LPR, NORM>(s, maxi, grid, p, x, nw, eps, n_items, n_units, n_cols);
+  return slab_maxi_switch<F, LPR, NORM>(s, maxi, grid, p, x, nw, eps, n_items, n_units, n_cols, in);
 }
 
 // Rows of up to 4096 columns (16, 32 or 64 units of 64 weights).
-template <bool NORM, class P>
+template <bool NORM, class P, class In = PlainIn>
 bool slab_narrow(hipStream_t s, const P &p, const float *x, const float *nw, float eps, uint32_t n_items,
-                 uint32_t n_cols, uint32_t n_cus) {
+                 uint32_t n_cols, uint32_t n_cus, const In &in = In{}) {
   const uint32_t n_units = n_cols / 64;
   switch (lanes_for(n_units)) {
-    case 16: return slab_lpr<Q4K8, 16, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols, n_cus);
-    case 32: return slab_lpr<Q4K8, 32, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols, n_cus);
-    case 64: return slab_lpr<Q4K8, 64, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols, n_cus);
+    case 16: return slab_lpr<Q4K8, 16, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols, n_cus, in);
+    case 32: return slab_lpr<Q4K8, 32, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols, n_cus, in);
+    case 64: return slab_lpr<Q4K8, 64, NORM>(s, p, x, nw, eps, n_items, n_units, n_cols, n_cus, in);
     default: return false;
   }
 }
@@ -87,6 +87,22 @@ bool slab_matvec(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_ro
   if (nw) return false;
   return accumulate ? slab_wide(s, PlainItems<true>{W, rb, y}, x, n_rows, n_cols, n_cus)
                     : slab_wide(s, PlainItems<false>{W, rb, y}, x, n_rows, n_cols, n_cus);
+}
+
+bool slab_split_supported(uint32_t format, uint32_t n_cols) {
+  const int lanes = lanes_for(n_cols / 64);  // the widths slab_narrow serves
+  return slab_format_ok(format, n_cols) && n_cols <= 4096 && (lanes == 16 || lanes == 32 || lanes == 64);
+}
+
+bool slab_matvec_split(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols,
+                       const SplitOut &in, float *y, uint32_t n_cus) {
+  if (!slab_split_supported(format, n_cols) || in.head_dim % 4 || in.defer > kDeferSplits || in.max_splits == 0 ||
+      in.kps == 0)
+    return false;
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  const PlainItems<true> p{W, rb, y};
+  if (in.gate) return slab_narrow<false>(s, p, in.out, nullptr, 0.f, n_rows, n_cols, n_cus, SplitIn<true>{in});
+  return slab_narrow<false>(s, p, in.out, nullptr, 0.f, n_rows, n_cols, n_cus, SplitIn<false>{in});
 }
 
 bool slab_matvec3(hipStream_t s, uint32_t format, const uint8_t *W0, const uint8_t *W1, const uint8_t *W2, uint32_t r0,

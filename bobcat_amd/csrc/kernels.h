@@ -41,7 +41,15 @@ struct AttnDecodeArgs {
   // many keys, else a group's heads share each workgroup (set by
   // run_attn_decode).
   uint32_t grouped_above;
+  // Decode: while the context has at most this many splits (0: never, at
+  // most kDeferSplits), every split only stores its partial (including the
+  // single split of a short context) and the out projection's input staging
+  // combines them (slab_matvec_split); no counters, no combining workgroup,
+  // and the output gate is left to that staging too.  Past it the launch
+  // combines as usual into `out`, gated.
+  uint32_t defer_splits;
 };
+constexpr uint32_t kDeferSplits = 4;
 uint32_t attn_decode_keys_per_split(uint32_t head_dim, bool kv_half);
 uint32_t attn_decode_max_splits(uint32_t n_ctx, uint32_t head_dim, bool kv_half);
 void run_attn_decode(hipStream_t s, const AttnDecodeArgs &a, bool kv_half);
@@ -94,6 +102,25 @@ bool slab_experts_swiglu(hipStream_t s, uint32_t format, const uint8_t *Wg, cons
 bool slab_conv(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_cols, const float *x, const float *nw,
                float eps, const float *taps, float *history, float *out, uint32_t n_embd, uint32_t ksize,
                uint32_t n_cus);
+// The decode attention's output as the out projection reads it: while the
+// context has at most `defer` splits (of `kps` keys, counted from *dpos),
+// the split partials (max, sum, pad, pad, output[head_dim] per head and
+// split; max_splits per head) combined here, times sigmoid(gate) when
+// gated; past it the combined, gated `out`.
+struct SplitOut {
+  const float *partials;
+  const float *out;
+  const float *gate;  // nullable: gate[h·gate_head_stride + e]
+  const uint32_t *dpos;
+  uint32_t kps, max_splits, head_dim, gate_head_stride, defer;
+};
+// The out projection y += W · attention output on the slab kernel, the
+// deferred splits combined while its input is staged; false (launching
+// nothing) for shapes it does not serve, which slab_split_supported tells
+// beforehand.
+bool slab_split_supported(uint32_t format, uint32_t n_cols);
+bool slab_matvec_split(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols,
+                       const SplitOut &in, float *y, uint32_t n_cus);
 bool slab_gdn_in(hipStream_t s, uint32_t format, const uint8_t *Wqkv, const uint8_t *Wz, const uint8_t *Wb,
                  const uint8_t *Wa, uint32_t conv_dim, uint32_t value_dim, uint32_t n_v, uint32_t n_cols,
                  const float *x, const float *nw, float eps, const float *taps, float *hist, uint32_t ksize,

@@ -86,7 +86,7 @@ struct bch_lfm2 : bch::Sequence {
     return static_cast<char *>(cache_layer(base, ci)) + (uint64_t)pos * kv_dim * (kv_half ? 2 : 4);
   }
 
-  void record_step(hipStream_t st, bool greedy_input, bool trace) override;
+  void record_step(hipStream_t st, bool greedy_input, bool trace, bool short_ctx) override;
   void record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool want_logits, bool trace) override;
   std::vector<std::pair<void *, uint64_t>> state_regions() const override {
     return {{conv_state, (uint64_t)n_conv * (conv_kernel - 1) * n_embd * 4}};
@@ -123,7 +123,7 @@ static void record_moe_token(bch_lfm2 *m, hipStream_t s, const Layer &L, const f
 // advances *dpos.  The logits leave their argmax partials behind for the
 // next such step.  With `trace`, activations are copied into m->trace:
 // embedding, each layer's output, final norm.
-static void lfm2_step(bch_lfm2 *m, hipStream_t s, bool greedy_input, bool trace) {
+static void lfm2_step(bch_lfm2 *m, hipStream_t s, bool greedy_input, bool trace, bool short_ctx) {
   const uint32_t n = m->n_embd, cus = m->ctx->n_cus;
   uint32_t *dp = m->dpos;
   const uint64_t tstride = (uint64_t)m->trace_rows * n;  // floats per traced activation
@@ -151,7 +151,7 @@ static void lfm2_step(bch_lfm2 *m, hipStream_t s, bool greedy_input, bool trace)
         run_matvec(s, L.wk.format, L.wk.data, m->kv_dim, n, m->hidden, m->k, L.attn_norm, m->norm_eps, false, cus);
         run_matvec(s, L.wv.format, L.wv.data, m->kv_dim, n, m->hidden, m->v, L.attn_norm, m->norm_eps, false, cus);
       }
-      AttnDecodeArgs ad;
+      AttnDecodeArgs ad{};
       ad.q = m->q;
       ad.k = m->k;
       ad.v = m->v;
@@ -174,8 +174,14 @@ static void lfm2_step(bch_lfm2 *m, hipStream_t s, bool greedy_input, bool trace)
       ad.n_rot = m->head_dim;
       ad.gate = nullptr;
       ad.gate_head_stride = 0;
+      // Short contexts leave the splits' combine to wo's input staging.
+      const bool defer = short_ctx && slab_split_supported(L.wo.format, m->q_dim);
+      ad.defer_splits = defer ? kDeferSplits : 0;
       run_attn_decode(s, ad, m->kv_half);
-      run_matvec(s, L.wo.format, L.wo.data, n, m->q_dim, m->attn, m->hidden, nullptr, 0.f, true, cus);
+      const SplitOut so{m->partials, m->attn, nullptr, dp, attn_decode_keys_per_split(m->head_dim, m->kv_half),
+                        ad.max_splits, m->head_dim, 0, ad.defer_splits};
+      if (!defer || !slab_matvec_split(s, L.wo.format, L.wo.data, n, m->q_dim, so, m->hidden, cus))
+        run_matvec(s, L.wo.format, L.wo.data, n, m->q_dim, m->attn, m->hidden, nullptr, 0.f, true, cus);
     }
     if (L.moe) {
       record_moe_token(m, s, L, m->hidden, L.ffn_norm, m->normed, m->route, m->hidden);
@@ -357,7 +363,9 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
 
 }  // namespace bch
 
-void bch_lfm2::record_step(hipStream_t st, bool greedy_input, bool trace) { lfm2_step(this, st, greedy_input, trace); }
+void bch_lfm2::record_step(hipStream_t st, bool greedy_input, bool trace, bool short_ctx) {
+  lfm2_step(this, st, greedy_input, trace, short_ctx);
+}
 void bch_lfm2::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool want_logits, bool trace) {
   lfm2_batch(this, st, pos, count, want_logits, trace);
 }
@@ -533,6 +541,9 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
            (rc = m->alloc_common()));
     if (rc) return cleanup(rc);
   }
+  // Decode steps at positions with at most kDeferSplits attention splits
+  // take the deferred-combine form.
+  m->short_below = deferred_combine_below(m->head_dim, m->kv_half);
   *out = m;
   return BCH_OK;
 }

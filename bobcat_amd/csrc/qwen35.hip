@@ -79,7 +79,7 @@ struct bch_qwen35 : bch::Sequence {
   float *conv_layer(uint32_t di) const { return conv_state + (uint64_t)di * conv_dim * (conv_kernel - 1); }
   float *state_layer(uint32_t di) const { return delta_state + (uint64_t)di * n_v * k_dim * v_dim; }
 
-  void record_step(hipStream_t st, bool greedy_input, bool trace) override;
+  void record_step(hipStream_t st, bool greedy_input, bool trace, bool short_ctx) override;
   void record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool want_logits, bool trace) override;
   std::vector<std::pair<void *, uint64_t>> state_regions() const override {
     return {{conv_state, (uint64_t)n_delta * conv_dim * (conv_kernel - 1) * 4},
@@ -87,7 +87,7 @@ struct bch_qwen35 : bch::Sequence {
   }
 };
 
-void bch_qwen35::record_step(hipStream_t st, bool greedy_input, bool trace) {
+void bch_qwen35::record_step(hipStream_t st, bool greedy_input, bool trace, bool short_ctx) {
   const uint32_t n = n_embd, cus = ctx->n_cus;
   uint32_t *dp = dpos;
   const uint64_t tstride = (uint64_t)trace_rows * n;
@@ -133,8 +133,15 @@ void bch_qwen35::record_step(hipStream_t st, bool greedy_input, bool trace) {
       ad.n_rot = n_rot;
       ad.gate = q_gate + head_dim;
       ad.gate_head_stride = 2 * head_dim;
+      // Short contexts leave the splits' combine (and the gate) to wo's
+      // input staging.
+      const bool defer = short_ctx && slab_split_supported(L.wo.format, q_dim);
+      ad.defer_splits = defer ? kDeferSplits : 0;
       run_attn_decode(st, ad, kv_half);
-      run_matvec(st, L.wo.format, L.wo.data, n, q_dim, attn, hidden, nullptr, 0.f, true, cus);
+      const SplitOut so{partials, attn, q_gate + head_dim, dp, attn_decode_keys_per_split(head_dim, kv_half),
+                        ad.max_splits, head_dim, 2 * head_dim, ad.defer_splits};
+      if (!defer || !slab_matvec_split(st, L.wo.format, L.wo.data, n, q_dim, so, hidden, cus))
+        run_matvec(st, L.wo.format, L.wo.data, n, q_dim, attn, hidden, nullptr, 0.f, true, cus);
     } else {
       const uint32_t di = L.cache_index;
       fast_matvec_gdn_in(st, L.qkv.format, L.qkv.data, L.z.data, L.beta.data, L.alpha.data, conv_dim, value_dim, n_v,
@@ -447,6 +454,9 @@ int bch_qwen35_new(bch_ctx *ctx, const bch_qwen35_model *md, uint32_t n_ctx, int
            (rc = m->alloc_common()));
     if (rc) return cleanup(rc);
   }
+  // Decode steps at positions with at most kDeferSplits attention splits
+  // take the deferred-combine form.
+  m->short_below = deferred_combine_below(m->head_dim, m->kv_half);
   *out = m;
   return BCH_OK;
 }

@@ -107,8 +107,14 @@ LFM2_TINY_MIXED = Lfm2Config("lfm2-tiny-mixed", n_embd=256, n_ff=512, n_heads=4,
                              tensor_formats={"wv": Format.Q6K, "token_embd": Format.Q6K, "0.out_proj": Format.Q8_0,
                                              "1.wo": Format.Q4_0, "2.down": Format.Q6K, "3.up": Format.Q5K,
                                              "3.gate": Format.Q5K, "0.in_proj": Format.Q8_0})
+# A tiny model with 16 query heads of 64 (a 1,024-wide attention output, as
+# LFM2-350M's), so its decode takes the short-context form whose out
+# projection combines the attention splits (positions below 1,024 with an
+# f16 cache).
+LFM2_TINY_WIDE = Lfm2Config("lfm2-tiny-wide", n_embd=256, n_ff=512, n_heads=16, n_kv_heads=4, n_vocab=1000,
+                            attention_layers=[0, 2], n_layers=3)
 CONFIGS = {c.name: c for c in (LFM2_350M, LFM2_2_6B, LFM2_TINY, LFM2_TINY_F16, LFM2_8B_A1B, LFM2_TINY_MOE,
-                               LFM2_TINY_MIXED)}
+                               LFM2_TINY_MIXED, LFM2_TINY_WIDE)}
 
 
 def _matrix(fmt: int, rows: int, cols: int, rng: np.random.Generator) -> np.ndarray:

@@ -19,7 +19,8 @@ import pytest
 
 import oracle
 from bobcat_amd import BobcatError
-from bobcat_amd.lfm2 import LFM2_TINY, LFM2_TINY_F16, LFM2_TINY_MIXED, LFM2_TINY_MOE, Lfm2Hip, Lfm2Weights
+from bobcat_amd.lfm2 import (LFM2_TINY, LFM2_TINY_F16, LFM2_TINY_MIXED, LFM2_TINY_MOE, LFM2_TINY_WIDE, Lfm2Hip,
+                              Lfm2Weights)
 
 pytestmark = pytest.mark.gpu
 
@@ -186,6 +187,36 @@ def test_decode_across_attention_splits(hip, kv_half, grouped, monkeypatch):
     for t in toks[1020:]:
         got, want = gpu.step(t), cpu.step(t)
         assert rel(got, want) < tol, (t, rel(got, want))
+    gpu.close()
+
+
+@pytest.mark.parametrize("kv_half", [False, True])
+def test_decode_across_deferred_combine(hip, kv_half):
+    """A 1,024-wide attention output: decode steps with at most four
+    attention splits (f16: positions below 1,024) leave the splits' combine
+    to the out projection's input staging, later ones combine in the
+    attention launch.  Steps at 1018-1029 cross from one form to the other
+    (f32 splits hold 128 positions, so the f32 cache crosses at 512 and stays
+    past it), each against the oracle; then generate() across the boundary
+    (one replay per position, the graph chosen per position) against the
+    oracle's greedy continuation."""
+    w = Lfm2Weights(LFM2_TINY_WIDE, seed=13)
+    toks = prompt(LFM2_TINY_WIDE, 1030, seed=10)
+    gpu = Lfm2Hip(hip, w, n_ctx=1100, kv_half=kv_half)
+    cpu = oracle.Lfm2State(w, n_ctx=1100)
+    gpu.prefill(toks[:1018], logits=False)
+    for t in toks[:1018]:
+        cpu.step(t)
+    tol = HALF_TOLERANCE if kv_half else TOLERANCE
+    for t in toks[1018:]:
+        got, want = gpu.step(t), cpu.step(t)
+        assert rel(got, want) < tol, (t, rel(got, want))
+    gpu.close()
+    start = toks[:1016]
+    want, gaps = greedy_oracle(w, start, 16, n_ctx=1100)
+    gpu = Lfm2Hip(hip, w, n_ctx=1100, kv_half=kv_half)
+    gpu.prefill(start)
+    assert_greedy_matches(gpu.generate(16).tolist(), want, gaps)
     gpu.close()
 
 
