@@ -14,7 +14,8 @@
 // the two kernels give the same sums.
 //
 // Layout: a group of LPR lanes spans a row (lane i owns unit i, as in
-// gemv.h).  Workgroup w owns items [w·n/grid, (w+1)·n/grid); group g of
+// gemv.h).  Workgroup w owns a contiguous slab of n/grid items (the first
+// n % grid workgroups one more); group g of
 // the workgroup takes items g, g+G, g+2G, ... of the slab, at most MAXI.
 #pragma once
 #include <type_traits>
@@ -97,8 +98,11 @@ __device__ __forceinline__ void slab_body(const P &p, const float *__restrict__ 
   const int g = tid / LPR, li = tid % LPR;
   const bool active = li < (int)n_units;
   const uint32_t unit = active ? (uint32_t)li : 0u;
-  const uint32_t begin = (uint32_t)((uint64_t)n_items * blockIdx.x / gridDim.x);
-  const uint32_t end = (uint32_t)((uint64_t)n_items * (blockIdx.x + 1) / gridDim.x);
+  // The first n_items % grid workgroups take one item more (one 32-bit
+  // division: the slab's bounds gate the first weight address).
+  const uint32_t per = n_items / gridDim.x, rem = n_items - per * gridDim.x;
+  const uint32_t begin = blockIdx.x * per + min(blockIdx.x, rem);
+  const uint32_t end = begin + per + (blockIdx.x < rem ? 1u : 0u);
 
   // 1. The input (and norm weights) into registers, then every weight load
   // of the slab.  Memory returns in issue order, so the input goes first:

@@ -506,8 +506,9 @@ __global__ __launch_bounds__(64 * NW) void k_gemm(const uint8_t *__restrict__ W,
   }
   const uint32_t row0 = rt * OR;
   const uint32_t n_stages = n_cols / kGk;
-  const uint32_t st0 = (uint32_t)((uint64_t)sp * n_stages / splits);
-  const uint32_t st1 = (uint32_t)((uint64_t)(sp + 1) * n_stages / splits);
+  // 32-bit: at most kMaxSplitK splits of at most 2^26 stages.
+  const uint32_t st0 = sp * n_stages / splits;
+  const uint32_t st1 = (sp + 1) * n_stages / splits;
   const uint32_t last = st1 - 1;
 
   // Dequantising role: weight row ar, part ac.  (Rows past the end are
