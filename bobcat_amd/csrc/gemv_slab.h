@@ -89,7 +89,8 @@ struct SplitIn {
 
 template <class F, int LPR, int MAXI, bool NORM, class P, class In>
 __device__ __forceinline__ void slab_body(const P &p, const float *__restrict__ x, const float *__restrict__ nw,
-                                          float eps, uint32_t n_items, uint32_t n_units, uint32_t n_cols,
+                                          float eps, uint32_t per, uint32_t rem, uint32_t n_units,
+                                          uint32_t n_cols,
                                           const In &in) {
   constexpr int T = LPR <= 64 ? 256 : LPR;  // threads per workgroup
   constexpr int G = T / LPR;                // groups per workgroup
@@ -98,9 +99,9 @@ __device__ __forceinline__ void slab_body(const P &p, const float *__restrict__ 
   const int g = tid / LPR, li = tid % LPR;
   const bool active = li < (int)n_units;
   const uint32_t unit = active ? (uint32_t)li : 0u;
-  // The first n_items % grid workgroups take one item more (one 32-bit
-  // division: the slab's bounds gate the first weight address).
-  const uint32_t per = n_items / gridDim.x, rem = n_items - per * gridDim.x;
+  // Workgroups take `per` items each and the first `rem` one more (per and
+  // rem come from the host: the slab's bounds gate the first weight
+  // address, and a division here stood before it).
   const uint32_t begin = blockIdx.x * per + min(blockIdx.x, rem);
   const uint32_t end = begin + per + (blockIdx.x < rem ? 1u : 0u);
 
@@ -264,15 +265,16 @@ __device__ __forceinline__ void slab_body(const P &p, const float *__restrict__ 
 
 template <class F, int LPR, int MAXI, bool NORM, class P>
 __global__ __launch_bounds__(256) void k_slab(P p, const float *__restrict__ x, const float *__restrict__ nw,
-                                              float eps, uint32_t n_items, uint32_t n_units, uint32_t n_cols) {
-  slab_body<F, LPR, MAXI, NORM>(p, x, nw, eps, n_items, n_units, n_cols, PlainIn{});
+                                              float eps, uint32_t per, uint32_t rem, uint32_t n_units,
+                                              uint32_t n_cols) {
+  slab_body<F, LPR, MAXI, NORM>(p, x, nw, eps, per, rem, n_units, n_cols, PlainIn{});
 }
 // The same with the input from an input policy (SplitIn).
 template <class F, int LPR, int MAXI, bool NORM, class P, class In>
 __global__ __launch_bounds__(256) void k_slab_in(P p, const float *__restrict__ x, const float *__restrict__ nw,
-                                                 float eps, uint32_t n_items, uint32_t n_units, uint32_t n_cols,
-                                                 In in) {
-  slab_body<F, LPR, MAXI, NORM>(p, x, nw, eps, n_items, n_units, n_cols, in);
+                                                 float eps, uint32_t per, uint32_t rem, uint32_t n_units,
+                                                 uint32_t n_cols, In in) {
+  slab_body<F, LPR, MAXI, NORM>(p, x, nw, eps, per, rem, n_units, n_cols, in);
 }
 
 // Launch with `grid` workgroups; the caller has checked that every group's
@@ -280,6 +282,7 @@ __global__ __launch_bounds__(256) void k_slab_in(P p, const float *__restrict__ 
 template <class F, int LPR, int MAXI, bool NORM, class P, class In = PlainIn>
 static void launch_slab(hipStream_t s, uint32_t grid, const P &p, const float *x, const float *nw, float eps,
                         uint32_t n_items, uint32_t n_units, uint32_t n_cols, const In &in = In{}) {
+  const uint32_t per = n_items / grid, rem = n_items % grid;
   constexpr int threads = LPR <= 64 ? 256 : LPR;
   constexpr uint32_t kSlot = F::kUnit + (F::kUnit >= 64 ? 4 : 0);
   const uint32_t lds = n_units * kSlot * 4;
@@ -288,13 +291,14 @@ static void launch_slab(hipStream_t s, uint32_t grid, const P &p, const float *x
         hipFuncSetAttribute(reinterpret_cast<const void *>(k_slab<F, LPR, MAXI, NORM, P>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, 256 * kSlot * 4) == hipSuccess;
     (void)lds_limit_set;
-    k_slab<F, LPR, MAXI, NORM, P><<<grid, threads, lds, s>>>(p, x, nw, eps, n_items, n_units, n_cols);
+    k_slab<F, LPR, MAXI, NORM, P><<<grid, threads, lds, s>>>(p, x, nw, eps, per, rem, n_units, n_cols);
   } else {
     static const bool lds_limit_set =
         hipFuncSetAttribute(reinterpret_cast<const void *>(k_slab_in<F, LPR, MAXI, NORM, P, In>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, 256 * kSlot * 4) == hipSuccess;
     (void)lds_limit_set;
-    k_slab_in<F, LPR, MAXI, NORM, P, In><<<grid, threads, lds, s>>>(p, x, nw, eps, n_items, n_units, n_cols, in);
+    k_slab_in<F, LPR, MAXI, NORM, P, In><<<grid, threads, lds, s>>>(p, x, nw, eps, per, rem, n_units, n_cols,
+                                                                    in);
   }
 }
 
