@@ -66,7 +66,7 @@ __device__ __forceinline__ void norm_rope_wave(const float *src, const float *w,
     ss = fmaf(v[j], v[j], ss);
   }
   ss = wave_sum(ss);
-  const float scale = (float)(1.0 / sqrt((double)ss / (double)hd + (double)eps));
+  const float scale = rsqrtf(ss / (float)hd + eps);
 #pragma unroll
   for (int j = 0; j < kHd / 64; j++) {
     const uint32_t i = lane + 64 * j;

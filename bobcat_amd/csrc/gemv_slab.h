@@ -189,7 +189,7 @@ __device__ __forceinline__ void slab_body(const P &p, const float *__restrict__ 
     ss = 0.f;
 #pragma unroll
     for (int w = 0; w < T / 64; w++) ss += ss_s[w];
-    scale = (float)(1.0 / sqrt((double)ss / (double)n_cols + (double)eps));
+    scale = rsqrtf(ss / (float)n_cols + eps);  // f32: off the path to the first dot product
   }
 
   // 3. Dot products, reductions and stores, item by item.

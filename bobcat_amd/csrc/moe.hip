@@ -120,7 +120,7 @@ __global__ __launch_bounds__(1024) void k_moe_route(const float *__restrict__ x,
   float scale = 1.f;
   if (norm_w) {
     ss = block_sum<1024>(ss, red);
-    scale = (float)(1.0 / sqrt((double)ss / (double)n_cols + (double)eps));
+    scale = rsqrtf(ss / (float)n_cols + eps);
   }
 #pragma unroll
   for (int j = 0; j < kX; j++) {
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(256) void k_moe_scores(const float *__restrict__ x,
     if (lane == 0) red[wave] = ss;
     lds_barrier();
     ss = red[0] + red[1] + red[2] + red[3];
-    scale = (float)(1.0 / sqrt((double)ss / (double)n_cols + (double)eps));
+    scale = rsqrtf(ss / (float)n_cols + eps);
   }
   // Staged as rms_norm computes it: w·(x·scale).
 #pragma unroll
