@@ -196,7 +196,7 @@ __global__ __launch_bounds__(256 * CB) void k_gdn_step(GdnArgs a) {
   float ss = 0.f;
 #pragma unroll
   for (int b = 0; b < CB; b++) ss += ss_s[b];
-  const float scale = (float)(1.0 / sqrt((double)ss / (double)a.v_dim + (double)a.norm_eps));
+  const float scale = rsqrtf(ss / (float)a.v_dim + a.norm_eps);
   orow[col] = nw * (o * scale) * (gz / (1.0f + expf(-gz)));
 }
 

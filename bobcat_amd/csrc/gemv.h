@@ -402,7 +402,7 @@ __global__ __launch_bounds__(256) void k_gemv(P p, const float *__restrict__ x, 
     ss = 0.f;
 #pragma unroll
     for (int w = 0; w < T / 64; w++) ss += ss_s[w];
-    scale = (float)(1.0 / sqrt((double)ss / (double)n_cols + (double)eps));
+    scale = rsqrtf(ss / (float)n_cols + eps);
   }
   constexpr int W = LPR > 64 ? LPR / 64 : 1;
   __shared__ float red[N * W];
