@@ -433,6 +433,64 @@ __global__ __launch_bounds__(256) void k_embed_next(uint32_t format, const uint8
   __syncthreads();
   const uint32_t tok = token_s;
   const uint8_t *row = W + (uint64_t)tok * row_bytes;
+  if (format == 12 && n_embd % 256 == 0 && reinterpret_cast<uintptr_t>(row) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(out) % 16 == 0) {
+    // Q4_K rows eight elements per thread: one 16-byte header load and one
+    // 8-byte load of the eight quants (dequant_elem's arithmetic, element
+    // by element, so the values are the same bits).
+    for (uint32_t c0 = 8 * threadIdx.x; c0 < n_embd; c0 += 8 * 256) {
+      const uint8_t *b = row + (c0 / 256) * 144;
+      const uint4 h = *reinterpret_cast<const uint4 *>(b);
+      const uint32_t i = c0 % 256, j = i / 32, l0 = i % 32;
+      const uint2 qq = *reinterpret_cast<const uint2 *>(b + 16 + 32 * (j / 2) + l0);
+      auto sbyte = [&](uint32_t k) -> uint32_t {
+        const uint32_t w = k < 4 ? h.y : k < 8 ? h.z : h.w;
+        return (w >> (8 * (k % 4))) & 0xffu;
+      };
+      const float d = half_bits_to_float(h.x & 0xffffu);
+      const float dmin = half_bits_to_float(h.x >> 16);
+      uint32_t sc, mn;
+      if (j < 4) {
+        sc = sbyte(j) & 63;
+        mn = sbyte(j + 4) & 63;
+      } else {
+        sc = (sbyte(j + 4) & 0xf) | ((sbyte(j - 4) >> 6) << 4);
+        mn = (sbyte(j + 4) >> 4) | ((sbyte(j) >> 6) << 4);
+      }
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const uint32_t q = ((e < 4 ? qq.x : qq.y) >> (8 * (e % 4))) & 0xffu;
+        const uint32_t nib = (j & 1) ? (q >> 4) : (q & 0xf);
+        v[e] = __fsub_rn(__fmul_rn(__fmul_rn(d, (float)sc), (float)nib), __fmul_rn(dmin, (float)mn));
+      }
+      reinterpret_cast<float4 *>(out + c0)[0] = make_float4(v[0], v[1], v[2], v[3]);
+      reinterpret_cast<float4 *>(out + c0)[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    if (threadIdx.x == 0) {
+      tokens[p + 1] = tok;
+      *dpos = p + 1;  // every thread read p above, before this store
+    }
+    return;
+  }
+  if (format == 1 && n_embd % 8 == 0 && reinterpret_cast<uintptr_t>(row) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(out) % 16 == 0) {
+    // F16 rows eight elements (one 16-byte load) per thread.
+    for (uint32_t c0 = 8 * threadIdx.x; c0 < n_embd; c0 += 8 * 256) {
+      const uint4 w = *reinterpret_cast<const uint4 *>(row + 2 * (uint64_t)c0);
+      reinterpret_cast<float4 *>(out + c0)[0] =
+          make_float4(half_bits_to_float(w.x & 0xffffu), half_bits_to_float(w.x >> 16),
+                      half_bits_to_float(w.y & 0xffffu), half_bits_to_float(w.y >> 16));
+      reinterpret_cast<float4 *>(out + c0)[1] =
+          make_float4(half_bits_to_float(w.z & 0xffffu), half_bits_to_float(w.z >> 16),
+                      half_bits_to_float(w.w & 0xffffu), half_bits_to_float(w.w >> 16));
+    }
+    if (threadIdx.x == 0) {
+      tokens[p + 1] = tok;
+      *dpos = p + 1;  // every thread read p above, before this store
+    }
+    return;
+  }
   // The thread's first kE elements are read before any is stored.
   constexpr int kE = 8;
   float v[kE];
