@@ -112,6 +112,17 @@ struct Sequence {
   int upload(Uploader &up);
   // The buffers every sequence has; called by the model's constructor.
   int alloc_common();
+  // The library SwiGLU pair of prefill batches (run_blas_pair): when it is
+  // enabled for this model (BCH_NO_BLAS unset, batches larger than
+  // kBlasPairMinTokens, at least kBlasPairMinWeights in the pair or
+  // BCH_BLAS_PAIR=1, n_ff a multiple of 4) and the format expands,
+  // *out receives the fp16 [gate rows; up rows] copy, else nullptr.
+  int expand_pair(const DevMatrix &gate, const DevMatrix &up, uint32_t n_ff, _Float16 **out);
+  // After the expansions: the pair's product and scale buffers (when any
+  // layer expanded), the library handle, and the expansions finished.
+  int finish_pairs(uint32_t n_ff);
+  float *pair_out = nullptr, *pair_us = nullptr;
+  bool any_pair = false;
 
   int reset();
   int step(uint32_t token, float *logits, float *trace_embedding, float *trace_layers, float *trace_final);

@@ -107,6 +107,34 @@ int Sequence::upload(Uploader &up) {
   return BCH_OK;
 }
 
+int Sequence::expand_pair(const DevMatrix &gate, const DevMatrix &up, uint32_t n_ff, _Float16 **out) {
+  *out = nullptr;
+  auto env_on = [](const char *name) {
+    const char *e = getenv(name);
+    return e && *e && *e != '0';
+  };
+  // Smaller pairs run as fast on the Q4_K tile (Qwen3.5-0.8B, LFM2-350M at
+  // 512 tokens); BCH_BLAS_PAIR=1 takes every size.
+  const bool big = 2ull * n_ff * n_embd >= kBlasPairMinWeights || env_on("BCH_BLAS_PAIR");
+  if (env_on("BCH_NO_BLAS") || !big || batch <= kBlasPairMinTokens || n_ff % 4 || gate.format != up.format ||
+      !expand_f16_supported(gate.format, n_embd))
+    return BCH_OK;
+  const uint64_t half = (uint64_t)n_ff * n_embd;
+  BCH_TRY(alloc_t(2 * half, out));
+  run_expand_f16(s, gate.format, gate.data, n_ff, n_embd, *out);
+  run_expand_f16(s, up.format, up.data, n_ff, n_embd, *out + half);
+  any_pair = true;
+  return BCH_OK;
+}
+
+int Sequence::finish_pairs(uint32_t n_ff) {
+  if (!any_pair) return BCH_OK;
+  BCH_TRY(alloc_t((uint64_t)batch * 2 * n_ff, &pair_out));
+  BCH_TRY(alloc_t((uint64_t)batch, &pair_us));
+  BCH_TRY(blas_prepare());
+  return check_hip(hipStreamSynchronize(s), "weight expansion");
+}
+
 int Sequence::alloc_common() {
   BCH_TRY(alloc_t(n_vocab, &logits));
   BCH_TRY(alloc_t((uint64_t)n_ctx + 2, &tokens));

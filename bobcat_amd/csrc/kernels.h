@@ -334,4 +334,33 @@ void run_matmul(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_row
                 float *y, uint32_t n_tokens, uint32_t store, void *scratch, uint64_t scratch_bytes,
                 bool split_ready = false, const uint8_t *W2 = nullptr, PendingSum *defer = nullptr);
 
+// Expanded fp16 copy of a weight matrix ([n_rows][n_cols], the values
+// k_gemm dequantises) for the library GEMM; n_cols a multiple of 64.
+bool expand_f16_supported(uint32_t format, uint32_t n_cols);
+void run_expand_f16(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols,
+                    _Float16 *out);
+// blas.hip.  D [n_tokens][n_rows] f32 = H [n_tokens][n_cols] fp16 · W16^T
+// through hipBLASLt (the device's handle and workspace made on first use,
+// or by blas_prepare).
+int blas_prepare();
+int run_blas_gemm_f16(hipStream_t s, const _Float16 *W16, uint32_t n_rows, uint32_t n_cols, const _Float16 *H,
+                      uint32_t n_tokens, float *D);
+// The SwiGLU of a library pair product D [n_tokens][2 n_ff] whose inputs
+// had the token scales us (1/us applied to each token's fp16 inputs): the
+// down projection's fp16 inputs go to `scratch` as run_matmul's
+// split_ready expects them, and ffn to f32 when given.
+void run_swiglu_split(hipStream_t s, const float *D, uint32_t n_ff, uint32_t n_tokens, const float *us, float *f32,
+                      void *scratch);
+// The SwiGLU pair of a prefill batch on the library GEMM (run_blas_gemm_f16
+// then run_swiglu_split): the inputs and token scales in `split` as
+// run_rms_norm_split leaves them, pair_out [n_tokens][2 n_ff] and pair_us
+// [n_tokens] its own buffers, ffn (optional) the f32 activations.  False
+// when the library call fails (printed); nothing was then written.
+bool run_blas_pair(hipStream_t s, const _Float16 *gate_up16, uint32_t n_ff, uint32_t n_cols, uint32_t n_tokens,
+                   void *split, float *pair_out, float *pair_us, float *ffn);
+// Prefill batches of more than this many tokens take the library pair.
+constexpr uint32_t kBlasPairMinTokens = 128;
+// Pairs of fewer weights (gate and up together) keep the Q4_K tile.
+constexpr uint64_t kBlasPairMinWeights = 1ull << 24;
+
 }  // namespace bch

@@ -43,7 +43,11 @@ struct Layer {
   bool moe = false;
   DevMatrix router, gate_exps, up_exps, down_exps;
   const float *expert_bias = nullptr;
+  // Dense SwiGLU: the gate rows then the up rows as fp16 [2 n_ff][n_embd]
+  // for the library GEMM of prefill batches (expanded once at creation).
+  _Float16 *gate_up16 = nullptr;
 };
+
 
 }  // namespace bch
 
@@ -337,11 +341,16 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
       }
       check_finite(s, "moe", il, m->hidden, (uint64_t)count * n);
     } else {
-      if (L.gate.format == L.up.format) {
+      // The pair through the library GEMM on the expanded weights when the
+      // model has them; its SwiGLU also writes the down projection's inputs.
+      const bool blas_pair = L.gate_up16 && count > kBlasPairMinTokens &&
+                             run_blas_pair(s, L.gate_up16, m->n_ff, n, count, m->split, m->pair_out, m->pair_us,
+                                           check_mode() ? m->ffn : nullptr);
+      if (!blas_pair && L.gate.format == L.up.format) {
         // Gate and up in one paired launch: ffn = silu(gate·x) ⊙ (up·x).
         run_matmul(s, L.gate.format, L.gate.data, m->n_ff, n, m->normed, m->ffn, count, 3, m->split, m->split_bytes,
                    true, L.up.data);
-      } else {
+      } else if (!blas_pair) {
         run_matmul(s, L.gate.format, L.gate.data, m->n_ff, n, m->normed, m->ffn, count, 0, m->split, m->split_bytes,
                    true);
         check_finite(s, "gate", il, m->ffn, (uint64_t)count * m->n_ff);
@@ -349,7 +358,7 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
       }
       check_finite(s, "swiglu", il, m->ffn, (uint64_t)count * m->n_ff);
       run_matmul(s, L.down.format, L.down.data, n, m->n_ff, m->ffn, m->hidden, count, 1, m->split, m->split_bytes,
-                 false, nullptr, defer);
+                 blas_pair, nullptr, defer);
       check_finite(s, "down", il, m->hidden, (uint64_t)count * n);
     }
     if (trace) run_copy(s, m->hidden, m->trace + (1 + il) * tstride, count * n, nullptr, 0);
@@ -541,6 +550,11 @@ int bch_lfm2_new(bch_ctx *ctx, const bch_lfm2_model *md, uint32_t n_ctx, int kv_
            (rc = m->alloc_common()));
     if (rc) return cleanup(rc);
   }
+  // The dense layers' SwiGLU pairs expanded for the library GEMM of prefill.
+  for (Layer &L : m->layers)
+    if (!L.moe)
+      if (int rc = m->expand_pair(L.gate, L.up, m->n_ff, &L.gate_up16)) return cleanup(rc);
+  if (int rc = m->finish_pairs(m->n_ff)) return cleanup(rc);
   // Decode steps at positions with at most kDeferSplits attention splits
   // take the deferred-combine form.
   m->short_below = deferred_combine_below(m->head_dim, m->kv_half);

@@ -1009,3 +1009,122 @@ extern "C" int bch_matmul(bch_ctx *ctx, uint32_t format, bch_view weights, uint3
     if (n_tokens) run_matmul(s, format, W, n_rows, n_cols, xp, yp, n_tokens, store, split, scratch_bytes);
   });
 }
+
+namespace bch {
+
+// ---------------------------------------------------------------------
+// Expanded fp16 weights and the SwiGLU hand-off of the library GEMM pair
+// ---------------------------------------------------------------------
+
+// out[r][c] = the fp16 weight k_gemm dequantises into LDS for row r,
+// column c (the same fetch and conversion code, so the same bits).  Two
+// threads per 64-column stage of a row, each 32 weights.
+template <uint32_t FMT>
+__global__ __launch_bounds__(256) void k_expand_f16(const uint8_t *__restrict__ W, uint64_t row_bytes, uint32_t n_rows,
+                                                    uint32_t n_cols, _Float16 *__restrict__ out) {
+  const uint32_t stages = n_cols / kGk;
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (uint64_t)n_rows * stages * 2) return;
+  const int c = (int)(i & 1);
+  const uint64_t rs = i >> 1;
+  const uint32_t row = (uint32_t)(rs / stages), k0 = (uint32_t)(rs % stages) * kGk;
+  const uint8_t *wr = W + (uint64_t)row * row_bytes;
+  GemmRaw r{};
+  gemm_fetch<FMT, 32>(wr, k0, c, r);
+  gemm_dequant_all<FMT, 32>(wr, k0, c, r, out + (uint64_t)row * n_cols + k0);
+}
+
+bool expand_f16_supported(uint32_t format, uint32_t n_cols) {
+  return n_cols % kGk == 0 && (format == 12 || format == 1 || format == 0 || format == 13 || format == 14 ||
+                               format == 8 || format == 2);
+}
+
+void run_expand_f16(hipStream_t s, uint32_t format, const uint8_t *W, uint32_t n_rows, uint32_t n_cols,
+                    _Float16 *out) {
+  const uint64_t rb = bch_row_bytes(format, n_cols);
+  const uint64_t threads = (uint64_t)n_rows * (n_cols / kGk) * 2;
+  const dim3 grid((uint32_t)div_ceil(threads, 256));
+  switch (format) {
+    case 12: k_expand_f16<12><<<grid, 256, 0, s>>>(W, rb, n_rows, n_cols, out); break;
+    case 1: k_expand_f16<1><<<grid, 256, 0, s>>>(W, rb, n_rows, n_cols, out); break;
+    case 14: k_expand_f16<14><<<grid, 256, 0, s>>>(W, rb, n_rows, n_cols, out); break;
+    case 13: k_expand_f16<13><<<grid, 256, 0, s>>>(W, rb, n_rows, n_cols, out); break;
+    case 8: k_expand_f16<8><<<grid, 256, 0, s>>>(W, rb, n_rows, n_cols, out); break;
+    case 2: k_expand_f16<2><<<grid, 256, 0, s>>>(W, rb, n_rows, n_cols, out); break;
+    default: k_expand_f16<0><<<grid, 256, 0, s>>>(W, rb, n_rows, n_cols, out); break;
+  }
+}
+
+// Token t of the pair product D [n_tokens][2 n_ff] (gate rows, then up
+// rows, of inputs scaled by 1/us[t]): ffn = silu(g·us)·(u·us), as k_gemm's
+// paired epilogue computes it, then the fp16 inputs of the down projection
+// exactly as k_split_hi makes them from ffn (H [n_tokens][n_ff], then
+// unscale [n_tokens]).  F32 (optional) receives ffn itself.  PER > 0: each
+// thread keeps its PER float4 of ffn in registers; PER = 0 recomputes.
+template <int PER>
+__global__ __launch_bounds__(256) void k_swiglu_split(const float *__restrict__ D, uint32_t n_ff,
+                                                      const float *__restrict__ us, float *__restrict__ F32,
+                                                      _Float16 *__restrict__ H, float *__restrict__ unscale) {
+  const uint32_t t = blockIdx.x, tid = threadIdx.x, n4 = n_ff / 4;
+  const float4 *g4 = reinterpret_cast<const float4 *>(D + (uint64_t)t * 2 * n_ff);
+  const float4 *u4 = g4 + n4;
+  const float s = us[t];
+  auto act = [&](uint32_t i) {
+    const float4 g = g4[i], u = u4[i];
+    return float4{silu_f(g.x * s) * (u.x * s), silu_f(g.y * s) * (u.y * s), silu_f(g.z * s) * (u.z * s),
+                  silu_f(g.w * s) * (u.w * s)};
+  };
+  auto amax = [](float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); };
+  float4 xv[PER > 0 ? PER : 1];
+  float mx = 0.f;
+  if constexpr (PER > 0) {
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+      const uint32_t i = tid + 256 * k;
+      xv[k] = i < n4 ? act(i) : float4{0.f, 0.f, 0.f, 0.f};
+      mx = fmaxf(mx, amax(xv[k]));
+    }
+  } else {
+    for (uint32_t i = tid; i < n4; i += 256) mx = fmaxf(mx, amax(act(i)));
+  }
+  __shared__ float red[4];
+  mx = block_max<256>(mx, red);
+  int ex = 0;
+  if (mx > 0.f) frexpf(mx, &ex);
+  const int k2 = max(-100, min(100, 14 - ex));
+  const float scale = ldexpf(1.0f, k2);
+  if (tid == 0) unscale[t] = ldexpf(1.0f, -k2);
+  half4_t *row = reinterpret_cast<half4_t *>(H + (uint64_t)t * n_ff);
+  float4 *f4 = F32 ? reinterpret_cast<float4 *>(F32 + (uint64_t)t * n_ff) : nullptr;
+  auto put = [&](uint32_t i, float4 v) {
+    half4_t o;
+    o[0] = (_Float16)(v.x * scale), o[1] = (_Float16)(v.y * scale);
+    o[2] = (_Float16)(v.z * scale), o[3] = (_Float16)(v.w * scale);
+    row[i] = o;
+    if (f4) f4[i] = v;
+  };
+  if constexpr (PER > 0) {
+#pragma unroll
+    for (int k = 0; k < PER; k++)
+      if (tid + 256 * k < n4) put(tid + 256 * k, xv[k]);
+  } else {
+    for (uint32_t i = tid; i < n4; i += 256) put(i, act(i));
+  }
+}
+
+void run_swiglu_split(hipStream_t s, const float *D, uint32_t n_ff, uint32_t n_tokens, const float *us, float *f32,
+                      void *scratch) {
+  _Float16 *H = static_cast<_Float16 *>(scratch);
+  float *unscale = reinterpret_cast<float *>(H + (uint64_t)n_tokens * n_ff);
+  const uint32_t n4 = n_ff / 4;
+  if (n4 <= 4 * 256)
+    k_swiglu_split<4><<<n_tokens, 256, 0, s>>>(D, n_ff, us, f32, H, unscale);
+  else if (n4 <= 8 * 256)
+    k_swiglu_split<8><<<n_tokens, 256, 0, s>>>(D, n_ff, us, f32, H, unscale);
+  else if (n4 <= 12 * 256)
+    k_swiglu_split<12><<<n_tokens, 256, 0, s>>>(D, n_ff, us, f32, H, unscale);
+  else
+    k_swiglu_split<0><<<n_tokens, 256, 0, s>>>(D, n_ff, us, f32, H, unscale);
+}
+
+}  // namespace bch

@@ -36,6 +36,9 @@ struct QwenLayer {
   DevMatrix qkv, z, beta, alpha, out;
   const float *taps = nullptr, *dt_bias = nullptr, *a = nullptr, *ssm_norm = nullptr;
   DevMatrix gate, up, down;
+  // The SwiGLU pair as fp16 [gate rows; up rows] for the library GEMM of
+  // prefill batches (Sequence::expand_pair), or nullptr.
+  _Float16 *gate_up16 = nullptr;
   // Prefill: rows of wq | wk | wv (attention) or qkv | z | beta | alpha
   // (DeltaNet) when they lie back to back in device memory in one format
   // (one GEMM), else 0.
@@ -289,15 +292,20 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
                  nullptr, defer);
     }
     run_rms_norm_split(st, hidden, L.ffn_norm, normed, n, count, norm_eps, split, &pend);
-    if (L.gate.format == L.up.format) {
+    // The pair through the library GEMM on the expanded weights when the
+    // model has them; its SwiGLU also writes the down projection's inputs.
+    const bool blas_pair = L.gate_up16 && count > kBlasPairMinTokens &&
+                           run_blas_pair(st, L.gate_up16, n_ff, n, count, split, pair_out, pair_us, nullptr);
+    if (!blas_pair && L.gate.format == L.up.format) {
       // Gate and up in one paired launch: ffn = silu(gate·x) ⊙ (up·x).
       run_matmul(st, L.gate.format, L.gate.data, n_ff, n, normed, ffn, count, 3, split, split_bytes, true,
                  L.up.data);
-    } else {
+    } else if (!blas_pair) {
       run_matmul(st, L.gate.format, L.gate.data, n_ff, n, normed, ffn, count, 0, split, split_bytes, true);
       run_matmul(st, L.up.format, L.up.data, n_ff, n, normed, ffn, count, 2, split, split_bytes, true);
     }
-    run_matmul(st, L.down.format, L.down.data, n, n_ff, ffn, hidden, count, 1, split, split_bytes, false, nullptr, defer);
+    run_matmul(st, L.down.format, L.down.data, n, n_ff, ffn, hidden, count, 1, split, split_bytes, blas_pair, nullptr,
+               defer);
     if (trace) run_copy(st, hidden, this->trace + (1 + il) * tstride, count * n, nullptr, 0);
   }
   finish_pending_sum(st, pend, hidden);
@@ -454,6 +462,10 @@ int bch_qwen35_new(bch_ctx *ctx, const bch_qwen35_model *md, uint32_t n_ctx, int
            (rc = m->alloc_common()));
     if (rc) return cleanup(rc);
   }
+  // The SwiGLU pairs expanded for the library GEMM of prefill.
+  for (QwenLayer &L : m->layers)
+    if (int rc = m->expand_pair(L.gate, L.up, m->n_ff, &L.gate_up16)) return cleanup(rc);
+  if (int rc = m->finish_pairs(m->n_ff)) return cleanup(rc);
   // Decode steps at positions with at most kDeferSplits attention splits
   // take the deferred-combine form.
   m->short_below = deferred_combine_below(m->head_dim, m->kv_half);

@@ -104,6 +104,39 @@ def test_prefill_trace_matches_oracle(hip, weights, kv_half):
     gpu.close()
 
 
+def test_prefill_library_pair_matches_oracle(hip, monkeypatch):
+    """A prefill batch of more than 128 tokens with the SwiGLU pair on the
+    library GEMM over the expanded fp16 weights (forced for this small
+    model with BCH_BLAS_PAIR=1; by default only pairs of 2^24 weights or
+    more take it), its SwiGLU writing the down projection's fp16 inputs:
+    every layer of every token against the oracle within the prefill bound,
+    and against the same prompt on the fused Q4_K tile (BCH_NO_BLAS=1),
+    which sums the same fp16 products in another order."""
+    w = Lfm2Weights(LFM2_TINY, seed=21)
+    cfg = w.cfg
+    toks = prompt(cfg, 160, seed=22)
+    monkeypatch.setenv("BCH_BLAS_PAIR", "1")
+    gpu = Lfm2Hip(hip, w, n_ctx=192, kv_half=False)
+    lg, (emb, layers, final) = gpu.prefill(toks, trace=True)
+    nxt = gpu.step(7)
+    gpu.close()
+    monkeypatch.setenv("BCH_NO_BLAS", "1")
+    tile = Lfm2Hip(hip, w, n_ctx=192, kv_half=False)
+    lg_tile = tile.prefill(toks)
+    nxt_tile = tile.step(7)
+    tile.close()
+    assert rel(lg, lg_tile) < 1e-4 and rel(nxt, nxt_tile) < 1e-4, (rel(lg, lg_tile), rel(nxt, nxt_tile))
+    cpu = oracle.Lfm2State(w, n_ctx=192)
+    worst = 0.0
+    for t, tok in enumerate(toks):
+        wl, (wemb, wlayers, wfinal) = cpu.step(tok, trace=True)
+        for i in range(cfg.n_layers):
+            worst = max(worst, rel(layers[i, t], wlayers[i * cfg.n_embd:(i + 1) * cfg.n_embd]))
+    assert worst < HALF_TOLERANCE, worst
+    assert rel(lg, wl) < HALF_TOLERANCE
+    assert rel(nxt, cpu.step(7)) < HALF_TOLERANCE
+
+
 def greedy_oracle(weights, tokens, n_gen, n_ctx):
     """Oracle greedy continuation and, per step, the gap between its top-2 logits."""
     cpu = oracle.Lfm2State(weights, n_ctx=n_ctx)
