@@ -20,11 +20,8 @@
 namespace bch {
 namespace {
 
-constexpr uint64_t kWorkspaceBytes = 32ull << 20;
-
 struct Blas {
   hipblasLtHandle_t handle = nullptr;
-  void *workspace = nullptr;
   hipblasLtMatmulDesc_t desc = nullptr;
   std::map<std::tuple<uint32_t, uint32_t, uint32_t>, hipblasLtMatmulAlgo_t> algos;
   bool broken = false;
@@ -37,7 +34,7 @@ int blas_fail(const char *what, int st) {
   return fail(BCH_ERR_EXECUTION, "hipBLASLt %s failed (status %d)", what, st);
 }
 
-// The device's handle, workspace and matmul description (f32 compute and
+// The device's handle and matmul description (f32 compute and
 // scale, D = W^T-view · H: transA = T, transB = N), created on first use.
 int blas_get(Blas **out) {
   int dev = 0;
@@ -49,10 +46,6 @@ int blas_get(Blas **out) {
     if ((st = hipblasLtCreate(&b.handle)) != HIPBLAS_STATUS_SUCCESS) {
       b.broken = true;
       return blas_fail("create", st);
-    }
-    if (hipMalloc(&b.workspace, kWorkspaceBytes) != hipSuccess) {
-      b.broken = true;
-      return fail(BCH_ERR_ALLOCATION, "hipBLASLt workspace (%llu bytes)", (unsigned long long)kWorkspaceBytes);
     }
     if ((st = hipblasLtMatmulDescCreate(&b.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F)) != HIPBLAS_STATUS_SUCCESS) {
       b.broken = true;
@@ -103,7 +96,8 @@ int run_blas_gemm_f16(hipStream_t s, const _Float16 *W16, uint32_t n_rows, uint3
   if (it == b->algos.end()) {
     hipblasLtMatmulPreference_t pref;
     if ((st = hipblasLtMatmulPreferenceCreate(&pref))) return blas_fail("preference", st);
-    const uint64_t ws = kWorkspaceBytes;
+    // Algorithms without a workspace only: nothing is shared between calls.
+    const uint64_t ws = 0;
     hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws));
     hipblasLtMatmulHeuristicResult_t res[1];
     int found = 0;
@@ -114,7 +108,7 @@ int run_blas_gemm_f16(hipStream_t s, const _Float16 *W16, uint32_t n_rows, uint3
   }
   const float alpha = 1.0f, beta = 0.0f;
   if ((st = hipblasLtMatmul(b->handle, b->desc, &alpha, W16, L.a, H, L.b, &beta, D, L.d, D, L.d, &it->second,
-                            b->workspace, kWorkspaceBytes, s)))
+                            nullptr, 0, s)))
     return blas_fail("matmul", st);
   return BCH_OK;
 }

@@ -121,7 +121,8 @@ struct Sequence {
   // After the expansions: the pair's product and scale buffers (when any
   // layer expanded), the library handle, and the expansions finished.
   int finish_pairs(uint32_t n_ff);
-  float *pair_out = nullptr, *pair_us = nullptr;
+  bool blas_wanted(uint32_t format, uint64_t weights, uint64_t min_weights) const;
+  float *pair_out = nullptr, *pair_us = nullptr;  // pair product; a copy of the batch's token scales
   bool any_pair = false;
 
   int reset();

@@ -104,20 +104,31 @@ int Sequence::upload(Uploader &up) {
     if (hipMemcpy(weights + up.offsets[i], up.items[i].first, up.items[i].second, hipMemcpyHostToDevice) != hipSuccess)
       return fail(BCH_ERR_ALLOCATION, "cannot copy the weights to the device");
   for (auto &f : up.fixups) *f.first = weights + up.offsets[f.second];
-  return BCH_OK;
+  // A copy from pageable host memory may return before its DMA has landed,
+  // and the model's stream (non-blocking) does not wait for the null
+  // stream: the first kernels to read the weights (the expansions, right
+  // after this) must not start before the copies are done.
+  return check_hip(hipDeviceSynchronize(), "weight upload");
+}
+
+static bool env_on(const char *name) {
+  const char *e = getenv(name);
+  return e && *e && *e != '0';
+}
+
+// The library path is on (BCH_NO_BLAS unset), the batch can exceed
+// kBlasPairMinTokens, and the matrix (or pair) of `weights` weights in
+// `format` is large enough or BCH_BLAS_PAIR=1 takes every size.
+bool Sequence::blas_wanted(uint32_t format, uint64_t weights, uint64_t min_weights) const {
+  return !env_on("BCH_NO_BLAS") && batch > kBlasPairMinTokens && expand_f16_supported(format, n_embd) &&
+         (weights >= min_weights || env_on("BCH_BLAS_PAIR"));
 }
 
 int Sequence::expand_pair(const DevMatrix &gate, const DevMatrix &up, uint32_t n_ff, _Float16 **out) {
   *out = nullptr;
-  auto env_on = [](const char *name) {
-    const char *e = getenv(name);
-    return e && *e && *e != '0';
-  };
   // Smaller pairs run as fast on the Q4_K tile (Qwen3.5-0.8B, LFM2-350M at
-  // 512 tokens); BCH_BLAS_PAIR=1 takes every size.
-  const bool big = 2ull * n_ff * n_embd >= kBlasPairMinWeights || env_on("BCH_BLAS_PAIR");
-  if (env_on("BCH_NO_BLAS") || !big || batch <= kBlasPairMinTokens || n_ff % 4 || gate.format != up.format ||
-      !expand_f16_supported(gate.format, n_embd))
+  // 512 tokens).
+  if (n_ff % 4 || gate.format != up.format || !blas_wanted(gate.format, 2ull * n_ff * n_embd, kBlasPairMinWeights))
     return BCH_OK;
   const uint64_t half = (uint64_t)n_ff * n_embd;
   BCH_TRY(alloc_t(2 * half, out));
