@@ -114,17 +114,13 @@ int run_blas_gemm_f16(hipStream_t s, const _Float16 *W16, uint32_t n_rows, uint3
 }
 
 // The SwiGLU pair of a prefill batch on the library GEMM: `split` holds the
-// batch's fp16 inputs and token scales (k_rms_norm_split's), gate_up16 the
-// expanded [2 n_ff][n_cols] weights.  The scales are copied out first
-// because the down projection's fp16 inputs overwrite them.  False (with
-// the error printed) when hipBLASLt fails, so the caller runs the Q4_K
-// tile instead.
+// batch's fp16 inputs (k_rms_norm_split's), pair_us their token scales,
+// gate_up16 the expanded [2 n_ff][n_cols] weights.  False (with the error
+// printed) when hipBLASLt fails, so the caller runs the Q4_K tile instead.
 bool run_blas_pair(hipStream_t s, const _Float16 *gate_up16, uint32_t n_ff, uint32_t n_cols, uint32_t n_tokens,
-                   void *split, float *pair_out, float *pair_us, float *ffn) {
-  const _Float16 *h = static_cast<const _Float16 *>(split);
-  if (hipMemcpyAsync(pair_us, h + (uint64_t)n_tokens * n_cols, (uint64_t)n_tokens * 4, hipMemcpyDeviceToDevice, s) !=
-          hipSuccess ||
-      run_blas_gemm_f16(s, gate_up16, 2 * n_ff, n_cols, h, n_tokens, pair_out) != BCH_OK) {
+                   void *split, float *pair_out, const float *pair_us, float *ffn) {
+  if (run_blas_gemm_f16(s, gate_up16, 2 * n_ff, n_cols, static_cast<const _Float16 *>(split), n_tokens, pair_out) !=
+      BCH_OK) {
     fprintf(stderr, "bobcat_hip: %s; the SwiGLU pair runs on the Q4_K tile\n", bch_last_error());
     return false;
   }

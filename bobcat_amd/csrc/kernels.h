@@ -320,8 +320,10 @@ void finish_pending_sum(hipStream_t s, PendingSum &p, float *y);
 // scratch, ..., split_ready = true) reads.  With `pending` (left by the
 // run_matmul that accumulated into x, on the same scratch) x first
 // receives that sum, written back to x; the pending sum is then cleared.
+// unscale_copy (optional, [rows]): a second copy of the token scales,
+// outside the scratch (run_blas_pair's).
 void run_rms_norm_split(hipStream_t s, float *x, const float *w, float *out, uint32_t n, uint32_t rows, float eps,
-                        void *scratch, PendingSum *pending = nullptr);
+                        void *scratch, PendingSum *pending = nullptr, float *unscale_copy = nullptr);
 // store 3: y = silu(W·x) ⊙ (W2·x), W and W2 the gate and up matrices of
 // a SwiGLU (same format and shape).  split_ready: the previous run_matmul
 // on this scratch had the same x, n_tokens and n_cols, so its fp16 inputs
@@ -352,12 +354,13 @@ int run_blas_gemm_f16(hipStream_t s, const _Float16 *W16, uint32_t n_rows, uint3
 void run_swiglu_split(hipStream_t s, const float *D, uint32_t n_ff, uint32_t n_tokens, const float *us, float *f32,
                       void *scratch);
 // The SwiGLU pair of a prefill batch on the library GEMM (run_blas_gemm_f16
-// then run_swiglu_split): the inputs and token scales in `split` as
-// run_rms_norm_split leaves them, pair_out [n_tokens][2 n_ff] and pair_us
-// [n_tokens] its own buffers, ffn (optional) the f32 activations.  False
-// when the library call fails (printed); nothing was then written.
+// then run_swiglu_split): the inputs in `split` as run_rms_norm_split
+// leaves them, their token scales also in pair_us (its unscale_copy: the
+// SwiGLU overwrites the ones in `split`), pair_out [n_tokens][2 n_ff] its
+// own buffer, ffn (optional) the f32 activations.  False when the library
+// call fails (printed); nothing was then written.
 bool run_blas_pair(hipStream_t s, const _Float16 *gate_up16, uint32_t n_ff, uint32_t n_cols, uint32_t n_tokens,
-                   void *split, float *pair_out, float *pair_us, float *ffn);
+                   void *split, float *pair_out, const float *pair_us, float *ffn);
 // Prefill batches of more than this many tokens take the library pair.
 constexpr uint32_t kBlasPairMinTokens = 128;
 // Pairs of fewer weights (gate and up together) keep the Q4_K tile.

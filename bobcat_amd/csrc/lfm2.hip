@@ -315,7 +315,9 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
       check_finite(s, "attn_output", il, m->hidden, (uint64_t)count * n);
     }
     // (The MoE experts' shared input is this norm's output too.)
-    run_rms_norm_split(s, m->hidden, L.ffn_norm, m->normed, n, count, m->norm_eps, m->split, &pend);
+    const bool pair_ok = L.gate_up16 && count > kBlasPairMinTokens;
+    run_rms_norm_split(s, m->hidden, L.ffn_norm, m->normed, n, count, m->norm_eps, m->split, &pend,
+                       pair_ok ? m->pair_us : nullptr);
     check_finite(s, "ffn_norm", il, m->normed, (uint64_t)count * n);
     if (L.moe) {
       // Route the whole batch in one launch, then each token's experts.
@@ -343,9 +345,8 @@ static void lfm2_batch(bch_lfm2 *m, hipStream_t s, uint32_t pos, uint32_t count,
     } else {
       // The pair through the library GEMM on the expanded weights when the
       // model has them; its SwiGLU also writes the down projection's inputs.
-      const bool blas_pair = L.gate_up16 && count > kBlasPairMinTokens &&
-                             run_blas_pair(s, L.gate_up16, m->n_ff, n, count, m->split, m->pair_out, m->pair_us,
-                                           check_mode() ? m->ffn : nullptr);
+      const bool blas_pair = pair_ok && run_blas_pair(s, L.gate_up16, m->n_ff, n, count, m->split, m->pair_out,
+                                                      m->pair_us, check_mode() ? m->ffn : nullptr);
       if (!blas_pair && L.gate.format == L.up.format) {
         // Gate and up in one paired launch: ffn = silu(gate·x) ⊙ (up·x).
         run_matmul(s, L.gate.format, L.gate.data, m->n_ff, n, m->normed, m->ffn, count, 3, m->split, m->split_bytes,

@@ -162,7 +162,8 @@ template <int PER, int SPLITS>
 __global__ __launch_bounds__(256) void k_rms_norm_split(float *__restrict__ x, const float *__restrict__ w,
                                                        float *__restrict__ out, uint32_t n, float eps,
                                                        _Float16 *__restrict__ H, float *__restrict__ unscale,
-                                                       const float *__restrict__ P, uint32_t splits) {
+                                                       const float *__restrict__ P, uint32_t splits,
+                                                       float *__restrict__ unscale_copy) {
   constexpr bool SUM = SPLITS > 0;
   __shared__ float red[4];
   const uint32_t t = blockIdx.x, tid = threadIdx.x;
@@ -239,7 +240,10 @@ __global__ __launch_bounds__(256) void k_rms_norm_split(float *__restrict__ x, c
   if (mx > 0.f) frexpf(mx, &ex);  // mx < 2^ex
   const int k2 = max(-100, min(100, 14 - ex));
   const float s2 = ldexpf(1.0f, k2);
-  if (tid == 0) unscale[t] = ldexpf(1.0f, -k2);
+  if (tid == 0) {
+    unscale[t] = ldexpf(1.0f, -k2);
+    if (unscale_copy) unscale_copy[t] = ldexpf(1.0f, -k2);
+  }
   if constexpr (PER > 0) {
 #pragma unroll
     for (int k = 0; k < PER; k++)
@@ -262,7 +266,7 @@ void finish_pending_sum(hipStream_t s, PendingSum &p, float *y) {
 }
 
 void run_rms_norm_split(hipStream_t s, float *x, const float *w, float *out, uint32_t n, uint32_t rows, float eps,
-                        void *scratch, PendingSum *pending) {
+                        void *scratch, PendingSum *pending, float *unscale_copy) {
   if (!rows) return;
   _Float16 *hx = static_cast<_Float16 *>(scratch);
   float *unscale = reinterpret_cast<float *>(hx + (uint64_t)rows * n);
@@ -280,13 +284,13 @@ void run_rms_norm_split(hipStream_t s, float *x, const float *w, float *out, uin
   auto go = [&](auto per) {
     constexpr int PER = decltype(per)::value;
     if (!sum)
-      k_rms_norm_split<PER, 0><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale, P, splits);
+      k_rms_norm_split<PER, 0><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale, P, splits, unscale_copy);
     else if (splits == 2)
-      k_rms_norm_split<PER, 2><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale, P, splits);
+      k_rms_norm_split<PER, 2><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale, P, splits, unscale_copy);
     else if (splits == 4)
-      k_rms_norm_split<PER, 4><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale, P, splits);
+      k_rms_norm_split<PER, 4><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale, P, splits, unscale_copy);
     else
-      k_rms_norm_split<PER, 8><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale, P, splits);
+      k_rms_norm_split<PER, 8><<<rows, 256, 0, s>>>(x, w, out, n, eps, hx, unscale, P, splits, unscale_copy);
   };
   if (n <= 1024)
     go(std::integral_constant<int, 4>{});

@@ -291,11 +291,11 @@ void bch_qwen35::record_batch(hipStream_t st, uint32_t pos, uint32_t count, bool
       run_matmul(st, L.out.format, L.out.data, n, value_dim, delta_out, hidden, count, 1, split, split_bytes, false,
                  nullptr, defer);
     }
-    run_rms_norm_split(st, hidden, L.ffn_norm, normed, n, count, norm_eps, split, &pend);
+    const bool pair_ok = L.gate_up16 && count > kBlasPairMinTokens;
+    run_rms_norm_split(st, hidden, L.ffn_norm, normed, n, count, norm_eps, split, &pend, pair_ok ? pair_us : nullptr);
     // The pair through the library GEMM on the expanded weights when the
     // model has them; its SwiGLU also writes the down projection's inputs.
-    const bool blas_pair = L.gate_up16 && count > kBlasPairMinTokens &&
-                           run_blas_pair(st, L.gate_up16, n_ff, n, count, split, pair_out, pair_us, nullptr);
+    const bool blas_pair = pair_ok && run_blas_pair(st, L.gate_up16, n_ff, n, count, split, pair_out, pair_us, nullptr);
     if (!blas_pair && L.gate.format == L.up.format) {
       // Gate and up in one paired launch: ffn = silu(gate·x) ⊙ (up·x).
       run_matmul(st, L.gate.format, L.gate.data, n_ff, n, normed, ffn, count, 3, split, split_bytes, true,
